@@ -1,0 +1,137 @@
+/*
+ * pgmoe -- MI355X (gfx950) quantized mixture-of-experts FFN layer, C ABI.
+ *
+ * Replaces the hot path of PyGGUF's sparse MoE block, GGUFSparseMoEMLP.forward
+ * (pygguf_engine/model.py:898-937), with HIP kernels.  The Python class
+ * pgmoe.HipSparseMoEMLP keeps the reference's constructor/forward surface and calls
+ * these entry points through ctypes.
+ *
+ * Conventions for every entry point:
+ *   - returns 0 (PGMOE_OK) or a negative PGMOE_E_* status; pgmoe_last_error() holds a
+ *     thread-local message for the last failure on the calling thread;
+ *   - pointers are device pointers unless stated; sizes are element counts;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream); work is
+ *     enqueued on it with no host synchronisation and no device allocation;
+ *   - activations are IEEE fp16 passed as uint16_t bits; outputs are fp32.
+ *
+ * Device weight layout (pgmoe_weights.base, matrices mat_stride bytes apart, each
+ * exactly as many bytes as the GGUF blocks it holds, see pgmoe_weight_bytes):
+ *   Q4_K (type 12): GGUF blocks unchanged (144 B = 9 x 16 B, already 16-B aligned).
+ *   Q6_K (type 14): three planes per matrix, nb = cols/256 blocks per row:
+ *       body  [rows][nb][4 units][48 B]; unit u = 2h + half holds
+ *             ql[64h + 16half : +16] | ql[64h + 32 + 16half : +16] | qh[32h + 16half : +16]
+ *       scale [rows][nb][4 units][4 B] = sc[8h + 2s + half] for s = 0..3
+ *       d     [rows][nb] fp16
+ *   Q8_0 (type 8): two planes per matrix: qs [rows][cols] int8, d [rows][cols/32] fp16.
+ * pgmoe_relayout_weights() converts GGUF bytes already on the device into this layout.
+ */
+#ifndef PGMOE_H
+#define PGMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PGMOE_ABI_VERSION 1
+
+#define PGMOE_OK 0
+#define PGMOE_E_INVALID (-1)     /* bad argument, shape or pointer */
+#define PGMOE_E_UNSUPPORTED (-2) /* qtype / shape the kernels do not cover */
+#define PGMOE_E_WORKSPACE (-3)   /* workspace too small */
+#define PGMOE_E_HIP (-4)         /* HIP runtime error (launch or query) */
+
+#define PGMOE_Q8_0 8
+#define PGMOE_Q4_K 12
+#define PGMOE_Q6_K 14
+
+typedef struct pgmoe_weights {
+    int32_t qtype;      /* PGMOE_Q4_K / PGMOE_Q6_K / PGMOE_Q8_0 */
+    int32_t n_rows;     /* N: output features per matrix */
+    int32_t n_cols;     /* K: input features (multiple of 256 for K-quants, 64 for Q8_0) */
+    int32_t n_mats;     /* experts (1 for a shared expert) */
+    const void* base;   /* device layout described above, 16-B aligned */
+    int64_t mat_stride; /* bytes between consecutive matrices */
+} pgmoe_weights;
+
+typedef struct pgmoe_layer {
+    int32_t hidden;     /* H */
+    int32_t n_experts;  /* E <= 1024 */
+    int32_t top_k;      /* K <= min(E, 16) */
+    int32_t norm_topk;  /* renormalise the top-k weights (model.py:906-907) */
+    const float* router_w;    /* [E, H] fp32 */
+    const float* router_bias; /* [E] fp32 or NULL (harness extension; reference has none) */
+    pgmoe_weights gate, up, down; /* [E, I, H], [E, I, H], [E, H, I] */
+    int32_t has_shared;
+    pgmoe_weights sh_gate, sh_up, sh_down; /* [I_s, H], [I_s, H], [H, I_s] */
+    const float* sh_inp_gate; /* [H] fp32 or NULL: sigmoid gate on the shared expert */
+} pgmoe_layer;
+
+int pgmoe_abi_version(void);
+const char* pgmoe_last_error(void);
+
+/* Bytes of one matrix in the device layout (== GGUF bytes); -1 if unsupported. */
+int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
+
+/* GGUF blocks (device, n_mats matrices back to back) -> device layout.
+ * Load-time replacement of repack_gguf_to_w4a16 / repack_gguf_to_w8a16
+ * (quant_kernels.py:854-1036), keeping the GGUF bits instead of re-quantising. */
+int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
+                           void* dst, void* stream);
+
+/* Workspace bytes pgmoe_moe_forward needs for M tokens. */
+size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M);
+
+/* One MoE layer: out[M, H] = GGUFSparseMoEMLP.forward(x[M, H]) (model.py:898-937).
+ * Host-sync free and allocation free (graph-capturable with a fixed M). */
+int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
+                      size_t ws_bytes, void* stream);
+
+/* ---- stages of the forward, exposed for tests and for callers that fuse around them ---- */
+
+/* R1+R2: logits[M, E] = f32(x) . W^T (+ bias) in the fixed order of the CPU oracle,
+ * softmax, top-k by (logit desc, id asc), optional renorm (model.py:902-907).
+ * logits may be NULL.  topk_idx/topk_w are [M, K]. */
+int pgmoe_router_topk(const uint16_t* x, const float* w, const float* bias, int32_t M, int32_t H,
+                      int32_t E, int32_t K, int32_t norm_topk, float* logits, int32_t* topk_idx,
+                      float* topk_w, void* stream);
+
+/* R3: stable counting sort of the M*K flat pair ids (t*K + k) by expert
+ * (topk_indices.unique() / torch.where / index_select, model.py:911-914).
+ * offsets[E+1]; perm[M*K] = flat id at each sorted position; inv[M*K] = position of
+ * each flat id; active[E] = experts with rows, ascending; n_active[1];
+ * tile_off[E+1] = exclusive scan of ceil(count/tile_rows) (tile_rows > 0). */
+int pgmoe_dispatch(const int32_t* topk_idx, int32_t M, int32_t K, int32_t E, int32_t tile_rows,
+                   int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active,
+                   int32_t* tile_off, void* stream);
+
+/* R4+R5: inter[P, I] = silu(x_p . Wg_e^T) * (x_p . Wu_e^T) for every sorted pair position p,
+ * fp32 accumulate and output (gate/up_exps.forward_expert + exec_fused_act_mul_rowscale,
+ * model.py:916-918).  mode 0 = wavefront GEMV (M <= 8), 1 = MFMA grouped GEMM. */
+int pgmoe_expert_gateup(const pgmoe_weights* gate, const pgmoe_weights* up, const uint16_t* x,
+                        int32_t M, int32_t K, const int32_t* offsets, const int32_t* perm,
+                        const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
+                        int32_t mode, float* inter, void* stream);
+
+/* R6: partial[P, H] = w_p * (inter_p . Wd_e^T) (down_exps.forward_expert(...) * row_scale
+ * * topk weight, model.py:919-921).  mode 1 first rescales inter to fp16 per row exactly
+ * as exec_fused_act_mul_rowscale does (a16/rs are scratch [P, I] fp16 and [P] fp32;
+ * may be NULL in mode 0). */
+int pgmoe_expert_down(const pgmoe_weights* down, const float* inter, int32_t M, int32_t K,
+                      const int32_t* offsets, const int32_t* perm, const int32_t* active,
+                      const int32_t* n_active, const int32_t* tile_off, const float* topk_w,
+                      int32_t mode, uint16_t* a16, float* rs, float* partial, void* stream);
+
+/* R7(+R8): out[t, :] = sum over the token's K pairs in ascending expert id of
+ * partial[inv[t*K+k], :] (index_add_, model.py:921-922), plus
+ * shared[t, :] * sigmoid(shared_logit[t]) when shared != NULL (model.py:931-935;
+ * shared_logit NULL = gate 1). */
+int pgmoe_combine(const float* partial, const int32_t* inv, int32_t M, int32_t K, int32_t H,
+                  const float* shared, const float* shared_logit, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PGMOE_H */

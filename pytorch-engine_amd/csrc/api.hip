@@ -1,0 +1,295 @@
+// extern "C" entry points of libpgmoe.so (declared in include/pgmoe.h).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+#include "launch.h"
+
+namespace pgmoe {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(PGMOE_E_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+    return PGMOE_OK;
+}
+
+static int64_t raw_weight_bytes(int qtype, int64_t rows, int64_t cols) {
+    switch (qtype) {
+    case PGMOE_Q4_K: return cols % 256 ? -1 : rows * (cols / 256) * 144;
+    case PGMOE_Q6_K: return cols % 256 ? -1 : rows * (cols / 256) * 210;
+    case PGMOE_Q8_0: return cols % 64 ? -1 : rows * (cols / 32) * 34;
+    default: return -1;
+    }
+}
+
+int check_weights(const pgmoe_weights* w, const char* what, Mats* out) {
+    if (!w) return fail(PGMOE_E_INVALID, "%s: NULL weights", what);
+    if (w->qtype != PGMOE_Q4_K && w->qtype != PGMOE_Q6_K && w->qtype != PGMOE_Q8_0)
+        return fail(PGMOE_E_UNSUPPORTED, "%s: qtype %d not supported (Q4_K=12, Q6_K=14, Q8_0=8)", what, w->qtype);
+    if (w->n_rows <= 0 || w->n_cols <= 0 || w->n_mats <= 0)
+        return fail(PGMOE_E_INVALID, "%s: bad shape [%d, %d, %d]", what, w->n_mats, w->n_rows, w->n_cols);
+    const int64_t need = raw_weight_bytes(w->qtype, w->n_rows, w->n_cols);
+    if (need < 0)
+        return fail(PGMOE_E_UNSUPPORTED, "%s: %d input features is not a multiple of %d", what, w->n_cols,
+                    w->qtype == PGMOE_Q8_0 ? 64 : 256);
+    if (!w->base || ((uintptr_t)w->base & 15))
+        return fail(PGMOE_E_INVALID, "%s: base must be a 16-byte aligned device pointer", what);
+    if (w->n_mats > 1 && (w->mat_stride < need || (w->mat_stride & 15)))
+        return fail(PGMOE_E_INVALID, "%s: mat_stride %lld below %lld bytes or not 16-byte aligned", what,
+                    (long long)w->mat_stride, (long long)need);
+    out->qtype = w->qtype;
+    out->N = w->n_rows;
+    out->K = w->n_cols;
+    out->n_mats = w->n_mats;
+    out->base = (const uint8_t*)w->base;
+    out->stride = w->mat_stride;
+    return PGMOE_OK;
+}
+
+static int check_pair(const Mats& g, const Mats& u, const char* what) {
+    if (g.qtype != u.qtype || g.N != u.N || g.K != u.K || g.n_mats != u.n_mats)
+        return fail(PGMOE_E_UNSUPPORTED, "%s: gate and up must share qtype and shape", what);
+    return PGMOE_OK;
+}
+
+// ---------------------------------------------------------------- workspace layout
+struct Layout {
+    size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, inter, a16, rs, partial;
+    size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
+    size_t total;
+};
+
+static size_t take(size_t& cur, size_t bytes) {
+    const size_t at = cur;
+    cur += (bytes + 255) & ~(size_t)255;
+    return at;
+}
+
+static Layout layout_for(const pgmoe_layer* L, int M) {
+    Layout o{};
+    const size_t E = L->n_experts, K = L->top_k, H = L->hidden, I = L->gate.n_rows;
+    const size_t P = (size_t)M * K;
+    const bool gemm = M > decode_max_rows();
+    size_t c = 0;
+    o.logits = take(c, (size_t)M * E * 4);
+    o.idx = take(c, P * 4);
+    o.w = take(c, P * 4);
+    o.offsets = take(c, (E + 1) * 4);
+    o.perm = take(c, P * 4);
+    o.inv = take(c, P * 4);
+    o.active = take(c, E * 4);
+    o.nact = take(c, 4);
+    o.tile_off = take(c, (E + 1) * 4);
+    o.inter = take(c, P * I * 4);
+    o.a16 = take(c, gemm ? P * I * 2 : 0);
+    o.rs = take(c, gemm ? P * 4 : 0);
+    o.partial = take(c, P * H * 4);
+    if (L->has_shared) {
+        const size_t Is = L->sh_gate.n_rows;
+        o.s_offsets = take(c, 2 * 4);
+        o.s_perm = take(c, (size_t)M * 4);
+        o.s_inv = take(c, (size_t)M * 4);
+        o.s_active = take(c, 4);
+        o.s_nact = take(c, 4);
+        o.s_tile_off = take(c, 2 * 4);
+        o.s_w = take(c, (size_t)M * 4);
+        o.s_logit = take(c, (size_t)M * 4);
+        o.s_inter = take(c, (size_t)M * Is * 4);
+        o.s_a16 = take(c, gemm ? (size_t)M * Is * 2 : 0);
+        o.s_rs = take(c, gemm ? (size_t)M * 4 : 0);
+        o.s_partial = take(c, (size_t)M * H * 4);
+    }
+    o.total = c;
+    return o;
+}
+
+struct LayerMats {
+    Mats gate, up, down, sg, su, sd;
+};
+
+static int check_layer(const pgmoe_layer* L, LayerMats* lm) {
+    if (!L) return fail(PGMOE_E_INVALID, "NULL layer");
+    if (L->hidden <= 0 || L->hidden % 64)
+        return fail(PGMOE_E_UNSUPPORTED, "hidden size %d must be a positive multiple of 64", L->hidden);
+    if (L->n_experts < 1 || L->n_experts > 512)
+        return fail(PGMOE_E_UNSUPPORTED, "n_experts %d outside [1, 512]", L->n_experts);
+    if (L->top_k < 1 || L->top_k > L->n_experts || L->top_k > 16)
+        return fail(PGMOE_E_UNSUPPORTED, "top_k %d outside [1, min(E, 16)]", L->top_k);
+    if (!L->router_w) return fail(PGMOE_E_INVALID, "NULL router weight");
+    int rc;
+    if ((rc = check_weights(&L->gate, "gate", &lm->gate)) || (rc = check_weights(&L->up, "up", &lm->up)) ||
+        (rc = check_weights(&L->down, "down", &lm->down)) || (rc = check_pair(lm->gate, lm->up, "experts")))
+        return rc;
+    const Mats& g = lm->gate;
+    const Mats& d = lm->down;
+    if (g.n_mats != L->n_experts || d.n_mats != L->n_experts || g.K != L->hidden || d.N != L->hidden || d.K != g.N)
+        return fail(PGMOE_E_INVALID, "expert shapes do not match E=%d H=%d (gate [%d,%d,%d], down [%d,%d,%d])",
+                    L->n_experts, L->hidden, g.n_mats, g.N, g.K, d.n_mats, d.N, d.K);
+    if (L->has_shared) {
+        if ((rc = check_weights(&L->sh_gate, "shared gate", &lm->sg)) ||
+            (rc = check_weights(&L->sh_up, "shared up", &lm->su)) ||
+            (rc = check_weights(&L->sh_down, "shared down", &lm->sd)) || (rc = check_pair(lm->sg, lm->su, "shared")))
+            return rc;
+        if (lm->sg.K != L->hidden || lm->sd.N != L->hidden || lm->sd.K != lm->sg.N)
+            return fail(PGMOE_E_INVALID, "shared expert shapes do not match hidden size %d", L->hidden);
+    }
+    return PGMOE_OK;
+}
+
+}  // namespace pgmoe
+
+using namespace pgmoe;
+
+extern "C" {
+
+int pgmoe_abi_version(void) { return PGMOE_ABI_VERSION; }
+
+const char* pgmoe_last_error(void) { return g_err; }
+
+int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols) {
+    const int64_t b = raw_weight_bytes(qtype, rows, cols);
+    return b < 0 ? -1 : (b + 255) & ~(int64_t)255;
+}
+
+int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols, void* dst,
+                           void* stream) {
+    const int64_t raw = raw_weight_bytes(qtype, rows, cols);
+    if (raw < 0) return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld columns", qtype, (long long)cols);
+    if (!src || !dst || n_mats < 1 || rows < 1) return fail(PGMOE_E_INVALID, "relayout: bad arguments");
+    if ((uintptr_t)dst & 255) return fail(PGMOE_E_INVALID, "relayout: dst must be 256-byte aligned");
+    return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, (uint8_t*)dst,
+                           pgmoe_weight_bytes(qtype, rows, cols), as_stream(stream));
+}
+
+size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M) {
+    LayerMats lm;
+    if (M < 0 || check_layer(L, &lm)) return 0;
+    return layout_for(L, M).total;
+}
+
+int pgmoe_router_topk(const uint16_t* x, const float* w, const float* bias, int32_t M, int32_t H, int32_t E,
+                      int32_t K, int32_t norm_topk, float* logits, int32_t* topk_idx, float* topk_w, void* stream) {
+    if (M < 0 || H <= 0 || H % 8 || E < 1 || E > 1024 || K < 1 || K > E || K > 64)
+        return fail(PGMOE_E_INVALID, "router_topk: bad sizes M=%d H=%d E=%d K=%d", M, H, E, K);
+    if (M == 0) return PGMOE_OK;
+    if (!x || !w || !logits || !topk_idx || !topk_w) return fail(PGMOE_E_INVALID, "router_topk: NULL pointer");
+    const hipStream_t st = as_stream(stream);
+    int rc = launch_router_logits(x, w, bias, M, H, E, logits, st);
+    if (rc) return rc;
+    return launch_topk(logits, M, E, K, norm_topk, topk_idx, topk_w, st);
+}
+
+int pgmoe_dispatch(const int32_t* topk_idx, int32_t M, int32_t K, int32_t E, int32_t tile_rows, int32_t* offsets,
+                   int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off,
+                   void* stream) {
+    if (M < 0 || K < 1 || E < 1 || E > 512 || tile_rows < 1)
+        return fail(PGMOE_E_INVALID, "dispatch: bad sizes M=%d K=%d E=%d tile_rows=%d", M, K, E, tile_rows);
+    if (!offsets || !perm || !inv || !active || !n_active || !tile_off || (M > 0 && !topk_idx))
+        return fail(PGMOE_E_INVALID, "dispatch: NULL pointer");
+    return launch_dispatch(topk_idx, M, K, E, tile_rows, offsets, perm, inv, active, n_active, tile_off,
+                           as_stream(stream));
+}
+
+int pgmoe_expert_gateup(const pgmoe_weights* gate, const pgmoe_weights* up, const uint16_t* x, int32_t M,
+                        int32_t K, const int32_t* offsets, const int32_t* perm, const int32_t* active,
+                        const int32_t* n_active, const int32_t* tile_off, int32_t mode, float* inter,
+                        void* stream) {
+    Mats g, u;
+    int rc;
+    if ((rc = check_weights(gate, "gate", &g)) || (rc = check_weights(up, "up", &u)) ||
+        (rc = check_pair(g, u, "gate/up")))
+        return rc;
+    if (M < 0 || K < 1 || (mode != 0 && mode != 1)) return fail(PGMOE_E_INVALID, "gateup: bad M/K/mode");
+    return launch_gateup(g, u, x, M, K, offsets, perm, active, n_active, tile_off, mode, inter, as_stream(stream));
+}
+
+int pgmoe_expert_down(const pgmoe_weights* down, const float* inter, int32_t M, int32_t K, const int32_t* offsets,
+                      const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
+                      const float* topk_w, int32_t mode, uint16_t* a16, float* rs, float* partial, void* stream) {
+    Mats d;
+    int rc;
+    if ((rc = check_weights(down, "down", &d))) return rc;
+    if (M < 0 || K < 1 || (mode != 0 && mode != 1)) return fail(PGMOE_E_INVALID, "down: bad M/K/mode");
+    return launch_down(d, inter, M, K, offsets, perm, active, n_active, tile_off, topk_w, mode, a16, rs, partial,
+                       as_stream(stream));
+}
+
+int pgmoe_combine(const float* partial, const int32_t* inv, int32_t M, int32_t K, int32_t H, const float* shared,
+                  const float* shared_logit, float* out, void* stream) {
+    if (M < 0 || K < 1 || H < 1) return fail(PGMOE_E_INVALID, "combine: bad sizes");
+    return launch_combine(partial, inv, M, K, H, shared, shared_logit, out, as_stream(stream));
+}
+
+int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws, size_t ws_bytes,
+                      void* stream) {
+    LayerMats lm;
+    int rc = check_layer(L, &lm);
+    if (rc) return rc;
+    if (M < 0) return fail(PGMOE_E_INVALID, "negative token count");
+    if (M == 0) return PGMOE_OK;
+    if (!x || !out || !ws) return fail(PGMOE_E_INVALID, "moe_forward: NULL pointer");
+    if ((uintptr_t)ws & 255) return fail(PGMOE_E_INVALID, "workspace must be 256-byte aligned");
+    const Layout o = layout_for(L, M);
+    if (ws_bytes < o.total)
+        return fail(PGMOE_E_WORKSPACE, "workspace %zu bytes, need %zu", ws_bytes, o.total);
+    uint8_t* b = (uint8_t*)ws;
+#define WS(T, f) reinterpret_cast<T*>(b + o.f)
+    const hipStream_t st = as_stream(stream);
+    const int E = L->n_experts, K = L->top_k, H = L->hidden;
+    const int mode = M > decode_max_rows() ? 1 : 0;
+    const int BM = gemm_tile_rows();
+    if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st))) return rc;
+    if ((rc = launch_topk(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w), st))) return rc;
+    if ((rc = launch_dispatch(WS(int32_t, idx), M, K, E, BM, WS(int32_t, offsets), WS(int32_t, perm),
+                              WS(int32_t, inv), WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), st)))
+        return rc;
+    if ((rc = launch_gateup(lm.gate, lm.up, x, M, K, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
+                            WS(int32_t, nact), WS(int32_t, tile_off), mode, WS(float, inter), st)))
+        return rc;
+    if ((rc = launch_down(lm.down, WS(float, inter), M, K, WS(int32_t, offsets), WS(int32_t, perm),
+                          WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), WS(float, w), mode,
+                          WS(uint16_t, a16), WS(float, rs), WS(float, partial), st)))
+        return rc;
+    const float* shared = nullptr;
+    const float* shared_logit = nullptr;
+    if (L->has_shared) {
+        if ((rc = launch_identity_dispatch(M, BM, WS(int32_t, s_offsets), WS(int32_t, s_perm), WS(int32_t, s_inv),
+                                           WS(int32_t, s_active), WS(int32_t, s_nact), WS(int32_t, s_tile_off),
+                                           WS(float, s_w), st)))
+            return rc;
+        if ((rc = launch_gateup(lm.sg, lm.su, x, M, 1, WS(int32_t, s_offsets), WS(int32_t, s_perm),
+                                WS(int32_t, s_active), WS(int32_t, s_nact), WS(int32_t, s_tile_off), mode,
+                                WS(float, s_inter), st)))
+            return rc;
+        if ((rc = launch_down(lm.sd, WS(float, s_inter), M, 1, WS(int32_t, s_offsets), WS(int32_t, s_perm),
+                              WS(int32_t, s_active), WS(int32_t, s_nact), WS(int32_t, s_tile_off), WS(float, s_w),
+                              mode, WS(uint16_t, s_a16), WS(float, s_rs), WS(float, s_partial), st)))
+            return rc;
+        shared = WS(float, s_partial);
+        if (L->sh_inp_gate) {
+            if ((rc = launch_router_logits(x, L->sh_inp_gate, nullptr, M, H, 1, WS(float, s_logit), st))) return rc;
+            shared_logit = WS(float, s_logit);
+        }
+    }
+    return launch_combine(WS(float, partial), WS(int32_t, inv), M, K, H, shared, shared_logit, out, st);
+#undef WS
+}
+
+}  // extern "C"

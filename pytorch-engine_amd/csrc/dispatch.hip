@@ -1,0 +1,150 @@
+// R3: token -> expert dispatch as a stable counting sort, entirely on the device.
+// Reference: pygguf_engine/model.py:911-914 (topk_indices.unique().tolist(), torch.where,
+// index_select) -- that loop needs a device->host sync per layer; this kernel does not.
+#include "common.h"
+#include "launch.h"
+
+namespace pgmoe {
+
+constexpr int kDispThreads = 1024;
+constexpr int kDispWaves = kDispThreads / 64;
+constexpr int kMaxExperts = 512;  // keeps the per-(wave, expert) counters at 32 KB of LDS
+
+// Inclusive scan of one int per thread over the block (Hillis-Steele in LDS).
+__device__ int block_inclusive_scan(int v, int* buf) {
+    const int t = threadIdx.x;
+    buf[t] = v;
+    __syncthreads();
+    for (int off = 1; off < kDispThreads; off <<= 1) {
+        const int add = t >= off ? buf[t - off] : 0;
+        __syncthreads();
+        buf[t] += add;
+        __syncthreads();
+    }
+    const int r = buf[t];
+    __syncthreads();
+    return r;
+}
+
+// Single workgroup.  Flat pair ids f = t*K + k are split into kDispWaves contiguous
+// chunks, one per wavefront.  Pass 1 counts ids per (wave, expert); a scan turns the
+// counts into per-(wave, expert) base positions; pass 2 walks each chunk in order,
+// 64 ids at a time, ranking equal ids among the lanes with ballots, which keeps the sort
+// stable (ascending f inside every expert, the order torch.where produces).
+__global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* __restrict__ idx, int P, int E,
+                                                                int tile_rows, int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ perm,
+                                                                int32_t* __restrict__ inv,
+                                                                int32_t* __restrict__ active,
+                                                                int32_t* __restrict__ n_active,
+                                                                int32_t* __restrict__ tile_off) {
+    __shared__ int cnt[kDispWaves][kMaxExperts];
+    __shared__ int scan_buf[kDispThreads];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    for (int i = t; i < kDispWaves * kMaxExperts; i += kDispThreads) (&cnt[0][0])[i] = 0;
+    __syncthreads();
+    const int chunk = (P + kDispWaves - 1) / kDispWaves;
+    const int c0 = wv * chunk, c1 = min(P, c0 + chunk);
+    // ids outside [0, E) are skipped (never written to LDS or to perm/inv)
+    for (int f = c0 + lane; f < c1; f += 64) {
+        const int id = idx[f];
+        if ((unsigned)id < (unsigned)E) atomicAdd(&cnt[wv][id], 1);
+    }
+    __syncthreads();
+
+    // per-expert totals -> offsets; per-(wave, expert) bases
+    const int e = t;
+    int total = 0;
+    if (e < E)
+        for (int w = 0; w < kDispWaves; ++w) total += cnt[w][e];
+    const int incl = block_inclusive_scan(e < E ? total : 0, scan_buf);
+    const int excl = incl - total;
+    if (e < E) {
+        offsets[e] = excl;
+        if (e == E - 1) offsets[E] = incl;
+        int run = excl;
+        for (int w = 0; w < kDispWaves; ++w) {
+            const int c = cnt[w][e];
+            cnt[w][e] = run;
+            run += c;
+        }
+    }
+    // active expert list and GEMM tile offsets
+    const int has = (e < E && total > 0) ? 1 : 0;
+    const int ai = block_inclusive_scan(has, scan_buf);
+    if (has) active[ai - 1] = e;
+    if (e == E - 1) *n_active = ai;
+    const int nt = (e < E) ? (total + tile_rows - 1) / tile_rows : 0;
+    const int ti = block_inclusive_scan(nt, scan_buf);
+    if (e < E) {
+        tile_off[e] = ti - nt;
+        if (e == E - 1) tile_off[E] = ti;
+    }
+    __syncthreads();
+
+    // pass 2: stable scatter; every wave runs the same number of steps
+    const int steps = (chunk + 63) / 64;
+    for (int s = 0; s < steps; ++s) {
+        const int f = c0 + 64 * s + lane;
+        const int id = f < c1 ? idx[f] : -1;
+        const bool valid = (unsigned)id < (unsigned)E;
+        // lanes holding the same id: intersect ballots over the id's bits
+        uint64_t same = __ballot(valid);
+        if (!valid) same = 0;
+        for (int b = 0; b < 9; ++b) {  // E <= 512 -> ids < 2^9
+            const bool bit = valid && ((id >> b) & 1);
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
+        }
+        if (valid) {
+            const uint64_t below = same & ((1ull << lane) - 1ull);
+            const int rank = __popcll(below);
+            const int pos = cnt[wv][id] + rank;
+            perm[pos] = f;
+            inv[f] = pos;
+            if ((same >> lane) == 1ull)  // highest lane of its id group advances the base
+                cnt[wv][id] += __popcll(same);
+        }
+        __syncthreads();
+    }
+}
+
+// Identity dispatch of M tokens to one matrix (shared expert): offsets {0, M},
+// perm = inv = 0..M-1, active {0}, n_active 1, tile_off {0, ceil(M / tile_rows)}, w = 1.
+__global__ void identity_dispatch_kernel(int M, int tile_rows, int32_t* offsets, int32_t* perm, int32_t* inv,
+                                         int32_t* active, int32_t* n_active, int32_t* tile_off, float* w) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < M) {
+        perm[i] = i;
+        inv[i] = i;
+        w[i] = 1.0f;
+    }
+    if (i == 0) {
+        offsets[0] = 0;
+        offsets[1] = M;
+        active[0] = 0;
+        *n_active = M > 0 ? 1 : 0;
+        tile_off[0] = 0;
+        tile_off[1] = (M + tile_rows - 1) / tile_rows;
+    }
+}
+
+int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int32_t* offsets, int32_t* perm,
+                    int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st) {
+    if (E > kMaxExperts) return fail(PGMOE_E_UNSUPPORTED, "dispatch supports at most %d experts", kMaxExperts);
+    if (tile_rows <= 0) return fail(PGMOE_E_INVALID, "tile_rows must be positive");
+    const int64_t P = (int64_t)M * K;
+    if (P > (1 << 30)) return fail(PGMOE_E_UNSUPPORTED, "too many token-expert pairs");
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, st, idx, (int)P, E, tile_rows, offsets,
+                       perm, inv, active, n_active, tile_off);
+    return check_launch("dispatch");
+}
+
+int launch_identity_dispatch(int M, int tile_rows, int32_t* offsets, int32_t* perm, int32_t* inv,
+                             int32_t* active, int32_t* n_active, int32_t* tile_off, float* w, hipStream_t st) {
+    hipLaunchKernelGGL(identity_dispatch_kernel, dim3(div_up(M > 0 ? M : 1, 256)), dim3(256), 0, st, M,
+                       tile_rows, offsets, perm, inv, active, n_active, tile_off, w);
+    return check_launch("identity_dispatch");
+}
+
+}  // namespace pgmoe

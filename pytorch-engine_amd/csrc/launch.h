@@ -1,0 +1,28 @@
+// Host-side launchers shared between the translation units of libpgmoe.so.
+#pragma once
+
+#include "common.h"
+
+namespace pgmoe {
+
+int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
+                         float* logits, hipStream_t st);
+int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w, hipStream_t st);
+int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int32_t* offsets, int32_t* perm,
+                    int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st);
+int launch_identity_dispatch(int M, int tile_rows, int32_t* offsets, int32_t* perm, int32_t* inv,
+                             int32_t* active, int32_t* n_active, int32_t* tile_off, float* w, hipStream_t st);
+int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
+                  const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
+                  int mode, float* inter, hipStream_t st);
+int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_t* offsets, const int32_t* perm,
+                const int32_t* active, const int32_t* n_active, const int32_t* tile_off, const float* topk_w,
+                int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st);
+int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H, const float* shared,
+                   const float* shared_logit, float* out, hipStream_t st);
+int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, uint8_t* dst,
+                    int64_t dst_stride, hipStream_t st);
+int gemm_tile_rows();
+int decode_max_rows();
+
+}  // namespace pgmoe

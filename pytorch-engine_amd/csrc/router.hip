@@ -1,0 +1,177 @@
+// R1 + R2: router logits in a fixed reduction order, then softmax / top-k / renorm.
+// Reference: pygguf_engine/model.py:902-907.
+#include "common.h"
+#include "launch.h"
+
+namespace pgmoe {
+
+// logits[m, e] = sum_h f32(x[m, h]) * W[e, h] (+ bias[e]).
+// One wavefront per (TM tokens, TE experts) tile.  Lane l is "slot" l: it owns the 8-wide
+// chunks c = l, l+64, l+128, ... of the row and runs one fmaf chain over them in
+// ascending order; the 64 slot sums are then combined by the xor tree
+// (l, l^32), (l, l^16), ..., (l, l^1); the bias is added last.  The CPU oracle
+// (or_router_logits) performs the same operations in the same order, so both produce
+// identical bits.
+template <int TM, int TE>
+__global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
+                                                            const float* __restrict__ W,
+                                                            const float* __restrict__ bias, int M, int H,
+                                                            int E, float* __restrict__ logits) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int n_etiles = (E + TE - 1) / TE;
+    const int mt = wave / n_etiles, et = wave % n_etiles;
+    const int m0 = mt * TM, e0 = et * TE;
+    if (m0 >= M) return;
+    const int C = H >> 3;
+    float acc[TM][TE];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
+    for (int c = lane; c < C; c += 64) {
+        float xv[TM][8];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int m = m0 + i < M ? m0 + i : M - 1;
+            const uint4 v = *(const uint4*)(x + (int64_t)m * H + 8 * c);
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                xv[i][2 * k] = lo_half(w4[k]);
+                xv[i][2 * k + 1] = hi_half(w4[k]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TE; ++j) {
+            const int e = e0 + j < E ? e0 + j : E - 1;
+            const float4 w0 = *(const float4*)(W + (int64_t)e * H + 8 * c);
+            const float4 w1 = *(const float4*)(W + (int64_t)e * H + 8 * c + 4);
+            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[i][j] = __builtin_fmaf(xv[i][k], wv[k], acc[i][j]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TE; ++j) {
+            float v = group_sum<64>(acc[i][j]);
+            const int m = m0 + i, e = e0 + j;
+            if (lane == 0 && m < M && e < E) {
+                if (bias) v = v + bias[e];
+                logits[(int64_t)m * E + e] = v;
+            }
+        }
+}
+
+// Per token: top-K experts by (logit desc, id asc); w = softmax prob (max-subtracted,
+// denominator over all E); optional renorm w / max(sum w, 1e-20).  One wavefront per token.
+// Selection on logits equals selection on softmax probabilities (monotone map).
+template <int R>  // logits held per lane: E <= 64 * R
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int M, int E, int K,
+                                                   int norm, int32_t* __restrict__ idx,
+                                                   float* __restrict__ w) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const float* l = logits + (int64_t)m * E;
+    float v[R];
+    bool taken[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int e = lane + 64 * r;
+        v[r] = e < E ? l[e] : 0.0f;
+        taken[r] = e >= E;
+    }
+    float top_logit = 0.0f, sum_sel = 0.0f;
+    float my_w = 0.0f;
+    int my_id = -1;
+    for (int k = 0; k < K; ++k) {
+        // lane-local best among untaken, lower id first on ties
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int e = lane + 64 * r;
+            if (!taken[r] && (bi == 0x7fffffff || v[r] > bv)) {
+                bv = v[r];
+                bi = e;
+            }
+        }
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) {
+            const float ov = __shfl_xor(bv, s, 64);
+            const int oi = __shfl_xor(bi, s, 64);
+            if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            if (lane + 64 * r == bi) taken[r] = true;
+        if (k == 0) top_logit = bv;
+        if (lane == k) {
+            my_id = bi;
+            my_w = bv;  // logit for now
+        }
+    }
+    // softmax denominator over all experts
+    float den = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        if (lane + 64 * r < E) den += expf(v[r] - top_logit);
+    den = group_sum<64>(den);
+    float p = lane < K ? expf(my_w - top_logit) / den : 0.0f;
+    sum_sel = group_sum<64>(p);
+    if (norm) p = p / fmaxf(sum_sel, 1e-20f);
+    if (lane < K) {
+        idx[(int64_t)m * K + lane] = my_id;
+        w[(int64_t)m * K + lane] = p;
+    }
+}
+
+int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
+                         float* logits, hipStream_t st) {
+    if (M <= 0) return PGMOE_OK;
+    const int threads = 256;
+    if (M <= 4) {
+        // decode: one wave per (all tokens, one expert) spreads the router read widely
+        constexpr int TM = 4, TE = 1;
+        const int waves = div_up(M, TM) * div_up(E, TE);
+        hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
+                           x, W, bias, M, H, E, logits);
+    } else if (M <= 8) {
+        constexpr int TM = 8, TE = 1;
+        const int waves = div_up(M, TM) * div_up(E, TE);
+        hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
+                           x, W, bias, M, H, E, logits);
+    } else {
+        constexpr int TM = 8, TE = 4;
+        const int waves = div_up(M, TM) * div_up(E, TE);
+        hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
+                           x, W, bias, M, H, E, logits);
+    }
+    return check_launch("router_logits");
+}
+
+int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w, hipStream_t st) {
+    if (M <= 0) return PGMOE_OK;
+    const dim3 grid(div_up(M, 4)), block(256);
+    if (E <= 64)
+        hipLaunchKernelGGL((topk_kernel<1>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+    else if (E <= 128)
+        hipLaunchKernelGGL((topk_kernel<2>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+    else if (E <= 256)
+        hipLaunchKernelGGL((topk_kernel<4>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+    else if (E <= 1024)
+        hipLaunchKernelGGL((topk_kernel<16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+    else
+        return fail(PGMOE_E_UNSUPPORTED, "top-k supports at most 1024 experts (got %d)", E);
+    return check_launch("topk");
+}
+
+}  // namespace pgmoe

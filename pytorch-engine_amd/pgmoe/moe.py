@@ -1,0 +1,218 @@
+"""HipSparseMoEMLP: drop-in replacement for PyGGUF's GGUFSparseMoEMLP on MI355X.
+
+Same constructor ``(gguf_file, config, layer_idx, device)`` and ``forward(x) -> fp32`` as
+pygguf_engine/model.py:849-937, reading the same tensors:
+
+    blk.{i}.ffn_gate_inp.weight            router [E, H] (F32 / F16 / BF16)
+    blk.{i}.ffn_{gate,up,down}_exps.weight  routed experts [E, I, H] / [E, H, I]
+    blk.{i}.ffn_{gate,up,down}_shexp.weight optional shared expert
+    blk.{i}.ffn_gate_inp_shexp.weight       optional shared-expert sigmoid gate [H]
+
+and the config fields ``n_experts``, ``n_experts_used``, ``norm_topk_prob`` and ``arch``.
+Expert weights stay in GGUF block form on the device (Q4_K as-is, Q6_K / Q8_0 moved
+into aligned planes of the same bits); the whole forward is one C-ABI call that
+enqueues router, top-k, dispatch, expert products and combine without a host sync.
+"""
+
+from __future__ import annotations
+
+import threading
+from typing import Any, Dict, Optional
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from . import ops
+from ._lib import SUPPORTED_QTYPES, Layer, Weights, check, lib
+
+_F32, _F16, _BF16 = 0, 1, 30
+_load_lock = threading.Lock()
+
+
+def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.Tensor:
+    """fp32 copy of an unquantised tensor on ``device`` (quant_kernels.py:1097-1116 for
+    F32 / F16 / BF16; quantised router weights are not supported here)."""
+    info = gguf_file.tensors[name]
+    raw = gguf_file.get_tensor_bytes(name)
+    if info.qtype == _F32:
+        arr = torch.from_numpy(np.frombuffer(raw, dtype=np.float32).reshape(info.shape).copy())
+    elif info.qtype == _F16:
+        arr = torch.from_numpy(np.frombuffer(raw, dtype=np.float16).reshape(info.shape).copy()).float()
+    elif info.qtype == _BF16:
+        u16 = np.frombuffer(raw, dtype=np.uint16).reshape(info.shape).copy()
+        arr = torch.from_numpy(u16.view(np.int16)).view(torch.bfloat16).float()
+    else:
+        raise NotImplementedError(f"{name}: router/gate tensors of ggml type {info.qtype} are not supported")
+    return arr.to(device=device, dtype=torch.float32).contiguous()
+
+
+class _ExpertTensor:
+    """One quantised weight tensor ([E, N, K] or [N, K]) held in the device layout."""
+
+    def __init__(self, gguf_file: Any, name: str, device: torch.device, three_d: bool):
+        info = gguf_file.tensors[name]
+        shape = tuple(int(s) for s in info.shape)
+        if three_d and len(shape) != 3:
+            raise ValueError(f"Expected 3D MoE tensor for {name}, got shape={shape}")
+        if not three_d and len(shape) != 2:
+            raise ValueError(f"Expected 2D tensor for {name}, got shape={shape}")
+        self.n_mats, self.rows, self.cols = (shape if three_d else (1,) + shape)
+        self.qtype = int(info.qtype)
+        if self.qtype not in SUPPORTED_QTYPES:
+            raise NotImplementedError(
+                f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
+                "has no HIP kernel (supported: Q4_K, Q6_K, Q8_0)")
+        if self.cols % (64 if self.qtype == 8 else 256):
+            raise ValueError(f"{name}: {self.cols} input features is not a whole number of kernel units")
+        raw_np = gguf_file.get_tensor_bytes(name)
+        raw = torch.from_numpy(np.asarray(raw_np)).to(device)  # H2D copy of the GGUF bytes
+        self.buf = ops.relayout(self.qtype, raw, self.n_mats, self.rows, self.cols)
+        del raw
+
+    def weights(self) -> Weights:
+        return ops.make_weights(self.qtype, self.buf, self.n_mats, self.rows, self.cols)
+
+    @property
+    def gguf_bytes_per_mat(self) -> int:
+        per, bb = ops.GGUF_BLOCK[self.qtype]
+        return self.rows * (self.cols // per) * bb
+
+
+class HipSparseMoEMLP(nn.Module):
+    """Sparse MoE FFN block (router -> top-k -> grouped GGUF expert SwiGLU -> combine)."""
+
+    def __init__(self, gguf_file: Any, config: Any, layer_idx: int, device: torch.device) -> None:
+        super().__init__()
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise ValueError("HipSparseMoEMLP runs on a HIP device (torch.device('cuda', i))")
+        if device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        lib()  # fail now, not at the first forward, when the HIP library is missing
+        self.config = config
+        self.device = device
+        self.n_experts = int(config.n_experts)
+        self.top_k = max(1, int(config.n_experts_used))
+        self.norm_topk_prob = bool(config.norm_topk_prob)
+        self.use_gelu = str(config.arch).startswith("gemma")
+        if self.use_gelu:
+            raise NotImplementedError("GeGLU experts (gemma) are not implemented by the HIP kernels")
+
+        prefix = f"blk.{layer_idx}"
+        with _load_lock, torch.cuda.device(device):
+            router = load_float_tensor(gguf_file, f"{prefix}.ffn_gate_inp.weight", device)
+            self.register_buffer("router_weight", router, persistent=False)
+            self.router_bias: Optional[torch.Tensor] = None
+            self.gate_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate_exps.weight", device, True)
+            self.up_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_up_exps.weight", device, True)
+            self.down_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_exps.weight", device, True)
+            self.shared_gate = self.shared_up = self.shared_down = None
+            self.shared_inp_gate: Optional[torch.Tensor] = None
+            if f"{prefix}.ffn_gate_shexp.weight" in gguf_file.tensors:
+                self.shared_gate = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate_shexp.weight", device, False)
+                self.shared_up = _ExpertTensor(gguf_file, f"{prefix}.ffn_up_shexp.weight", device, False)
+                self.shared_down = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_shexp.weight", device, False)
+                gname = f"{prefix}.ffn_gate_inp_shexp.weight"
+                if gname in gguf_file.tensors:
+                    self.shared_inp_gate = load_float_tensor(gguf_file, gname, device).reshape(-1).contiguous()
+            torch.cuda.current_stream(device).synchronize()  # uploads done before host buffers go away
+        self.hidden = int(self.router_weight.shape[1])
+        if self.router_weight.shape[0] != self.n_experts:
+            raise ValueError(f"router has {self.router_weight.shape[0]} rows, config says {self.n_experts} experts")
+        self._ws: Dict[int, torch.Tensor] = {}
+        self._layer = self._build_layer()
+
+    # ------------------------------------------------------------------ plumbing
+    def set_router_bias(self, bias: Optional[torch.Tensor]) -> None:
+        """Harness-only extension: add bias[e] to the router logits before softmax."""
+        if bias is not None:
+            bias = bias.to(device=self.device, dtype=torch.float32).reshape(-1).contiguous()
+            if bias.numel() != self.n_experts:
+                raise ValueError("router bias must have n_experts entries")
+        self.router_bias = bias
+        self._layer = self._build_layer()
+
+    def _build_layer(self) -> Layer:
+        L = Layer()
+        L.hidden = self.hidden
+        L.n_experts = self.n_experts
+        L.top_k = self.top_k
+        L.norm_topk = int(self.norm_topk_prob)
+        L.router_w = self.router_weight.data_ptr()
+        L.router_bias = self.router_bias.data_ptr() if self.router_bias is not None else None
+        L.gate = self.gate_exps.weights()
+        L.up = self.up_exps.weights()
+        L.down = self.down_exps.weights()
+        if self.shared_gate is not None:
+            L.has_shared = 1
+            L.sh_gate = self.shared_gate.weights()
+            L.sh_up = self.shared_up.weights()
+            L.sh_down = self.shared_down.weights()
+            L.sh_inp_gate = self.shared_inp_gate.data_ptr() if self.shared_inp_gate is not None else None
+        return L
+
+    def workspace_bytes(self, M: int) -> int:
+        n = lib().pgmoe_workspace_bytes(self._layer, M)
+        if n == 0 and M > 0:
+            check(-1, "pgmoe_workspace_bytes")
+        return int(n)
+
+    def _workspace(self, M: int) -> torch.Tensor:
+        ws = self._ws.get(M)
+        if ws is None:
+            n = self.workspace_bytes(M) + 256
+            raw = torch.empty(n, dtype=torch.uint8, device=self.device)
+            off = (-raw.data_ptr()) % 256
+            ws = raw[off:]
+            self._ws = {M: ws}  # keep one size: callers alternate between few M values
+        return ws
+
+    # ------------------------------------------------------------------ forward
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        orig_shape = x.shape
+        x_2d = x.reshape(-1, orig_shape[-1])
+        if x_2d.shape[1] != self.hidden:
+            raise ValueError(f"expected hidden size {self.hidden}, got {x_2d.shape[1]}")
+        if x_2d.device != self.device:
+            x_2d = x_2d.to(self.device, non_blocking=True)
+        if x_2d.dtype != torch.float16:
+            x_2d = x_2d.to(torch.float16)
+        x_2d = x_2d.contiguous()
+        M = x_2d.shape[0]
+        out = torch.empty((M, self.hidden), dtype=torch.float32, device=self.device)
+        if M:
+            ws = self._workspace(M)
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            check(lib().pgmoe_moe_forward(self._layer, x_2d.data_ptr(), M, out.data_ptr(), ws.data_ptr(),
+                                          ws.numel(), stream), "pgmoe_moe_forward")
+        return out.reshape(orig_shape)
+
+    def replica(self) -> "HipSparseMoEMLP":
+        """A copy of this layer with its own device copy of every expert weight (used to
+        rotate weight sets in benchmarks so reads come from HBM, not the 256 MB MALL)."""
+        import copy
+
+        r = copy.copy(self)
+        r._modules = dict(self._modules)
+        r._buffers = dict(self._buffers)
+        for name in ("gate_exps", "up_exps", "down_exps", "shared_gate", "shared_up", "shared_down"):
+            t = getattr(self, name)
+            if t is not None:
+                c = copy.copy(t)
+                c.buf = t.buf.clone()
+                object.__setattr__(r, name, c)
+        r._ws = {}
+        r._layer = r._build_layer()
+        return r
+
+    # ------------------------------------------------------------------ accounting
+    def active_weight_bytes(self, n_distinct: int) -> int:
+        """GGUF bytes of `n_distinct` routed experts (gate + up + down)."""
+        per = sum(t.gguf_bytes_per_mat for t in (self.gate_exps, self.up_exps, self.down_exps))
+        return n_distinct * per
+
+    def shared_weight_bytes(self) -> int:
+        if self.shared_gate is None:
+            return 0
+        return sum(t.gguf_bytes_per_mat for t in (self.shared_gate, self.shared_up, self.shared_down))

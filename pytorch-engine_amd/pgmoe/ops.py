@@ -1,0 +1,132 @@
+"""Tensor-level wrappers of the C ABI stages (device tensors in, device tensors out).
+
+Each function enqueues work on the current HIP stream of the tensors' device and returns
+without synchronising.  They mirror the steps of GGUFSparseMoEMLP.forward
+(pygguf_engine/model.py:898-937) and exist for tests and for callers that want to fuse
+around individual stages; ``HipSparseMoEMLP`` uses the one-call ``pgmoe_moe_forward``.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from ._lib import Q4_K, Q6_K, Q8_0, Weights, check, lib
+
+GGUF_BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _need_cuda(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError("pgmoe kernels take device tensors")
+        if not t.is_contiguous():
+            raise ValueError("pgmoe kernels take contiguous tensors")
+        dev = t.device
+    assert dev is not None
+    return dev
+
+
+def weight_stride(qtype: int, rows: int, cols: int) -> int:
+    n = lib().pgmoe_weight_bytes(qtype, rows, cols)
+    if n < 0:
+        raise ValueError(f"qtype {qtype} with {cols} columns is not supported by the HIP kernels")
+    return int(n)
+
+
+def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int) -> torch.Tensor:
+    """GGUF bytes on the device -> pgmoe device layout (uint8 [n_mats * stride])."""
+    dev = _need_cuda(raw)
+    stride = weight_stride(qtype, rows, cols)
+    per, bb = GGUF_BLOCK[qtype]
+    if raw.numel() != n_mats * rows * (cols // per) * bb:
+        raise ValueError("raw byte count does not match the tensor shape")
+    dst = torch.empty(n_mats * stride, dtype=torch.uint8, device=dev)
+    check(lib().pgmoe_relayout_weights(qtype, raw.data_ptr(), n_mats, rows, cols, dst.data_ptr(), _stream(dev)),
+          "pgmoe_relayout_weights")
+    return dst
+
+
+def make_weights(qtype: int, buf: torch.Tensor, n_mats: int, rows: int, cols: int) -> Weights:
+    return Weights(qtype, rows, cols, n_mats, buf.data_ptr(), weight_stride(qtype, rows, cols))
+
+
+def router_topk(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], k: int, norm: bool
+                ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    dev = _need_cuda(x, w, bias)
+    M, H = x.shape
+    E = w.shape[0]
+    logits = torch.empty((M, E), dtype=torch.float32, device=dev)
+    idx = torch.empty((M, k), dtype=torch.int32, device=dev)
+    tw = torch.empty((M, k), dtype=torch.float32, device=dev)
+    check(lib().pgmoe_router_topk(x.data_ptr(), w.data_ptr(), _ptr(bias), M, H, E, k, int(norm),
+                                  logits.data_ptr(), idx.data_ptr(), tw.data_ptr(), _stream(dev)),
+          "pgmoe_router_topk")
+    return logits, idx, tw
+
+
+def dispatch(idx: torch.Tensor, n_experts: int, tile_rows: int = 64):
+    dev = _need_cuda(idx)
+    M, K = idx.shape
+    P = M * K
+    i32 = dict(dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_experts + 1, **i32)
+    perm = torch.empty(max(P, 1), **i32)
+    inv = torch.empty(max(P, 1), **i32)
+    active = torch.empty(n_experts, **i32)
+    n_active = torch.empty(1, **i32)
+    tile_off = torch.empty(n_experts + 1, **i32)
+    check(lib().pgmoe_dispatch(idx.data_ptr(), M, K, n_experts, tile_rows, offsets.data_ptr(), perm.data_ptr(),
+                               inv.data_ptr(), active.data_ptr(), n_active.data_ptr(), tile_off.data_ptr(),
+                               _stream(dev)), "pgmoe_dispatch")
+    return offsets, perm[:P], inv[:P], active, n_active, tile_off
+
+
+def expert_gateup(gate: Weights, up: Weights, x: torch.Tensor, top_k: int, disp, mode: int) -> torch.Tensor:
+    dev = _need_cuda(x)
+    offsets, perm, inv, active, n_active, tile_off = disp
+    M = x.shape[0]
+    inter = torch.empty((M * top_k, gate.n_rows), dtype=torch.float32, device=dev)
+    check(lib().pgmoe_expert_gateup(gate, up, x.data_ptr(), M, top_k, offsets.data_ptr(), perm.data_ptr(),
+                                    active.data_ptr(), n_active.data_ptr(), tile_off.data_ptr(), mode,
+                                    inter.data_ptr(), _stream(dev)), "pgmoe_expert_gateup")
+    return inter
+
+
+def expert_down(down: Weights, inter: torch.Tensor, M: int, top_k: int, disp, topk_w: torch.Tensor, mode: int
+                ) -> torch.Tensor:
+    dev = _need_cuda(inter, topk_w)
+    offsets, perm, inv, active, n_active, tile_off = disp
+    P = M * top_k
+    partial = torch.empty((P, down.n_rows), dtype=torch.float32, device=dev)
+    a16 = rs = None
+    if mode == 1:
+        a16 = torch.empty((P, down.n_cols), dtype=torch.float16, device=dev)
+        rs = torch.empty(P, dtype=torch.float32, device=dev)
+    check(lib().pgmoe_expert_down(down, inter.data_ptr(), M, top_k, offsets.data_ptr(), perm.data_ptr(),
+                                  active.data_ptr(), n_active.data_ptr(), tile_off.data_ptr(), topk_w.data_ptr(),
+                                  mode, _ptr(a16), _ptr(rs), partial.data_ptr(), _stream(dev)),
+          "pgmoe_expert_down")
+    return partial
+
+
+def combine(partial: torch.Tensor, inv: torch.Tensor, M: int, top_k: int,
+            shared: Optional[torch.Tensor] = None, shared_logit: Optional[torch.Tensor] = None) -> torch.Tensor:
+    dev = _need_cuda(partial, inv, shared, shared_logit)
+    H = partial.shape[1]
+    out = torch.empty((M, H), dtype=torch.float32, device=dev)
+    check(lib().pgmoe_combine(partial.data_ptr(), inv.data_ptr(), M, top_k, H, _ptr(shared), _ptr(shared_logit),
+                              out.data_ptr(), _stream(dev)), "pgmoe_combine")
+    return out

@@ -1,0 +1,185 @@
+"""CPU-side checks of the C ABI and the host code (no GPU work is launched here):
+the library loads and exports every symbol of include/pgmoe.h, argument validation
+returns the documented status codes, and the GGUF reader/writer round-trips."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from pgmoe import _lib
+from pgmoe.gguf import GGMLType, GGUFFile, GGUFWriter, InMemoryGGUF
+from pgmoe.synth import CONFIGS, SyntheticLayer, random_blocks
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "pgmoe.h")
+
+
+def test_library_exports_every_header_symbol():
+    L = _lib.lib()
+    text = open(HEADER).read()
+    names = sorted(set(re.findall(r"\b(pgmoe_[a-z_0-9]+)\s*\(", text)))
+    assert names, "no declarations parsed"
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in pgmoe.h but not exported"
+    assert set(_lib.EXPORTS) <= set(names)
+    assert L.pgmoe_abi_version() == _lib.ABI_VERSION
+
+
+def test_weight_bytes_are_gguf_bytes_rounded_to_256():
+    L = _lib.lib()
+    for qt, rows, cols, per, bb in [(12, 768, 2048, 256, 144), (14, 2048, 768, 256, 210),
+                                    (8, 2560, 3584, 32, 34), (14, 1, 256, 256, 210)]:
+        raw = rows * (cols // per) * bb
+        assert L.pgmoe_weight_bytes(qt, rows, cols) == (raw + 255) // 256 * 256
+    assert L.pgmoe_weight_bytes(12, 4, 100) == -1  # not a whole K-quant block row
+    assert L.pgmoe_weight_bytes(2, 4, 256) == -1   # Q4_0 has no kernel
+    assert L.pgmoe_weight_bytes(8, 4, 96) == -1    # Q8_0 rows must be whole 64-weight units
+
+
+def _fake_layer(E=8, K=2, H=1024, I=512, qt=12, shared=False):
+    """A layer struct with aligned fake device pointers (validation never dereferences)."""
+    W = _lib.Weights
+    stride = _lib.lib().pgmoe_weight_bytes(qt, I, H)
+    L = _lib.Layer()
+    L.hidden, L.n_experts, L.top_k, L.norm_topk = H, E, K, 1
+    L.router_w = 0x10000
+    L.gate = W(qt, I, H, E, 0x100000, stride)
+    L.up = W(qt, I, H, E, 0x200000, stride)
+    L.down = W(qt, H, I, E, 0x300000, _lib.lib().pgmoe_weight_bytes(qt, H, I))
+    if shared:
+        L.has_shared = 1
+        L.sh_gate = W(qt, 2 * I, H, 1, 0x400000, 0)
+        L.sh_up = W(qt, 2 * I, H, 1, 0x500000, 0)
+        L.sh_down = W(qt, H, 2 * I, 1, 0x600000, 0)
+    return L
+
+
+def test_workspace_bytes_and_zero_tokens():
+    L = _lib.lib()
+    lay = _fake_layer()
+    w1 = L.pgmoe_workspace_bytes(lay, 1)
+    w16 = L.pgmoe_workspace_bytes(lay, 16)
+    assert 0 < w1 < w16
+    assert L.pgmoe_workspace_bytes(_fake_layer(shared=True), 16) > w16
+    # M = 0 validates and returns without touching the device
+    assert L.pgmoe_moe_forward(lay, None, 0, None, None, 0, None) == 0
+
+
+@pytest.mark.parametrize("mutate,code,msg", [
+    (lambda l: setattr(l.gate, "qtype", 2), -2, "qtype"),
+    (lambda l: setattr(l.up, "base", 0x200008), -1, "aligned"),
+    (lambda l: setattr(l, "top_k", 9), -2, "top_k"),
+    (lambda l: setattr(l, "hidden", 1000), -2, "hidden"),
+    (lambda l: setattr(l.down, "n_rows", 512), -1, "shapes"),
+    (lambda l: setattr(l.gate, "mat_stride", 64), -1, "mat_stride"),
+    (lambda l: setattr(l, "n_experts", 600), -2, "n_experts"),
+])
+def test_forward_validation_errors(mutate, code, msg):
+    L = _lib.lib()
+    lay = _fake_layer()
+    mutate(lay)
+    rc = L.pgmoe_moe_forward(lay, 0x1000, 4, 0x2000, 0x3000, 1 << 30, None)
+    assert rc == code
+    assert msg in L.pgmoe_last_error().decode()
+
+
+def test_workspace_too_small_reported():
+    L = _lib.lib()
+    lay = _fake_layer()
+    need = L.pgmoe_workspace_bytes(lay, 4)
+    rc = L.pgmoe_moe_forward(lay, 0x1000, 4, 0x2000, 0x3000, need - 1, None)
+    assert rc == -3 and "workspace" in L.pgmoe_last_error().decode()
+    rc = L.pgmoe_moe_forward(lay, 0x1000, 4, 0x2000, 0x3008, need, None)
+    assert rc == -1  # misaligned workspace
+
+
+def test_stage_validation_errors():
+    L = _lib.lib()
+    assert L.pgmoe_router_topk(0x1000, 0x2000, None, 4, 100, 8, 2, 1, 0x3000, 0x4000, 0x5000, None) == -1
+    assert L.pgmoe_router_topk(0x1000, 0x2000, None, 4, 128, 8, 9, 1, 0x3000, 0x4000, 0x5000, None) == -1
+    assert L.pgmoe_dispatch(0x1000, 4, 2, 600, 64, 1, 1, 1, 1, 1, 1, None) == -1
+    assert L.pgmoe_dispatch(0x1000, 4, 2, 8, 0, 1, 1, 1, 1, 1, 1, None) == -1
+    bad = _lib.Weights(12, 100, 300, 1, 0x1000, 0)
+    good = _lib.Weights(12, 100, 256, 1, 0x1000, 0)
+    assert L.pgmoe_expert_gateup(bad, bad, 0x1000, 1, 1, 1, 1, 1, 1, 1, 0, 0x2000, None) == -2
+    q6 = _lib.Weights(14, 100, 256, 1, 0x2000, 0)
+    assert L.pgmoe_expert_gateup(good, q6, 0x1000, 1, 1, 1, 1, 1, 1, 1, 0, 0x2000, None) == -2
+    assert L.pgmoe_relayout_weights(12, 0x1000, 1, 4, 256, 0x2010, None) == -1
+    assert L.pgmoe_combine(0x1000, 0x2000, 3, 0, 16, None, None, 0x3000, None) == -1
+
+
+def test_module_rejects_cpu_device():
+    import torch
+    from pgmoe import HipSparseMoEMLP
+    lay = SyntheticLayer(CONFIGS["tiny"], seed=0, scale=0.01)
+    with pytest.raises(ValueError):
+        HipSparseMoEMLP(lay.gguf, lay.config, 0, torch.device("cpu"))
+
+
+def test_gguf_writer_reader_roundtrip(tmp_path):
+    rng = np.random.default_rng(0)
+    w = GGUFWriter()
+    w.add_meta("general.architecture", "qwen3moe")
+    w.add_meta("qwen3moe.expert_count", 4)
+    w.add_meta("qwen3moe.expert_used_count", 2)
+    w.add_meta("qwen3moe.embedding_length", 256)
+    q4 = random_blocks(rng, 12, 4 * 128, 256)
+    q8 = random_blocks(rng, 8, 256, 64)
+    r = rng.standard_normal((4, 256)).astype(np.float32)
+    w.add_tensor("blk.0.ffn_gate_exps.weight", (4, 128, 256), 12, q4)
+    w.add_tensor("blk.0.ffn_gate_inp.weight", (4, 256), 0, r.view(np.uint8))
+    w.add_tensor("x.weight", (256, 64), 8, q8)
+    p = tmp_path / "t.gguf"
+    w.write(p)
+    with GGUFFile(p) as g:
+        assert g.version == 3
+        info = g.tensors["blk.0.ffn_gate_exps.weight"]
+        assert info.shape == (4, 128, 256) and info.ggml_dims == (256, 128, 4) and info.qtype == 12
+        assert np.array_equal(g.get_tensor_bytes("blk.0.ffn_gate_exps.weight"), q4)
+        assert np.array_equal(g.get_tensor_bytes("x.weight"), q8)
+        assert np.array_equal(g.get_tensor_bytes("blk.0.ffn_gate_inp.weight").view(np.float32).reshape(4, 256), r)
+        cfg = g.build_model_config()
+        assert (cfg.n_experts, cfg.n_experts_used, cfg.norm_topk_prob, cfg.hidden_size) == (4, 2, True, 256)
+        assert g.tensor_data_offset % 32 == 0
+
+
+def test_gguf_reader_rejects_garbage(tmp_path):
+    p = tmp_path / "bad.gguf"
+    p.write_bytes(b"NOPE" + b"\0" * 64)
+    with pytest.raises(ValueError):
+        GGUFFile(p)
+
+
+def test_config_defaults_follow_arch():
+    g = InMemoryGGUF({"general.architecture": "qwen2moe", "qwen2moe.expert_count": 64,
+                      "qwen2moe.expert_used_count": 8})
+    assert g.build_model_config().norm_topk_prob is False
+    g2 = InMemoryGGUF({"general.architecture": "mixtral"})
+    assert g2.build_model_config().norm_topk_prob is True
+
+
+def test_synthetic_generator_is_seeded_and_shaped():
+    a = SyntheticLayer(CONFIGS["tiny"], seed=1)
+    b = SyntheticLayer(CONFIGS["tiny"], seed=1)
+    for name in a.gguf.tensors:
+        assert np.array_equal(a.gguf.get_tensor_bytes(name), b.gguf.get_tensor_bytes(name))
+    assert a.gguf.tensors["blk.0.ffn_down_exps.weight"].shape == (8, 1024, 512)
+    x1, x2 = a.draw_x(16), b.draw_x(16)
+    assert x1.dtype == np.float16 and np.array_equal(x1, x2)
+    blk = a.tensor("ffn_gate_exps.weight").reshape(-1, 144)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float32)
+    assert np.all(d >= 0) and 0.005 < np.median(d) < 0.03  # |N(0,1)| * 0.02
+
+
+def test_zipf_bias_skews_loads():
+    import oracle
+    lay = SyntheticLayer(CONFIGS["qwen3_30b_a3b_zipf"], seed=0)
+    assert lay.router_bias is not None and lay.router_bias.shape == (128,)
+    ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config, router_bias=lay.router_bias)
+    x = lay.draw_x(512)
+    _, idx, _ = ol.route(x)
+    counts = np.bincount(idx.reshape(-1), minlength=128)
+    assert counts.max() > 8 * counts.mean()

@@ -1,0 +1,228 @@
+"""GPU parity of the individual C-ABI stages against the CPU oracle.
+
+Integer/index stages (router logits in their fixed order, top-k ids, dispatch) must be
+bit-exact; floating-point stages are checked with the tolerances stated per test.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_helpers import log
+from pgmoe.synth import random_blocks
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+Q4_K, Q6_K, Q8_0 = 12, 14, 8
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda", 0)
+
+
+def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
+    """The device layout of include/pgmoe.h, built with numpy."""
+    out = np.zeros(n_mats * stride, dtype=np.uint8)
+    if qtype == Q4_K:
+        mb = rows * (cols // 256) * 144
+        for m in range(n_mats):
+            out[m * stride:m * stride + mb] = raw[m * mb:(m + 1) * mb]
+        return out
+    if qtype == Q8_0:
+        nbm = rows * (cols // 32)
+        blk = raw.reshape(n_mats, nbm, 34)
+        for m in range(n_mats):
+            base = m * stride
+            out[base:base + nbm * 32] = blk[m, :, 2:].reshape(-1)
+            out[base + nbm * 32:base + nbm * 34] = blk[m, :, 0:2].reshape(-1)
+        return out
+    nbm = rows * (cols // 256)
+    blk = raw.reshape(n_mats, nbm, 210)
+    for m in range(n_mats):
+        base = m * stride
+        b = blk[m]
+        body = np.zeros((nbm, 4, 48), np.uint8)
+        scl = np.zeros((nbm, 4, 4), np.uint8)
+        for un in range(4):
+            h, half = un >> 1, un & 1
+            body[:, un, 0:16] = b[:, 64 * h + 16 * half:64 * h + 16 * half + 16]
+            body[:, un, 16:32] = b[:, 64 * h + 32 + 16 * half:64 * h + 48 + 16 * half]
+            body[:, un, 32:48] = b[:, 128 + 32 * h + 16 * half:128 + 32 * h + 16 * half + 16]
+            for s in range(4):
+                scl[:, un, s] = b[:, 192 + 8 * h + 2 * s + half]
+        out[base:base + nbm * 192] = body.reshape(-1)
+        out[base + nbm * 192:base + nbm * 208] = scl.reshape(-1)
+        out[base + nbm * 208:base + nbm * 210] = b[:, 208:210].reshape(-1)
+    return out
+
+
+@pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q8_0, 5, 192, 2),
+                                                    (Q6_K, 2048, 768, 2)])
+def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
+    from pgmoe import ops
+    rng = np.random.default_rng(rows * cols)
+    raw = np.concatenate([random_blocks(rng, qtype, rows, cols) for _ in range(n_mats)])
+    buf = ops.relayout(qtype, torch.from_numpy(raw).to(dev), n_mats, rows, cols)
+    stride = ops.weight_stride(qtype, rows, cols)
+    got = buf.cpu().numpy()
+    ref = _np_relayout(qtype, raw, n_mats, rows, cols, stride)
+    # padding bytes between matrices are unspecified
+    mb = rows * (cols // ops.GGUF_BLOCK[qtype][0]) * ops.GGUF_BLOCK[qtype][1]
+    for m in range(n_mats):
+        assert np.array_equal(got[m * stride:m * stride + mb], ref[m * stride:m * stride + mb])
+
+
+@pytest.mark.parametrize("M,H,E,K,bias", [(1, 2048, 128, 8, False), (8, 2048, 128, 8, False),
+                                          (333, 2048, 128, 8, True), (4096, 2048, 128, 8, True),
+                                          (5, 1024, 8, 2, False), (64, 3584, 64, 8, False),
+                                          (17, 4096, 8, 2, False), (3, 512, 512, 16, False)])
+def test_router_topk_bitexact(dev, M, H, E, K, bias):
+    from pgmoe import ops
+    log(f"router M={M} H={H} E={E} K={K}")
+    rng = np.random.default_rng(M + H + E)
+    x = rng.standard_normal((M, H), dtype=np.float32).astype(np.float16)
+    w = (rng.standard_normal((E, H), dtype=np.float32) * 0.02).astype(np.float32)
+    b = rng.standard_normal(E).astype(np.float32) if bias else None
+    lg, idx, tw = ops.router_topk(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                                  None if b is None else torch.from_numpy(b).to(dev), K, True)
+    ref_lg = oracle.router_logits(x, w, b)
+    ref_idx, ref_w = oracle.topk(ref_lg, K, True)
+    assert np.array_equal(lg.cpu().numpy().view(np.uint32), ref_lg.view(np.uint32))
+    assert np.array_equal(idx.cpu().numpy(), ref_idx)
+    np.testing.assert_allclose(tw.cpu().numpy(), ref_w, rtol=2e-6, atol=1e-7)
+    _, _, tw2 = ops.router_topk(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                                None if b is None else torch.from_numpy(b).to(dev), K, False)
+    _, ref_w2 = oracle.topk(ref_lg, K, False)
+    np.testing.assert_allclose(tw2.cpu().numpy(), ref_w2, rtol=2e-6, atol=1e-8)
+
+
+def test_topk_ties_lower_id_wins(dev):
+    from pgmoe import ops
+    H, E, K, M = 512, 16, 4, 6
+    x = np.zeros((M, H), np.float16)
+    x[:, 0] = 1.0
+    w = np.zeros((E, H), np.float32)
+    w[:, 0] = np.array([1, 3, 3, 2, 3, 0, 3, 1, 2, 2, 0, 0, 3, 1, 1, 2], np.float32)
+    _, idx, _ = ops.router_topk(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev), None, K, True)
+    assert np.all(idx.cpu().numpy() == np.array([1, 2, 4, 6], np.int32))
+
+
+@pytest.mark.parametrize("M,K,E,skew", [(1, 8, 128, None), (8, 8, 128, None), (4096, 8, 128, None),
+                                        (4096, 8, 128, "one"), (16, 2, 8, None), (1000, 1, 1, None),
+                                        (512, 8, 64, "half"), (3, 16, 512, None), (0, 8, 128, None)])
+def test_dispatch_bitexact(dev, M, K, E, skew):
+    from pgmoe import ops
+    log(f"dispatch M={M} K={K} E={E} skew={skew}")
+    rng = np.random.default_rng(M * 7 + K)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32).reshape(M, K)
+    if skew == "one" and M:
+        idx[:, 0] = 5  # every token picks expert 5 ...
+        for t in range(M):  # ... keeping ids distinct per token
+            row = [e for e in rng.permutation(E) if e != 5][:K - 1]
+            idx[t, 1:] = row
+    if skew == "half" and M:
+        idx = np.stack([np.sort(rng.permutation(E // 2)[:K]) for _ in range(M)]).astype(np.int32)
+    offsets, perm, inv, active, n_active, tile_off = ops.dispatch(torch.from_numpy(idx).to(dev), E, 64)
+    r_off, r_perm, r_inv = oracle.dispatch(idx, E)
+    assert np.array_equal(offsets.cpu().numpy(), r_off)
+    assert np.array_equal(perm.cpu().numpy(), r_perm)
+    assert np.array_equal(inv.cpu().numpy(), r_inv)
+    counts = np.diff(r_off)
+    act = np.nonzero(counts)[0]
+    assert int(n_active.cpu()[0]) == len(act)
+    assert np.array_equal(active.cpu().numpy()[:len(act)], act)
+    tiles = (counts + 63) // 64
+    assert np.array_equal(tile_off.cpu().numpy(), np.concatenate([[0], np.cumsum(tiles)]))
+
+
+def _dense(qtype, raw, n_mats, rows, cols):
+    return oracle.dequant(qtype, raw, n_mats * rows, cols).reshape(n_mats, rows, cols).astype(np.float64)
+
+
+@pytest.mark.parametrize("qg,qd,H,I,E,K,M,mode", [
+    (Q4_K, Q6_K, 512, 256, 8, 2, 1, 0), (Q4_K, Q6_K, 512, 256, 8, 2, 8, 0),
+    (Q4_K, Q4_K, 256, 512, 4, 2, 5, 0), (Q8_0, Q8_0, 192, 320, 6, 3, 7, 0),
+    (Q4_K, Q6_K, 512, 256, 8, 2, 40, 1), (Q4_K, Q4_K, 256, 512, 4, 2, 130, 1),
+    (Q8_0, Q8_0, 192, 320, 6, 3, 70, 1), (Q6_K, Q8_0, 256, 256, 3, 1, 9, 1),
+    (Q4_K, Q6_K, 512, 256, 8, 2, 3, 1)])
+def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
+    """inter and the weighted down partials against float64 numpy over decoded weights.
+    Tolerance: GEMV keeps fp32 everywhere (rel-L2 1e-5); GEMM uses fp16 weights/x and a
+    per-row fp16 down input (rel-L2 2e-3, i.e. fp16 rounding, same as the reference's
+    own GPU prefill path)."""
+    from pgmoe import ops
+    log(f"stages qg={qg} qd={qd} H={H} I={I} E={E} K={K} M={M} mode={mode}")
+    rng = np.random.default_rng(H + I + M)
+    gr = np.concatenate([random_blocks(rng, qg, I, H) for _ in range(E)])
+    ur = np.concatenate([random_blocks(rng, qg, I, H) for _ in range(E)])
+    dr = np.concatenate([random_blocks(rng, qd, H, I) for _ in range(E)])
+    x = rng.standard_normal((M, H), dtype=np.float32).astype(np.float16)
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32)
+    tw = rng.random((M, K)).astype(np.float32)
+    gb = ops.relayout(qg, torch.from_numpy(gr).to(dev), E, I, H)
+    ub = ops.relayout(qg, torch.from_numpy(ur).to(dev), E, I, H)
+    db = ops.relayout(qd, torch.from_numpy(dr).to(dev), E, H, I)
+    Wg, Wu, Wd = ops.make_weights(qg, gb, E, I, H), ops.make_weights(qg, ub, E, I, H), ops.make_weights(qd, db, E, H, I)
+    disp = ops.dispatch(torch.from_numpy(idx).to(dev), E, 64)
+    xd = torch.from_numpy(x).to(dev)
+    inter = ops.expert_gateup(Wg, Wu, xd, K, disp, mode)
+    tw_d = torch.from_numpy(tw).to(dev)
+    partial = ops.expert_down(Wd, inter, M, K, disp, tw_d, mode)
+    torch.cuda.synchronize()
+    _, perm, _ = oracle.dispatch(idx, E)
+    g = _dense(qg, gr, E, I, H)
+    u = _dense(qg, ur, E, I, H)
+    d = _dense(qd, dr, E, H, I)
+    xf = x.astype(np.float64)
+    P = M * K
+    ref_inter = np.empty((P, I))
+    for p in range(P):
+        f = perm[p]
+        t, k = divmod(int(f), K)
+        e = idx[t, k]
+        gv, uv = g[e] @ xf[t], u[e] @ xf[t]
+        ref_inter[p] = gv / (1 + np.exp(-gv)) * uv
+    got_inter = inter.cpu().numpy()
+    tol = 1e-5 if mode == 0 else 2e-3
+    assert oracle.rel_l2(got_inter, ref_inter) < tol
+    ref_part = np.empty((P, H))
+    gi = got_inter.astype(np.float64)
+    for p in range(P):
+        t, k = divmod(int(perm[p]), K)
+        ref_part[p] = tw[t, k] * (d[idx[t, k]] @ gi[p])
+    assert oracle.rel_l2(partial.cpu().numpy(), ref_part) < tol
+    assert oracle.max_rel(partial.cpu().numpy(), ref_part) < 50 * tol
+
+
+def test_combine_order_and_shared(dev):
+    from pgmoe import ops
+    rng = np.random.default_rng(5)
+    M, K, H, E = 9, 4, 128, 16
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32)
+    _, perm, inv = oracle.dispatch(idx, E)
+    part = rng.standard_normal((M * K, H)).astype(np.float32) * np.float32(1e4)
+    sh = rng.standard_normal((M, H)).astype(np.float32)
+    slog = rng.standard_normal(M).astype(np.float32)
+    out = ops.combine(torch.from_numpy(part).to(dev), torch.from_numpy(inv).to(dev), M, K,
+                      torch.from_numpy(sh).to(dev), torch.from_numpy(slog).to(dev)).cpu().numpy()
+    ref = np.zeros((M, H), np.float32)
+    for t in range(M):
+        acc = np.zeros(H, np.float32)
+        for k in np.argsort(idx[t], kind="stable"):  # ascending expert id
+            acc = acc + part[inv[t * K + k]]
+        gate = np.float32(1.0) / (np.float32(1.0) + np.exp(-slog[t]))
+        ref[t] = acc + sh[t] * gate
+    np.testing.assert_allclose(out, ref, rtol=1e-6, atol=1e-6)
+    # routed part alone is summed in ascending expert order: bitwise
+    out2 = ops.combine(torch.from_numpy(part).to(dev), torch.from_numpy(inv).to(dev), M, K).cpu().numpy()
+    ref2 = np.zeros((M, H), np.float32)
+    for t in range(M):
+        acc = np.zeros(H, np.float32)
+        for k in np.argsort(idx[t], kind="stable"):
+            acc = acc + part[inv[t * K + k]]
+        ref2[t] = acc
+    assert np.array_equal(out2, ref2)
