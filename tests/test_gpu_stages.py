@@ -118,7 +118,7 @@ def test_dispatch_bitexact(dev, M, K, E, skew):
     from pgmoe import ops
     log(f"dispatch M={M} K={K} E={E} skew={skew}")
     rng = np.random.default_rng(M * 7 + K)
-    idx = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32).reshape(M, K)
+    idx = np.array([rng.permutation(E)[:K] for _ in range(M)], dtype=np.int32).reshape(M, K)
     if skew == "one" and M:
         idx[:, 0] = 5  # every token picks expert 5 ...
         for t in range(M):  # ... keeping ids distinct per token
