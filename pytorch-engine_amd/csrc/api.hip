@@ -30,25 +30,15 @@ int check_launch(const char* what) {
     return PGMOE_OK;
 }
 
-static int64_t raw_weight_bytes(int qtype, int64_t rows, int64_t cols) {
-    switch (qtype) {
-    case PGMOE_Q4_K: return cols % 256 ? -1 : rows * (cols / 256) * 144;
-    case PGMOE_Q6_K: return cols % 256 ? -1 : rows * (cols / 256) * 210;
-    case PGMOE_Q8_0: return cols % 64 ? -1 : rows * (cols / 32) * 34;
-    default: return -1;
-    }
-}
-
 int check_weights(const pgmoe_weights* w, const char* what, Mats* out) {
     if (!w) return fail(PGMOE_E_INVALID, "%s: NULL weights", what);
     if (w->qtype != PGMOE_Q4_K && w->qtype != PGMOE_Q6_K && w->qtype != PGMOE_Q8_0)
         return fail(PGMOE_E_UNSUPPORTED, "%s: qtype %d not supported (Q4_K=12, Q6_K=14, Q8_0=8)", what, w->qtype);
     if (w->n_rows <= 0 || w->n_cols <= 0 || w->n_mats <= 0)
         return fail(PGMOE_E_INVALID, "%s: bad shape [%d, %d, %d]", what, w->n_mats, w->n_rows, w->n_cols);
-    const int64_t need = raw_weight_bytes(w->qtype, w->n_rows, w->n_cols);
+    const int64_t need = layout_bytes(w->qtype, w->n_rows, w->n_cols);
     if (need < 0)
-        return fail(PGMOE_E_UNSUPPORTED, "%s: %d input features is not a multiple of %d", what, w->n_cols,
-                    w->qtype == PGMOE_Q8_0 ? 64 : 256);
+        return fail(PGMOE_E_UNSUPPORTED, "%s: %d input features is not a multiple of 256", what, w->n_cols);
     if (!w->base || ((uintptr_t)w->base & 15))
         return fail(PGMOE_E_INVALID, "%s: base must be a 16-byte aligned device pointer", what);
     if (w->n_mats > 1 && (w->mat_stride < need || (w->mat_stride & 15)))
@@ -71,6 +61,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
+    size_t counters, s_disp;
     size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, inter, a16, rs, partial;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
@@ -86,8 +77,11 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     Layout o{};
     const size_t E = L->n_experts, K = L->top_k, H = L->hidden, I = L->gate.n_rows;
     const size_t P = (size_t)M * K;
-    const bool gemm = M > decode_max_rows();
+    const bool gemm = M > decode_tokens_max();
     size_t c = 0;
+    // self-resetting completion counters: [0] router, [16 + rg] down row groups
+    o.counters = take(c, (16 + (size_t)row_groups((int)H)) * 4);
+    o.s_disp = take(c, (4 + (size_t)M) * 4);
     o.logits = take(c, (size_t)M * E * 4);
     o.idx = take(c, P * 4);
     o.w = take(c, P * 4);
@@ -126,8 +120,8 @@ struct LayerMats {
 
 static int check_layer(const pgmoe_layer* L, LayerMats* lm) {
     if (!L) return fail(PGMOE_E_INVALID, "NULL layer");
-    if (L->hidden <= 0 || L->hidden % 64)
-        return fail(PGMOE_E_UNSUPPORTED, "hidden size %d must be a positive multiple of 64", L->hidden);
+    if (L->hidden <= 0 || L->hidden % 256 || L->hidden > 65536)
+        return fail(PGMOE_E_UNSUPPORTED, "hidden size %d must be a positive multiple of 256 (<= 65536)", L->hidden);
     if (L->n_experts < 1 || L->n_experts > 512)
         return fail(PGMOE_E_UNSUPPORTED, "n_experts %d outside [1, 512]", L->n_experts);
     if (L->top_k < 1 || L->top_k > L->n_experts || L->top_k > 16)
@@ -164,14 +158,14 @@ int pgmoe_abi_version(void) { return PGMOE_ABI_VERSION; }
 const char* pgmoe_last_error(void) { return g_err; }
 
 int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols) {
-    const int64_t b = raw_weight_bytes(qtype, rows, cols);
+    const int64_t b = layout_bytes(qtype, rows, cols);
     return b < 0 ? -1 : (b + 255) & ~(int64_t)255;
 }
 
 int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols, void* dst,
                            void* stream) {
-    const int64_t raw = raw_weight_bytes(qtype, rows, cols);
-    if (raw < 0) return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld columns", qtype, (long long)cols);
+    if (layout_bytes(qtype, rows, cols) < 0)
+        return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld columns", qtype, (long long)cols);
     if (!src || !dst || n_mats < 1 || rows < 1) return fail(PGMOE_E_INVALID, "relayout: bad arguments");
     if ((uintptr_t)dst & 255) return fail(PGMOE_E_INVALID, "relayout: dst must be 256-byte aligned");
     return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, (uint8_t*)dst,
@@ -253,8 +247,36 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
 #define WS(T, f) reinterpret_cast<T*>(b + o.f)
     const hipStream_t st = as_stream(stream);
     const int E = L->n_experts, K = L->top_k, H = L->hidden;
-    const int mode = M > decode_max_rows() ? 1 : 0;
+    const int mode = M > decode_tokens_max() ? 1 : 0;
     const int BM = gemm_tile_rows();
+    int32_t* counters = WS(int32_t, counters);
+    if (mode == 0) {
+        // decode: route (+ shared identity dispatch) -> gate/up -> [shared] -> down + combine
+        int32_t* sd = L->has_shared ? WS(int32_t, s_disp) : nullptr;
+        if ((rc = launch_route_small(x, L->router_w, L->router_bias, L->has_shared ? L->sh_inp_gate : nullptr, M, H, E,
+                                     K, L->norm_topk, WS(float, logits), WS(float, s_logit), WS(int32_t, idx),
+                                     WS(float, w), WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv),
+                                     WS(int32_t, active), WS(int32_t, nact), sd, WS(float, s_w), counters, st)))
+            return rc;
+        const int max_active = M * K < E ? M * K : E;
+        if ((rc = launch_dec_gateup(lm.gate, lm.up, x, K, WS(int32_t, offsets), WS(int32_t, perm),
+                                    WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, inter), st)))
+            return rc;
+        const float* shared = nullptr;
+        const float* shared_logit = nullptr;
+        if (L->has_shared) {
+            if ((rc = launch_dec_gateup(lm.sg, lm.su, x, 1, sd, sd + 4, sd + 2, sd + 3, 1, WS(float, s_inter), st)))
+                return rc;
+            if ((rc = launch_dec_down(lm.sd, WS(float, s_inter), sd, sd + 4, sd + 2, sd + 3, 1, WS(float, s_w),
+                                      WS(float, s_partial), M, 1, nullptr, nullptr, nullptr, nullptr, nullptr, st)))
+                return rc;
+            shared = WS(float, s_partial);
+            if (L->sh_inp_gate) shared_logit = WS(float, s_logit);
+        }
+        return launch_dec_down(lm.down, WS(float, inter), WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
+                               WS(int32_t, nact), max_active, WS(float, w), WS(float, partial), M, K, WS(int32_t, inv),
+                               shared, shared_logit, out, counters + 16, st);
+    }
     if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st))) return rc;
     if ((rc = launch_topk(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w), st))) return rc;
     if ((rc = launch_dispatch(WS(int32_t, idx), M, K, E, BM, WS(int32_t, offsets), WS(int32_t, perm),

@@ -38,26 +38,50 @@ __device__ __forceinline__ float group_sum(float v) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
+// ---------------------------------------------------------------- device weight layout
+// Every matrix [N rows, K cols] (K a multiple of 256) is stored as tiles of 64 rows x one
+// 256-weight super-block.  A tile holds CH 16-byte chunks per row, chunk-major:
+//     tile(rg, b) = base + (rg * nb + b) * CH * 1024,   chunk c of row r at + c*1024 + r*16
+// so the 64 lanes of a wavefront reading chunk c of 64 consecutive rows touch 1 KB of
+// contiguous memory.  Chunk contents (same bits as the GGUF block):
+//   Q4_K (CH 9):  c0 = d, dmin, 12 scale bytes;  c1..c8 = qs[16(c-1) .. +16]
+//   Q6_K (CH 13): c0..c7 = ql[16c ..];  c8..c11 = qh[16(c-8) ..];  c12 = sc[16];
+//                 fp16 d in a plane after all tiles: d(rg, b, r) at
+//                 base + ng*nb*13*1024 + ((rg*nb + b)*64 + r)*2
+//   Q8_0 (CH 17): c0..c15 = qs of the 8 Q8_0 blocks in order (16 weights per chunk);
+//                 c16 = their 8 fp16 d
+// N is padded to a multiple of 64 (padding rows are zero and never stored to outputs).
+template <int QT> struct Tile;
+template <> struct Tile<PGMOE_Q4_K> { static constexpr int CH = 9; };
+template <> struct Tile<PGMOE_Q6_K> { static constexpr int CH = 13; };
+template <> struct Tile<PGMOE_Q8_0> { static constexpr int CH = 17; };
+
+__host__ __device__ inline int row_groups(int N) { return (N + 63) >> 6; }
+
+template <int QT>
+__device__ __forceinline__ const uint8_t* tile_ptr(const uint8_t* mat, int nb, int rg, int b) {
+    return mat + ((int64_t)rg * nb + b) * (Tile<QT>::CH * 1024);
+}
+
 // ---------------------------------------------------------------- quant groups
-// Every supported format is processed in "units" of 64 weights of one row, each made of
-// four groups of 16 weights sharing one affine scale: w = a*q - b.  Unit u of a row
-// covers row elements  unit_col(u, g) + [0, 16)  for g = 0..3:
-//   Q4_K: block u/4, 32-byte qs chunk c = u%4: groups at 64c + {0,16,32,48}
+// The MFMA GEMM stages weights in units of 64 consecutive weights of one row (four
+// groups of 16 sharing an affine scale, w = a*q - b).  Unit u covers row elements
+//   unit_col(u, g) + [0, 16) for g = 0..3:
+//   Q4_K: block u/4, qs bytes [32c, 32c+32) with c = u%4: groups at 64c + {0,16,32,48}
 //         (low nibbles -> sub-block 2c, high nibbles -> sub-block 2c+1)
 //   Q6_K: block u/4, (h, half) = ((u%4)>>1, u&1): groups s at 128h + 16half + 32s
-//   Q8_0: blocks 2u, 2u+1: groups at 64u' + {0,16,32,48} (g<2 -> block 2u)
+//   Q8_0: block u/4, Q8_0 blocks 2(u%4), 2(u%4)+1: groups at 64(u%4) + 16g
 template <int QT> struct Fmt;
 
 template <> struct Fmt<PGMOE_Q4_K> {
     __device__ static __forceinline__ int col(int u, int g) { return 64 * u + 16 * g; }
-    // q[16] (integers 0..15 as float), scale a, offset b for group g of unit u of `row`.
     __device__ static __forceinline__ void group(const uint8_t* mat, int K, int N, int row, int u, int g,
                                                  float q[16], float& a, float& b) {
         const int nb = K >> 8;
-        const uint8_t* blk = mat + ((int64_t)row * nb + (u >> 2)) * 144;
+        const uint8_t* t = tile_ptr<PGMOE_Q4_K>(mat, nb, row >> 6, u >> 2) + (row & 63) * 16;
         const int c = u & 3;
-        const uint4 hdr = *(const uint4*)blk;
-        const uint4 qv = *(const uint4*)(blk + 16 + 32 * c + 16 * (g & 1));
+        const uint4 hdr = *(const uint4*)t;
+        const uint4 qv = *(const uint4*)(t + (1 + 2 * c + (g & 1)) * 1024);
         const int s = 2 * c + (g >> 1);
         const uint32_t D = hdr.y, Mb = hdr.z, MD = hdr.w;  // scale bytes 0-3, 4-7, 8-11
         int sc, mn;
@@ -87,14 +111,15 @@ template <> struct Fmt<PGMOE_Q6_K> {
     __device__ static __forceinline__ void group(const uint8_t* mat, int K, int N, int row, int u, int g,
                                                  float q[16], float& a, float& b) {
         const int nb = K >> 8;
-        const int64_t blk = (int64_t)row * nb + (u >> 2);
-        const int64_t unit = blk * 4 + (u & 3);
-        const uint8_t* body = mat + unit * 48;
-        const uint4 lo = *(const uint4*)(body + 16 * (g & 1));  // ql chunk A (s even) or B (s odd)
-        const uint4 hi = *(const uint4*)(body + 32);            // qh chunk
-        const uint32_t scw = *(const uint32_t*)(mat + (int64_t)N * nb * 192 + unit * 4);
-        const uint16_t db = *(const uint16_t*)(mat + (int64_t)N * nb * 208 + blk * 2);
-        const int sc = (int)(int8_t)((scw >> (8 * g)) & 0xff);
+        const int rg = row >> 6, r = row & 63, blk = u >> 2, h = (u & 3) >> 1, half = u & 1;
+        const uint8_t* t = tile_ptr<PGMOE_Q6_K>(mat, nb, rg, blk) + r * 16;
+        const uint4 lo = *(const uint4*)(t + (4 * h + 2 * (g & 1) + half) * 1024);  // ql[64h + 32(s&1) + 16half ..]
+        const uint4 hi = *(const uint4*)(t + (8 + 2 * h + half) * 1024);           // qh[32h + 16half ..]
+        const int scb = 8 * h + 2 * g + half;
+        const uint32_t scw = *(const uint32_t*)(t + 12 * 1024 + (scb & ~3));
+        const int64_t dplane = (int64_t)row_groups(N) * nb * 13 * 1024;
+        const uint16_t db = *(const uint16_t*)(mat + dplane + (((int64_t)rg * nb + blk) * 64 + r) * 2);
+        const int sc = (int)(int8_t)((scw >> (8 * (scb & 3))) & 0xff);
         a = h2f(db) * (float)sc;
         b = 32.0f * a;
         const int lsh = 4 * (g >> 1), hsh = 2 * g;
@@ -113,9 +138,12 @@ template <> struct Fmt<PGMOE_Q8_0> {
     __device__ static __forceinline__ int col(int u, int g) { return 64 * u + 16 * g; }
     __device__ static __forceinline__ void group(const uint8_t* mat, int K, int N, int row, int u, int g,
                                                  float q[16], float& a, float& b) {
-        const uint4 qv = *(const uint4*)(mat + (int64_t)row * K + 64 * u + 16 * g);
-        const uint16_t db = *(const uint16_t*)(mat + (int64_t)N * K + ((int64_t)row * (K >> 5) + 2 * u + (g >> 1)) * 2);
-        a = h2f(db);
+        const int nb = K >> 8;
+        const uint8_t* t = tile_ptr<PGMOE_Q8_0>(mat, nb, row >> 6, u >> 2) + (row & 63) * 16;
+        const int j = u & 3;
+        const uint4 qv = *(const uint4*)(t + (4 * j + g) * 1024);
+        const uint32_t dw = *(const uint32_t*)(t + 16 * 1024 + 4 * j);  // d of Q8_0 blocks 2j, 2j+1
+        a = (g < 2) ? lo_half(dw) : hi_half(dw);
         b = 0.0f;
         const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll

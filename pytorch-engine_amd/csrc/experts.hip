@@ -1,6 +1,6 @@
 // R4-R7: grouped expert products over the dispatched (sorted) token-expert pairs.
-//   decode  (M <= 8): wavefront-group-per-row GEMV streaming GGUF units, in-register dequant
-//   prefill (M > 8) : LDS-staged dequant-to-fp16 tiles feeding v_mfma_f32_16x16x32_f16
+//   prefill (M > 8): LDS-staged dequant-to-fp16 tiles feeding v_mfma_f32_16x16x32_f16
+//   (the decode GEMVs live in decode.hip)
 // Reference: GGUFQuantMoEExperts.forward_expert (quant_kernels.py:1990-2011) ->
 // exec_w4a16_matmul / exec_w8a16_matmul (:1165-1420), exec_fused_act_mul_rowscale
 // (:1423-1475), and the per-expert loop of model.py:911-922.
@@ -9,159 +9,7 @@
 
 namespace pgmoe {
 
-constexpr int kMaxDecodeRows = 8;  // tokens per expert handled by the GEMV kernels
-constexpr int kBM = 64;            // pair rows per GEMM tile
-
-// --------------------------------------------------------------------------- GEMV
-// x for group (u, g) of one token: 16 fp16 values -> fp32
-__device__ __forceinline__ void load_x16(const uint16_t* p, float xs[16]) {
-    const uint4 v0 = *(const uint4*)p, v1 = *(const uint4*)(p + 8);
-    const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        xs[2 * i] = lo_half(w[i]);
-        xs[2 * i + 1] = hi_half(w[i]);
-    }
-}
-
-__device__ __forceinline__ void load_x16(const float* p, float xs[16]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 v = *(const float4*)(p + 4 * i);
-        xs[4 * i] = v.x;
-        xs[4 * i + 1] = v.y;
-        xs[4 * i + 2] = v.z;
-        xs[4 * i + 3] = v.w;
-    }
-}
-
-// One block = 256/G rows of one active expert; G lanes share a row and stride over its
-// 64-weight units.  Gate and up rows with the same index are computed together so the
-// SwiGLU is applied in registers: inter[p, row] = silu(x_p.g_row) * (x_p.u_row).
-template <int QT, int G>
-__global__ __launch_bounds__(256) void gemv_gateup_kernel(const uint8_t* __restrict__ gbase,
-                                                          const uint8_t* __restrict__ ubase, int64_t gstride,
-                                                          int64_t ustride, int N, int K,
-                                                          const uint16_t* __restrict__ x, int topk,
-                                                          const int32_t* __restrict__ offsets,
-                                                          const int32_t* __restrict__ perm,
-                                                          const int32_t* __restrict__ active,
-                                                          const int32_t* __restrict__ n_active,
-                                                          float* __restrict__ inter) {
-    const int a = blockIdx.y;
-    if (a >= *n_active) return;
-    const int e = active[a];
-    const int cnt = offsets[e + 1] - offsets[e];
-    constexpr int RPB = 256 / G;
-    const int row = blockIdx.x * RPB + threadIdx.x / G;
-    const int gl = threadIdx.x % G;
-    if (row >= N) return;
-    const uint8_t* gm = gbase + (int64_t)e * gstride;
-    const uint8_t* um = ubase + (int64_t)e * ustride;
-    // rows of this expert in chunks of kMaxDecodeRows (one chunk whenever M <= 8)
-    for (int p0 = offsets[e]; p0 < offsets[e] + cnt; p0 += kMaxDecodeRows) {
-    const int me = min(offsets[e] + cnt - p0, kMaxDecodeRows);
-    int tok[kMaxDecodeRows];
-    float ag[kMaxDecodeRows], au[kMaxDecodeRows];
-#pragma unroll
-    for (int t = 0; t < kMaxDecodeRows; ++t) {
-        tok[t] = t < me ? perm[p0 + t] / topk : 0;
-        ag[t] = 0.0f;
-        au[t] = 0.0f;
-    }
-    const int units = K >> 6;
-    for (int u = gl; u < units; u += G) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            float qg[16], qu[16], a_g, b_g, a_u, b_u;
-            Fmt<QT>::group(gm, K, N, row, u, g, qg, a_g, b_g);
-            Fmt<QT>::group(um, K, N, row, u, g, qu, a_u, b_u);
-            const int col = Fmt<QT>::col(u, g);
-#pragma unroll
-            for (int t = 0; t < kMaxDecodeRows; ++t) {
-                if (t < me) {
-                    float xs[16];
-                    load_x16(x + (int64_t)tok[t] * K + col, xs);
-                    float sg = 0.0f, su = 0.0f, sx = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        sg = __builtin_fmaf(qg[i], xs[i], sg);
-                        su = __builtin_fmaf(qu[i], xs[i], su);
-                        sx += xs[i];
-                    }
-                    ag[t] += a_g * sg - b_g * sx;
-                    au[t] += a_u * su - b_u * sx;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < kMaxDecodeRows; ++t) {
-        if (t < me) {
-            const float gs = group_sum<G>(ag[t]);
-            const float us = group_sum<G>(au[t]);
-            if (gl == 0) inter[(int64_t)(p0 + t) * N + row] = silu(gs) * us;
-        }
-    }
-    }
-}
-
-// partial[p, row] = w[perm[p]] * (inter_p . d_row) for the pairs of one active expert.
-template <int QT, int G>
-__global__ __launch_bounds__(256) void gemv_down_kernel(const uint8_t* __restrict__ dbase, int64_t dstride,
-                                                        int N, int K, const float* __restrict__ inter,
-                                                        const int32_t* __restrict__ offsets,
-                                                        const int32_t* __restrict__ perm,
-                                                        const int32_t* __restrict__ active,
-                                                        const int32_t* __restrict__ n_active,
-                                                        const float* __restrict__ topk_w,
-                                                        float* __restrict__ partial) {
-    const int a = blockIdx.y;
-    if (a >= *n_active) return;
-    const int e = active[a];
-    const int cnt = offsets[e + 1] - offsets[e];
-    constexpr int RPB = 256 / G;
-    const int row = blockIdx.x * RPB + threadIdx.x / G;
-    const int gl = threadIdx.x % G;
-    if (row >= N) return;
-    const uint8_t* dm = dbase + (int64_t)e * dstride;
-    for (int p0 = offsets[e]; p0 < offsets[e] + cnt; p0 += kMaxDecodeRows) {
-    const int me = min(offsets[e] + cnt - p0, kMaxDecodeRows);
-    float acc[kMaxDecodeRows];
-#pragma unroll
-    for (int t = 0; t < kMaxDecodeRows; ++t) acc[t] = 0.0f;
-    const int units = K >> 6;
-    for (int u = gl; u < units; u += G) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            float q[16], av, bv;
-            Fmt<QT>::group(dm, K, N, row, u, g, q, av, bv);
-            const int col = Fmt<QT>::col(u, g);
-#pragma unroll
-            for (int t = 0; t < kMaxDecodeRows; ++t) {
-                if (t < me) {
-                    float xs[16];
-                    load_x16(inter + (int64_t)(p0 + t) * K + col, xs);
-                    float s = 0.0f, sx = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        s = __builtin_fmaf(q[i], xs[i], s);
-                        sx += xs[i];
-                    }
-                    acc[t] += av * s - bv * sx;
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < kMaxDecodeRows; ++t) {
-        if (t < me) {
-            const float v = group_sum<G>(acc[t]);
-            if (gl == 0) partial[(int64_t)(p0 + t) * N + row] = topk_w[perm[p0 + t]] * v;
-        }
-    }
-    }
-}
+constexpr int kBM = 64;  // pair rows per GEMM tile
 
 // --------------------------------------------------------------------------- GEMM
 // Tile lookup: tile_off is the exclusive scan of per-expert tile counts; the expert of
@@ -397,66 +245,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 }
 
 // --------------------------------------------------------------------------- launchers
-static int pick_group(int units) {
-    for (int g = 64; g >= 8; g >>= 1)
-        if (units % g == 0) return g;
-    return 4;
-}
-
-template <int QT>
-static void gateup_gemv_q(const Mats& g, const Mats& u, const uint16_t* x, int topk, const int32_t* offsets,
-                          const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
-                          float* inter, hipStream_t st) {
-    const int G = pick_group(g.K >> 6);
-    const dim3 block(256);
-#define PG_GU(GG)                                                                                              \
-    hipLaunchKernelGGL((gemv_gateup_kernel<QT, GG>), dim3(div_up(g.N, 256 / GG), max_active), block, 0, st,      \
-                       g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, offsets, perm, active, n_active, \
-                       inter)
-    switch (G) {
-    case 64: PG_GU(64); break;
-    case 32: PG_GU(32); break;
-    case 16: PG_GU(16); break;
-    case 8: PG_GU(8); break;
-    default: PG_GU(4); break;
-    }
-#undef PG_GU
-}
-
-template <int QT>
-static void down_gemv_q(const Mats& d, const float* inter, const int32_t* offsets, const int32_t* perm,
-                        const int32_t* active, const int32_t* n_active, int max_active, const float* topk_w,
-                        float* partial, hipStream_t st) {
-    const int G = pick_group(d.K >> 6);
-    const dim3 block(256);
-#define PG_DN(GG)                                                                                           \
-    hipLaunchKernelGGL((gemv_down_kernel<QT, GG>), dim3(div_up(d.N, 256 / GG), max_active), block, 0, st,     \
-                       d.base, d.stride, d.N, d.K, inter, offsets, perm, active, n_active, topk_w, partial)
-    switch (G) {
-    case 64: PG_DN(64); break;
-    case 32: PG_DN(32); break;
-    case 16: PG_DN(16); break;
-    case 8: PG_DN(8); break;
-    default: PG_DN(4); break;
-    }
-#undef PG_DN
-}
-
 int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                   const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
                   int mode, float* inter, hipStream_t st) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
-    if (mode == 0) {
-        const int max_active = (int)(P < E ? P : E);
-        switch (g.qtype) {
-        case PGMOE_Q4_K: gateup_gemv_q<PGMOE_Q4_K>(g, u, x, topk, offsets, perm, active, n_active, max_active, inter, st); break;
-        case PGMOE_Q6_K: gateup_gemv_q<PGMOE_Q6_K>(g, u, x, topk, offsets, perm, active, n_active, max_active, inter, st); break;
-        case PGMOE_Q8_0: gateup_gemv_q<PGMOE_Q8_0>(g, u, x, topk, offsets, perm, active, n_active, max_active, inter, st); break;
-        }
-        return check_launch("gemv_gateup");
-    }
+    if (mode == 0) return launch_dec_gateup(g, u, x, topk, offsets, perm, active, n_active, (int)(P < E ? P : E),
+                                            inter, st);
     const int max_tiles = div_up(P, kBM) + (int)(P < E ? P : E);
     const dim3 grid(max_tiles, div_up(g.N, 32)), block(256);
     switch (g.qtype) {
@@ -473,15 +269,9 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
-    if (mode == 0) {
-        const int max_active = (int)(P < E ? P : E);
-        switch (d.qtype) {
-        case PGMOE_Q4_K: down_gemv_q<PGMOE_Q4_K>(d, inter, offsets, perm, active, n_active, max_active, topk_w, partial, st); break;
-        case PGMOE_Q6_K: down_gemv_q<PGMOE_Q6_K>(d, inter, offsets, perm, active, n_active, max_active, topk_w, partial, st); break;
-        case PGMOE_Q8_0: down_gemv_q<PGMOE_Q8_0>(d, inter, offsets, perm, active, n_active, max_active, topk_w, partial, st); break;
-        }
-        return check_launch("gemv_down");
-    }
+    if (mode == 0)
+        return launch_dec_down(d, inter, offsets, perm, active, n_active, (int)(P < E ? P : E), topk_w, partial, M,
+                               topk, nullptr, nullptr, nullptr, nullptr, nullptr, st);
     if (!a16 || !rs) return fail(PGMOE_E_INVALID, "GEMM mode needs a16 and rs scratch");
     hipLaunchKernelGGL(rowscale_kernel, dim3((unsigned)P), dim3(256), 0, st, inter, d.K, a16, rs);
     int rc = check_launch("rowscale");
@@ -505,6 +295,5 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
 }
 
 int gemm_tile_rows() { return kBM; }
-int decode_max_rows() { return kMaxDecodeRows; }
 
 }  // namespace pgmoe

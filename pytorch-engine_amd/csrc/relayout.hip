@@ -1,4 +1,4 @@
-// Load-time GGUF -> device layout conversion (same bits, aligned planes).
+// Load-time GGUF -> device layout conversion (same bits, 64-row interleaved tiles).
 // Replaces the reference's CPU numpy repack (quant_kernels.py:854-1036), which
 // re-quantises into W4/W8 arrays; here the GGUF bits are kept and only moved.
 #include "common.h"
@@ -6,67 +6,99 @@
 
 namespace pgmoe {
 
-// One thread per Q6_K block (210 B: ql[128] qh[64] sc[16] d[2]).
-__global__ void relayout_q6k_kernel(const uint8_t* __restrict__ src, int64_t n_blocks, int64_t blocks_per_mat,
-                                    uint8_t* __restrict__ dst, int64_t dst_stride) {
-    const int64_t gb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gb >= n_blocks) return;
-    const int64_t mat = gb / blocks_per_mat, b = gb % blocks_per_mat;  // b = row * nb + block
-    const uint8_t* s = src + gb * 210;
-    uint8_t* d = dst + mat * dst_stride;
-    uint8_t* body = d + b * 192;
-    uint8_t* scale = d + blocks_per_mat * 192 + b * 16;
-    for (int un = 0; un < 4; ++un) {
-        const int h = un >> 1, half = un & 1;
-        for (int i = 0; i < 16; ++i) {
-            body[un * 48 + i] = s[64 * h + 16 * half + i];
-            body[un * 48 + 16 + i] = s[64 * h + 32 + 16 * half + i];
-            body[un * 48 + 32 + i] = s[128 + 32 * h + 16 * half + i];
-        }
-        for (int q = 0; q < 4; ++q) scale[un * 4 + q] = s[192 + 8 * h + 2 * q + half];
-    }
-    uint8_t* dd = d + blocks_per_mat * 208 + b * 2;
-    dd[0] = s[208];
-    dd[1] = s[209];
+template <int QT> struct Gguf;
+template <> struct Gguf<PGMOE_Q4_K> { static constexpr int per = 256, bytes = 144; };
+template <> struct Gguf<PGMOE_Q6_K> { static constexpr int per = 256, bytes = 210; };
+template <> struct Gguf<PGMOE_Q8_0> { static constexpr int per = 32, bytes = 34; };
+
+__device__ __forceinline__ void copy16(uint8_t* d, const uint8_t* s) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d[i] = s[i];
 }
 
-// One thread per Q8_0 block (34 B: d[2] q[32]).
-__global__ void relayout_q8_0_kernel(const uint8_t* __restrict__ src, int64_t n_blocks, int64_t blocks_per_mat,
-                                     uint8_t* __restrict__ dst, int64_t dst_stride) {
-    const int64_t gb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gb >= n_blocks) return;
-    const int64_t mat = gb / blocks_per_mat, b = gb % blocks_per_mat;
-    const uint8_t* s = src + gb * 34;
-    uint8_t* d = dst + mat * dst_stride;
-    for (int i = 0; i < 32; ++i) d[b * 32 + i] = s[2 + i];
-    d[blocks_per_mat * 32 + b * 2] = s[0];
-    d[blocks_per_mat * 32 + b * 2 + 1] = s[1];
+__device__ __forceinline__ void zero16(uint8_t* d) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d[i] = 0;
+}
+
+// One thread per (matrix, padded row, 256-weight block).
+template <int QT>
+__global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats, int N, int nb,
+                                uint8_t* __restrict__ dst, int64_t dst_stride) {
+    const int ng = row_groups(N);
+    const int64_t per_mat = (int64_t)ng * 64 * nb;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= per_mat * n_mats) return;
+    const int64_t mat = gid / per_mat;
+    const int64_t rem = gid % per_mat;
+    const int row = (int)(rem / nb), b = (int)(rem % nb);
+    const int rg = row >> 6, r = row & 63;
+    constexpr int CH = Tile<QT>::CH;
+    uint8_t* md = dst + mat * dst_stride;
+    uint8_t* t = md + ((int64_t)rg * nb + b) * (CH * 1024) + r * 16;
+    const bool real = row < N;
+    // GGUF bytes of this (row, 256-weight block)
+    constexpr int sb = Gguf<QT>::bytes * (256 / Gguf<QT>::per);
+    const uint8_t* s = src + mat * (int64_t)N * nb * sb + ((int64_t)row * nb + b) * sb;
+    if (QT == PGMOE_Q4_K || QT == PGMOE_Q6_K) {
+        for (int c = 0; c < CH; ++c) {
+            if (real) copy16(t + c * 1024, s + 16 * c);
+            else zero16(t + c * 1024);
+        }
+        if (QT == PGMOE_Q6_K) {
+            uint8_t* d = md + (int64_t)ng * nb * CH * 1024 + (((int64_t)rg * nb + b) * 64 + r) * 2;
+            d[0] = real ? s[208] : 0;
+            d[1] = real ? s[209] : 0;
+        }
+    } else {  // Q8_0: eight 34-byte blocks per 256 weights
+        for (int j = 0; j < 8; ++j) {
+            const uint8_t* bj = s + 34 * j;
+            if (real) {
+                copy16(t + (2 * j) * 1024, bj + 2);
+                copy16(t + (2 * j + 1) * 1024, bj + 18);
+                t[16 * 1024 + 2 * j] = bj[0];
+                t[16 * 1024 + 2 * j + 1] = bj[1];
+            } else {
+                zero16(t + (2 * j) * 1024);
+                zero16(t + (2 * j + 1) * 1024);
+                t[16 * 1024 + 2 * j] = 0;
+                t[16 * 1024 + 2 * j + 1] = 0;
+            }
+        }
+    }
+}
+
+int64_t layout_bytes(int qtype, int64_t rows, int64_t cols) {
+    if (cols % 256 || rows < 1) return -1;
+    const int64_t ng = (rows + 63) / 64, nb = cols / 256;
+    switch (qtype) {
+    case PGMOE_Q4_K: return ng * nb * 9 * 1024;
+    case PGMOE_Q6_K: return ng * nb * (13 * 1024 + 128);
+    case PGMOE_Q8_0: return ng * nb * 17 * 1024;
+    default: return -1;
+    }
 }
 
 int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, uint8_t* dst,
                     int64_t dst_stride, hipStream_t st) {
-    if (qtype == PGMOE_Q4_K) {
-        const int64_t mb = rows * (cols / 256) * 144;
-        if (dst_stride == mb) {
-            if (hipMemcpyAsync(dst, src, mb * n_mats, hipMemcpyDeviceToDevice, st) != hipSuccess)
-                return fail(PGMOE_E_HIP, "relayout copy failed");
-        } else {
-            for (int64_t m = 0; m < n_mats; ++m)
-                if (hipMemcpyAsync(dst + m * dst_stride, src + m * mb, mb, hipMemcpyDeviceToDevice, st) != hipSuccess)
-                    return fail(PGMOE_E_HIP, "relayout copy failed");
-        }
-        return PGMOE_OK;
-    }
-    const int per = qtype == PGMOE_Q6_K ? 256 : 32;
-    const int64_t bpm = rows * (cols / per);
-    const int64_t nb = bpm * n_mats;
-    if (nb == 0) return PGMOE_OK;
+    const int nb = (int)(cols / 256);
+    const int64_t n = n_mats * (int64_t)row_groups((int)rows) * 64 * nb;
+    if (n == 0) return PGMOE_OK;
     const int threads = 256;
-    const int64_t grid = (nb + threads - 1) / threads;
-    if (qtype == PGMOE_Q6_K)
-        hipLaunchKernelGGL(relayout_q6k_kernel, dim3((unsigned)grid), dim3(threads), 0, st, src, nb, bpm, dst, dst_stride);
-    else
-        hipLaunchKernelGGL(relayout_q8_0_kernel, dim3((unsigned)grid), dim3(threads), 0, st, src, nb, bpm, dst, dst_stride);
+    const dim3 grid((unsigned)((n + threads - 1) / threads));
+    switch (qtype) {
+    case PGMOE_Q4_K:
+        hipLaunchKernelGGL(relayout_kernel<PGMOE_Q4_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        break;
+    case PGMOE_Q6_K:
+        hipLaunchKernelGGL(relayout_kernel<PGMOE_Q6_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        break;
+    case PGMOE_Q8_0:
+        hipLaunchKernelGGL(relayout_kernel<PGMOE_Q8_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        break;
+    default:
+        return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d", qtype);
+    }
     return check_launch("relayout");
 }
 

@@ -63,8 +63,8 @@ class _ExpertTensor:
             raise NotImplementedError(
                 f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
                 "has no HIP kernel (supported: Q4_K, Q6_K, Q8_0)")
-        if self.cols % (64 if self.qtype == 8 else 256):
-            raise ValueError(f"{name}: {self.cols} input features is not a whole number of kernel units")
+        if self.cols % 256:
+            raise ValueError(f"{name}: {self.cols} input features is not a multiple of 256")
         raw_np = gguf_file.get_tensor_bytes(name)
         raw = torch.from_numpy(np.asarray(raw_np)).to(device)  # H2D copy of the GGUF bytes
         self.buf = ops.relayout(self.qtype, raw, self.n_mats, self.rows, self.cols)
@@ -162,7 +162,8 @@ class HipSparseMoEMLP(nn.Module):
         ws = self._ws.get(M)
         if ws is None:
             n = self.workspace_bytes(M) + 256
-            raw = torch.empty(n, dtype=torch.uint8, device=self.device)
+            # zeroed once: the workspace starts with self-resetting completion counters
+            raw = torch.zeros(n, dtype=torch.uint8, device=self.device)
             off = (-raw.data_ptr()) % 256
             ws = raw[off:]
             self._ws = {M: ws}  # keep one size: callers alternate between few M values

@@ -28,15 +28,19 @@ def test_library_exports_every_header_symbol():
     assert L.pgmoe_abi_version() == _lib.ABI_VERSION
 
 
-def test_weight_bytes_are_gguf_bytes_rounded_to_256():
+def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
     L = _lib.lib()
     for qt, rows, cols, per, bb in [(12, 768, 2048, 256, 144), (14, 2048, 768, 256, 210),
-                                    (8, 2560, 3584, 32, 34), (14, 1, 256, 256, 210)]:
-        raw = rows * (cols // per) * bb
+                                    (8, 2560, 3584, 32, 34), (14, 1, 256, 256, 210), (8, 100, 512, 32, 34)]:
+        padded_rows = (rows + 63) // 64 * 64
+        raw = padded_rows * (cols // per) * bb
         assert L.pgmoe_weight_bytes(qt, rows, cols) == (raw + 255) // 256 * 256
+        if rows % 64 == 0:  # no padding: exactly the GGUF bytes
+            assert L.pgmoe_weight_bytes(qt, rows, cols) == rows * (cols // per) * bb
     assert L.pgmoe_weight_bytes(12, 4, 100) == -1  # not a whole K-quant block row
     assert L.pgmoe_weight_bytes(2, 4, 256) == -1   # Q4_0 has no kernel
-    assert L.pgmoe_weight_bytes(8, 4, 96) == -1    # Q8_0 rows must be whole 64-weight units
+    assert L.pgmoe_weight_bytes(8, 4, 96) == -1    # rows must be whole 256-weight tiles
+    assert L.pgmoe_weight_bytes(8, 4, 320) == -1
 
 
 def _fake_layer(E=8, K=2, H=1024, I=512, qt=12, shared=False):

@@ -25,43 +25,36 @@ def dev():
 
 
 def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
-    """The device layout of include/pgmoe.h, built with numpy."""
+    """The device layout of include/pgmoe.h (64-row tiles of 16-byte chunks), in numpy."""
     out = np.zeros(n_mats * stride, dtype=np.uint8)
-    if qtype == Q4_K:
-        mb = rows * (cols // 256) * 144
-        for m in range(n_mats):
-            out[m * stride:m * stride + mb] = raw[m * mb:(m + 1) * mb]
-        return out
-    if qtype == Q8_0:
-        nbm = rows * (cols // 32)
-        blk = raw.reshape(n_mats, nbm, 34)
-        for m in range(n_mats):
-            base = m * stride
-            out[base:base + nbm * 32] = blk[m, :, 2:].reshape(-1)
-            out[base + nbm * 32:base + nbm * 34] = blk[m, :, 0:2].reshape(-1)
-        return out
-    nbm = rows * (cols // 256)
-    blk = raw.reshape(n_mats, nbm, 210)
+    nb, ng = cols // 256, (rows + 63) // 64
+    bpb = {Q4_K: 144, Q6_K: 210, Q8_0: 272}[qtype]  # GGUF bytes per 256 weights
+    CH = {Q4_K: 9, Q6_K: 13, Q8_0: 17}[qtype]
+    sb = raw.reshape(n_mats, rows, nb, bpb)
     for m in range(n_mats):
         base = m * stride
-        b = blk[m]
-        body = np.zeros((nbm, 4, 48), np.uint8)
-        scl = np.zeros((nbm, 4, 4), np.uint8)
-        for un in range(4):
-            h, half = un >> 1, un & 1
-            body[:, un, 0:16] = b[:, 64 * h + 16 * half:64 * h + 16 * half + 16]
-            body[:, un, 16:32] = b[:, 64 * h + 32 + 16 * half:64 * h + 48 + 16 * half]
-            body[:, un, 32:48] = b[:, 128 + 32 * h + 16 * half:128 + 32 * h + 16 * half + 16]
-            for s in range(4):
-                scl[:, un, s] = b[:, 192 + 8 * h + 2 * s + half]
-        out[base:base + nbm * 192] = body.reshape(-1)
-        out[base + nbm * 192:base + nbm * 208] = scl.reshape(-1)
-        out[base + nbm * 208:base + nbm * 210] = b[:, 208:210].reshape(-1)
+        for r in range(rows):
+            g, rr = divmod(r, 64)
+            for b in range(nb):
+                blk = sb[m, r, b]
+                t = base + (g * nb + b) * CH * 1024 + rr * 16
+                if qtype in (Q4_K, Q6_K):
+                    for c in range(CH):
+                        out[t + c * 1024:t + c * 1024 + 16] = blk[16 * c:16 * c + 16]
+                    if qtype == Q6_K:
+                        d = base + ng * nb * CH * 1024 + ((g * nb + b) * 64 + rr) * 2
+                        out[d:d + 2] = blk[208:210]
+                else:
+                    for j in range(8):
+                        bj = blk[34 * j:34 * j + 34]
+                        out[t + 2 * j * 1024:t + 2 * j * 1024 + 16] = bj[2:18]
+                        out[t + (2 * j + 1) * 1024:t + (2 * j + 1) * 1024 + 16] = bj[18:34]
+                        out[t + 16 * 1024 + 2 * j:t + 16 * 1024 + 2 * j + 2] = bj[0:2]
     return out
 
 
-@pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q8_0, 5, 192, 2),
-                                                    (Q6_K, 2048, 768, 2)])
+@pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q8_0, 5, 256, 2),
+                                                    (Q6_K, 130, 768, 2), (Q8_0, 64, 512, 1)])
 def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
     from pgmoe import ops
     rng = np.random.default_rng(rows * cols)
@@ -70,8 +63,9 @@ def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
     stride = ops.weight_stride(qtype, rows, cols)
     got = buf.cpu().numpy()
     ref = _np_relayout(qtype, raw, n_mats, rows, cols, stride)
-    # padding bytes between matrices are unspecified
-    mb = rows * (cols // ops.GGUF_BLOCK[qtype][0]) * ops.GGUF_BLOCK[qtype][1]
+    # bytes past the tiles (alignment padding between matrices) are unspecified
+    ng, nb = (rows + 63) // 64, cols // 256
+    mb = ng * nb * {Q4_K: 9 * 1024, Q6_K: 13 * 1024 + 128, Q8_0: 17 * 1024}[qtype]
     for m in range(n_mats):
         assert np.array_equal(got[m * stride:m * stride + mb], ref[m * stride:m * stride + mb])
 
@@ -145,10 +139,11 @@ def _dense(qtype, raw, n_mats, rows, cols):
 
 @pytest.mark.parametrize("qg,qd,H,I,E,K,M,mode", [
     (Q4_K, Q6_K, 512, 256, 8, 2, 1, 0), (Q4_K, Q6_K, 512, 256, 8, 2, 8, 0),
-    (Q4_K, Q4_K, 256, 512, 4, 2, 5, 0), (Q8_0, Q8_0, 192, 320, 6, 3, 7, 0),
+    (Q4_K, Q4_K, 256, 512, 4, 2, 5, 0), (Q8_0, Q8_0, 256, 512, 6, 3, 7, 0),
+    (Q6_K, Q8_0, 768, 256, 3, 1, 6, 0), (Q4_K, Q6_K, 2304, 512, 5, 2, 8, 0),
     (Q4_K, Q6_K, 512, 256, 8, 2, 40, 1), (Q4_K, Q4_K, 256, 512, 4, 2, 130, 1),
-    (Q8_0, Q8_0, 192, 320, 6, 3, 70, 1), (Q6_K, Q8_0, 256, 256, 3, 1, 9, 1),
-    (Q4_K, Q6_K, 512, 256, 8, 2, 3, 1)])
+    (Q8_0, Q8_0, 256, 512, 6, 3, 70, 1), (Q6_K, Q8_0, 256, 256, 3, 1, 9, 1),
+    (Q4_K, Q6_K, 512, 256, 8, 2, 3, 1), (Q8_0, Q4_K, 512, 256, 3, 2, 17, 1)])
 def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
     """inter and the weighted down partials against float64 numpy over decoded weights.
     Tolerance: GEMV keeps fp32 everywhere (rel-L2 1e-5); GEMM uses fp16 weights/x and a
