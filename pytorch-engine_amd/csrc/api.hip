@@ -61,7 +61,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
-    size_t counters, s_disp;
+    size_t s_disp;
     size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, inter, a16, rs, partial;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
@@ -79,8 +79,6 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     const size_t P = (size_t)M * K;
     const bool gemm = M > decode_tokens_max();
     size_t c = 0;
-    // self-resetting completion counters: [0] router, [16 + rg] down row groups
-    o.counters = take(c, (16 + (size_t)row_groups((int)H)) * 4);
     o.s_disp = take(c, (4 + (size_t)M) * 4);
     o.logits = take(c, (size_t)M * E * 4);
     o.idx = take(c, P * 4);
@@ -249,14 +247,16 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
     const int E = L->n_experts, K = L->top_k, H = L->hidden;
     const int mode = M > decode_tokens_max() ? 1 : 0;
     const int BM = gemm_tile_rows();
-    int32_t* counters = WS(int32_t, counters);
     if (mode == 0) {
-        // decode: route (+ shared identity dispatch) -> gate/up -> [shared] -> down + combine
+        // decode: router (+ shared gate row) -> top-k/dispatch -> gate/up -> [shared] -> down -> combine
         int32_t* sd = L->has_shared ? WS(int32_t, s_disp) : nullptr;
-        if ((rc = launch_route_small(x, L->router_w, L->router_bias, L->has_shared ? L->sh_inp_gate : nullptr, M, H, E,
-                                     K, L->norm_topk, WS(float, logits), WS(float, s_logit), WS(int32_t, idx),
-                                     WS(float, w), WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv),
-                                     WS(int32_t, active), WS(int32_t, nact), sd, WS(float, s_w), counters, st)))
+        const float* sgw = L->has_shared ? L->sh_inp_gate : nullptr;
+        if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st, sgw,
+                                       sgw ? WS(float, s_logit) : nullptr)))
+            return rc;
+        if ((rc = launch_topk_dispatch_small(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w),
+                                             WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv),
+                                             WS(int32_t, active), WS(int32_t, nact), sd, WS(float, s_w), st)))
             return rc;
         const int max_active = M * K < E ? M * K : E;
         if ((rc = launch_dec_gateup(lm.gate, lm.up, x, K, WS(int32_t, offsets), WS(int32_t, perm),
@@ -268,14 +268,16 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
             if ((rc = launch_dec_gateup(lm.sg, lm.su, x, 1, sd, sd + 4, sd + 2, sd + 3, 1, WS(float, s_inter), st)))
                 return rc;
             if ((rc = launch_dec_down(lm.sd, WS(float, s_inter), sd, sd + 4, sd + 2, sd + 3, 1, WS(float, s_w),
-                                      WS(float, s_partial), M, 1, nullptr, nullptr, nullptr, nullptr, nullptr, st)))
+                                      WS(float, s_partial), st)))
                 return rc;
             shared = WS(float, s_partial);
-            if (L->sh_inp_gate) shared_logit = WS(float, s_logit);
+            if (sgw) shared_logit = WS(float, s_logit);
         }
-        return launch_dec_down(lm.down, WS(float, inter), WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
-                               WS(int32_t, nact), max_active, WS(float, w), WS(float, partial), M, K, WS(int32_t, inv),
-                               shared, shared_logit, out, counters + 16, st);
+        if ((rc = launch_dec_down(lm.down, WS(float, inter), WS(int32_t, offsets), WS(int32_t, perm),
+                                  WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, w),
+                                  WS(float, partial), st)))
+            return rc;
+        return launch_combine(WS(float, partial), WS(int32_t, inv), M, K, H, shared, shared_logit, out, st);
     }
     if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st))) return rc;
     if ((rc = launch_topk(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w), st))) return rc;

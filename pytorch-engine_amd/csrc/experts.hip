@@ -213,14 +213,15 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const float* __restrict__
         a16[p * I + i] = __builtin_bit_cast(uint16_t, (half_t)(row[i] / s));
 }
 
-// out[t, :] = sum of the token's K pair rows in ascending sorted position (= ascending
-// expert id), then + shared[t, :] * sigmoid(shared_logit[t]).
+// out[t, h] = sum of the token's K pair rows in ascending sorted position (= ascending
+// expert id), then + shared[t, h] * sigmoid(shared_logit[t]).  Block = (token, 256 columns).
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
                                                       const int32_t* __restrict__ inv, int K, int H,
                                                       const float* __restrict__ shared,
                                                       const float* __restrict__ shared_logit,
                                                       float* __restrict__ out) {
     const int t = blockIdx.x;
+    const int h = blockIdx.y * 256 + threadIdx.x;
     int pos[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) pos[k] = k < K ? inv[(int64_t)t * K + k] : 0x7fffffff;
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     }
     float gate = 1.0f;
     if (shared_logit) gate = 1.0f / (1.0f + expf(-shared_logit[t]));
-    for (int h = threadIdx.x; h < H; h += 256) {
+    if (h < H) {
         float acc = 0.0f;
         for (int k = 0; k < K; ++k) acc += partial[(int64_t)pos[k] * H + h];
         if (shared) acc += shared[(int64_t)t * H + h] * gate;
@@ -270,8 +271,7 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
     if (mode == 0)
-        return launch_dec_down(d, inter, offsets, perm, active, n_active, (int)(P < E ? P : E), topk_w, partial, M,
-                               topk, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+        return launch_dec_down(d, inter, offsets, perm, active, n_active, (int)(P < E ? P : E), topk_w, partial, st);
     if (!a16 || !rs) return fail(PGMOE_E_INVALID, "GEMM mode needs a16 and rs scratch");
     hipLaunchKernelGGL(rowscale_kernel, dim3((unsigned)P), dim3(256), 0, st, inter, d.K, a16, rs);
     int rc = check_launch("rowscale");
@@ -290,7 +290,8 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
                    const float* shared_logit, float* out, hipStream_t st) {
     if (M <= 0) return PGMOE_OK;
     if (K > 16) return fail(PGMOE_E_UNSUPPORTED, "combine supports top_k <= 16");
-    hipLaunchKernelGGL(combine_kernel, dim3(M), dim3(256), 0, st, partial, inv, K, H, shared, shared_logit, out);
+    hipLaunchKernelGGL(combine_kernel, dim3(M, div_up(H, 256)), dim3(256), 0, st, partial, inv, K, H, shared,
+                       shared_logit, out);
     return check_launch("combine");
 }
 

@@ -6,7 +6,7 @@
 namespace pgmoe {
 
 int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
-                         float* logits, hipStream_t st);
+                         float* logits, hipStream_t st, const float* extra_w = nullptr, float* extra_out = nullptr);
 int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w, hipStream_t st);
 int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int32_t* offsets, int32_t* perm,
                     int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st);
@@ -27,12 +27,10 @@ int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, int topk,
                       float* inter, hipStream_t st);
 int launch_dec_down(const Mats& d, const float* inter, const int32_t* offsets, const int32_t* perm,
                     const int32_t* active, const int32_t* n_active, int max_active, const float* topk_w,
-                    float* partial, int M, int topk, const int32_t* inv, const float* shared,
-                    const float* shared_logit, float* out, int32_t* counters, hipStream_t st);
-int launch_route_small(const uint16_t* x, const float* W, const float* bias, const float* sh_w, int M, int H, int E,
-                       int K, int norm, float* logits, float* s_logit, int32_t* idx, float* w, int32_t* offsets,
-                       int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active, int32_t* s_disp, float* s_w,
-                       int32_t* counter, hipStream_t st);
+                    float* partial, hipStream_t st);
+int launch_topk_dispatch_small(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w,
+                               int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active,
+                               int32_t* s_disp, float* s_w, hipStream_t st);
 int64_t layout_bytes(int qtype, int64_t rows, int64_t cols);
 int gemm_tile_rows();
 int decode_tokens_max();

@@ -12,14 +12,19 @@ namespace pgmoe {
 // (l, l^32), (l, l^16), ..., (l, l^1); the bias is added last.  The CPU oracle
 // (or_router_logits) performs the same operations in the same order, so both produce
 // identical bits.
+// An optional extra row (the shared expert's sigmoid-gate vector) is treated as expert E
+// and written to extra_out[m] instead of logits.
 template <int TM, int TE>
 __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
                                                             const float* __restrict__ W,
                                                             const float* __restrict__ bias, int M, int H,
-                                                            int E, float* __restrict__ logits) {
+                                                            int E, float* __restrict__ logits,
+                                                            const float* __restrict__ extra_w,
+                                                            float* __restrict__ extra_out) {
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int n_etiles = (E + TE - 1) / TE;
+    const int rows = E + (extra_w ? 1 : 0);
+    const int n_etiles = (rows + TE - 1) / TE;
     const int mt = wave / n_etiles, et = wave % n_etiles;
     const int m0 = mt * TM, e0 = et * TE;
     if (m0 >= M) return;
@@ -44,9 +49,10 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
         }
 #pragma unroll
         for (int j = 0; j < TE; ++j) {
-            const int e = e0 + j < E ? e0 + j : E - 1;
-            const float4 w0 = *(const float4*)(W + (int64_t)e * H + 8 * c);
-            const float4 w1 = *(const float4*)(W + (int64_t)e * H + 8 * c + 4);
+            const int e = e0 + j < rows ? e0 + j : rows - 1;
+            const float* wr = e < E ? W + (int64_t)e * H : extra_w;
+            const float4 w0 = *(const float4*)(wr + 8 * c);
+            const float4 w1 = *(const float4*)(wr + 8 * c + 4);
             const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -63,6 +69,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
             if (lane == 0 && m < M && e < E) {
                 if (bias) v = v + bias[e];
                 logits[(int64_t)m * E + e] = v;
+            } else if (lane == 0 && m < M && e == E && extra_w) {
+                extra_out[m] = v;
             }
         }
 }
@@ -135,25 +143,26 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 }
 
 int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
-                         float* logits, hipStream_t st) {
+                         float* logits, hipStream_t st, const float* extra_w, float* extra_out) {
     if (M <= 0) return PGMOE_OK;
     const int threads = 256;
+    const int rows = E + (extra_w ? 1 : 0);
     if (M <= 4) {
         // decode: one wave per (all tokens, one expert) spreads the router read widely
         constexpr int TM = 4, TE = 1;
-        const int waves = div_up(M, TM) * div_up(E, TE);
+        const int waves = div_up(M, TM) * div_up(rows, TE);
         hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits);
+                           x, W, bias, M, H, E, logits, extra_w, extra_out);
     } else if (M <= 8) {
         constexpr int TM = 8, TE = 1;
-        const int waves = div_up(M, TM) * div_up(E, TE);
+        const int waves = div_up(M, TM) * div_up(rows, TE);
         hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits);
+                           x, W, bias, M, H, E, logits, extra_w, extra_out);
     } else {
         constexpr int TM = 8, TE = 4;
-        const int waves = div_up(M, TM) * div_up(E, TE);
+        const int waves = div_up(M, TM) * div_up(rows, TE);
         hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits);
+                           x, W, bias, M, H, E, logits, extra_w, extra_out);
     }
     return check_launch("router_logits");
 }

@@ -146,9 +146,10 @@ def _dense(qtype, raw, n_mats, rows, cols):
     (Q4_K, Q6_K, 512, 256, 8, 2, 3, 1), (Q8_0, Q4_K, 512, 256, 3, 2, 17, 1)])
 def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
     """inter and the weighted down partials against float64 numpy over decoded weights.
-    Tolerance: GEMV keeps fp32 everywhere (rel-L2 1e-5); GEMM uses fp16 weights/x and a
-    per-row fp16 down input (rel-L2 2e-3, i.e. fp16 rounding, same as the reference's
-    own GPU prefill path)."""
+    Tolerance: the decode GEMV forms exact fp16 products of (1024 + code) and x and
+    removes the 1024 * sum(x) offset after fp32 accumulation, which costs ~2e-5 rel-L2
+    (bound 1e-4); the MFMA GEMM uses fp16 weights/x and a per-row fp16 down input
+    (rel-L2 2e-3, i.e. fp16 rounding, as in the reference's own GPU prefill path)."""
     from pgmoe import ops
     log(f"stages qg={qg} qd={qd} H={H} I={I} E={E} K={K} M={M} mode={mode}")
     rng = np.random.default_rng(H + I + M)
@@ -182,7 +183,7 @@ def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
         gv, uv = g[e] @ xf[t], u[e] @ xf[t]
         ref_inter[p] = gv / (1 + np.exp(-gv)) * uv
     got_inter = inter.cpu().numpy()
-    tol = 1e-5 if mode == 0 else 2e-3
+    tol = 1e-4 if mode == 0 else 2e-3
     assert oracle.rel_l2(got_inter, ref_inter) < tol
     ref_part = np.empty((P, H))
     gi = got_inter.astype(np.float64)
