@@ -61,7 +61,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
-    size_t s_disp;
+    size_t s_disp, xsum, isum, s_isum;
     size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, inter, a16, rs, partial;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
@@ -80,6 +80,9 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     const bool gemm = M > decode_tokens_max();
     size_t c = 0;
     o.s_disp = take(c, (4 + (size_t)M) * 4);
+    o.xsum = take(c, gemm ? 0 : (size_t)M * (H / 16) * 4);
+    o.isum = take(c, gemm ? 0 : P * (I / 16) * 4);
+    o.s_isum = take(c, (gemm || !L->has_shared) ? 0 : (size_t)M * (L->sh_gate.n_rows / 16) * 4);
     o.logits = take(c, (size_t)M * E * 4);
     o.idx = take(c, P * 4);
     o.w = take(c, P * 4);
@@ -252,29 +255,31 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
         int32_t* sd = L->has_shared ? WS(int32_t, s_disp) : nullptr;
         const float* sgw = L->has_shared ? L->sh_inp_gate : nullptr;
         if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st, sgw,
-                                       sgw ? WS(float, s_logit) : nullptr)))
+                                       sgw ? WS(float, s_logit) : nullptr, WS(float, xsum))))
             return rc;
         if ((rc = launch_topk_dispatch_small(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w),
                                              WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv),
                                              WS(int32_t, active), WS(int32_t, nact), sd, WS(float, s_w), st)))
             return rc;
         const int max_active = M * K < E ? M * K : E;
-        if ((rc = launch_dec_gateup(lm.gate, lm.up, x, K, WS(int32_t, offsets), WS(int32_t, perm),
-                                    WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, inter), st)))
+        if ((rc = launch_dec_gateup(lm.gate, lm.up, x, WS(float, xsum), K, M, WS(int32_t, offsets), WS(int32_t, perm),
+                                    WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, inter),
+                                    WS(float, isum), st)))
             return rc;
         const float* shared = nullptr;
         const float* shared_logit = nullptr;
         if (L->has_shared) {
-            if ((rc = launch_dec_gateup(lm.sg, lm.su, x, 1, sd, sd + 4, sd + 2, sd + 3, 1, WS(float, s_inter), st)))
+            if ((rc = launch_dec_gateup(lm.sg, lm.su, x, WS(float, xsum), 1, M, sd, sd + 4, sd + 2, sd + 3, 1,
+                                        WS(float, s_inter), WS(float, s_isum), st)))
                 return rc;
-            if ((rc = launch_dec_down(lm.sd, WS(float, s_inter), sd, sd + 4, sd + 2, sd + 3, 1, WS(float, s_w),
-                                      WS(float, s_partial), st)))
+            if ((rc = launch_dec_down(lm.sd, WS(float, s_inter), WS(float, s_isum), M, sd, sd + 4, sd + 2, sd + 3, 1,
+                                      WS(float, s_w), WS(float, s_partial), st)))
                 return rc;
             shared = WS(float, s_partial);
             if (sgw) shared_logit = WS(float, s_logit);
         }
-        if ((rc = launch_dec_down(lm.down, WS(float, inter), WS(int32_t, offsets), WS(int32_t, perm),
-                                  WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, w),
+        if ((rc = launch_dec_down(lm.down, WS(float, inter), WS(float, isum), M, WS(int32_t, offsets),
+                                  WS(int32_t, perm), WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, w),
                                   WS(float, partial), st)))
             return rc;
         return launch_combine(WS(float, partial), WS(int32_t, inv), M, K, H, shared, shared_logit, out, st);

@@ -252,8 +252,9 @@ int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int to
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
-    if (mode == 0) return launch_dec_gateup(g, u, x, topk, offsets, perm, active, n_active, (int)(P < E ? P : E),
-                                            inter, st);
+    if (mode == 0)
+        return launch_dec_gateup(g, u, x, nullptr, topk, M, offsets, perm, active, n_active, (int)(P < E ? P : E),
+                                 inter, nullptr, st);
     const int max_tiles = div_up(P, kBM) + (int)(P < E ? P : E);
     const dim3 grid(max_tiles, div_up(g.N, 32)), block(256);
     switch (g.qtype) {
@@ -271,7 +272,8 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
     if (mode == 0)
-        return launch_dec_down(d, inter, offsets, perm, active, n_active, (int)(P < E ? P : E), topk_w, partial, st);
+        return launch_dec_down(d, inter, nullptr, M, offsets, perm, active, n_active, (int)(P < E ? P : E), topk_w,
+                               partial, st);
     if (!a16 || !rs) return fail(PGMOE_E_INVALID, "GEMM mode needs a16 and rs scratch");
     hipLaunchKernelGGL(rowscale_kernel, dim3((unsigned)P), dim3(256), 0, st, inter, d.K, a16, rs);
     int rc = check_launch("rowscale");

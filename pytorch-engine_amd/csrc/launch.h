@@ -6,7 +6,8 @@
 namespace pgmoe {
 
 int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
-                         float* logits, hipStream_t st, const float* extra_w = nullptr, float* extra_out = nullptr);
+                         float* logits, hipStream_t st, const float* extra_w = nullptr, float* extra_out = nullptr,
+                         float* xsum = nullptr);
 int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w, hipStream_t st);
 int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int32_t* offsets, int32_t* perm,
                     int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st);
@@ -22,12 +23,12 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
                    const float* shared_logit, float* out, hipStream_t st);
 int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, uint8_t* dst,
                     int64_t dst_stride, hipStream_t st);
-int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, int topk, const int32_t* offsets,
-                      const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
-                      float* inter, hipStream_t st);
-int launch_dec_down(const Mats& d, const float* inter, const int32_t* offsets, const int32_t* perm,
-                    const int32_t* active, const int32_t* n_active, int max_active, const float* topk_w,
-                    float* partial, hipStream_t st);
+int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
+                      const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
+                      int max_active, float* inter, float* isum, hipStream_t st);
+int launch_dec_down(const Mats& d, const float* inter, const float* isum, int M, const int32_t* offsets,
+                    const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
+                    const float* topk_w, float* partial, hipStream_t st);
 int launch_topk_dispatch_small(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w,
                                int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active,
                                int32_t* s_disp, float* s_w, hipStream_t st);

@@ -20,7 +20,19 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
                                                             const float* __restrict__ bias, int M, int H,
                                                             int E, float* __restrict__ logits,
                                                             const float* __restrict__ extra_w,
-                                                            float* __restrict__ extra_out) {
+                                                            float* __restrict__ extra_out,
+                                                            float* __restrict__ xsum) {
+    if (xsum) {  // side output for the decode GEMVs: 16-element sums of every x row
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < M * (H >> 4); i += gridDim.x * blockDim.x) {
+            const uint16_t* p = x + (int64_t)(i / (H >> 4)) * H + 16 * (i % (H >> 4));
+            const uint4 a = *(const uint4*)p, b = *(const uint4*)(p + 8);
+            const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            float s = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s += lo_half(v[k]) + hi_half(v[k]);
+            xsum[i] = s;
+        }
+    }
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int rows = E + (extra_w ? 1 : 0);
@@ -143,7 +155,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 }
 
 int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
-                         float* logits, hipStream_t st, const float* extra_w, float* extra_out) {
+                         float* logits, hipStream_t st, const float* extra_w, float* extra_out, float* xsum) {
     if (M <= 0) return PGMOE_OK;
     const int threads = 256;
     const int rows = E + (extra_w ? 1 : 0);
@@ -152,17 +164,17 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
         constexpr int TM = 4, TE = 1;
         const int waves = div_up(M, TM) * div_up(rows, TE);
         hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits, extra_w, extra_out);
+                           x, W, bias, M, H, E, logits, extra_w, extra_out, xsum);
     } else if (M <= 8) {
         constexpr int TM = 8, TE = 1;
         const int waves = div_up(M, TM) * div_up(rows, TE);
         hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits, extra_w, extra_out);
+                           x, W, bias, M, H, E, logits, extra_w, extra_out, xsum);
     } else {
         constexpr int TM = 8, TE = 4;
         const int waves = div_up(M, TM) * div_up(rows, TE);
         hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits, extra_w, extra_out);
+                           x, W, bias, M, H, E, logits, extra_w, extra_out, xsum);
     }
     return check_launch("router_logits");
 }
