@@ -61,7 +61,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
-    size_t s_disp, xsum, isum, s_isum;
+    size_t desc, xsum, isum, s_isum;
     size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, inter, a16, rs, partial;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
@@ -79,7 +79,7 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     const size_t P = (size_t)M * K;
     const bool gemm = M > decode_tokens_max();
     size_t c = 0;
-    o.s_disp = take(c, (4 + (size_t)M) * 4);
+    o.desc = take(c, gemm ? 0 : (size_t)decode_desc_words() * 4);
     o.xsum = take(c, gemm ? 0 : (size_t)M * (H / 16) * 4);
     o.isum = take(c, gemm ? 0 : P * (I / 16) * 4);
     o.s_isum = take(c, (gemm || !L->has_shared) ? 0 : (size_t)M * (L->sh_gate.n_rows / 16) * 4);
@@ -95,7 +95,8 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     o.inter = take(c, P * I * 4);
     o.a16 = take(c, gemm ? P * I * 2 : 0);
     o.rs = take(c, gemm ? P * 4 : 0);
-    o.partial = take(c, P * H * 4);
+    // the fused decode down kernel combines in place; otherwise per-pair partial rows
+    o.partial = take(c, (gemm || !decode_fused_down((int)P, (int)I)) ? P * H * 4 : 0);
     if (L->has_shared) {
         const size_t Is = L->sh_gate.n_rows;
         o.s_offsets = take(c, 2 * 4);
@@ -251,33 +252,37 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
     const int mode = M > decode_tokens_max() ? 1 : 0;
     const int BM = gemm_tile_rows();
     if (mode == 0) {
-        // decode: router (+ shared gate row) -> top-k/dispatch -> gate/up -> [shared] -> down -> combine
-        int32_t* sd = L->has_shared ? WS(int32_t, s_disp) : nullptr;
+        // decode: router (+ shared gate row, x sums) -> gate/up with in-block routing ->
+        // [shared gate/up -> shared down] -> down + combine
         const float* sgw = L->has_shared ? L->sh_inp_gate : nullptr;
         if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st, sgw,
                                        sgw ? WS(float, s_logit) : nullptr, WS(float, xsum))))
             return rc;
-        if ((rc = launch_topk_dispatch_small(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w),
-                                             WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv),
-                                             WS(int32_t, active), WS(int32_t, nact), sd, WS(float, s_w), st)))
-            return rc;
         const int max_active = M * K < E ? M * K : E;
-        if ((rc = launch_dec_gateup(lm.gate, lm.up, x, WS(float, xsum), K, M, WS(int32_t, offsets), WS(int32_t, perm),
-                                    WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, inter),
-                                    WS(float, isum), st)))
+        const bool fused = decode_fused_down(M * K, lm.down.K);
+        DecFlat flat{};
+        if (!fused)
+            flat = DecFlat{WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv), WS(int32_t, active),
+                           WS(int32_t, nact), WS(float, w)};
+        if ((rc = launch_dec_gateup_routed(lm.gate, lm.up, x, WS(float, xsum), K, M, WS(float, logits), E,
+                                           L->norm_topk, WS(int32_t, desc), flat, max_active, WS(float, inter),
+                                           WS(float, isum), st)))
             return rc;
         const float* shared = nullptr;
         const float* shared_logit = nullptr;
         if (L->has_shared) {
-            if ((rc = launch_dec_gateup(lm.sg, lm.su, x, WS(float, xsum), 1, M, sd, sd + 4, sd + 2, sd + 3, 1,
-                                        WS(float, s_inter), WS(float, s_isum), st)))
+            if ((rc = launch_dec_gateup_ident(lm.sg, lm.su, x, WS(float, xsum), M, WS(float, s_inter),
+                                              WS(float, s_isum), st)))
                 return rc;
-            if ((rc = launch_dec_down(lm.sd, WS(float, s_inter), WS(float, s_isum), M, sd, sd + 4, sd + 2, sd + 3, 1,
-                                      WS(float, s_w), WS(float, s_partial), st)))
+            if ((rc = launch_dec_down_ident(lm.sd, WS(float, s_inter), WS(float, s_isum), M, WS(float, s_partial),
+                                            st)))
                 return rc;
             shared = WS(float, s_partial);
             if (sgw) shared_logit = WS(float, s_logit);
         }
+        if (fused)
+            return launch_dec_down_combine(lm.down, WS(float, inter), WS(float, isum), WS(int32_t, desc), M, K,
+                                           max_active, shared, shared_logit, out, st);
         if ((rc = launch_dec_down(lm.down, WS(float, inter), WS(float, isum), M, WS(int32_t, offsets),
                                   WS(int32_t, perm), WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, w),
                                   WS(float, partial), st)))

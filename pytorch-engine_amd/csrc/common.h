@@ -6,6 +6,20 @@
 
 #include "pgmoe.h"
 
+// Phase timestamps for profiling builds only: a build that defines PG_TRACE also defines
+// `__device__ unsigned long long pg_trace[]` in the same translation unit, and thread 0 of
+// each block stores wall_clock64() (100 MHz) at slot [kernel][block][point].  Without
+// PG_TRACE the marks compile to nothing.
+#ifdef PG_TRACE
+#define PG_MARK(kern, pt)                                                                                  \
+    do {                                                                                                   \
+        const unsigned pg_b = blockIdx.y * gridDim.x + blockIdx.x;                                         \
+        if (threadIdx.x == 0 && pg_b < 8192) pg_trace[((kern) * 8192 + pg_b) * 8 + (pt)] = wall_clock64(); \
+    } while (0)
+#else
+#define PG_MARK(kern, pt) ((void)0)
+#endif
+
 namespace pgmoe {
 
 typedef _Float16 half_t;

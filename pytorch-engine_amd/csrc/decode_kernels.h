@@ -1,7 +1,9 @@
-// Decode path (M <= 8 tokens), five short launches per layer, no host sync:
-//   router logits (router.hip, fixed order) -> top-k + dispatch (one block) ->
-//   gate/up + SwiGLU -> down -> combine (experts.hip, ascending expert id).
-// Expert kernels: a block owns RB rows of one active expert; lane = (row, K-slice), so
+// Decode path (M <= 8 tokens), three launches per layer (five with a shared expert), no
+// host sync:
+//   router logits (router.hip, fixed order, also the 16-element sums of x) ->
+//   gate/up + SwiGLU, each block routing the tokens itself from the logits ->
+//   down + combine fused (every block owns a few output rows across all active experts).
+// Per-expert kernels: a block owns RB rows of one active expert; lane = (row, K-slice), so
 // each lane streams whole 256-weight super-blocks of one row from the 64-row tile
 // layout (coalesced 16-byte chunks), activations are wave-uniform (LDS / broadcast),
 // and partial sums meet through a few shuffles and one LDS pass.  Weight loads are
@@ -11,6 +13,8 @@
 // Reference: pygguf_engine/model.py:898-937; quant_kernels.py:68-311 (GEMV kernels it
 // replaces), :1423-1475 (SwiGLU + row-scale).
 #pragma once
+#include <utility>
+
 #include "common.h"
 #include "launch.h"
 
@@ -326,40 +330,326 @@ __device__ __forceinline__ float kslot_sum(float v) {
     return v;
 }
 
+// ============================================================================ routing in a block
+// Decode forward: the router kernel writes logits [M][E]; every gate/up block re-derives
+// the top-k sets of the M <= 8 tokens from them (about a microsecond of register work
+// instead of a launch and its dependent global round trips), and block (0, 0) also
+// publishes a compact routing descriptor for the fused down + combine kernel:
+//   int32 words: [0] n_active; slot a at kDescSlot + 4a = {expert, first sorted pair,
+//   pair count, 0}; sorted pair p at kDescPair + 2p = {token, weight bits}.
+// Active slots are in ascending expert id; the pairs of an expert in ascending token
+// order (the order of the reference's torch.where over the expert mask, model.py:912-914).
+constexpr int kDescSlot = 16;
+constexpr int kDescPair = kDescSlot + 4 * 128;
+constexpr int kDescWords = kDescPair + 2 * 128;
+
+struct RouteShared {
+    uint32_t pres[kDecTM][16];  // token x expert membership bits (E <= 512)
+    int mem_e[kDecTM * 16];     // the K members of token m at [m*K, m*K+K), ascending id
+    float mem_w[kDecTM * 16];   // their combine weights (publishing block only)
+    int n_act, e, p_begin, count;
+    int tok[kDecTM];
+};
+
+// Selection key of (logit v, expert e): larger key = earlier in (logit desc, id asc).
+// -0.0 is folded into +0.0 first so that the key order equals the float order.
+__device__ __forceinline__ uint64_t route_key(float v, int e) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v + 0.0f);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 9) | (uint64_t)(511 - e);
+}
+
+// Top-k membership of every token (one wave per token): the K-th largest key is found by
+// a 41-step radix descent on the key bits (ballot counts), and the members are exactly
+// the keys at or above it (keys are distinct).  With `weights`, also the softmax weights
+// of the members (max-subtracted, denominator over all E, optional renorm; model.py:903-907).
+// sl: LDS scratch of M*E floats.  Every thread of the block calls this.
+template <int RE>
+__device__ __forceinline__ uint64_t radix_kth(const uint64_t (&key)[8], int K) {
+    uint64_t thr = 0;
+    for (int b = 40; b >= 0; --b) {
+        const uint64_t cand = thr | (1ull << b);
+        int cnt = 0;
+#pragma unroll
+        for (int r = 0; r < RE; ++r) cnt += __popcll(__ballot(key[r] >= cand));
+        if (cnt >= K) thr = cand;
+    }
+    return thr;
+}
+
+// Block-wide copy of n elements: element i moves from src(i) to dst(i), U loads in flight
+// per thread before the first store (expanded over an index sequence so the staging
+// values stay in registers).
+template <typename T, typename Src, typename Dst, int... I>
+__device__ __forceinline__ void copy_step(int i0, int n, int nth, Src src, Dst dst, std::integer_sequence<int, I...>) {
+    T v[sizeof...(I)];
+    ((v[I] = (i0 + I * nth < n) ? *src(i0 + I * nth) : T{}), ...);
+    ((i0 + I * nth < n ? (void)(*dst(i0 + I * nth) = v[I]) : (void)0), ...);
+}
+
+template <int U, typename T, typename Src, typename Dst>
+__device__ __forceinline__ void copy_idx(int n, int tid, int nth, Src src, Dst dst) {
+    for (int i0 = tid; i0 < n; i0 += U * nth) copy_step<T>(i0, n, nth, src, dst, std::make_integer_sequence<int, U>{});
+}
+
+template <int U, typename T>
+__device__ __forceinline__ void copy_words(T* dst, const T* __restrict__ src, int n, int tid, int nth) {
+    copy_idx<U, T>(n, tid, nth, [=](int i) { return src + i; }, [=](int i) { return dst + i; });
+}
+
+__device__ __forceinline__ void route_in_block(const float* __restrict__ logits, int M, int E, int K, float* sl,
+                                               RouteShared& R, bool weights, int norm) {
+    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6;
+    copy_words<8>(sl, logits, M * E, tid, nth);
+    __syncthreads();
+    const int RE = (E + 63) >> 6;
+    for (int m = wv; m < M; m += nth >> 6) {
+        uint64_t key[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int e = lane + 64 * r;
+            key[r] = (r < RE && e < E) ? route_key(sl[m * E + e], e) : 0ull;
+        }
+        uint64_t thr;
+        switch (RE) {
+        case 1: thr = radix_kth<1>(key, K); break;
+        case 2: thr = radix_kth<2>(key, K); break;
+        case 3: thr = radix_kth<3>(key, K); break;
+        case 4: thr = radix_kth<4>(key, K); break;
+        case 5: thr = radix_kth<5>(key, K); break;
+        case 6: thr = radix_kth<6>(key, K); break;
+        case 7: thr = radix_kth<7>(key, K); break;
+        default: thr = radix_kth<8>(key, K); break;
+        }
+        float top = -INFINITY, den = 0.f;
+        if (weights) {
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r < RE && lane + 64 * r < E) top = fmaxf(top, sl[m * E + lane + 64 * r]);
+#pragma unroll
+            for (int s = 32; s >= 1; s >>= 1) top = fmaxf(top, __shfl_xor(top, s, 64));
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                if (r < RE && lane + 64 * r < E) den += expf(sl[m * E + lane + 64 * r] - top);
+            den = group_sum<64>(den);
+        }
+        int base = 0;
+        float psel = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            if (r < RE) {
+                const bool in = key[r] >= thr && lane + 64 * r < E;
+                const uint64_t mask = __ballot(in);
+                if (lane == 0) {
+                    if (2 * r < 16) R.pres[m][2 * r] = (uint32_t)mask;
+                    if (2 * r + 1 < 16) R.pres[m][2 * r + 1] = (uint32_t)(mask >> 32);
+                }
+                const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
+                if (in && pos < K) {  // exactly K members unless logits hold NaNs
+                    R.mem_e[m * K + pos] = lane + 64 * r;
+                    if (weights) {
+                        const float p = expf(sl[m * E + lane + 64 * r] - top) / den;
+                        R.mem_w[m * K + pos] = p;
+                        psel += p;
+                    }
+                }
+                base += __popcll(mask);
+            }
+        }
+        if (weights && norm) {
+            psel = group_sum<64>(psel);
+            for (int i = lane; i < K; i += 64) R.mem_w[m * K + i] = R.mem_w[m * K + i] / fmaxf(psel, 1e-20f);
+        }
+        if (lane == 0)
+            for (int q = 2 * RE; q < 16; ++q) R.pres[m][q] = 0u;
+    }
+    __syncthreads();
+}
+
+// Expert of active slot a (the a-th expert in ascending id that some token selected), its
+// first sorted pair (pairs of lower experts) and its pair count.  Returns false when
+// a >= n_active.
+__device__ __forceinline__ bool route_slot(const RouteShared& R, int M, int E, int a, int& e, int& p_begin,
+                                           int& count) {
+    const int nw = (E + 31) >> 5;
+    int seen = 0;
+    e = -1;
+    for (int q = 0; q < nw && e < 0; ++q) {
+        uint32_t u = 0;
+        for (int m = 0; m < M; ++m) u |= R.pres[m][q];
+        const int c = __popc(u);
+        if (a < seen + c) {
+            for (int k = a - seen; k > 0; --k) u &= u - 1u;  // drop the lower set bits
+            e = 32 * q + __builtin_ctz(u);
+        }
+        seen += c;
+    }
+    if (e < 0) return false;
+    const int q = e >> 5;
+    const uint32_t below = (1u << (e & 31)) - 1u;
+    p_begin = 0;
+    count = 0;
+    for (int m = 0; m < M; ++m) {
+        for (int w = 0; w < q; ++w) p_begin += __popc(R.pres[m][w]);
+        p_begin += __popc(R.pres[m][q] & below);
+        count += (R.pres[m][q] >> (e & 31)) & 1u;
+    }
+    return true;
+}
+
+__device__ __forceinline__ int route_n_active(const RouteShared& R, int M, int E) {
+    int n = 0;
+    for (int q = 0; q < ((E + 31) >> 5); ++q) {
+        uint32_t u = 0;
+        for (int m = 0; m < M; ++m) u |= R.pres[m][q];
+        n += __popc(u);
+    }
+    return n;
+}
+
+// Flat routing arrays of a counting-sort dispatch (the stage API's layout), written by the
+// routing block when the down stage runs per expert: offsets [E+1], perm / inv / w [M*K]
+// (pair f = token*K + i, members i in ascending expert id), active [n_active], n_active.
+struct FlatRoute {
+    int32_t *offsets, *perm, *inv, *active, *n_active;
+    float* w;
+};
+
+// Publish the routing descriptor (block (0, 0) only; R holds the weights), and the flat
+// arrays when fl.offsets is set.
+__device__ __forceinline__ void publish_route(const RouteShared& R, int M, int E, int K, int32_t* __restrict__ desc,
+                                              const FlatRoute& fl) {
+    const int tid = threadIdx.x, nth = blockDim.x;
+    if (fl.offsets) {
+        for (int e = tid; e <= E; e += nth) {
+            int o = 0;
+            for (int m = 0; m < M; ++m) {
+                for (int w = 0; w < (e >> 5); ++w) o += __popc(R.pres[m][w]);
+                if (e < E) o += __popc(R.pres[m][e >> 5] & ((1u << (e & 31)) - 1u));
+                else if (E & 31) o += __popc(R.pres[m][E >> 5] & ((1u << (E & 31)) - 1u));
+            }
+            fl.offsets[e] = o;
+        }
+    }
+    for (int a = tid; a < M * K; a += nth) {
+        int e, pb, c;
+        if (route_slot(R, M, E, a, e, pb, c)) {
+            desc[kDescSlot + 4 * a] = e;
+            desc[kDescSlot + 4 * a + 1] = pb;
+            desc[kDescSlot + 4 * a + 2] = c;
+        }
+    }
+    for (int f = tid; f < M * K; f += nth) {
+        const int m = f / K, e = R.mem_e[f], q = e >> 5;
+        int pos = 0;
+        for (int m2 = 0; m2 < M; ++m2) {
+            for (int w = 0; w < q; ++w) pos += __popc(R.pres[m2][w]);
+            pos += __popc(R.pres[m2][q] & ((1u << (e & 31)) - 1u));
+            pos += m2 < m ? (R.pres[m2][q] >> (e & 31)) & 1u : 0u;
+        }
+        desc[kDescPair + 2 * pos] = m;
+        desc[kDescPair + 2 * pos + 1] = __builtin_bit_cast(int32_t, R.mem_w[f]);
+        if (fl.offsets) {
+            fl.perm[pos] = f;
+            fl.inv[f] = pos;
+            fl.w[f] = R.mem_w[f];
+        }
+    }
+    if (fl.offsets) {
+        for (int a = tid; a < M * K; a += nth) {
+            int e, pb, c;
+            if (route_slot(R, M, E, a, e, pb, c)) fl.active[a] = e;
+        }
+    }
+    if (tid == 0) {
+        const int n = route_n_active(R, M, E);
+        desc[0] = n;
+        if (fl.offsets) *fl.n_active = n;
+    }
+}
+
 // ============================================================================ kernels
-// Block = RB rows of one active expert, W waves; lane (r, ks): row = RB*blockIdx.x + r,
-// super-blocks j = ks + KS*w, + KS*W, ...  Pairs of the expert are taken TM at a time.
-// LDS: xs [TM][K] fp16 | xs_sum [TM][K/16] f32; partials and the SwiGLU row reuse xs.
-// xsum (optional): 16-element sums of x rows, [M][K/16]; isum (optional output):
-// 16-element sums of the inter rows, [P][N/16].
+// Where a decode expert kernel finds its pairs:
+//   kDispatch: offsets / perm / active / n_active of a counting-sort dispatch (stage API);
+//   kRoute   : derived in the block from the router logits (decode forward; block (0, 0)
+//              also publishes the routing descriptor);
+//   kIdent   : one expert (matrix 0) applied to every token with weight 1 (shared expert).
+enum DecMode { kDispatch = 0, kRoute = 1, kIdent = 2 };
+
+struct DecDisp {
+    int mode;  // DecMode
+    const int32_t *offsets, *perm, *active, *n_active;
+    const float* logits;  // kRoute
+    int32_t* desc;        // kRoute: published by block (0, 0)
+    int M, E, norm;       // M: tokens (kRoute, kIdent)
+    FlatRoute flat;       // kRoute: optional flat arrays, published by block (0, 0)
+};
+
+// Gate/up + SwiGLU.  Block = RB rows of one active expert, W waves; lane (r, ks):
+// row = RB*blockIdx.x + r, super-blocks j = ks + KS*w, + KS*W, ...  Pairs of the expert
+// are taken TM at a time.  inter / isum rows are indexed by sorted pair.
+// Dynamic LDS: max(xs [TM][K] fp16 + xs_sum [TM][K/16] f32, logits [M][E] f32 (kRoute),
+// partials [W][TM][2][RB] + SwiGLU row [TM][RB]).
+// xsum (optional): 16-element sums of x rows [M][K/16]; isum (optional output):
+// 16-element sums of inter rows [P][N/16].
 template <int QT, int RB, int W, int TM>
 __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __restrict__ gbase,
                                                             const uint8_t* __restrict__ ubase, int64_t gstride,
                                                             int64_t ustride, int N, int K,
                                                             const uint16_t* __restrict__ x,
-                                                            const float* __restrict__ xsum, int topk,
-                                                            const int32_t* __restrict__ offsets,
-                                                            const int32_t* __restrict__ perm,
-                                                            const int32_t* __restrict__ active,
-                                                            const int32_t* __restrict__ n_active,
+                                                            const float* __restrict__ xsum, int topk, DecDisp dp,
                                                             float* __restrict__ inter, float* __restrict__ isum) {
     constexpr int KS = 64 / RB;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ RouteShared R;
     const int a = blockIdx.y;
-    if (a >= *n_active) return;
-    const int e = active[a];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int MODE = dp.mode;
+    int e, p_begin, p_end;
+    PG_MARK(1, 0);
+    if (MODE == kRoute) {
+        const bool pub = blockIdx.x == 0 && a == 0;
+        route_in_block(dp.logits, dp.M, dp.E, topk, (float*)smem, R, pub, dp.norm);
+        PG_MARK(1, 1);
+        if (pub) publish_route(R, dp.M, dp.E, topk, dp.desc, dp.flat);
+        if (tid == 0) {
+            int ee, pb, c;
+            R.n_act = route_slot(R, dp.M, dp.E, a, ee, pb, c) ? 1 : 0;
+            if (R.n_act) {
+                R.e = ee;
+                R.p_begin = pb;
+                R.count = c;
+                int n = 0;
+                for (int m = 0; m < dp.M; ++m)
+                    if ((R.pres[m][ee >> 5] >> (ee & 31)) & 1u) R.tok[n++] = m;
+            }
+        }
+        __syncthreads();
+        PG_MARK(1, 2);
+        if (!R.n_act) return;
+        e = R.e;
+        p_begin = R.p_begin;
+        p_end = p_begin + R.count;
+    } else if (MODE == kIdent) {
+        e = 0;
+        p_begin = 0;
+        p_end = dp.M;
+    } else {
+        if (a >= *dp.n_active) return;
+        e = dp.active[a];
+        p_begin = dp.offsets[e];
+        p_end = dp.offsets[e + 1];
+    }
     const int r = lane % RB, ks = lane / RB;
     const int row = blockIdx.x * RB + r;  // < row_groups(N) * 64: padded tile rows are readable
     const int nb = K >> 8;
     const int j0 = ks + KS * w;
     uint16_t* xs = (uint16_t*)smem;
     float* xss = (float*)(smem + (size_t)TM * K * 2);
-    float* red = (float*)smem;            // [W][TM][2][RB] after the K loop
-    float* act = red + W * TM * 2 * RB;   // [TM][RB] SwiGLU values
+    float* red = (float*)smem;           // [W][TM][2][RB] after the K loop
+    float* act = red + W * TM * 2 * RB;  // [TM][RB] SwiGLU values
     const uint8_t* gm = gbase + (int64_t)e * gstride;
     const uint8_t* um = ubase + (int64_t)e * ustride;
-    const int p_begin = offsets[e], p_end = offsets[e + 1];
     for (int p0 = p_begin; p0 < p_end; p0 += TM) {
         const int me = min(TM, p_end - p0);
         Raw<QT> rg, ru;
@@ -370,13 +660,15 @@ __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __res
         __syncthreads();
         for (int i = tid; i < me * (K >> 3); i += W * 64) {
             const int t = i / (K >> 3), c = i % (K >> 3);
-            const int tok = perm[p0 + t] / topk;
+            const int tok = MODE == kRoute ? R.tok[p0 - p_begin + t] : MODE == kIdent ? p0 + t : dp.perm[p0 + t] / topk;
             *(uint4*)(xs + t * K + 8 * c) = *(const uint4*)(x + (int64_t)tok * K + 8 * c);
         }
         if (xsum) {
             for (int i = tid; i < me * (K >> 4); i += W * 64) {
                 const int t = i / (K >> 4), c = i % (K >> 4);
-                xss[i] = xsum[(int64_t)(perm[p0 + t] / topk) * (K >> 4) + c];
+                const int tok =
+                    MODE == kRoute ? R.tok[p0 - p_begin + t] : MODE == kIdent ? p0 + t : dp.perm[p0 + t] / topk;
+                xss[i] = xsum[(int64_t)tok * (K >> 4) + c];
             }
         }
         __syncthreads();
@@ -390,6 +682,7 @@ __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __res
             }
             __syncthreads();
         }
+        PG_MARK(1, 3);
         float ag[TM], au[TM];
 #pragma unroll
         for (int t = 0; t < TM; ++t) ag[t] = au[t] = 0.f;
@@ -401,6 +694,7 @@ __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __res
             gu_compute<TM>(rg, xs + 256 * j, xss + 16 * j, K, me, ag);
             gu_compute<TM>(ru, xs + 256 * j, xss + 16 * j, K, me, au);
         }
+        PG_MARK(1, 4);
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
             ag[t] = kslot_sum<RB>(ag[t]);
@@ -443,61 +737,90 @@ __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __res
             }
         }
     }
+    PG_MARK(1, 5);
 }
 
-// partial[p, row] = w[perm[p]] * (inter_p . d_row) for the pairs of one active expert.
-// isum (optional input): 16-element sums of inter rows [P][K/16]; otherwise computed.
-// LDS: isum staging [TM][K/16] f32 (only without isum) | red [W][TM][RB] f32.
+// Per-expert down GEMV: partial[p, row] = w[perm[p]] * (inter_p . d_row) for the pairs of
+// one active expert (stage API; kIdent: the shared expert, weight 1, partial = its output).
+// The K loop steps JW = KS*W super-blocks at a time; each step stages the matching
+// column chunk of the TM inter rows of the chunk in LDS (fp32), and the next step's
+// weights are loaded before the current step is computed.  isum (optional input):
+// 16-element sums of inter rows [P][K/16]; otherwise computed from the staged chunk.
+// LDS: xs [TM][JW*256] f32 | iss [TM][JW*16] f32 | red [W][TM][RB] f32.
 template <int QT, int RB, int W, int TM>
 __global__ __launch_bounds__(W * 64) void dec_down_kernel(const uint8_t* __restrict__ dbase, int64_t dstride, int N,
                                                           int K, const float* __restrict__ inter,
-                                                          const float* __restrict__ isum_in,
-                                                          const int32_t* __restrict__ offsets,
-                                                          const int32_t* __restrict__ perm,
-                                                          const int32_t* __restrict__ active,
-                                                          const int32_t* __restrict__ n_active,
+                                                          const float* __restrict__ isum_in, DecDisp dp,
                                                           const float* __restrict__ topk_w,
                                                           float* __restrict__ partial) {
     constexpr int KS = 64 / RB;
+    constexpr int JW = KS * W;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int a = blockIdx.y;
-    if (a >= *n_active) return;
-    const int e = active[a];
+    const int MODE = dp.mode;
+    int e, p_begin, p_end;
+    if (MODE == kIdent) {
+        e = 0;
+        p_begin = 0;
+        p_end = dp.M;
+    } else {
+        if (a >= *dp.n_active) return;
+        e = dp.active[a];
+        p_begin = dp.offsets[e];
+        p_end = dp.offsets[e + 1];
+    }
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r = lane % RB, ks = lane / RB;
     const int row = blockIdx.x * RB + r;
     const int nb = K >> 8;
-    const int j0 = ks + KS * w;
-    float* iss = (float*)smem;
-    float* red = (float*)(smem + (isum_in ? 0 : (size_t)TM * (K >> 4) * 4));
+    const int j0 = ks + KS * w;  // this lane's super-block within a step
+    float* xs = (float*)smem;
+    float* iss = xs + TM * JW * 256;
+    float* red = iss + TM * JW * 16;
     const uint8_t* dm = dbase + (int64_t)e * dstride;
-    const int p_begin = offsets[e], p_end = offsets[e + 1];
     for (int p0 = p_begin; p0 < p_end; p0 += TM) {
         const int me = min(TM, p_end - p0);
-        Raw<QT> rw;
-        if (j0 < nb) load_raw<QT>(rw, dm, N, nb, row, j0);
-        const float* sums = isum_in ? isum_in + (int64_t)p0 * (K >> 4) : iss;
-        if (!isum_in) {
-            __syncthreads();
-            for (int i = tid; i < me * (K >> 4); i += W * 64) {
-                const float* p = inter + (int64_t)(p0 + i / (K >> 4)) * K + 16 * (i % (K >> 4));
-                float sm = 0.f;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) sm += p[k];
-                iss[i] = sm;
-            }
-            __syncthreads();
-        }
         float acc[TM];
 #pragma unroll
         for (int t = 0; t < TM; ++t) acc[t] = 0.f;
-        for (int j = j0; j < nb; j += KS * W) {
-            if (j != j0) load_raw<QT>(rw, dm, N, nb, row, j);
-            dn_compute<TM>(rw, inter + (int64_t)p0 * K + 256 * j, sums + 16 * j, K, me, acc);
+        Raw<QT> rw;
+        if (j0 < nb) load_raw<QT>(rw, dm, N, nb, row, j0);
+        for (int jb = 0; jb < nb; jb += JW) {
+            const int nbj = min(JW, nb - jb);
+            __syncthreads();  // the previous step's LDS reads are done
+            {
+                const int n4 = nbj * 64;  // 16-byte words of one row chunk
+                copy_idx<8, uint4>(
+                    me * n4, tid, W * 64,
+                    [=](int i) { return (const uint4*)(inter + (int64_t)(p0 + i / n4) * K + 256 * jb + 4 * (i % n4)); },
+                    [=](int i) { return (uint4*)(xs + (i / n4) * (JW * 256) + 4 * (i % n4)); });
+                if (isum_in) {
+                    for (int i = tid; i < me * nbj * 16; i += W * 64) {
+                        const int t = i / (nbj * 16), c = i % (nbj * 16);
+                        iss[t * (JW * 16) + c] = isum_in[(int64_t)(p0 + t) * (K >> 4) + 16 * jb + c];
+                    }
+                }
+            }
+            __syncthreads();
+            if (!isum_in) {
+                for (int i = tid; i < me * nbj * 16; i += W * 64) {
+                    const int t = i / (nbj * 16), c = i % (nbj * 16);
+                    const float* p = xs + t * (JW * 256) + 16 * c;
+                    float sm = 0.f;
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) sm += p[k];
+                    iss[t * (JW * 16) + c] = sm;
+                }
+                __syncthreads();
+            }
+            const int j = jb + j0;
+            Raw<QT> rn;
+            if (j + JW < nb) load_raw<QT>(rn, dm, N, nb, row, j + JW);
+            if (j < nb) dn_compute<TM>(rw, xs + 256 * j0, iss + 16 * j0, JW * 256, me, acc);
+            rw = rn;
         }
 #pragma unroll
         for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
-        __syncthreads();
         if (ks == 0) {
 #pragma unroll
             for (int t = 0; t < TM; ++t)
@@ -510,10 +833,124 @@ __global__ __launch_bounds__(W * 64) void dec_down_kernel(const uint8_t* __restr
 #pragma unroll
             for (int ww = 0; ww < W; ++ww) v += red[(ww * TM + t) * RB + rr];
             const int orow = blockIdx.x * RB + rr;
-            if (orow < N) partial[(int64_t)(p0 + t) * N + orow] = topk_w[perm[p0 + t]] * v;
+            if (orow < N) partial[(int64_t)(p0 + t) * N + orow] = MODE == kIdent ? v : topk_w[dp.perm[p0 + t]] * v;
         }
     }
 }
+
+// Fused down + combine.  Block = RB output rows for all M tokens; its W waves x KS lane
+// groups walk the slices (active slot a, super-block j), slice s = ks + KS*w + KS*W*i, each
+// lane accumulating w_(t,a) * (inter_(t,a) . d_a,row(j)) per token, with the next slice's
+// weights loaded before the current one is computed; a fixed shuffle + LDS tree sums the
+// slices.  out[t, row] = that sum (+ shared[t, row] * sigmoid(shared_logit[t])).
+// Inputs: the routing descriptor (P = M*K pairs), inter / isum rows in sorted pair order,
+// all P rows staged in LDS together with the descriptor (the host uses this kernel only
+// when P*K*4 + P*K/16*4 fits).  The slice order depends only on the routing, so results
+// are reproducible run to run.
+// Dynamic LDS: xs [P][K] f32 | iss [P][K/16] f32.
+template <int QT, int RB, int W, int TM>
+__global__ __launch_bounds__(W * 64) void dec_down_combine_kernel(
+    const uint8_t* __restrict__ dbase, int64_t dstride, int N, int K, const float* __restrict__ inter,
+    const float* __restrict__ isum, const int32_t* __restrict__ desc, int M, int P, const float* __restrict__ shared,
+    const float* __restrict__ shared_logit, float* __restrict__ out) {
+    constexpr int KS = 64 / RB;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int d_slot[128 * 3];
+    __shared__ int d_tok[128];
+    __shared__ float d_w[128];
+    __shared__ float red[W][TM][RB];
+    __shared__ int s_nact;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    float* xs = (float*)smem;
+    float* iss = xs + P * K;
+    PG_MARK(3, 0);
+    {
+        int v[5] = {0, 0, 0, 0, 0};
+        const bool has = tid < P;
+        if (has) {
+            v[0] = desc[kDescSlot + 4 * tid];
+            v[1] = desc[kDescSlot + 4 * tid + 1];
+            v[2] = desc[kDescSlot + 4 * tid + 2];
+            v[3] = desc[kDescPair + 2 * tid];
+            v[4] = desc[kDescPair + 2 * tid + 1];
+        }
+        const int n0 = tid == 0 ? desc[0] : 0;
+        copy_words<8>((uint4*)xs, (const uint4*)inter, P * (K >> 2), tid, W * 64);
+        copy_words<4>((uint4*)iss, (const uint4*)isum, P * (K >> 6), tid, W * 64);
+        if (has) {
+            d_slot[3 * tid] = v[0];
+            d_slot[3 * tid + 1] = v[1];
+            d_slot[3 * tid + 2] = v[2];
+            d_tok[tid] = v[3];
+            d_w[tid] = __builtin_bit_cast(float, v[4]);
+        }
+        if (tid == 0) s_nact = n0;
+    }
+    __syncthreads();
+    PG_MARK(3, 1);
+    const int nact = s_nact;
+    const int r = lane % RB, ks = lane / RB;
+    const int row = blockIdx.x * RB + r;
+    const int nb = K >> 8;
+    const int S = nact * nb;
+    float acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+    int s = ks + KS * w;
+    Raw<QT> rw;
+    if (s < S) load_raw<QT>(rw, dbase + (int64_t)d_slot[3 * (s / nb)] * dstride, N, nb, row, s % nb);
+    while (s < S) {
+        const int sn = s + KS * W;
+        Raw<QT> rn;
+        if (sn < S) load_raw<QT>(rn, dbase + (int64_t)d_slot[3 * (sn / nb)] * dstride, N, nb, row, sn % nb);
+        const int a = s / nb, j = s % nb;
+        const int p0 = d_slot[3 * a + 1], cnt = d_slot[3 * a + 2];
+        float part[TM];
+#pragma unroll
+        for (int t = 0; t < TM; ++t) part[t] = 0.f;
+        dn_compute<TM>(rw, xs + p0 * K + 256 * j, iss + p0 * (K >> 4) + 16 * j, K, cnt, part);
+#pragma unroll
+        for (int q = 0; q < TM; ++q) {
+            if (q < cnt) {
+                const int tq = d_tok[p0 + q];
+                const float v = d_w[p0 + q] * part[q];
+#pragma unroll
+                for (int t = 0; t < TM; ++t)
+                    if (t == tq) acc[t] += v;
+            }
+        }
+        rw = rn;
+        s = sn;
+        PG_MARK(3, 2);
+    }
+    PG_MARK(3, 3);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+    if (ks == 0) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) red[w][t][r] = acc[t];
+    }
+    __syncthreads();
+    for (int i = tid; i < M * RB; i += W * 64) {
+        const int t = i / RB, rr = i % RB;
+        float v = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < W; ++ww) v += red[ww][t][rr];
+        const int orow = blockIdx.x * RB + rr;
+        if (orow < N) {
+            if (shared) {
+                const float g = shared_logit ? 1.0f / (1.0f + expf(-shared_logit[t])) : 1.0f;
+                v += shared[(int64_t)t * N + orow] * g;
+            }
+            out[(int64_t)t * N + orow] = v;
+        }
+    }
+    PG_MARK(3, 4);
+}
+
+// LDS bytes the fused down + combine kernel stages (all P inter rows and their sums).
+inline size_t dc_stage_bytes(int P, int K) { return (size_t)P * K * 4 + (size_t)P * (K / 16) * 4; }
+constexpr size_t kDcStageMax = 52 * 1024;
 
 // ============================================================================ launch plumbing
 // Block shapes (rows per block RB, waves W <= 4 so every wave may use up to 512 VGPRs):
@@ -524,8 +961,7 @@ struct DecShape {
 };
 
 inline DecShape pick_shape(int nb) {
-    static const DecShape menu[] = {{16, 1}, {16, 2}, {16, 4}, {32, 1}, {32, 2}, {32, 4},
-                                    {64, 1}, {64, 2}, {64, 3}, {64, 4}};
+    static const DecShape menu[] = {{16, 1}, {16, 2}, {16, 4}, {32, 1}, {64, 1}, {64, 3}};
     for (const DecShape& s : menu)
         if ((64 / s.RB) * s.W == nb) return s;
     return {16, 4};
@@ -539,25 +975,41 @@ inline int tile_tokens(int M, int K) {
     return t;
 }
 
-template <int QT, int RB, int W, int TM>
-inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk,
-                      const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
-                      int max_active, float* inter, float* isum, hipStream_t st) {
-    const size_t stage = (size_t)TM * g.K * 2 + (size_t)TM * (g.K / 16) * 4;
-    const size_t tail = (size_t)W * TM * 2 * RB * 4 + (size_t)TM * RB * 4;
-    const size_t sh = stage > tail ? stage : tail;
-    hipLaunchKernelGGL((dec_gateup_kernel<QT, RB, W, TM>), dim3(div_up(g.N, RB), max_active), dim3(64 * W), sh, st,
-                       g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, offsets, perm, active, n_active,
-                       inter, isum);
+// Down: per K step, t rows of JW super-blocks staged as fp32 (1088 bytes a super-block
+// with its sums) plus the [W][t][RB] partials; t halves while that exceeds 60 KB.
+inline size_t down_lds_bytes(int t, int RB, int W) { return (size_t)t * (64 / RB) * W * 1088 + (size_t)W * t * RB * 4; }
+inline int down_tile_tokens(int M, const DecShape& sp) {
+    int t = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    while (t > 1 && down_lds_bytes(t, sp.RB, sp.W) > 60 * 1024) t >>= 1;
+    return t;
 }
 
 template <int QT, int RB, int W, int TM>
-inline void dn_launch(const Mats& d, const float* inter, const float* isum, const int32_t* offsets,
-                      const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
+inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, const DecDisp& dp,
+                      int max_active, float* inter, float* isum, hipStream_t st) {
+    const size_t stage = (size_t)TM * g.K * 2 + (size_t)TM * (g.K / 16) * 4;
+    const size_t tail = (size_t)W * TM * 2 * RB * 4 + (size_t)TM * RB * 4;
+    const size_t logits = dp.mode == kRoute ? (size_t)dp.M * dp.E * 4 : 0;
+    size_t sh = stage > tail ? stage : tail;
+    sh = sh > logits ? sh : logits;
+    hipLaunchKernelGGL((dec_gateup_kernel<QT, RB, W, TM>), dim3(div_up(g.N, RB), max_active), dim3(64 * W), sh,
+                       st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, inter, isum);
+}
+
+template <int QT, int RB, int W, int TM>
+inline void dn_launch(const Mats& d, const float* inter, const float* isum, const DecDisp& dp, int max_active,
                       const float* topk_w, float* partial, hipStream_t st) {
-    const size_t sh = (isum ? 0 : (size_t)TM * (d.K / 16) * 4) + (size_t)W * TM * RB * 4;
-    hipLaunchKernelGGL((dec_down_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB), max_active), dim3(64 * W), sh, st,
-                       d.base, d.stride, d.N, d.K, inter, isum, offsets, perm, active, n_active, topk_w, partial);
+    const size_t sh = down_lds_bytes(TM, RB, W);
+    hipLaunchKernelGGL((dec_down_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB), max_active), dim3(64 * W), sh,
+                       st, d.base, d.stride, d.N, d.K, inter, isum, dp, topk_w, partial);
+}
+
+template <int QT, int RB, int W, int TM>
+inline void dc_launch(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
+                      const float* shared, const float* shared_logit, float* out, hipStream_t st) {
+    hipLaunchKernelGGL((dec_down_combine_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB)), dim3(64 * W),
+                       dc_stage_bytes(P, d.K), st, d.base,
+                       d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out);
 }
 
 #define PG_TM(F, QT, RB, W, ...)                   \
@@ -568,52 +1020,86 @@ inline void dn_launch(const Mats& d, const float* inter, const float* isum, cons
     default: F<QT, RB, W, 8>(__VA_ARGS__); break; \
     }
 
+// Block shapes for the per-expert kernels: the shapes pick_shape returns.
 #define PG_SHAPES(F, QT, ...)                                  \
     switch (sp.RB * 16 + sp.W) {                               \
     case 16 * 16 + 1: PG_TM(F, QT, 16, 1, __VA_ARGS__); break; \
     case 16 * 16 + 2: PG_TM(F, QT, 16, 2, __VA_ARGS__); break; \
     case 32 * 16 + 1: PG_TM(F, QT, 32, 1, __VA_ARGS__); break; \
-    case 32 * 16 + 2: PG_TM(F, QT, 32, 2, __VA_ARGS__); break; \
-    case 32 * 16 + 4: PG_TM(F, QT, 32, 4, __VA_ARGS__); break; \
     case 64 * 16 + 1: PG_TM(F, QT, 64, 1, __VA_ARGS__); break; \
-    case 64 * 16 + 2: PG_TM(F, QT, 64, 2, __VA_ARGS__); break; \
     case 64 * 16 + 3: PG_TM(F, QT, 64, 3, __VA_ARGS__); break; \
-    case 64 * 16 + 4: PG_TM(F, QT, 64, 4, __VA_ARGS__); break; \
     default: PG_TM(F, QT, 16, 4, __VA_ARGS__); break;          \
+    }
+
+// Fused down + combine: rows per block and waves chosen so the grid has >= 256 blocks
+// where the output allows it and each lane walks few slices.
+struct DcShape {
+    int RB, W;
+};
+inline DcShape pick_dc_shape(int N, int slices) {
+    const int rb = N >= 256 * 16 ? 16 : 8;
+    const int ks = 64 / rb;
+    int w = (slices + ks - 1) / ks;
+    w = w < 1 ? 1 : w > 4 ? 4 : w;
+    return {rb, w};
+}
+
+#define PG_DC_SHAPES(QT, ...)                                    \
+    switch (dsp.RB * 16 + dsp.W) {                               \
+    case 8 * 16 + 1: PG_TM(dc_launch, QT, 8, 1, __VA_ARGS__); break;  \
+    case 8 * 16 + 2: PG_TM(dc_launch, QT, 8, 2, __VA_ARGS__); break;  \
+    case 8 * 16 + 3: PG_TM(dc_launch, QT, 8, 3, __VA_ARGS__); break;  \
+    case 8 * 16 + 4: PG_TM(dc_launch, QT, 8, 4, __VA_ARGS__); break;  \
+    case 16 * 16 + 1: PG_TM(dc_launch, QT, 16, 1, __VA_ARGS__); break; \
+    case 16 * 16 + 2: PG_TM(dc_launch, QT, 16, 2, __VA_ARGS__); break; \
+    case 16 * 16 + 3: PG_TM(dc_launch, QT, 16, 3, __VA_ARGS__); break; \
+    default: PG_TM(dc_launch, QT, 16, 4, __VA_ARGS__); break;          \
     }
 
 // Per-qtype launchers (defined in decode_q4k.hip / decode_q6k.hip / decode_q8_0.hip).
 template <int QT>
-int dec_gateup_q(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
-                 const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
-                 int max_active, float* inter, float* isum, hipStream_t st);
+int dec_gateup_q(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M, int mode,
+                 const DecDisp& dp, int max_active, float* inter, float* isum, hipStream_t st);
 template <int QT>
-int dec_down_q(const Mats& d, const float* inter, const float* isum, int M, const int32_t* offsets,
-               const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
-               const float* topk_w, float* partial, hipStream_t st);
+int dec_down_q(const Mats& d, const float* inter, const float* isum, int M, int mode, const DecDisp& dp,
+               int max_active, const float* topk_w, float* partial, hipStream_t st);
+template <int QT>
+int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
+                       int max_active, const float* shared, const float* shared_logit, float* out, hipStream_t st);
 
-#define PG_DEFINE_DECODE_LAUNCHERS(QT)                                                                                \
-    template <>                                                                                                      \
-    int dec_gateup_q<QT>(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,       \
-                         const int32_t* offsets, const int32_t* perm, const int32_t* active,                        \
-                         const int32_t* n_active, int max_active, float* inter, float* isum, hipStream_t st) {      \
-        const DecShape sp = pick_shape(g.K >> 8);                                                                    \
-        const int TM = tile_tokens(M, g.K);                                                                          \
-        if ((size_t)TM * g.K * 2 + (size_t)TM * (g.K / 16) * 4 > 64 * 1024)                                         \
-            return fail(PGMOE_E_UNSUPPORTED, "decode gate/up: %d inputs exceed the LDS stage", g.K);                 \
-        PG_SHAPES(gu_launch, QT, g, u, x, xsum, topk, offsets, perm, active, n_active, max_active, inter, isum, st);  \
-        return check_launch("dec_gateup");                                                                           \
-    }                                                                                                                \
-    template <>                                                                                                      \
-    int dec_down_q<QT>(const Mats& d, const float* inter, const float* isum, int M, const int32_t* offsets,         \
-                       const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,         \
-                       const float* topk_w, float* partial, hipStream_t st) {                                        \
-        const DecShape sp = pick_shape(d.K >> 8);                                                                    \
-        const int TM = tile_tokens(M, 0);                                                                            \
-        if (!isum && (size_t)TM * (d.K / 16) * 4 + (size_t)sp.W * TM * sp.RB * 4 > 64 * 1024)                        \
-            return fail(PGMOE_E_UNSUPPORTED, "decode down: LDS stage too large");                                    \
-        PG_SHAPES(dn_launch, QT, d, inter, isum, offsets, perm, active, n_active, max_active, topk_w, partial, st);   \
-        return check_launch("dec_down");                                                                             \
+#define PG_DEFINE_DECODE_GATEUP(QT)                                                                                  \
+    template <>                                                                                                     \
+    int dec_gateup_q<QT>(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,      \
+                         int mode, const DecDisp& dp, int max_active, float* inter, float* isum, hipStream_t st) {  \
+        const DecShape sp = pick_shape(g.K >> 8);                                                                   \
+        const int TM = tile_tokens(M, g.K);                                                                         \
+        if ((size_t)TM * g.K * 2 + (size_t)TM * (g.K / 16) * 4 > 64 * 1024)                                        \
+            return fail(PGMOE_E_UNSUPPORTED, "decode gate/up: %d inputs exceed the LDS stage", g.K);                \
+        PG_SHAPES(gu_launch, QT, g, u, x, xsum, topk, dp, max_active, inter, isum, st);                  \
+        return check_launch("dec_gateup");                                                                          \
+    }
+
+#define PG_DEFINE_DECODE_DOWN(QT)                                                                                    \
+    template <>                                                                                                     \
+    int dec_down_q<QT>(const Mats& d, const float* inter, const float* isum, int M, int mode, const DecDisp& dp,   \
+                       int max_active, const float* topk_w, float* partial, hipStream_t st) {                       \
+        const DecShape sp = pick_shape(d.K >> 8);                                                                   \
+        const int TM = down_tile_tokens(M, sp);                                                                     \
+        PG_SHAPES(dn_launch, QT, d, inter, isum, dp, max_active, topk_w, partial, st);                   \
+        return check_launch("dec_down");                                                                            \
+    }
+
+#define PG_DEFINE_DECODE_DOWN_COMBINE(QT)                                                                            \
+    template <>                                                                                                     \
+    int dec_down_combine_q<QT>(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M,   \
+                               int P, int max_active, const float* shared, const float* shared_logit, float* out,   \
+                               hipStream_t st) {                                                                    \
+        const DcShape dsp = pick_dc_shape(d.N, max_active * (d.K >> 8));                                            \
+        const int TM = tile_tokens(M, 0);                                                                           \
+        if (dc_stage_bytes(P, d.K) > kDcStageMax)                                                                   \
+            return fail(PGMOE_E_UNSUPPORTED, "decode down + combine: %d pairs of %d inputs exceed LDS", P, d.K);    \
+        PG_DC_SHAPES(QT, d, inter, isum, desc, M, P, shared, shared_logit, out, st);                                 \
+        return check_launch("dec_down_combine");                                                                    \
     }
 
 }  // namespace pgmoe

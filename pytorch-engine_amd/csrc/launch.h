@@ -23,15 +23,30 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
                    const float* shared_logit, float* out, hipStream_t st);
 int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, uint8_t* dst,
                     int64_t dst_stride, hipStream_t st);
+// Decode expert stages (M <= decode_tokens_max()).
 int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
                       int max_active, float* inter, float* isum, hipStream_t st);
 int launch_dec_down(const Mats& d, const float* inter, const float* isum, int M, const int32_t* offsets,
                     const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
                     const float* topk_w, float* partial, hipStream_t st);
-int launch_topk_dispatch_small(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w,
-                               int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active,
-                               int32_t* s_disp, float* s_w, hipStream_t st);
+// Flat routing outputs of the routed gate/up (all null: only the descriptor is written).
+struct DecFlat {
+    int32_t *offsets, *perm, *inv, *active, *n_active;
+    float* w;
+};
+int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
+                             const float* logits, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
+                             float* inter, float* isum, hipStream_t st);
+int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
+                            float* isum, hipStream_t st);
+int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st);
+int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int K,
+                            int max_active, const float* shared, const float* shared_logit, float* out,
+                            hipStream_t st);
+int decode_desc_words();
+// Whether the fused down + combine kernel can stage P inter rows of K values.
+bool decode_fused_down(int P, int K);
 int64_t layout_bytes(int qtype, int64_t rows, int64_t cols);
 int gemm_tile_rows();
 int decode_tokens_max();

@@ -14,6 +14,8 @@ namespace pgmoe {
 // identical bits.
 // An optional extra row (the shared expert's sigmoid-gate vector) is treated as expert E
 // and written to extra_out[m] instead of logits.
+// xsum (optional side output for the decode expert kernels): 16-element sums of every x
+// row, computed by the blocks past the first rblocks (which hold the router waves).
 template <int TM, int TE>
 __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __restrict__ x,
                                                             const float* __restrict__ W,
@@ -21,9 +23,11 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
                                                             int E, float* __restrict__ logits,
                                                             const float* __restrict__ extra_w,
                                                             float* __restrict__ extra_out,
-                                                            float* __restrict__ xsum) {
-    if (xsum) {  // side output for the decode GEMVs: 16-element sums of every x row
-        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < M * (H >> 4); i += gridDim.x * blockDim.x) {
+                                                            float* __restrict__ xsum, int rblocks) {
+    PG_MARK(0, 0);
+    if ((int)blockIdx.x >= rblocks) {
+        const int i = (blockIdx.x - rblocks) * blockDim.x + threadIdx.x;
+        if (xsum && i < M * (H >> 4)) {
             const uint16_t* p = x + (int64_t)(i / (H >> 4)) * H + 16 * (i % (H >> 4));
             const uint4 a = *(const uint4*)p, b = *(const uint4*)(p + 8);
             const uint32_t v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
@@ -32,6 +36,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
             for (int k = 0; k < 8; ++k) s += lo_half(v[k]) + hi_half(v[k]);
             xsum[i] = s;
         }
+        return;
     }
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -46,30 +51,52 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
-    for (int c = lane; c < C; c += 64) {
-        float xv[TM][8];
+    // Chunks are processed PF at a time with every load of the group issued before the
+    // first FMA, so each group costs one memory round trip.  The FMA order per slot is
+    // unchanged: chunks ascending, elements 0..7.
+    constexpr int PF = TM * TE <= 8 ? 4 : 2;
+    for (int c0 = lane; c0 < C; c0 += 64 * PF) {
+        uint4 xq[PF][TM];
+        float4 wq[PF][TE][2];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int m = m0 + i < M ? m0 + i : M - 1;
-            const uint4 v = *(const uint4*)(x + (int64_t)m * H + 8 * c);
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+        for (int q = 0; q < PF; ++q) {
+            const int c = c0 + 64 * q;
+            if (c < C) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                xv[i][2 * k] = lo_half(w4[k]);
-                xv[i][2 * k + 1] = hi_half(w4[k]);
+                for (int i = 0; i < TM; ++i) {
+                    const int m = m0 + i < M ? m0 + i : M - 1;
+                    xq[q][i] = *(const uint4*)(x + (int64_t)m * H + 8 * c);
+                }
+#pragma unroll
+                for (int j = 0; j < TE; ++j) {
+                    const int e = e0 + j < rows ? e0 + j : rows - 1;
+                    const float* wr = e < E ? W + (int64_t)e * H : extra_w;
+                    wq[q][j][0] = *(const float4*)(wr + 8 * c);
+                    wq[q][j][1] = *(const float4*)(wr + 8 * c + 4);
+                }
             }
         }
 #pragma unroll
-        for (int j = 0; j < TE; ++j) {
-            const int e = e0 + j < rows ? e0 + j : rows - 1;
-            const float* wr = e < E ? W + (int64_t)e * H : extra_w;
-            const float4 w0 = *(const float4*)(wr + 8 * c);
-            const float4 w1 = *(const float4*)(wr + 8 * c + 4);
-            const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        for (int q = 0; q < PF; ++q) {
+            if (c0 + 64 * q < C) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i) {
+                    const uint32_t w4[4] = {xq[q][i].x, xq[q][i].y, xq[q][i].z, xq[q][i].w};
+                    float xv[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[i][j] = __builtin_fmaf(xv[i][k], wv[k], acc[i][j]);
+                    for (int k = 0; k < 4; ++k) {
+                        xv[2 * k] = lo_half(w4[k]);
+                        xv[2 * k + 1] = hi_half(w4[k]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < TE; ++j) {
+                        const float wv[8] = {wq[q][j][0].x, wq[q][j][0].y, wq[q][j][0].z, wq[q][j][0].w,
+                                             wq[q][j][1].x, wq[q][j][1].y, wq[q][j][1].z, wq[q][j][1].w};
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) acc[i][j] = __builtin_fmaf(xv[k], wv[k], acc[i][j]);
+                    }
+                }
+            }
         }
     }
 #pragma unroll
@@ -85,6 +112,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
                 extra_out[m] = v;
             }
         }
+    PG_MARK(0, 1);
 }
 
 // Per token: top-K experts by (logit desc, id asc); w = softmax prob (max-subtracted,
@@ -159,23 +187,20 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
     if (M <= 0) return PGMOE_OK;
     const int threads = 256;
     const int rows = E + (extra_w ? 1 : 0);
-    if (M <= 4) {
-        // decode: one wave per (all tokens, one expert) spreads the router read widely
-        constexpr int TM = 4, TE = 1;
-        const int waves = div_up(M, TM) * div_up(rows, TE);
-        hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits, extra_w, extra_out, xsum);
-    } else if (M <= 8) {
-        constexpr int TM = 8, TE = 1;
-        const int waves = div_up(M, TM) * div_up(rows, TE);
-        hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits, extra_w, extra_out, xsum);
-    } else {
-        constexpr int TM = 8, TE = 4;
-        const int waves = div_up(M, TM) * div_up(rows, TE);
-        hipLaunchKernelGGL((router_logits_kernel<TM, TE>), dim3(div_up(waves, 4)), dim3(threads), 0, st,
-                           x, W, bias, M, H, E, logits, extra_w, extra_out, xsum);
-    }
+    const int xblocks = xsum ? div_up(M * (H >> 4), threads) : 0;
+#define PG_ROUTER(TM_, TE_)                                                                                   \
+    do {                                                                                                      \
+        const int rb = div_up(div_up(M, TM_) * div_up(rows, TE_), 4);                                        \
+        hipLaunchKernelGGL((router_logits_kernel<TM_, TE_>), dim3(rb + xblocks), dim3(threads), 0, st, x, W, bias, \
+                           M, H, E, logits, extra_w, extra_out, xsum, rb);                                    \
+    } while (0)
+    if (M <= 4)
+        PG_ROUTER(4, 1);  // decode: one wave per (all tokens, one expert) spreads the router read widely
+    else if (M <= 8)
+        PG_ROUTER(8, 1);
+    else
+        PG_ROUTER(8, 4);
+#undef PG_ROUTER
     return check_launch("router_logits");
 }
 
