@@ -2,19 +2,27 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-A "step" is one HipSparseMoEMLP.forward (router -> top-k -> dispatch -> gate/up+SwiGLU ->
+A "step" is one HipSparseMoEMLP.forward (router -> top-k -> dispatch -> gate/up + SwiGLU ->
 down -> combine) over one batch of synthetic tokens already resident in HBM.  The headline
-`value` is decode tok/s at M=1; the same JSON line carries M=2/4/8
-decode, M=4096 Zipf-skewed prefill (config 3), the roofline of the dominant kernel and
-the CPU baseline (the torch-CPU restatement of the reference path, timed on this host).
+`value` is decode tok/s at M = 1.  Each step runs one layer forward,
+replayed from a HIP graph (one graph per weight copy, no host work inside the timed region).
+The same JSON line carries M = 2 / 4 / 8 decode, the M = 4096 Zipf-skewed prefill (config
+3), the roofline of the dominant kernel, and the CPU baseline.  The CPU baseline is the
+torch-CPU restatement of the reference path, timed on this host.
 
-Weights are rotated over >= 8 device copies so decode reads come from HBM rather than the
-256 MB Infinity Cache.  Only the GGUF bytes of distinct active experts count as traffic.
+Weights are rotated over `--copies` device copies (default 8; 3.1 GB for this layer), so
+decode reads come from HBM rather than the 256 MB Infinity Cache.  Only the GGUF bytes of
+the distinct active experts count as algorithmic traffic.
+
+Kernel durations come from pgmoe_moe_forward_timed.  Every kernel of the forward records
+HIP events at its own begin and end on the stream it runs on, which is the interval a
+kernel trace (rocprofv3 --kernel-trace) reports.
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -25,8 +33,10 @@ for p in (REPO, os.path.join(REPO, "pytorch-engine_amd")):
     if p not in sys.path:
         sys.path.insert(0, p)
 
-HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, published
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+METRIC = "MoE layer tok/s at M=1 and M=4096 (Qwen3-30B-A3B shape); % HBM / MFMA roofline"
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_dec_gateup_qwen3_m1.json")
 
 
 def log(msg: str) -> None:
@@ -36,80 +46,150 @@ def log(msg: str) -> None:
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--copies", type=int, default=8, help="rotated weight copies (MALL defeat)")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--m-list", default="1,2,4,8", help="decode token counts to time (1 is the headline)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 256 MiB device copy (calibrates FETCH/WRITE_SIZE counters)")
     return ap.parse_args()
 
 
-class Timer:
-    """HIP events on the current stream."""
+# ----------------------------------------------------------------------------- HIP events
+class Hip:
+    """The HIP runtime torch loaded (so events and kernels share one runtime)."""
 
-    def __init__(self, torch):
-        self.torch = torch
-        self.a = torch.cuda.Event(enable_timing=True)
-        self.b = torch.cuda.Event(enable_timing=True)
+    def __init__(self) -> None:
+        path = None
+        for line in open("/proc/self/maps"):
+            if "libamdhip64" in line:
+                path = line.split()[-1]
+                break
+        self.L = ctypes.CDLL(path or "libamdhip64.so")
+        self.L.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.L.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.L.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.L.hipEventDestroy.argtypes = [ctypes.c_void_p]
 
-    def __enter__(self):
-        self.torch.cuda.synchronize()
-        self.a.record()
-        return self
+    def events(self, n: int):
+        out = (ctypes.c_void_p * n)()
+        for i in range(n):
+            h = ctypes.c_void_p()
+            if self.L.hipEventCreate(ctypes.byref(h)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            out[i] = h.value
+        return out
 
-    def __exit__(self, *exc):
-        self.b.record()
-        self.torch.cuda.synchronize()
-        self.ms = self.a.elapsed_time(self.b)
+    def elapsed_ms(self, a, b) -> float:
+        f = ctypes.c_float()
+        if self.L.hipEventElapsedTime(ctypes.byref(f), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return float(f.value)
 
 
-def time_forward(torch, mods, xs, steps, warmup):
+def kernel_durations(torch, hip, mods, x, reps: int):
+    """Average duration (ms) of each kernel of the forward, over `reps` forwards that rotate
+    the weight copies, from the events the kernels record themselves."""
+    from pgmoe._lib import check, lib
+    n_ev = 32
+    starts, stops = hip.events(n_ev), hip.events(n_ev)
+    M = x.shape[0]
+    sums, names_n = None, 0
+    for i in range(reps + 2):
+        m = mods[i % len(mods)]
+        out = torch.empty((M, m.hidden), dtype=torch.float32, device=x.device)
+        ws = m._workspace(M)
+        nl = ctypes.c_int32()
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        check(lib().pgmoe_moe_forward_timed(m._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                            stream, starts, stops, n_ev, ctypes.byref(nl)), "forward_timed")
+        torch.cuda.synchronize()
+        if i < 2:
+            continue  # warm-up
+        names_n = nl.value
+        d = [hip.elapsed_ms(starts[k], stops[k]) for k in range(min(names_n, n_ev))]
+        sums = d if sums is None else [s + v for s, v in zip(sums, d)]
+    return [s / reps for s in sums]
+
+
+# ----------------------------------------------------------------------------- timing
+def graph_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
+    """Per-step time of exactly `steps` forwards replayed from HIP graphs: one graph holds
+    one forward of every weight copy in turn (so a replay is `len(mods)` steps), and a
+    second graph of the first `steps % len(mods)` copies completes the count.  The timed
+    region is bracketed by synchronizations and holds no host work besides the replays."""
+    n = len(mods)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    outs = []
+
+    def capture(ms):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            o = [m(x) for m in ms]
+        return g, o
+
+    with torch.cuda.stream(s):
+        for m in mods:
+            m(x)  # allocate the workspaces outside capture
+        torch.cuda.synchronize()
+        full, outs = capture(mods)
+        rem = steps % n
+        part = capture(mods[:rem])[0] if rem else None
+    torch.cuda.synchronize()
+    for _ in range(max(1, warmup // n)):
+        full.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps // n):
+        full.replay()
+    if part is not None:
+        part.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    full.replay()
+    torch.cuda.synchronize()
+    for m, o in zip(mods, outs):  # the replays compute what eager forwards compute
+        if not torch.equal(o, m(x)):
+            raise RuntimeError("graph replay differs from the eager forward")
+    del full, part
+    return ms
+
+
+def eager_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
     n = len(mods)
     for i in range(warmup):
-        mods[i % n](xs[i % len(xs)])
-    with Timer(torch) as t:
-        for i in range(steps):
-            mods[i % n](xs[i % len(xs)])
-    return t.ms / steps
-
-
-def stage_kernel_times(torch, mods, x, steps):
-    """Average duration of the gate/up and down expert kernels, measured with events
-    around each launch while running the staged forward on the current stream."""
-    from pgmoe import ops
-    n = len(mods)
-    m0 = mods[0]
-    M = x.shape[0]
-    mode = 0 if M <= 8 else 1
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    prep = []
-    for m in mods:
-        _, idx, tw = ops.router_topk(x, m.router_weight, m.router_bias, m.top_k, m.norm_topk_prob)
-        prep.append((ops.dispatch(idx, m.n_experts, 64), tw))
+        mods[i % n](x)
     torch.cuda.synchronize()
-    for i in range(steps + 3):
-        m = mods[i % n]
-        disp, tw = prep[i % n]
-        e = ev[i - 3] if i >= 3 else None
-        if e:
-            e[0].record()
-        inter = ops.expert_gateup(m.gate_exps.weights(), m.up_exps.weights(), x, m.top_k, disp, mode)
-        if e:
-            e[1].record()
-        ops.expert_down(m.down_exps.weights(), inter, M, m.top_k, disp, tw, mode)
-        if e:
-            e[2].record()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        mods[i % n](x)
+    b.record()
     torch.cuda.synchronize()
-    gu = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
-    dn = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
-    n_active = int(prep[0][0][4].cpu()[0])
-    return gu, dn, n_active
+    return a.elapsed_time(b) / steps
 
 
-def cpu_baseline(spec, lay, M, seconds):
-    import numpy as np
+def copy_probe(torch) -> None:
+    """A plain device copy of known size, run when the counters are being calibrated."""
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy probe: 4 x {n} byte device copies")
+
+
+def cpu_baseline(lay, M: int, seconds: float):
     import torch
     import oracle
     from oracle import torch_port
@@ -119,70 +199,101 @@ def cpu_baseline(spec, lay, M, seconds):
     ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config, router_bias=lay.router_bias)
     port = torch_port.PortMoE(ol)
     x = torch.from_numpy(lay.draw_x(64))
-    port.forward(x[0:M], faithful=True)  # warmup
+    port.forward(x[0:M], faithful=True)  # warm-up
     n, t0 = 0, time.perf_counter()
     while True:
         port.forward(x[(n * M) % 64:(n * M) % 64 + M], faithful=True)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 200:
+        if el >= seconds or n >= 400:
             break
     return {"value": round(n * M / el, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n} forwards of M={M} tokens of the same layer (torch-CPU restatement of the "
-                      f"reference CPU path, fp16 casts kept), {el:.1f} s, {cores} threads"}
+            "sample": f"{n} forwards of M={M} token(s) of the benchmarked layer: oracle/torch_port.py, the "
+                      f"torch-CPU restatement of the reference CPU path (repacked W4/W8, chunked fp32 dequant + "
+                      f"F.linear, fp16 casts kept), {el:.1f} s on {cores} threads"}
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+        return rec.get("bytes_per_launch"), rec
+    except (OSError, ValueError):
+        return None, None
 
 
 def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU figures are not produced",
-                          "n_gpus": args.gpus}))
+                          "n_gpus": args.gpus}), flush=True)
         return 2
     import numpy as np
     import torch
     import oracle
-    from pgmoe import HipSparseMoEMLP
+    from pgmoe import HipSparseMoEMLP, ops
     from pgmoe.synth import CONFIGS, SyntheticLayer
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    hip = Hip()
     props = torch.cuda.get_device_properties(dev)
     spec = CONFIGS["qwen3_30b_a3b"]
-    log(f"[bench] device {props.name} CUs={props.multi_processor_count}; building {spec.name}")
+    log(f"[bench] device {props.name} CUs={props.multi_processor_count}; building {spec.name} "
+        f"+ {args.copies - 1} weight copies")
+    if args.copy_probe:
+        copy_probe(torch)
     lay = SyntheticLayer(spec, seed=0)
     base = HipSparseMoEMLP(lay.gguf, lay.config, 0, dev)
     mods = [base] + [base.replica() for _ in range(max(0, args.copies - 1))]
-    per_expert = base.active_weight_bytes(1)
     ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config)
 
-    # correctness gate on the benchmarked layer
-    x1 = lay.draw_x(1)
-    got = base(torch.from_numpy(x1).to(dev)).cpu().numpy()
-    logits, idx, w = ol.route(x1)
-    ref = ol.forward_tokens(x1, idx, w)
-    gate = {"rel_l2": oracle.rel_l2(got, ref), "max_rel": oracle.max_rel(got, ref),
-            "min_topk_margin": oracle.min_topk_margin(logits, spec.top_k)}
-    log(f"[bench] parity M=1: {gate}")
-    if not (gate["rel_l2"] <= 1e-3 and gate["max_rel"] <= 2e-2):
-        log("[bench] PARITY FAILED")
-        return 1
+    # ---- correctness gate on the benchmarked layer (M = 1 and M = 8)
+    gate = {}
+    for M in (1, 8):
+        xg = lay.draw_x(M)
+        xt = torch.from_numpy(xg).to(dev)
+        got = base(xt).cpu().numpy()
+        logits, idx, w = ol.route(xg)
+        ref = ol.forward_tokens(xg, idx, w)
+        _, gidx, _ = ops.router_topk(xt, base.router_weight, None, base.top_k, base.norm_topk_prob)
+        gate[M] = {"rel_l2": oracle.rel_l2(got, ref), "max_rel": oracle.max_rel(got, ref),
+                   "topk_bit_exact": bool(np.array_equal(gidx.cpu().numpy(), idx)),
+                   "min_topk_margin": oracle.min_topk_margin(logits, spec.top_k)}
+        log(f"[bench] parity M={M}: {gate[M]}")
+        if not (gate[M]["rel_l2"] <= 1e-3 and gate[M]["max_rel"] <= 2e-2 and gate[M]["topk_bit_exact"]):
+            log("[bench] PARITY FAILED")
+            return 1
 
+    # ---- decode: graph-replayed steps (headline M = 1), eager for reference
     decode = {}
-    for M in (1, 2, 4, 8):
-        xs = [torch.from_numpy(lay.draw_x(M)).to(dev)]
-        ms = time_forward(torch, mods, xs, args.steps, args.warmup)
-        decode[M] = {"ms_per_step": ms, "tok_per_s": M / (ms * 1e-3)}
-        log(f"[bench] decode M={M}: {ms * 1e3:.2f} us/layer, {M / (ms * 1e-3):.0f} tok/s")
-    xk = torch.from_numpy(x1).to(dev)
-    gu_ms, dn_ms, n_act = stage_kernel_times(torch, mods, xk, args.steps)
-    gu_bytes = n_act * (base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat)
-    dn_bytes = n_act * base.down_exps.gguf_bytes_per_mat
-    gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    dn_gbs = dn_bytes / (dn_ms * 1e-3) / 1e9
-    both_gbs = (gu_bytes + dn_bytes) / ((gu_ms + dn_ms) * 1e-3) / 1e9
-    log(f"[bench] kernels M=1: gateup {gu_ms * 1e3:.2f} us {gu_gbs:.0f} GB/s; down {dn_ms * 1e3:.2f} us "
-        f"{dn_gbs:.0f} GB/s; experts {both_gbs:.0f} GB/s ({n_act} experts)")
+    m_list = sorted({1} | {int(v) for v in args.m_list.split(",") if v})
+    for M in m_list:
+        x = torch.from_numpy(lay.draw_x(M)).to(dev)
+        steps = args.steps if M == 1 else max(50, args.steps // 4)
+        warm = args.warmup if M == 1 else max(10, args.warmup // 4)
+        ms = graph_step_ms(torch, mods, x, steps, warm)
+        ms_eager = eager_step_ms(torch, mods, x, max(50, steps // 4), 10)
+        _, idx, _ = ol.route(lay.draw_x(M))
+        n_act = len(np.unique(idx))
+        kd = kernel_durations(torch, hip, mods, x, 50)
+        decode[M] = {"us_per_step": round(ms * 1e3, 3), "tok_per_s": round(M / (ms * 1e-3), 1),
+                     "steps": steps, "eager_us_per_step": round(ms_eager * 1e3, 3),
+                     "active_experts": n_act, "kernel_us": [round(v * 1e3, 3) for v in kd],
+                     "active_weight_bytes": base.active_weight_bytes(n_act)}
+        log(f"[bench] decode M={M}: {decode[M]}")
 
+    # dominant kernel at M = 1: the routed gate/up (launch 1 of router, gate/up, down+combine)
+    d1 = decode[1]
+    gu_us = d1["kernel_us"][1]
+    gu_bytes = d1["active_experts"] * (base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat)
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    dn_us = d1["kernel_us"][2]
+    dn_bytes = d1["active_experts"] * base.down_exps.gguf_bytes_per_mat
+    layer_gbs = d1["active_weight_bytes"] / (d1["us_per_step"] * 1e-6) / 1e9
+    traffic, traffic_rec = load_traffic()
+
+    # ---- prefill M = 4096 with the Zipf router bias (config 3)
     prefill = None
     if not args.no_prefill:
         del mods
@@ -193,55 +304,62 @@ def main() -> int:
         pm.set_router_bias(torch.from_numpy(play.router_bias))
         pmods = [pm, pm.replica()]
         M = 4096
-        xp = torch.from_numpy(play.draw_x(M)).to(dev)
-        ms = time_forward(torch, pmods, [xp], args.prefill_steps, 2)
-        gu_p, dn_p, n_act_p = stage_kernel_times(torch, pmods, xp, args.prefill_steps)
+        xp_np = play.draw_x(M)
+        xp = torch.from_numpy(xp_np).to(dev)
+        ms = eager_step_ms(torch, pmods, xp, args.prefill_steps, 2)
+        kd = kernel_durations(torch, hip, pmods, xp, max(3, args.prefill_steps // 2))
+        # launches: router, top-k, dispatch, gate/up, row-scale, down, combine
         P = M * pspec.top_k
         fl_gu = 2.0 * P * pspec.hidden * 2 * pspec.inter
         fl_dn = 2.0 * P * pspec.inter * pspec.hidden
-        mfma = (fl_gu + fl_dn) / ((gu_p + dn_p) * 1e-3) / 1e12
-        prefill = {"M": M, "ms_per_step": round(ms, 4), "tok_per_s": round(M / (ms * 1e-3), 1),
-                   "gateup_ms": round(gu_p, 4), "down_ms": round(dn_p, 4),
-                   "gemm_tflops": round(mfma, 2), "mfma_frac": round(mfma / FP16_PEAK_TFLOPS, 4),
-                   "active_experts": n_act_p}
+        gu_tf = fl_gu / (kd[3] * 1e-3) / 1e12
+        dn_tf = fl_dn / (kd[5] * 1e-3) / 1e12
+        both_tf = (fl_gu + fl_dn) / ((kd[3] + kd[5]) * 1e-3) / 1e12
+        prefill = {"M": M, "us_per_step": round(ms * 1e3, 2), "tok_per_s": round(M / (ms * 1e-3), 1),
+                   "kernel_us": [round(v * 1e3, 2) for v in kd],
+                   "kernels": ["router", "topk", "dispatch", "gemm_gateup", "rowscale", "gemm_down", "combine"],
+                   "gemm_gateup_tflops": round(gu_tf, 1), "gemm_down_tflops": round(dn_tf, 1),
+                   "gemm_tflops": round(both_tf, 1), "mfma_frac": round(both_tf / FP16_PEAK_TFLOPS, 4),
+                   "layer_tflops": round((fl_gu + fl_dn) / (ms * 1e-3) / 1e12, 1)}
         log(f"[bench] prefill M=4096: {prefill}")
         del pmods, pm
         torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(spec, lay, 1, args.cpu_seconds)
+        cpu = cpu_baseline(lay, 1, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu}")
 
-    ms1 = decode[1]["ms_per_step"]
     rec = {
-        "metric": "MoE layer tok/s at M=1 (Qwen3-30B-A3B shape)",
-        "value": round(decode[1]["tok_per_s"], 1),
+        "metric": METRIC,
+        "value": d1["tok_per_s"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms1, 5),
+        "ms_per_step": round(d1["us_per_step"] / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": "qwen3_30b_a3b MoE layer decode M=1: H=2048, E=128, top-8, I=768, "
-                               "gate/up Q4_K, down Q6_K, fp16 activations",
-                   "weight_copies": args.copies},
+        "config": {"workload": "qwen3_30b_a3b MoE layer decode, M=1 token per step (H=2048, E=128, top-8, "
+                               "I=768, gate/up Q4_K, down Q6_K, fp16 activations, fp32 accumulate)",
+                   "weight_copies": args.copies, "timing": "one forward per HIP graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "gemv_gateup_kernel (gate+up GGUF bytes of the distinct active experts)"},
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "dec_gateup_kernel (routed gate/up + SwiGLU), M=1",
+                     "algorithmic_bytes": gu_bytes, "kernel_us": gu_us,
+                     "traffic_source": traffic_rec.get("source") if traffic_rec else None},
         "cpu_baseline": cpu,
-        "decode": {str(k): {"tok_per_s": round(v["tok_per_s"], 1), "us_per_step": round(v["ms_per_step"] * 1e3, 2)}
-                   for k, v in decode.items()},
-        "kernels_m1": {"gateup_us": round(gu_ms * 1e3, 3), "gateup_gbs": round(gu_gbs, 1),
-                       "down_us": round(dn_ms * 1e3, 3), "down_gbs": round(dn_gbs, 1),
-                       "experts_gbs": round(both_gbs, 1), "experts_hbm_frac": round(both_gbs / HBM_PEAK_GBS, 4),
-                       "active_bytes": int(gu_bytes + dn_bytes)},
+        "decode": {str(k): v for k, v in decode.items()},
+        "kernels_m1": {"names": ["router_logits", "dec_gateup", "dec_down_combine"], "us": d1["kernel_us"],
+                       "down_combine_gbs": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1),
+                       "layer_active_gbs": round(layer_gbs, 1),
+                       "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "prefill": prefill,
-        "parity": {k: float(f"{v:.3e}") for k, v in gate.items()},
+        "parity": {str(M): {k: (float(f"{v:.3e}") if isinstance(v, float) else v) for k, v in g.items()}
+                   for M, g in gate.items()},
     }
     print(json.dumps(rec), flush=True)
     return 0

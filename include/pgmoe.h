@@ -89,6 +89,18 @@ size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M);
 int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
                       size_t ws_bytes, void* stream);
 
+/* pgmoe_moe_forward with per-kernel timing.  No counterpart in the reference: it is for
+ * benchmarks and profilers that want each kernel's duration from the caller's own stream.
+ * The i-th kernel the call launches (i < n_events) records start_events[i] when it begins
+ * and stop_events[i] when it ends (hipEvent_t handles created by the caller; either array
+ * may be NULL).  *n_launches (if not NULL) receives the number of kernels launched.
+ * Launch order: decode (M <= 8): router, gate/up, [shared gate/up, shared down], down +
+ * combine (or down, combine); prefill: router, top-k, dispatch, gate/up, row-scale, down,
+ * [shared: identity dispatch, gate/up, row-scale, down, shared gate], combine. */
+int pgmoe_moe_forward_timed(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
+                            size_t ws_bytes, void* stream, void** start_events, void** stop_events,
+                            int32_t n_events, int32_t* n_launches);
+
 /* ---- stages of the forward, exposed for tests and for callers that fuse around them ---- */
 
 /* R1+R2: logits[M, E] = f32(x) . W^T (+ bias) in the fixed order of the CPU oracle,

@@ -9,6 +9,11 @@ namespace pgmoe {
 
 static thread_local char g_err[512] = "";
 
+LaunchTiming*& launch_timing() {
+    static thread_local LaunchTiming* t = nullptr;
+    return t;
+}
+
 void set_error(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
@@ -324,6 +329,18 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
     }
     return launch_combine(WS(float, partial), WS(int32_t, inv), M, K, H, shared, shared_logit, out, st);
 #undef WS
+}
+
+int pgmoe_moe_forward_timed(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
+                            size_t ws_bytes, void* stream, void** start_events, void** stop_events, int32_t n_events,
+                            int32_t* n_launches) {
+    if (n_events < 0) return fail(PGMOE_E_INVALID, "negative event count");
+    LaunchTiming t{(hipEvent_t*)start_events, (hipEvent_t*)stop_events, n_events, 0};
+    launch_timing() = &t;
+    const int rc = pgmoe_moe_forward(L, x, M, out, ws, ws_bytes, stream);
+    launch_timing() = nullptr;
+    if (n_launches) *n_launches = t.next;
+    return rc;
 }
 
 }  // extern "C"

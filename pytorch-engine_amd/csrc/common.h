@@ -6,11 +6,12 @@
 
 #include "pgmoe.h"
 
-// Phase timestamps for profiling builds only: a build that defines PG_TRACE also defines
-// `__device__ unsigned long long pg_trace[]` in the same translation unit, and thread 0 of
+// Phase timestamps for profiling builds only: a build that defines PG_TRACE (relocatable
+// device code) also defines `__device__ unsigned long long pg_trace[]`, and thread 0 of
 // each block stores wall_clock64() (100 MHz) at slot [kernel][block][point].  Without
 // PG_TRACE the marks compile to nothing.
 #ifdef PG_TRACE
+extern __device__ unsigned long long pg_trace[];
 #define PG_MARK(kern, pt)                                                                                  \
     do {                                                                                                   \
         const unsigned pg_b = blockIdx.y * gridDim.x + blockIdx.x;                                         \

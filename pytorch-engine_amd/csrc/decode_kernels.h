@@ -345,10 +345,14 @@ constexpr int kDescWords = kDescPair + 2 * 128;
 
 struct RouteShared {
     uint32_t pres[kDecTM][16];  // token x expert membership bits (E <= 512)
+    uint32_t used[16];          // union of pres over the tokens
+    int wc[16];                 // active experts in the words before q
+    int wp[16];                 // (token, expert) pairs in the words before q
     int mem_e[kDecTM * 16];     // the K members of token m at [m*K, m*K+K), ascending id
     float mem_w[kDecTM * 16];   // their combine weights (publishing block only)
     int n_act, e, p_begin, count;
     int tok[kDecTM];
+    uint64_t wbuf[4][64];       // per-wave selection scratch
 };
 
 // Selection key of (logit v, expert e): larger key = earlier in (logit desc, id asc).
@@ -357,24 +361,6 @@ __device__ __forceinline__ uint64_t route_key(float v, int e) {
     const uint32_t u = __builtin_bit_cast(uint32_t, v + 0.0f);
     const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((uint64_t)o << 9) | (uint64_t)(511 - e);
-}
-
-// Top-k membership of every token (one wave per token): the K-th largest key is found by
-// a 41-step radix descent on the key bits (ballot counts), and the members are exactly
-// the keys at or above it (keys are distinct).  With `weights`, also the softmax weights
-// of the members (max-subtracted, denominator over all E, optional renorm; model.py:903-907).
-// sl: LDS scratch of M*E floats.  Every thread of the block calls this.
-template <int RE>
-__device__ __forceinline__ uint64_t radix_kth(const uint64_t (&key)[8], int K) {
-    uint64_t thr = 0;
-    for (int b = 40; b >= 0; --b) {
-        const uint64_t cand = thr | (1ull << b);
-        int cnt = 0;
-#pragma unroll
-        for (int r = 0; r < RE; ++r) cnt += __popcll(__ballot(key[r] >= cand));
-        if (cnt >= K) thr = cand;
-    }
-    return thr;
 }
 
 // Block-wide copy of n elements: element i moves from src(i) to dst(i), U loads in flight
@@ -397,114 +383,200 @@ __device__ __forceinline__ void copy_words(T* dst, const T* __restrict__ src, in
     copy_idx<U, T>(n, tid, nth, [=](int i) { return src + i; }, [=](int i) { return dst + i; });
 }
 
-__device__ __forceinline__ void route_in_block(const float* __restrict__ logits, int M, int E, int K, float* sl,
-                                               RouteShared& R, bool weights, int norm) {
-    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6;
-    copy_words<8>(sl, logits, M * E, tid, nth);
-    __syncthreads();
-    const int RE = (E + 63) >> 6;
-    for (int m = wv; m < M; m += nth >> 6) {
-        uint64_t key[8];
+// K-th largest of the distinct keys of one token held by a wave (lane l: experts l + 64r),
+// by a 41-step radix descent on the key bits (ballot counts).  Exact for any keys; used
+// when the candidate select below has too many candidates.
+template <int RE>
+__device__ __forceinline__ uint64_t kth_key_radix(const uint64_t (&key)[RE], int K) {
+    uint64_t thr = 0;
+    for (int b = 40; b >= 0; --b) {
+        const uint64_t cand = thr | (1ull << b);
+        int cnt = 0;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
+        for (int r = 0; r < RE; ++r) cnt += __popcll(__ballot(key[r] >= cand));
+        thr = cnt >= K ? cand : thr;
+    }
+    return thr;
+}
+
+// Rank of v among n 64-bit values in LDS (number strictly greater), n even.
+__device__ __forceinline__ int lds_rank(const uint64_t* buf, int n, uint64_t v) {
+    int c = 0;
+    for (int j = 0; j < n; j += 2) {
+        const uint64_t a = buf[j], b = buf[j + 1];
+        c += a > v ? 1 : 0;
+        c += b > v ? 1 : 0;
+    }
+    return c;
+}
+
+// K-th largest key of one token (keys distinct, at least K of them nonzero; 1 <= K <= 16).
+// 1. T = the K-th largest of the 64 lane maxima.  At most K lanes have a maximum >= the
+//    K-th largest key k* (each such maximum is a distinct key >= k*), so T <= k*.
+// 2. The candidates (keys >= T) hold the K largest keys; they are ranked among
+//    themselves and the one of rank K-1 is k*.  More than 64 candidates (keys bunched in
+//    few lanes) take the radix descent instead.
+// wbuf: this wave's 64-word LDS scratch.
+template <int RE>
+__device__ __forceinline__ uint64_t kth_key(const uint64_t (&key)[RE], int K, int lane, uint64_t* wbuf) {
+    uint64_t lm = 0;
+#pragma unroll
+    for (int r = 0; r < RE; ++r) lm = key[r] > lm ? key[r] : lm;
+    wbuf[lane] = lm;
+    __builtin_amdgcn_wave_barrier();
+    const int c1 = lds_rank(wbuf, 64, lm);
+    const uint64_t b1 = __ballot(lm != 0 && c1 == K - 1);
+    const int l1 = __ffsll((unsigned long long)b1) - 1;
+    const uint64_t T = ((uint64_t)__shfl(uint32_t(lm >> 32), l1, 64) << 32) | __shfl(uint32_t(lm), l1, 64);
+    int C = 0;
+#pragma unroll
+    for (int r = 0; r < RE; ++r) C += __popcll(__ballot(key[r] >= T));
+    if (C > 64) return kth_key_radix<RE>(key, K);
+    __builtin_amdgcn_wave_barrier();
+    int base = 0;
+#pragma unroll
+    for (int r = 0; r < RE; ++r) {
+        const bool in = key[r] >= T;
+        const uint64_t mk = __ballot(in);
+        if (in) wbuf[base + __popcll(mk & ((1ull << lane) - 1ull))] = key[r];
+        base += __popcll(mk);
+    }
+    if ((C & 1) && lane == C) wbuf[C] = 0;  // pad to an even count (0 is below every key)
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t ci = lane < C ? wbuf[lane] : 0;
+    const int c2 = lds_rank(wbuf, (C + 1) & ~1, ci);
+    const uint64_t b2 = __ballot(lane < C && c2 == K - 1);
+    const int l2 = __ffsll((unsigned long long)b2) - 1;
+    return ((uint64_t)__shfl(uint32_t(ci >> 32), l2, 64) << 32) | __shfl(uint32_t(ci), l2, 64);
+}
+
+// Top-k membership of NT tokens handled by one wave (tokens m = wv + nw*i, i < NT; those
+// >= M are skipped).  Lane l holds the keys of experts l + 64r, r < RE; the members of a
+// token are exactly its keys at or above its K-th largest key (keys are distinct).  With
+// `weights`, also the softmax weights of the members (max-subtracted, denominator over
+// all E, optional renorm; model.py:903-907).
+template <int RE, int NT>
+__device__ __forceinline__ void route_tokens(const float* sl, int M, int E, int K, RouteShared& R, bool weights,
+                                             int norm, int wv, int nw, int lane) {
+    uint64_t key[NT][RE];
+    uint64_t thr[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int m = wv + nw * i;
+#pragma unroll
+        for (int r = 0; r < RE; ++r) {
             const int e = lane + 64 * r;
-            key[r] = (r < RE && e < E) ? route_key(sl[m * E + e], e) : 0ull;
+            key[i][r] = (m < M && e < E) ? route_key(sl[m * E + e], e) : 0ull;
         }
-        uint64_t thr;
-        switch (RE) {
-        case 1: thr = radix_kth<1>(key, K); break;
-        case 2: thr = radix_kth<2>(key, K); break;
-        case 3: thr = radix_kth<3>(key, K); break;
-        case 4: thr = radix_kth<4>(key, K); break;
-        case 5: thr = radix_kth<5>(key, K); break;
-        case 6: thr = radix_kth<6>(key, K); break;
-        case 7: thr = radix_kth<7>(key, K); break;
-        default: thr = radix_kth<8>(key, K); break;
-        }
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) thr[i] = wv + nw * i < M ? kth_key<RE>(key[i], K, lane, R.wbuf[wv]) : ~0ull;
+    if (wv == 0) PG_MARK(1, 7);
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int m = wv + nw * i;
+        if (m >= M) continue;
         float top = -INFINITY, den = 0.f;
         if (weights) {
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (r < RE && lane + 64 * r < E) top = fmaxf(top, sl[m * E + lane + 64 * r]);
+            for (int r = 0; r < RE; ++r)
+                if (lane + 64 * r < E) top = fmaxf(top, sl[m * E + lane + 64 * r]);
 #pragma unroll
             for (int s = 32; s >= 1; s >>= 1) top = fmaxf(top, __shfl_xor(top, s, 64));
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                if (r < RE && lane + 64 * r < E) den += expf(sl[m * E + lane + 64 * r] - top);
+            for (int r = 0; r < RE; ++r)
+                if (lane + 64 * r < E) den += expf(sl[m * E + lane + 64 * r] - top);
             den = group_sum<64>(den);
         }
         int base = 0;
         float psel = 0.f;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            if (r < RE) {
-                const bool in = key[r] >= thr && lane + 64 * r < E;
-                const uint64_t mask = __ballot(in);
-                if (lane == 0) {
-                    if (2 * r < 16) R.pres[m][2 * r] = (uint32_t)mask;
-                    if (2 * r + 1 < 16) R.pres[m][2 * r + 1] = (uint32_t)(mask >> 32);
-                }
-                const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
-                if (in && pos < K) {  // exactly K members unless logits hold NaNs
-                    R.mem_e[m * K + pos] = lane + 64 * r;
-                    if (weights) {
-                        const float p = expf(sl[m * E + lane + 64 * r] - top) / den;
-                        R.mem_w[m * K + pos] = p;
-                        psel += p;
-                    }
-                }
-                base += __popcll(mask);
+        for (int r = 0; r < RE; ++r) {
+            const bool in = key[i][r] >= thr[i] && lane + 64 * r < E;
+            const uint64_t mask = __ballot(in);
+            if (lane == 0) {
+                R.pres[m][2 * r] = (uint32_t)mask;
+                R.pres[m][2 * r + 1] = (uint32_t)(mask >> 32);
             }
+            const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
+            if (in && pos < K) {  // exactly K members unless logits hold NaNs
+                R.mem_e[m * K + pos] = lane + 64 * r;
+                if (weights) {
+                    const float p = expf(sl[m * E + lane + 64 * r] - top) / den;
+                    R.mem_w[m * K + pos] = p;
+                    psel += p;
+                }
+            }
+            base += __popcll(mask);
         }
         if (weights && norm) {
             psel = group_sum<64>(psel);
-            for (int i = lane; i < K; i += 64) R.mem_w[m * K + i] = R.mem_w[m * K + i] / fmaxf(psel, 1e-20f);
+            for (int j = lane; j < K; j += 64) R.mem_w[m * K + j] = R.mem_w[m * K + j] / fmaxf(psel, 1e-20f);
         }
-        if (lane == 0)
-            for (int q = 2 * RE; q < 16; ++q) R.pres[m][q] = 0u;
+        if (lane < 16 && lane >= 2 * RE) R.pres[m][lane] = 0u;
+    }
+}
+
+// Routing of the M <= 8 tokens in one block from the logits [M][E] (sl: LDS scratch of
+// M*E floats), then the per-word prefix counts: used / wc / wp / n_act.  Every thread of
+// the block calls this.  NT = tokens per wave, a compile-time bound >= ceil(M / waves).
+template <int NT>
+__device__ __forceinline__ void route_in_block(const float* __restrict__ logits, int M, int E, int K, float* sl,
+                                               RouteShared& R, bool weights, int norm) {
+    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6, nw = nth >> 6;
+    copy_words<8>(sl, logits, M * E, tid, nth);
+    __syncthreads();
+    PG_MARK(1, 6);
+    if (E <= 64)
+        route_tokens<1, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
+    else if (E <= 128)
+        route_tokens<2, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
+    else if (E <= 256)
+        route_tokens<4, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
+    else
+        route_tokens<8, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
+    __syncthreads();
+    if (wv == 0) {  // lane q: word q of the expert bitmaps; wave prefix sums over the words
+        uint32_t u = 0;
+        int pc = 0;
+        if (lane < 16) {
+            for (int m = 0; m < M; ++m) {
+                const uint32_t w = R.pres[m][lane];
+                u |= w;
+                pc += __popc(w);
+            }
+        }
+        int ca = __popc(u), cp = pc;
+#pragma unroll
+        for (int s = 1; s < 16; s <<= 1) {
+            const int oa = __shfl_up(ca, s, 64), op = __shfl_up(cp, s, 64);
+            if (lane >= s) {
+                ca += oa;
+                cp += op;
+            }
+        }
+        if (lane < 16) {
+            R.used[lane] = u;
+            R.wc[lane] = ca - __popc(u);
+            R.wp[lane] = cp - pc;
+        }
+        if (lane == 15) R.n_act = ca;
     }
     __syncthreads();
 }
 
-// Expert of active slot a (the a-th expert in ascending id that some token selected), its
-// first sorted pair (pairs of lower experts) and its pair count.  Returns false when
-// a >= n_active.
-__device__ __forceinline__ bool route_slot(const RouteShared& R, int M, int E, int a, int& e, int& p_begin,
-                                           int& count) {
-    const int nw = (E + 31) >> 5;
-    int seen = 0;
-    e = -1;
-    for (int q = 0; q < nw && e < 0; ++q) {
-        uint32_t u = 0;
-        for (int m = 0; m < M; ++m) u |= R.pres[m][q];
-        const int c = __popc(u);
-        if (a < seen + c) {
-            for (int k = a - seen; k > 0; --k) u &= u - 1u;  // drop the lower set bits
-            e = 32 * q + __builtin_ctz(u);
-        }
-        seen += c;
-    }
-    if (e < 0) return false;
+// Expert e's active-slot index (or -1), its first sorted pair and pair count.
+__device__ __forceinline__ int route_expert(const RouteShared& R, int M, int e, int& p_begin, int& count) {
     const int q = e >> 5;
-    const uint32_t below = (1u << (e & 31)) - 1u;
-    p_begin = 0;
+    const uint32_t bit = 1u << (e & 31), below = bit - 1u;
+    if (!(R.used[q] & bit)) return -1;
+    p_begin = R.wp[q];
     count = 0;
     for (int m = 0; m < M; ++m) {
-        for (int w = 0; w < q; ++w) p_begin += __popc(R.pres[m][w]);
         p_begin += __popc(R.pres[m][q] & below);
-        count += (R.pres[m][q] >> (e & 31)) & 1u;
+        count += (R.pres[m][q] & bit) ? 1 : 0;
     }
-    return true;
-}
-
-__device__ __forceinline__ int route_n_active(const RouteShared& R, int M, int E) {
-    int n = 0;
-    for (int q = 0; q < ((E + 31) >> 5); ++q) {
-        uint32_t u = 0;
-        for (int m = 0; m < M; ++m) u |= R.pres[m][q];
-        n += __popc(u);
-    }
-    return n;
+    return R.wc[q] + __popc(R.used[q] & below);
 }
 
 // Flat routing arrays of a counting-sort dispatch (the stage API's layout), written by the
@@ -516,36 +588,33 @@ struct FlatRoute {
 };
 
 // Publish the routing descriptor (block (0, 0) only; R holds the weights), and the flat
-// arrays when fl.offsets is set.
+// arrays when fl.offsets is set.  One thread per expert, then one per pair.
 __device__ __forceinline__ void publish_route(const RouteShared& R, int M, int E, int K, int32_t* __restrict__ desc,
                                               const FlatRoute& fl) {
     const int tid = threadIdx.x, nth = blockDim.x;
-    if (fl.offsets) {
-        for (int e = tid; e <= E; e += nth) {
-            int o = 0;
-            for (int m = 0; m < M; ++m) {
-                for (int w = 0; w < (e >> 5); ++w) o += __popc(R.pres[m][w]);
-                if (e < E) o += __popc(R.pres[m][e >> 5] & ((1u << (e & 31)) - 1u));
-                else if (E & 31) o += __popc(R.pres[m][E >> 5] & ((1u << (E & 31)) - 1u));
-            }
-            fl.offsets[e] = o;
-        }
-    }
-    for (int a = tid; a < M * K; a += nth) {
-        int e, pb, c;
-        if (route_slot(R, M, E, a, e, pb, c)) {
+    for (int e = tid; e < E; e += nth) {
+        int pb = 0, c = 0;
+        const int a = route_expert(R, M, e, pb, c);
+        if (a >= 0) {
             desc[kDescSlot + 4 * a] = e;
             desc[kDescSlot + 4 * a + 1] = pb;
             desc[kDescSlot + 4 * a + 2] = c;
+            if (fl.offsets) fl.active[a] = e;
+        }
+        if (fl.offsets) {  // pairs of the experts below e
+            const int q = e >> 5;
+            int o = R.wp[q];
+            for (int m = 0; m < M; ++m) o += __popc(R.pres[m][q] & ((1u << (e & 31)) - 1u));
+            fl.offsets[e] = o;
         }
     }
     for (int f = tid; f < M * K; f += nth) {
         const int m = f / K, e = R.mem_e[f], q = e >> 5;
-        int pos = 0;
+        const uint32_t bit = 1u << (e & 31);
+        int pos = R.wp[q];
         for (int m2 = 0; m2 < M; ++m2) {
-            for (int w = 0; w < q; ++w) pos += __popc(R.pres[m2][w]);
-            pos += __popc(R.pres[m2][q] & ((1u << (e & 31)) - 1u));
-            pos += m2 < m ? (R.pres[m2][q] >> (e & 31)) & 1u : 0u;
+            pos += __popc(R.pres[m2][q] & (bit - 1u));
+            pos += (m2 < m && (R.pres[m2][q] & bit)) ? 1 : 0;
         }
         desc[kDescPair + 2 * pos] = m;
         desc[kDescPair + 2 * pos + 1] = __builtin_bit_cast(int32_t, R.mem_w[f]);
@@ -555,16 +624,12 @@ __device__ __forceinline__ void publish_route(const RouteShared& R, int M, int E
             fl.w[f] = R.mem_w[f];
         }
     }
-    if (fl.offsets) {
-        for (int a = tid; a < M * K; a += nth) {
-            int e, pb, c;
-            if (route_slot(R, M, E, a, e, pb, c)) fl.active[a] = e;
-        }
-    }
     if (tid == 0) {
-        const int n = route_n_active(R, M, E);
-        desc[0] = n;
-        if (fl.offsets) *fl.n_active = n;
+        desc[0] = R.n_act;
+        if (fl.offsets) {
+            fl.offsets[E] = M * K;
+            *fl.n_active = R.n_act;
+        }
     }
 }
 
@@ -609,13 +674,16 @@ __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __res
     PG_MARK(1, 0);
     if (MODE == kRoute) {
         const bool pub = blockIdx.x == 0 && a == 0;
-        route_in_block(dp.logits, dp.M, dp.E, topk, (float*)smem, R, pub, dp.norm);
+        // tokens per wave: sized from TM, or for kDecTM when the LDS limit made TM < M
+        if (dp.M <= ((TM + W - 1) / W) * W)
+            route_in_block<(TM + W - 1) / W>(dp.logits, dp.M, dp.E, topk, (float*)smem, R, pub, dp.norm);
+        else
+            route_in_block<(kDecTM + W - 1) / W>(dp.logits, dp.M, dp.E, topk, (float*)smem, R, pub, dp.norm);
         PG_MARK(1, 1);
-        if (pub) publish_route(R, dp.M, dp.E, topk, dp.desc, dp.flat);
-        if (tid == 0) {
-            int ee, pb, c;
-            R.n_act = route_slot(R, dp.M, dp.E, a, ee, pb, c) ? 1 : 0;
-            if (R.n_act) {
+        if (a >= R.n_act) return;  // uniform: every block computed the same n_act
+        for (int ee = tid; ee < dp.E; ee += W * 64) {  // the expert of this block's slot
+            int pb = 0, c = 0;
+            if (route_expert(R, dp.M, ee, pb, c) == a) {
                 R.e = ee;
                 R.p_begin = pb;
                 R.count = c;
@@ -626,7 +694,6 @@ __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __res
         }
         __syncthreads();
         PG_MARK(1, 2);
-        if (!R.n_act) return;
         e = R.e;
         p_begin = R.p_begin;
         p_end = p_begin + R.count;
@@ -737,6 +804,9 @@ __global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __res
             }
         }
     }
+    // block (0, 0) publishes the routing last: its stores then stay off the block's own
+    // critical path (a barrier would wait for them)
+    if (MODE == kRoute && blockIdx.x == 0 && a == 0) publish_route(R, dp.M, dp.E, topk, dp.desc, dp.flat);
     PG_MARK(1, 5);
 }
 
@@ -992,7 +1062,7 @@ inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const flo
     const size_t logits = dp.mode == kRoute ? (size_t)dp.M * dp.E * 4 : 0;
     size_t sh = stage > tail ? stage : tail;
     sh = sh > logits ? sh : logits;
-    hipLaunchKernelGGL((dec_gateup_kernel<QT, RB, W, TM>), dim3(div_up(g.N, RB), max_active), dim3(64 * W), sh,
+    PG_LAUNCH((dec_gateup_kernel<QT, RB, W, TM>), dim3(div_up(g.N, RB), max_active), dim3(64 * W), sh,
                        st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, inter, isum);
 }
 
@@ -1000,14 +1070,14 @@ template <int QT, int RB, int W, int TM>
 inline void dn_launch(const Mats& d, const float* inter, const float* isum, const DecDisp& dp, int max_active,
                       const float* topk_w, float* partial, hipStream_t st) {
     const size_t sh = down_lds_bytes(TM, RB, W);
-    hipLaunchKernelGGL((dec_down_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB), max_active), dim3(64 * W), sh,
+    PG_LAUNCH((dec_down_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB), max_active), dim3(64 * W), sh,
                        st, d.base, d.stride, d.N, d.K, inter, isum, dp, topk_w, partial);
 }
 
 template <int QT, int RB, int W, int TM>
 inline void dc_launch(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
                       const float* shared, const float* shared_logit, float* out, hipStream_t st) {
-    hipLaunchKernelGGL((dec_down_combine_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB)), dim3(64 * W),
+    PG_LAUNCH((dec_down_combine_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB)), dim3(64 * W),
                        dc_stage_bytes(P, d.K), st, d.base,
                        d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out);
 }

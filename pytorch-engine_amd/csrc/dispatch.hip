@@ -135,14 +135,14 @@ int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int3
     if (tile_rows <= 0) return fail(PGMOE_E_INVALID, "tile_rows must be positive");
     const int64_t P = (int64_t)M * K;
     if (P > (1 << 30)) return fail(PGMOE_E_UNSUPPORTED, "too many token-expert pairs");
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, st, idx, (int)P, E, tile_rows, offsets,
+    PG_LAUNCH(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, st, idx, (int)P, E, tile_rows, offsets,
                        perm, inv, active, n_active, tile_off);
     return check_launch("dispatch");
 }
 
 int launch_identity_dispatch(int M, int tile_rows, int32_t* offsets, int32_t* perm, int32_t* inv,
                              int32_t* active, int32_t* n_active, int32_t* tile_off, float* w, hipStream_t st) {
-    hipLaunchKernelGGL(identity_dispatch_kernel, dim3(div_up(M > 0 ? M : 1, 256)), dim3(256), 0, st, M,
+    PG_LAUNCH(identity_dispatch_kernel, dim3(div_up(M > 0 ? M : 1, 256)), dim3(256), 0, st, M,
                        tile_rows, offsets, perm, inv, active, n_active, tile_off, w);
     return check_launch("identity_dispatch");
 }

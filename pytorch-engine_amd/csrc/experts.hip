@@ -258,9 +258,9 @@ int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int to
     const int max_tiles = div_up(P, kBM) + (int)(P < E ? P : E);
     const dim3 grid(max_tiles, div_up(g.N, 32)), block(256);
     switch (g.qtype) {
-    case PGMOE_Q4_K: hipLaunchKernelGGL((gemm_gateup_kernel<PGMOE_Q4_K>), grid, block, 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, E, offsets, perm, tile_off, inter); break;
-    case PGMOE_Q6_K: hipLaunchKernelGGL((gemm_gateup_kernel<PGMOE_Q6_K>), grid, block, 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, E, offsets, perm, tile_off, inter); break;
-    case PGMOE_Q8_0: hipLaunchKernelGGL((gemm_gateup_kernel<PGMOE_Q8_0>), grid, block, 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, E, offsets, perm, tile_off, inter); break;
+    case PGMOE_Q4_K: PG_LAUNCH((gemm_gateup_kernel<PGMOE_Q4_K>), grid, block, 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, E, offsets, perm, tile_off, inter); break;
+    case PGMOE_Q6_K: PG_LAUNCH((gemm_gateup_kernel<PGMOE_Q6_K>), grid, block, 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, E, offsets, perm, tile_off, inter); break;
+    case PGMOE_Q8_0: PG_LAUNCH((gemm_gateup_kernel<PGMOE_Q8_0>), grid, block, 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, E, offsets, perm, tile_off, inter); break;
     }
     return check_launch("gemm_gateup");
 }
@@ -275,15 +275,15 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
         return launch_dec_down(d, inter, nullptr, M, offsets, perm, active, n_active, (int)(P < E ? P : E), topk_w,
                                partial, st);
     if (!a16 || !rs) return fail(PGMOE_E_INVALID, "GEMM mode needs a16 and rs scratch");
-    hipLaunchKernelGGL(rowscale_kernel, dim3((unsigned)P), dim3(256), 0, st, inter, d.K, a16, rs);
+    PG_LAUNCH(rowscale_kernel, dim3((unsigned)P), dim3(256), 0, st, inter, d.K, a16, rs);
     int rc = check_launch("rowscale");
     if (rc) return rc;
     const int max_tiles = div_up(P, kBM) + (int)(P < E ? P : E);
     const dim3 grid(max_tiles, div_up(d.N, 64)), block(256);
     switch (d.qtype) {
-    case PGMOE_Q4_K: hipLaunchKernelGGL((gemm_down_kernel<PGMOE_Q4_K>), grid, block, 0, st, d.base, d.stride, d.N, d.K, a16, rs, E, offsets, perm, tile_off, topk_w, partial); break;
-    case PGMOE_Q6_K: hipLaunchKernelGGL((gemm_down_kernel<PGMOE_Q6_K>), grid, block, 0, st, d.base, d.stride, d.N, d.K, a16, rs, E, offsets, perm, tile_off, topk_w, partial); break;
-    case PGMOE_Q8_0: hipLaunchKernelGGL((gemm_down_kernel<PGMOE_Q8_0>), grid, block, 0, st, d.base, d.stride, d.N, d.K, a16, rs, E, offsets, perm, tile_off, topk_w, partial); break;
+    case PGMOE_Q4_K: PG_LAUNCH((gemm_down_kernel<PGMOE_Q4_K>), grid, block, 0, st, d.base, d.stride, d.N, d.K, a16, rs, E, offsets, perm, tile_off, topk_w, partial); break;
+    case PGMOE_Q6_K: PG_LAUNCH((gemm_down_kernel<PGMOE_Q6_K>), grid, block, 0, st, d.base, d.stride, d.N, d.K, a16, rs, E, offsets, perm, tile_off, topk_w, partial); break;
+    case PGMOE_Q8_0: PG_LAUNCH((gemm_down_kernel<PGMOE_Q8_0>), grid, block, 0, st, d.base, d.stride, d.N, d.K, a16, rs, E, offsets, perm, tile_off, topk_w, partial); break;
     }
     return check_launch("gemm_down");
 }
@@ -292,7 +292,7 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
                    const float* shared_logit, float* out, hipStream_t st) {
     if (M <= 0) return PGMOE_OK;
     if (K > 16) return fail(PGMOE_E_UNSUPPORTED, "combine supports top_k <= 16");
-    hipLaunchKernelGGL(combine_kernel, dim3(M, div_up(H, 256)), dim3(256), 0, st, partial, inv, K, H, shared,
+    PG_LAUNCH(combine_kernel, dim3(M, div_up(H, 256)), dim3(256), 0, st, partial, inv, K, H, shared,
                        shared_logit, out);
     return check_launch("combine");
 }

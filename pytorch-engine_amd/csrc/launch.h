@@ -1,9 +1,43 @@
 // Host-side launchers shared between the translation units of libpgmoe.so.
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "common.h"
 
 namespace pgmoe {
+
+// Per-launch timing for pgmoe_moe_forward_timed: while armed on this thread, the i-th
+// kernel launch records start[i] / stop[i] at the kernel's own begin and end (the events
+// hipExtLaunchKernel stamps, the same interval a kernel trace reports).
+struct LaunchTiming {
+    hipEvent_t* start;
+    hipEvent_t* stop;
+    int n, next;
+};
+LaunchTiming*& launch_timing();  // this thread's armed timing (nullptr when off)
+
+inline void timing_events(hipEvent_t* s, hipEvent_t* e) {
+    LaunchTiming* t = launch_timing();
+    if (t) {
+        if (t->next < t->n) {
+            *s = t->start ? t->start[t->next] : nullptr;
+            *e = t->stop ? t->stop[t->next] : nullptr;
+        }
+        ++t->next;
+    }
+}
+
+// Kernel launch on `st`; records the armed timing events, if any.
+#define PG_LAUNCH(kernel, grid, block, shmem, st, ...)                                            \
+    do {                                                                                          \
+        hipEvent_t pg_ev_s = nullptr, pg_ev_e = nullptr;                                          \
+        ::pgmoe::timing_events(&pg_ev_s, &pg_ev_e);                                               \
+        if (pg_ev_s || pg_ev_e)                                                                   \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, pg_ev_s, pg_ev_e, 0, __VA_ARGS__); \
+        else                                                                                      \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, st, __VA_ARGS__);                      \
+    } while (0)
 
 int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
                          float* logits, hipStream_t st, const float* extra_w = nullptr, float* extra_out = nullptr,

@@ -88,13 +88,13 @@ int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows,
     const dim3 grid((unsigned)((n + threads - 1) / threads));
     switch (qtype) {
     case PGMOE_Q4_K:
-        hipLaunchKernelGGL(relayout_kernel<PGMOE_Q4_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q4_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
         break;
     case PGMOE_Q6_K:
-        hipLaunchKernelGGL(relayout_kernel<PGMOE_Q6_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q6_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
         break;
     case PGMOE_Q8_0:
-        hipLaunchKernelGGL(relayout_kernel<PGMOE_Q8_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q8_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
         break;
     default:
         return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d", qtype);

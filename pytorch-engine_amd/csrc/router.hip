@@ -191,7 +191,7 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
 #define PG_ROUTER(TM_, TE_)                                                                                   \
     do {                                                                                                      \
         const int rb = div_up(div_up(M, TM_) * div_up(rows, TE_), 4);                                        \
-        hipLaunchKernelGGL((router_logits_kernel<TM_, TE_>), dim3(rb + xblocks), dim3(threads), 0, st, x, W, bias, \
+        PG_LAUNCH((router_logits_kernel<TM_, TE_>), dim3(rb + xblocks), dim3(threads), 0, st, x, W, bias, \
                            M, H, E, logits, extra_w, extra_out, xsum, rb);                                    \
     } while (0)
     if (M <= 4)
@@ -208,13 +208,13 @@ int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx
     if (M <= 0) return PGMOE_OK;
     const dim3 grid(div_up(M, 4)), block(256);
     if (E <= 64)
-        hipLaunchKernelGGL((topk_kernel<1>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        PG_LAUNCH((topk_kernel<1>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
     else if (E <= 128)
-        hipLaunchKernelGGL((topk_kernel<2>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        PG_LAUNCH((topk_kernel<2>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
     else if (E <= 256)
-        hipLaunchKernelGGL((topk_kernel<4>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        PG_LAUNCH((topk_kernel<4>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
     else if (E <= 1024)
-        hipLaunchKernelGGL((topk_kernel<16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        PG_LAUNCH((topk_kernel<16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
     else
         return fail(PGMOE_E_UNSUPPORTED, "top-k supports at most 1024 experts (got %d)", E);
     return check_launch("topk");

@@ -1,9 +1,16 @@
-"""Summarise a rocprofv3 results database (kernel trace) into a per-kernel table.
+"""Summarise rocprofv3 results databases.
 
-    python -m pgmoe.prof_summary gpurun_out/prof/run_results.db
+    python -m pgmoe.prof_summary RUN_results.db                 # kernel trace table
+    python -m pgmoe.prof_summary --pmc RUN_results.db [NAME]    # counters per kernel
 
-Groups dispatches by kernel name and grid, reporting calls and average / min / max
-duration in microseconds plus the kernel's register and LDS use.
+The kernel-trace mode groups dispatches by kernel name, grid and block. For each group it
+reports the number of calls, the average / min / max duration in microseconds, and the
+kernel's register and LDS use.
+
+The counter mode (a `rocprofv3 --pmc ...` database) sums each counter over its instances
+within a dispatch (XCDs, channels), then averages over the dispatches of each kernel. The
+result is one row per kernel whose name contains NAME; by default these are the pgmoe
+kernels and the runtime's copy kernels.
 """
 
 import collections
@@ -31,5 +38,42 @@ def summarise(db: str) -> str:
     return "\n".join(out)
 
 
+def pmc_table(db: str, pattern: str = "") -> dict:
+    """{kernel: {counter: mean per-dispatch value, "_dispatches": n}}."""
+    c = sqlite3.connect(db)
+    rows = c.execute("select dispatch_id, name, counter_name, counter_value from pmc_events").fetchall()
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    names = {}
+    for d, n, cn, cv in rows:
+        per[d][cn] += cv
+        names[d] = n.split("(")[0]
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for d, cs in per.items():
+        n = names[d]
+        if pattern and pattern not in n:
+            continue
+        if not pattern and "pgmoe" not in n and "copy" not in n.lower() and "elementwise" not in n:
+            continue
+        for cn, v in cs.items():
+            agg[n][cn].append(v)
+    out = {}
+    for n, cs in agg.items():
+        out[n] = {cn: sum(vs) / len(vs) for cn, vs in cs.items()}
+        out[n]["_dispatches"] = max(len(vs) for vs in cs.values())
+    return out
+
+
+def summarise_pmc(db: str, pattern: str = "") -> str:
+    t = pmc_table(db, pattern)
+    lines = ["| kernel | dispatches | counters (mean per dispatch) |", "|---|---|---|"]
+    for n, cs in sorted(t.items()):
+        vals = ", ".join(f"{k}={v:.6g}" for k, v in sorted(cs.items()) if not k.startswith("_"))
+        lines.append(f"| `{n}` | {cs['_dispatches']} | {vals} |")
+    return "\n".join(lines)
+
+
 if __name__ == "__main__":
-    print(summarise(sys.argv[1]))
+    if len(sys.argv) >= 3 and sys.argv[1] == "--pmc":
+        print(summarise_pmc(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else ""))
+    else:
+        print(summarise(sys.argv[1]))

@@ -49,3 +49,29 @@ def sample_tokens(M: int, n: int, seed: int = 0) -> np.ndarray:
         return np.arange(M, dtype=np.int32)
     rng = np.random.default_rng(seed)
     return np.sort(rng.choice(M, size=n, replace=False)).astype(np.int32)
+
+
+class HipEvents:
+    """hipEvent_t handles from the HIP runtime torch loaded (for pgmoe_moe_forward_timed)."""
+
+    def __init__(self, n: int):
+        import ctypes
+        path = None
+        for line in open("/proc/self/maps"):
+            if "libamdhip64" in line:
+                path = line.split()[-1]
+                break
+        self.L = ctypes.CDLL(path or "libamdhip64.so")
+        self.L.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.L.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.ev = (ctypes.c_void_p * n)()
+        for i in range(n):
+            h = ctypes.c_void_p()
+            assert self.L.hipEventCreate(ctypes.byref(h)) == 0
+            self.ev[i] = h.value
+
+    def elapsed_ms(self, a, b) -> float:
+        import ctypes
+        f = ctypes.c_float()
+        assert self.L.hipEventElapsedTime(ctypes.byref(f), a, b) == 0
+        return float(f.value)

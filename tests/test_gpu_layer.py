@@ -159,3 +159,58 @@ def test_all_tokens_one_expert_and_top_k_equals_e():
         _, idx, w = ol1.route(x)
         assert np.all(idx == 6)
         check_layer_output(got, ol1.forward_tokens(x, idx, w), abs_tol=2e-2 if M <= 8 else None)
+
+
+def test_timed_forward_matches_forward_and_times_every_launch():
+    """pgmoe_moe_forward_timed: same bits as the forward; one event pair per kernel."""
+    import ctypes
+    from gpu_helpers import HipEvents
+    from pgmoe._lib import check, lib
+    lay, ol, mod = _pair("tiny")
+    starts, stops = HipEvents(16), HipEvents(16)
+    for M, n_expected in ((1, 3), (16, 7)):  # decode: router, gate/up, down+combine; prefill: 7 kernels
+        x = torch.from_numpy(lay.draw_x(M)).to("cuda:0")
+        ref = mod(x)
+        out = torch.empty_like(ref)
+        ws = mod._workspace(M)
+        n = ctypes.c_int32()
+        stream = torch.cuda.current_stream().cuda_stream
+        check(lib().pgmoe_moe_forward_timed(mod._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(),
+                                            ws.numel(), stream, starts.ev, stops.ev, 16, ctypes.byref(n)),
+              "forward_timed")
+        torch.cuda.synchronize()
+        assert n.value == n_expected
+        assert torch.equal(out, ref)
+        for i in range(n.value):
+            d = starts.elapsed_ms(starts.ev[i], stops.ev[i])
+            assert 0.0 < d < 50.0, (M, i, d)
+        # fewer events than launches: the rest run untimed, same result
+        check(lib().pgmoe_moe_forward_timed(mod._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(),
+                                            ws.numel(), stream, starts.ev, None, 1, None), "forward_timed")
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+
+
+def test_graph_replay_equals_eager():
+    """A captured forward replays to the eager result, replay after replay, with other
+    eager forwards (different inputs) run between the replays."""
+    lay, ol, mod = _pair("tiny")
+    for M in (1, 16):
+        x = torch.from_numpy(lay.draw_x(M)).to("cuda:0")
+        x2 = torch.from_numpy(lay.draw_x(M + 1)[1:]).to("cuda:0")
+        ref = mod(x).clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            mod(x)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                out = mod(x)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            other = mod(x2)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+            assert not torch.equal(other, ref)
