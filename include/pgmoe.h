@@ -114,14 +114,16 @@ int pgmoe_router_topk(const uint16_t* x, const float* w, const float* bias, int3
  * (topk_indices.unique() / torch.where / index_select, model.py:911-914).
  * offsets[E+1]; perm[M*K] = flat id at each sorted position; inv[M*K] = position of
  * each flat id; active[E] = experts with rows, ascending; n_active[1];
- * tile_off[E+1] = exclusive scan of ceil(count/tile_rows) (tile_rows > 0). */
+ * tile_off[E+1] = exclusive scan of ceil(count/tile_rows) (tile_rows > 0; the mode-1
+ * expert products below take tile_off computed with tile_rows = 256). */
 int pgmoe_dispatch(const int32_t* topk_idx, int32_t M, int32_t K, int32_t E, int32_t tile_rows,
                    int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active,
                    int32_t* tile_off, void* stream);
 
 /* R4+R5: inter[P, I] = silu(x_p . Wg_e^T) * (x_p . Wu_e^T) for every sorted pair position p,
  * fp32 accumulate and output (gate/up_exps.forward_expert + exec_fused_act_mul_rowscale,
- * model.py:916-918).  mode 0 = wavefront GEMV (M <= 8), 1 = MFMA grouped GEMM. */
+ * model.py:916-918).  mode 0 = wavefront GEMV (M <= 8), 1 = MFMA grouped GEMM over
+ * 256-pair tiles (tile_off from pgmoe_dispatch with tile_rows = 256). */
 int pgmoe_expert_gateup(const pgmoe_weights* gate, const pgmoe_weights* up, const uint16_t* x,
                         int32_t M, int32_t K, const int32_t* offsets, const int32_t* perm,
                         const int32_t* active, const int32_t* n_active, const int32_t* tile_off,

@@ -81,6 +81,13 @@ int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum
 int decode_desc_words();
 // Whether the fused down + combine kernel can stage P inter rows of K values.
 bool decode_fused_down(int P, int K);
+// Prefill grouped GEMMs (gemm.hip); tile_off counts gemm_tile_pairs()-row tiles.
+int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
+                       const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st);
+int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M, int topk, const int32_t* offsets,
+                     const int32_t* perm, const int32_t* tile_off, const float* topk_w, float* partial,
+                     hipStream_t st);
+int gemm_tile_pairs();
 int64_t layout_bytes(int qtype, int64_t rows, int64_t cols);
 int gemm_tile_rows();
 int decode_tokens_max();

@@ -77,7 +77,7 @@ def router_topk(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], 
     return logits, idx, tw
 
 
-def dispatch(idx: torch.Tensor, n_experts: int, tile_rows: int = 64):
+def dispatch(idx: torch.Tensor, n_experts: int, tile_rows: int = 256):
     dev = _need_cuda(idx)
     M, K = idx.shape
     P = M * K

@@ -163,7 +163,7 @@ def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
     ub = ops.relayout(qg, torch.from_numpy(ur).to(dev), E, I, H)
     db = ops.relayout(qd, torch.from_numpy(dr).to(dev), E, H, I)
     Wg, Wu, Wd = ops.make_weights(qg, gb, E, I, H), ops.make_weights(qg, ub, E, I, H), ops.make_weights(qd, db, E, H, I)
-    disp = ops.dispatch(torch.from_numpy(idx).to(dev), E, 64)
+    disp = ops.dispatch(torch.from_numpy(idx).to(dev), E, 256)  # the GEMM's tile size
     xd = torch.from_numpy(x).to(dev)
     inter = ops.expert_gateup(Wg, Wu, xd, K, disp, mode)
     tw_d = torch.from_numpy(tw).to(dev)
