@@ -51,7 +51,44 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// group_sum<64> of N values at once (N a power of two <= 64), as a reduce-scatter: at
+// stride s each lane keeps the half of its values whose index bit matches its own lane
+// bit and receives its partner's partial of that half, so lane l ends holding the total of
+// value (l mod N), after N - 1 exchanges instead of 6 N.  Every level adds the same two
+// partial sums as group_sum<64> (IEEE addition commutes), so the totals have its bits.
+template <int N>
+__device__ __forceinline__ float scatter_sum64(float (&v)[N], int lane) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+        if (s >= N) {  // more lanes than values: plain xor step on all of them
+#pragma unroll
+            for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], s, kWave);
+        } else {
+            // selects by mask: a select between two array elements would become a select
+            // of addresses and push the array to scratch memory
+            const uint32_t up = (lane & s) ? 0xffffffffu : 0u;
+#pragma unroll
+            for (int i = 0; i < s; ++i) {
+                const uint32_t lo = __builtin_bit_cast(uint32_t, v[i]), hi = __builtin_bit_cast(uint32_t, v[s + i]);
+                const float send = __builtin_bit_cast(float, (lo & up) | (hi & ~up));
+                const float keep = __builtin_bit_cast(float, (hi & up) | (lo & ~up));
+                v[i] = keep + __shfl_xor(send, s, kWave);
+            }
+        }
+    }
+    return v[0];
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes at g land at
+// lds + 16 * l, so one wave fills 1 KB of LDS and holds no registers for the data.  `lds`
+// must be the same for every lane of the wave.  The copy is counted by vmcnt: wait_dma()
+// before the barrier that hands the LDS to other waves.
+__device__ __forceinline__ void dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---------------------------------------------------------------- device weight layout
 // Every matrix [N rows, K cols] (K a multiple of 256) is stored as tiles of 64 rows x one

@@ -10,55 +10,101 @@
 namespace pgmoe {
 
 // exec_fused_act_mul_rowscale's second half on an fp32 inter row: rs = max(max|v|/16384, 1),
-// a16 = fp16(v / rs)  (quant_kernels.py:1467-1475).  One block per row.
-__global__ __launch_bounds__(256) void rowscale_kernel(const float* __restrict__ inter, int I,
+// a16 = fp16(v / rs)  (quant_kernels.py:1467-1475).  One wave per row; rows of up to
+// 64 * 4 * NV values are read once into registers, longer rows are read twice.
+template <int NV>
+__global__ __launch_bounds__(256) void rowscale_kernel(const float* __restrict__ inter, int P, int I,
                                                        uint16_t* __restrict__ a16, float* __restrict__ rs) {
-    __shared__ float red[4];
-    const int64_t p = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int64_t p = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (p >= P) return;
     const float* row = inter + p * I;
+    const int n4 = I >> 2;  // float4 words of the row (I % 4 == 0)
+    float4 v[NV > 0 ? NV : 1];
     float mx = 0.0f;
-    for (int i = threadIdx.x; i < I; i += 256) mx = fmaxf(mx, fabsf(row[i]));
+    if (NV > 0) {
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            const int i = lane + 64 * q;
+            v[q] = i < n4 ? *(const float4*)(row + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)), fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
+        }
+    } else {
+        for (int i = lane; i < n4; i += 64) {
+            const float4 u = *(const float4*)(row + 4 * i);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+        }
+    }
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const float s = fmaxf(mx * (1.0f / 16384.0f), 1.0f);
-    if (threadIdx.x == 0) rs[p] = s;
-    for (int i = threadIdx.x; i < I; i += 256)
-        a16[p * I + i] = __builtin_bit_cast(uint16_t, (half_t)(row[i] / s));
+    const float sc = fmaxf(mx * (1.0f / 16384.0f), 1.0f);
+    if (lane == 0) rs[p] = sc;
+    uint16_t* orow = a16 + p * I;
+    auto put = [&](int i, float4 u) {
+        const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.x / sc)) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.y / sc)) << 16);
+        const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.z / sc)) |
+                            ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.w / sc)) << 16);
+        *(uint2*)(orow + 4 * i) = make_uint2(lo, hi);
+    };
+    if (NV > 0) {
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            const int i = lane + 64 * q;
+            if (i < n4) put(i, v[q]);
+        }
+    } else {
+        for (int i = lane; i < n4; i += 64) put(i, *(const float4*)(row + 4 * i));
+    }
 }
 
 // out[t, h] = sum of the token's K pair rows in ascending sorted position (= ascending
-// expert id), then + shared[t, h] * sigmoid(shared_logit[t]).  Block = (token, 256 columns).
+// expert id), then + shared[t, h] * sigmoid(shared_logit[t]).  Thread = 4 columns of one
+// token; the K positions are ordered by an unrolled selection (no indexed local array),
+// then all K row loads are issued before the in-order sum.
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ partial,
                                                       const int32_t* __restrict__ inv, int K, int H,
                                                       const float* __restrict__ shared,
                                                       const float* __restrict__ shared_logit,
                                                       float* __restrict__ out) {
     const int t = blockIdx.x;
-    const int h = blockIdx.y * 256 + threadIdx.x;
+    const int c = blockIdx.y * 256 + threadIdx.x;  // float4 column
+    if (4 * c >= H) return;
     int pos[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) pos[k] = k < K ? inv[(int64_t)t * K + k] : 0x7fffffff;
-    // insertion sort (K <= 16)
-    for (int a = 1; a < K; ++a) {
-        const int v = pos[a];
-        int b = a - 1;
-        while (b >= 0 && pos[b] > v) {
-            pos[b + 1] = pos[b];
-            --b;
+    int srt[16];
+    int last = -1;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        int best = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) best = (pos[k] > last && pos[k] < best) ? pos[k] : best;
+        srt[s] = best;
+        last = best;
+    }
+    float4 rows[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+        if (s < K) rows[s] = *(const float4*)(partial + (int64_t)srt[s] * H + 4 * c);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+        if (s < K) {
+            acc.x += rows[s].x;
+            acc.y += rows[s].y;
+            acc.z += rows[s].z;
+            acc.w += rows[s].w;
         }
-        pos[b + 1] = v;
+    if (shared) {
+        const float gate = shared_logit ? 1.0f / (1.0f + expf(-shared_logit[t])) : 1.0f;
+        const float4 sv = *(const float4*)(shared + (int64_t)t * H + 4 * c);
+        acc.x += sv.x * gate;
+        acc.y += sv.y * gate;
+        acc.z += sv.z * gate;
+        acc.w += sv.w * gate;
     }
-    float gate = 1.0f;
-    if (shared_logit) gate = 1.0f / (1.0f + expf(-shared_logit[t]));
-    if (h < H) {
-        float acc = 0.0f;
-        for (int k = 0; k < K; ++k) acc += partial[(int64_t)pos[k] * H + h];
-        if (shared) acc += shared[(int64_t)t * H + h] * gate;
-        out[(int64_t)t * H + h] = acc;
-    }
+    *(float4*)(out + (int64_t)t * H + 4 * c) = acc;
 }
 
 // --------------------------------------------------------------------------- launchers
@@ -84,7 +130,14 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
         return launch_dec_down(d, inter, nullptr, M, offsets, perm, active, n_active, (int)(P < E ? P : E), topk_w,
                                partial, st);
     if (!a16 || !rs) return fail(PGMOE_E_INVALID, "GEMM mode needs a16 and rs scratch");
-    PG_LAUNCH(rowscale_kernel, dim3((unsigned)P), dim3(256), 0, st, inter, d.K, a16, rs);
+    const int I = d.K;  // a multiple of 256 (checked with the weights)
+    const dim3 rgrid(div_up(P, 4));
+    if (I <= 1024)
+        PG_LAUNCH(rowscale_kernel<4>, rgrid, dim3(256), 0, st, inter, (int)P, I, a16, rs);
+    else if (I <= 4096)
+        PG_LAUNCH(rowscale_kernel<16>, rgrid, dim3(256), 0, st, inter, (int)P, I, a16, rs);
+    else
+        PG_LAUNCH(rowscale_kernel<0>, rgrid, dim3(256), 0, st, inter, (int)P, I, a16, rs);
     int rc = check_launch("rowscale");
     if (rc) return rc;
     return launch_gemm_down(d, a16, rs, M, topk, offsets, perm, tile_off, topk_w, partial, st);
@@ -94,8 +147,9 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
                    const float* shared_logit, float* out, hipStream_t st) {
     if (M <= 0) return PGMOE_OK;
     if (K > 16) return fail(PGMOE_E_UNSUPPORTED, "combine supports top_k <= 16");
-    PG_LAUNCH(combine_kernel, dim3(M, div_up(H, 256)), dim3(256), 0, st, partial, inv, K, H, shared,
-                       shared_logit, out);
+    if (H % 4) return fail(PGMOE_E_UNSUPPORTED, "combine: H %d is not a multiple of 4", H);
+    PG_LAUNCH(combine_kernel, dim3(M, div_up(H / 4, 256)), dim3(256), 0, st, partial, inv, K, H, shared,
+              shared_logit, out);
     return check_launch("combine");
 }
 

@@ -171,21 +171,46 @@ __device__ __forceinline__ int gemm_tile_expert(const int32_t* tile_off, int E, 
 // full matrix-core rate on gfx950; 16x16x32 runs at half).  Operand layout: lane l holds
 // A[l%32][8(l/32) .. +8] and B[8(l/32) .. +8][l%32]; register v of D is
 // D[8(v/4) + 4(l/32) + v%4][l%32].
+// NI = the wave's 32-row slices that hold pairs (1..4); the others are skipped.
+template <int NI>
 __device__ __forceinline__ void gemm_half(const _Float16* As, const _Float16* Bs, int wm, int wn, int lane, int ko0,
                                           gf16 (&acc)[4][2]) {
 #pragma unroll
     for (int ks = 0; ks < 32; ks += 16) {
         const int ko = ko0 + ks + 8 * (lane >> 5);
-        gh8 af[4];
+        gh8 af[NI];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = *(const gh8*)&As[(128 * wm + 32 * i + (lane & 31)) * kGP + ko];
+        for (int i = 0; i < NI; ++i) af[i] = *(const gh8*)&As[(128 * wm + 32 * i + (lane & 31)) * kGP + ko];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const gh8 bf = *(const gh8*)&Bs[(64 * wn + 32 * j + (lane & 31)) * kGP + ko];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < NI; ++i)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[i][j], 0, 0, 0);
         }
+    }
+}
+
+__device__ __forceinline__ void gemm_unit(const _Float16* As, const _Float16* Bs, int wm, int wn, int lane, int ni,
+                                          gf16 (&acc)[4][2]) {
+    switch (ni) {
+    case 4:
+        gemm_half<4>(As, Bs, wm, wn, lane, 0, acc);
+        gemm_half<4>(As, Bs, wm, wn, lane, 32, acc);
+        break;
+    case 3:
+        gemm_half<3>(As, Bs, wm, wn, lane, 0, acc);
+        gemm_half<3>(As, Bs, wm, wn, lane, 32, acc);
+        break;
+    case 2:
+        gemm_half<2>(As, Bs, wm, wn, lane, 0, acc);
+        gemm_half<2>(As, Bs, wm, wn, lane, 32, acc);
+        break;
+    case 1:
+        gemm_half<1>(As, Bs, wm, wn, lane, 0, acc);
+        gemm_half<1>(As, Bs, wm, wn, lane, 32, acc);
+        break;
+    default: break;
     }
 }
 
@@ -252,6 +277,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_kernel(
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
     const bool active = 128 * wm < mrows;
+    const int ni = active ? min(4, (mrows - 128 * wm + 31) >> 5) : 0;  // 32-row slices with pairs
     const bool store_first = wave >= 4;
     // Two register sets of raw staging data and two LDS stages.  The loads are
     // unconditional (every index is valid), so every step issues the same instructions and
@@ -297,10 +323,7 @@ __global__ __launch_bounds__(kGThreads) void gemm_kernel(
     do {                                                                                  \
         PG_GLOAD(ARF, BRF, (ULOAD));                                                      \
         if (store_first) PG_GSTORE(ARN, BRN, (UNEXT), AN, BN);                            \
-        if (active) {                                                                     \
-            gemm_half(AC, BC, wm, wn, lane, 0, acc);                                      \
-            gemm_half(AC, BC, wm, wn, lane, 32, acc);                                     \
-        }                                                                                 \
+        gemm_unit(AC, BC, wm, wn, lane, ni, acc);                                         \
         if (!store_first) PG_GSTORE(ARN, BRN, (UNEXT), AN, BN);                           \
         __syncthreads();                                                                  \
     } while (0)

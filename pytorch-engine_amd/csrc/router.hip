@@ -115,6 +115,85 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
     PG_MARK(0, 1);
 }
 
+// Prefill logits (M > 8, no extra row): the same arithmetic as router_logits_kernel, tiled
+// for reuse.  A block of 4 waves owns 16 tokens x 16 experts; wave w holds tokens
+// 8 (w >> 1) .. +7 and experts 8 (w & 1) .. +7 (64 accumulators per lane).  The h axis is
+// walked in rounds of 512 (round i = chunks 64i .. 64i+63): the block copies those x (fp16)
+// and W (fp32) columns straight from HBM into LDS, and lane l extends, for each of its
+// 8 x 8 (token, expert) pairs, the fmaf chain of slot l by chunk 64i + l (elements 0..7
+// in order).  The slot sums then meet by the same xor tree (32, 16, ..., 1) and the bias
+// is added last, so every logit has the bits of router_logits_kernel and of the CPU
+// oracle.  48 KB of LDS and ~110 VGPRs: three blocks share a CU, so one block's copies
+// overlap the others' FMAs.
+constexpr int kRgT = 16, kRgE = 16, kRgH = 512;
+
+__global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __restrict__ x, const float* __restrict__ W,
+                                                          const float* __restrict__ bias, int M, int H, int E,
+                                                          float* __restrict__ logits) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[kRgT * kRgH];  // 16 KB
+    __shared__ __attribute__((aligned(16))) float ws[kRgE * kRgH];     // 32 KB
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: row bases stay scalar
+    const int m0 = blockIdx.x * kRgT, e0 = blockIdx.y * kRgE;
+    const int wt = wave >> 1, we = wave & 1;
+    float acc[8][8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[t][j] = 0.0f;
+    for (int h0 = 0; h0 < H; h0 += kRgH) {
+        __syncthreads();
+        // stage by direct HBM -> LDS copies, 1 KB per wave instruction: x rows (16 x 1 KB)
+        // and W rows (16 x 2 KB); wave w copies x rows w + 4q and W half-rows w + 4q
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int t = wave + 4 * q;
+            dma16(x + (int64_t)min(m0 + t, M - 1) * H + h0 + 8 * lane, &xs[t * kRgH]);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int hr = wave + 4 * q, r = hr >> 1, half = hr & 1;
+            dma16(W + (int64_t)min(e0 + r, E - 1) * H + h0 + 256 * half + 4 * lane, &ws[r * kRgH + 256 * half]);
+        }
+        wait_dma();
+        __syncthreads();
+        float xv[8][8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint4 q = *(const uint4*)&xs[(8 * wt + t) * kRgH + 8 * lane];
+            const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                xv[t][2 * k] = lo_half(w4[k]);
+                xv[t][2 * k + 1] = hi_half(w4[k]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4 wa = *(const float4*)&ws[(8 * we + j) * kRgH + 8 * lane];
+            const float4 wb = *(const float4*)&ws[(8 * we + j) * kRgH + 8 * lane + 4];
+            const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[t][j] = __builtin_fmaf(xv[t][k], wv[k], acc[t][j]);
+        }
+    }
+    // slot sums -> logits: the xor tree as a reduce-scatter leaves pair l = (t, j) = (l / 8,
+    // l % 8) of the wave's 64 in lane l
+    float flat[64];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) flat[t * 8 + j] = acc[t][j];
+    float mine = scatter_sum64<64>(flat, lane);
+    const int m = m0 + 8 * wt + (lane >> 3), e = e0 + 8 * we + (lane & 7);
+    if (m < M && e < E) {
+        if (bias) mine = mine + bias[e];
+        logits[(int64_t)m * E + e] = mine;
+    }
+}
+
 // Per token: top-K experts by (logit desc, id asc); w = softmax prob (max-subtracted,
 // denominator over all E); optional renorm w / max(sum w, 1e-20).  One wavefront per token.
 // Selection on logits equals selection on softmax probabilities (monotone map).
@@ -198,7 +277,10 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
         PG_ROUTER(4, 1);  // decode: one wave per (all tokens, one expert) spreads the router read widely
     else if (M <= 8)
         PG_ROUTER(8, 1);
-    else
+    else if (!extra_w && !xsum && E >= 16 && H % kRgH == 0) {
+        PG_LAUNCH(router_gemm_kernel, dim3(div_up(M, kRgT), div_up(E, kRgE)), dim3(256), 0, st, x, W, bias, M, H, E,
+                  logits);
+    } else
         PG_ROUTER(8, 4);
 #undef PG_ROUTER
     return check_launch("router_logits");

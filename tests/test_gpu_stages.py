@@ -73,7 +73,8 @@ def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
 @pytest.mark.parametrize("M,H,E,K,bias", [(1, 2048, 128, 8, False), (8, 2048, 128, 8, False),
                                           (333, 2048, 128, 8, True), (4096, 2048, 128, 8, True),
                                           (5, 1024, 8, 2, False), (64, 3584, 64, 8, False),
-                                          (17, 4096, 8, 2, False), (3, 512, 512, 16, False)])
+                                          (17, 4096, 8, 2, False), (3, 512, 512, 16, False),
+                                          (40, 1024, 24, 4, True)])
 def test_router_topk_bitexact(dev, M, H, E, K, bias):
     from pgmoe import ops
     log(f"router M={M} H={H} E={E} K={K}")
