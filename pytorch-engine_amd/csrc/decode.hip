@@ -15,7 +15,7 @@ int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const flo
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
                       int max_active, float* inter, float* isum, hipStream_t st) {
     const DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, M, g.n_mats, 0, {}};
-#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, kDispatch, dp, max_active, inter, isum, st)
+#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, dp, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
 }
@@ -28,7 +28,7 @@ int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, co
         return fail(PGMOE_E_UNSUPPORTED, "routed decode: top_k <= 16, E <= 512, M*top_k <= 128");
     const DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, logits, desc, M, E, norm,
                      {flat.offsets, flat.perm, flat.inv, flat.active, flat.n_active, flat.w}};
-#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, kRoute, dp, max_active, inter, isum, st)
+#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, dp, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
 }
@@ -36,7 +36,7 @@ int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, co
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
                             float* isum, hipStream_t st) {
     const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
-#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, 1, M, kIdent, dp, 1, inter, isum, st)
+#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, 1, M, dp, 1, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
 }
@@ -66,7 +66,22 @@ int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum
 #undef CALL
 }
 
-bool decode_fused_down(int P, int K) { return P <= 128 && dc_stage_bytes(P, K) <= kDcStageMax; }
+bool decode_fused_down(int P, int K) { return P <= 128 && dc_lds_bytes(P, K) <= dec_lds_limit(); }
+
+// The device's LDS per block less 16 KB for the decode kernels' static arrays, cached per
+// device (hipDeviceAttributeMaxSharedMemoryPerBlock).
+size_t dec_lds_limit() {
+    static size_t cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 48 * 1024;
+    if (!cached[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 64 * 1024;
+        cached[dev] = (size_t)v - 16 * 1024;
+    }
+    return cached[dev];
+}
 
 int decode_tokens_max() { return kDecTM; }
 int decode_desc_words() { return kDescWords; }

@@ -3,13 +3,15 @@
 //   router logits (router.hip, fixed order, also the 16-element sums of x) ->
 //   gate/up + SwiGLU, each block routing the tokens itself from the logits ->
 //   down + combine fused (every block owns a few output rows across all active experts).
-// Per-expert kernels: a block owns RB rows of one active expert; lane = (row, K-slice), so
-// each lane streams whole 256-weight super-blocks of one row from the 64-row tile
-// layout (coalesced 16-byte chunks), activations are wave-uniform (LDS / broadcast),
-// and partial sums meet through a few shuffles and one LDS pass.  Weight loads are
-// issued before the activation staging so both latencies overlap.
+// Work is spread one quarter super-block (64 weights) per lane: a layer's active weights
+// cover ~200K lanes, every lane has its 3-5 weight loads in flight at once, and the
+// activations (every token row, staged in LDS before the block knows its expert) are
+// read as wave-uniform broadcasts.  The 64-row tile layout keeps each load instruction
+// on whole 128-byte lines.
 //   gate/up: fp16 magic-number dequant (1024 + code) feeding v_dot2_f32_f16
 //   down   : fp32 FMA on the fp32 SwiGLU output
+// The per-expert down kernel (stage API, shared expert, many pairs) streams whole
+// super-blocks per lane.
 // Reference: pygguf_engine/model.py:898-937; quant_kernels.py:68-311 (GEMV kernels it
 // replaces), :1423-1475 (SwiGLU + row-scale).
 #pragma once
@@ -75,54 +77,150 @@ __device__ __forceinline__ void load_raw(Raw<QT>& r, const uint8_t* mat, int N, 
     }
 }
 
-// ---------------------------------------------------------------- gate/up (fp16 dot2)
-// acc[t] += x_t . w(row, block) for t < me (TM a compile-time bound); xs = LDS fp16 x rows
-// (stride K) offset to the block; xsum = 16-element sums of those rows (stride K/16)
-// offset to the block.
-__device__ __forceinline__ uint4 ld128(const uint16_t* p) { return *(const uint4*)p; }
+// ---------------------------------------------------------------- quarter super-blocks
+// The routed decode kernels give every lane one quarter (64 weights) of one 256-weight
+// super-block of one row, so a layer's active weights spread over ~200K lanes (a dozen
+// waves per CU) and each lane issues 3-5 independent 16-byte loads.  Quarter p of a
+// super-block:
+//   Q4_K: elements 64p .. 64p+63 (sub-blocks 2p: low nibbles, 2p+1: high nibbles of
+//         qs[32p .. 32p+31]) -> chunks 0 (d, dmin, scales), 1+2p, 2+2p
+//   Q6_K: (h, g) = (p >> 1, p & 1): elements 128h + 32s + 16g + [0, 16) for s = 0..3
+//         (sub-blocks 8h + 2s + g) -> ql chunks 4h+g, 4h+2+g, qh chunk 8+2h+g, scale
+//         bytes 8h .. 8h+7 and d
+//   Q8_0: Q8_0 blocks 2p, 2p+1 = elements 64p .. 64p+63 -> chunks 4p .. 4p+3 and the two
+//         fp16 scales at chunk 16 bytes 4p .. 4p+3
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+__device__ __forceinline__ u32x4 ldq(const uint8_t* p) { return *(const u32x4*)p; }
+
+template <int QT> struct Qtr;
+template <> struct Qtr<PGMOE_Q4_K> { u32x4 h, a, b; };
+template <> struct Qtr<PGMOE_Q6_K> { u32x4 la, lb, qh; u32x2 sc; uint32_t d; };
+template <> struct Qtr<PGMOE_Q8_0> { u32x4 c0, c1, c2, c3; uint32_t d; };
+
+template <int QT>
+__device__ __forceinline__ void load_qtr(Qtr<QT>& q, const uint8_t* mat, int N, int nb, int row, int j, int p) {
+    const uint8_t* t = tile_ptr<QT>(mat, nb, row >> 6, j) + (row & 63) * 16;
+    if constexpr (QT == PGMOE_Q4_K) {
+        q.h = ldq(t);
+        q.a = ldq(t + (1 + 2 * p) * 1024);
+        q.b = ldq(t + (2 + 2 * p) * 1024);
+    } else if constexpr (QT == PGMOE_Q6_K) {
+        const int h = p >> 1, g = p & 1;
+        q.la = ldq(t + (4 * h + g) * 1024);
+        q.lb = ldq(t + (4 * h + 2 + g) * 1024);
+        q.qh = ldq(t + (8 + 2 * h + g) * 1024);
+        q.sc = *(const u32x2*)(t + 12 * 1024 + 8 * h);
+        const int64_t dpl = (int64_t)row_groups(N) * nb * 13 * 1024;
+        q.d = *(const uint16_t*)(mat + dpl + (((int64_t)(row >> 6) * nb + j) * 64 + (row & 63)) * 2);
+    } else {
+        q.c0 = ldq(t + (4 * p) * 1024);
+        q.c1 = ldq(t + (4 * p + 1) * 1024);
+        q.c2 = ldq(t + (4 * p + 2) * 1024);
+        q.c3 = ldq(t + (4 * p + 3) * 1024);
+        q.d = *(const uint32_t*)(t + 16 * 1024 + 4 * p);
+    }
+}
+
+// Staged activations: row element e of a token at unit (e >> 6) * XU + (e & 63), with
+// XU = 72 halves (gate/up, fp16) or 68 floats (down, fp32) per 64-element unit; the
+// padding puts the four quarters' units of one super-block on different LDS banks.
+constexpr int kXuH = 72, kXuF = 68;
+__device__ __forceinline__ int xpos_h(int e) { return (e >> 6) * kXuH + (e & 63); }
+__device__ __forceinline__ int xpos_f(int e) { return (e >> 6) * kXuF + (e & 63); }
+
+// Token t of a lane's pair list: 4-bit fields of `toks`.
+__device__ __forceinline__ int tok_of(uint32_t toks, int t) { return (toks >> (4 * t)) & 15; }
+
+// 16 fp16 x values (32 bytes) at xr as 8 half2 words.
+__device__ __forceinline__ void ldx16(const uint16_t* xr, uint32_t (&v)[8]) {
+    const u32x4 a = *(const u32x4*)xr, b = *(const u32x4*)(xr + 8);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// ---------------------------------------------------------------- gate/up quarter (fp16 x)
+// acc[t] += x_tok(t) . w(row, quarter p of super-block j) for the cnt <= TM pairs.  xs: the
+// staged fp16 token rows (row stride xrs halves), xss: their 16-element sums (row stride
+// srs).  Codes enter v_dot2_f32_f16 as fp16 (1024 + code); the offset returns through the
+// 16-element sums, as in the whole-super-block path.
 template <int TM>
-__device__ __forceinline__ void gu_compute(const Raw<PGMOE_Q4_K>& r, const uint16_t* xs, const float* xsum, int K,
-                                           int me, float* acc) {
-    const uint4 h = r.c[0];
-    const float dd = lo_half(h.x), dm = hi_half(h.x);
+__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const uint16_t* xs, int xrs,
+                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
+    const float dd = lo_half(q.h.x), dm = hi_half(q.h.x);
+    int s0, m0, s1, m1;
+    kscale(q.h.y, q.h.z, q.h.w, 2 * p, s0, m0);
+    kscale(q.h.y, q.h.z, q.h.w, 2 * p + 1, s1, m1);
+    const float a0 = dd * (float)s0, b0 = dm * (float)m0 + 1024.0f * a0;
+    const float a1 = dd * (float)s1, b1 = dm * (float)m1 + 1024.0f * a1;
+    const uint32_t w8[8] = {q.a.x, q.a.y, q.a.z, q.a.w, q.b.x, q.b.y, q.b.z, q.b.w};
+    uint32_t lo[16], hi[16];
 #pragma unroll
-    for (int c2 = 0; c2 < 4; ++c2) {  // qs bytes 32c2..32c2+31: sub-blocks 2c2 (low), 2c2+1 (high)
-        int s0, m0, s1, m1;
-        kscale(h.y, h.z, h.w, 2 * c2, s0, m0);
-        kscale(h.y, h.z, h.w, 2 * c2 + 1, s1, m1);
-        const float a0 = dd * (float)s0, b0 = dm * (float)m0 + 1024.0f * a0;
-        const float a1 = dd * (float)s1, b1 = dm * (float)m1 + 1024.0f * a1;
-        const uint4 qa = r.c[1 + 2 * c2], qb = r.c[2 + 2 * c2];
-        const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        uint32_t lo[16], hi[16];
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t l = w8[k] & 0x0f0f0f0fu, hh = (w8[k] >> 4) & 0x0f0f0f0fu;
+        lo[2 * k] = magic2(l, kSel01);
+        lo[2 * k + 1] = magic2(l, kSel23);
+        hi[2 * k] = magic2(hh, kSel01);
+        hi[2 * k + 1] = magic2(hh, kSel23);
+    }
+    const int xo = xpos_h(256 * j + 64 * p), so = 16 * j + 4 * p;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t l = w8[k] & 0x0f0f0f0fu, hh = (w8[k] >> 4) & 0x0f0f0f0fu;
-            lo[2 * k] = magic2(l, kSel01);
-            lo[2 * k + 1] = magic2(l, kSel23);
-            hi[2 * k] = magic2(hh, kSel01);
-            hi[2 * k + 1] = magic2(hh, kSel23);
+    for (int t = 0; t < TM; ++t) {
+        if (t < cnt) {
+            const int m = tok_of(toks, t);
+            const uint16_t* xr = xs + m * xrs + xo;
+            float tl = 0.f, th = 0.f;
+#pragma unroll
+            for (int h16 = 0; h16 < 2; ++h16) {
+                uint32_t xl[8], xh[8];
+                ldx16(xr + 16 * h16, xl);
+                ldx16(xr + 32 + 16 * h16, xh);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    tl = dot2(lo[8 * h16 + k], xl[k], tl);
+                    th = dot2(hi[8 * h16 + k], xh[k], th);
+                }
+            }
+            const float* sx = xss + m * srs + so;
+            acc[t] += a0 * tl - b0 * (sx[0] + sx[1]) + a1 * th - b1 * (sx[2] + sx[3]);
         }
+    }
+}
+
+// fp16 value 1024 + q6 (6-bit code), weight = d * sc * (q6 - 32).
+template <int TM>
+__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q6_K>& q, int j, int p, const uint16_t* xs, int xrs,
+                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
+    const float d = h2f((uint16_t)q.d);
+    const int h = p >> 1, g = p & 1;
+    const uint32_t la[4] = {q.la.x, q.la.y, q.la.z, q.la.w};
+    const uint32_t lb[4] = {q.lb.x, q.lb.y, q.lb.z, q.lb.w};
+    const uint32_t qh[4] = {q.qh.x, q.qh.y, q.qh.z, q.qh.w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        uint32_t mm[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t code = q6_word(la[k], lb[k], qh[k], s);
+            mm[2 * k] = magic2(code, kSel01);
+            mm[2 * k + 1] = magic2(code, kSel23);
+        }
+        const int bi = 2 * s + g;  // scale byte within bytes 8h .. 8h+7
+        const uint32_t sw = bi < 4 ? q.sc.x : q.sc.y;
+        const float a = d * (float)(int8_t)((sw >> (8 * (bi & 3))) & 0xff);
+        const int e0 = 256 * j + 128 * h + 32 * s + 16 * g;
+        const int xo = xpos_h(e0);
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-            if (t < me) {
-                const uint16_t* xr = xs + t * K + 64 * c2;
-                uint32_t xl[16], xh[16];
+            if (t < cnt) {
+                const int m = tok_of(toks, t);
+                uint32_t xv[8];
+                ldx16(xs + m * xrs + xo, xv);
+                float T = 0.f;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint4 v = ld128(xr + 8 * q), u = ld128(xr + 32 + 8 * q);
-                    xl[4 * q] = v.x; xl[4 * q + 1] = v.y; xl[4 * q + 2] = v.z; xl[4 * q + 3] = v.w;
-                    xh[4 * q] = u.x; xh[4 * q + 1] = u.y; xh[4 * q + 2] = u.z; xh[4 * q + 3] = u.w;
-                }
-                float tl = 0.f, th = 0.f;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    tl = dot2(lo[k], xl[k], tl);
-                    th = dot2(hi[k], xh[k], th);
-                }
-                const float* sx = xsum + t * (K >> 4) + 4 * c2;
-                acc[t] += a0 * tl - b0 * (sx[0] + sx[1]) + a1 * th - b1 * (sx[2] + sx[3]);
+                for (int k = 0; k < 8; ++k) T = dot2(mm[k], xv[k], T);
+                acc[t] += a * (T - 1056.0f * xss[m * srs + (e0 >> 4)]);
             }
         }
     }
@@ -130,86 +228,145 @@ __device__ __forceinline__ void gu_compute(const Raw<PGMOE_Q4_K>& r, const uint1
 
 // Q8_0 code q in [-128, 127]: byte ^ 0x80 = q + 128, so the fp16 value is 1152 + q.
 template <int TM>
-__device__ __forceinline__ void gu_compute(const Raw<PGMOE_Q8_0>& r, const uint16_t* xs, const float* xsum, int K,
-                                           int me, float* acc) {
-    const uint32_t dw[4] = {r.c[16].x, r.c[16].y, r.c[16].z, r.c[16].w};
+__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q8_0>& q, int j, int p, const uint16_t* xs, int xrs,
+                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float d = (j & 1) ? hi_half(dw[j >> 1]) : lo_half(dw[j >> 1]);
-        const uint4 qa = r.c[2 * j], qb = r.c[2 * j + 1];
-        const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        uint32_t m[16];
+    for (int jj = 0; jj < 2; ++jj) {
+        const float d = jj ? hi_half(q.d) : lo_half(q.d);
+        const u32x4 ca = jj ? q.c2 : q.c0, cb = jj ? q.c3 : q.c1;
+        const uint32_t w8[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+        uint32_t mm[16];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t v = w8[k] ^ 0x80808080u;
-            m[2 * k] = magic2(v, kSel01);
-            m[2 * k + 1] = magic2(v, kSel23);
+            mm[2 * k] = magic2(v, kSel01);
+            mm[2 * k + 1] = magic2(v, kSel23);
         }
+        const int e0 = 256 * j + 64 * p + 32 * jj;
+        const int xo = xpos_h(e0);
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
-            if (t < me) {
-                const uint16_t* xr = xs + t * K + 32 * j;
-                uint32_t xv[16];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint4 v = ld128(xr + 8 * q);
-                    xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
-                }
+            if (t < cnt) {
+                const int m = tok_of(toks, t);
+                const uint16_t* xr = xs + m * xrs + xo;
                 float T = 0.f;
 #pragma unroll
-                for (int k = 0; k < 16; ++k) T = dot2(m[k], xv[k], T);
-                const float* sx = xsum + t * (K >> 4) + 2 * j;
+                for (int h16 = 0; h16 < 2; ++h16) {
+                    uint32_t xv[8];
+                    ldx16(xr + 16 * h16, xv);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) T = dot2(mm[8 * h16 + k], xv[k], T);
+                }
+                const float* sx = xss + m * srs + (e0 >> 4);
                 acc[t] += d * (T - 1152.0f * (sx[0] + sx[1]));
             }
         }
     }
 }
 
-// fp16 value 1024 + q6 (6-bit code), weight = d * sc * (q6 - 32).
+// ---------------------------------------------------------------- down quarter (fp32 x)
+// part[c] = inter_(p0+c) . w(row, quarter p of super-block j) for c < cnt <= TM; xs: the
+// staged fp32 inter rows from pair p0 on (row stride xrs floats), iss: their 16-element
+// sums (row stride srs).
+__device__ __forceinline__ void bytes_f(uint32_t v, float* f) {
+    f[0] = (float)(v & 0xff);
+    f[1] = (float)((v >> 8) & 0xff);
+    f[2] = (float)((v >> 16) & 0xff);
+    f[3] = (float)(v >> 24);
+}
+
+template <int N>
+__device__ __forceinline__ float dotf(const float* qf, const float* xr) {
+    float T = 0.f;
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        const floatx4 v = *(const floatx4*)(xr + i);
+        T = __builtin_fmaf(qf[i], v.x, T);
+        T = __builtin_fmaf(qf[i + 1], v.y, T);
+        T = __builtin_fmaf(qf[i + 2], v.z, T);
+        T = __builtin_fmaf(qf[i + 3], v.w, T);
+    }
+    return T;
+}
+
 template <int TM>
-__device__ __forceinline__ void gu_compute(const Raw<PGMOE_Q6_K>& r, const uint16_t* xs, const float* xsum, int K,
-                                           int me, float* acc) {
-    const float d = h2f((uint16_t)r.d);
-    const uint32_t scw[4] = {r.c[12].x, r.c[12].y, r.c[12].z, r.c[12].w};
+__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const float* xs, int xrs,
+                                       const float* iss, int srs, int cnt, float* part) {
+    const float dd = lo_half(q.h.x), dm = hi_half(q.h.x);
+    const uint32_t w8[8] = {q.a.x, q.a.y, q.a.z, q.a.w, q.b.x, q.b.y, q.b.z, q.b.w};
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int hi = 0; hi < 2; ++hi) {
+        int sc, mn;
+        kscale(q.h.y, q.h.z, q.h.w, 2 * p + hi, sc, mn);
+        const float a = dd * (float)sc, bm = dm * (float)mn;
+        float qf[32];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            uint32_t m[16];
+        for (int k = 0; k < 8; ++k) bytes_f((w8[k] >> (4 * hi)) & 0x0f0f0f0fu, qf + 4 * k);
+        const int e0 = 256 * j + 64 * p + 32 * hi;
+        const int xo = xpos_f(e0);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int wa = 16 * h + k, wb = 16 * h + 8 + k, wq = 8 * h + k;  // word indices
-                const uint32_t qa = ((const uint32_t*)&r.c[wa >> 2])[wa & 3];
-                const uint32_t qb = ((const uint32_t*)&r.c[wb >> 2])[wb & 3];
-                const uint32_t qh = ((const uint32_t*)&r.c[8 + (wq >> 2)])[wq & 3];
-                const uint32_t q = q6_word(qa, qb, qh, s);
-                m[2 * k] = magic2(q, kSel01);
-                m[2 * k + 1] = magic2(q, kSel23);
-            }
-            const int sb = 8 * h + 2 * s;
-            const float a0 = d * (float)(int8_t)((scw[sb >> 2] >> (8 * (sb & 3))) & 0xff);
-            const float a1 = d * (float)(int8_t)((scw[(sb + 1) >> 2] >> (8 * ((sb + 1) & 3))) & 0xff);
-#pragma unroll
-            for (int t = 0; t < TM; ++t) {
-                if (t < me) {
-                    const uint16_t* xr = xs + t * K + 128 * h + 32 * s;
-                    uint32_t xv[16];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const uint4 v = ld128(xr + 8 * q);
-                        xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
-                    }
-                    float T0 = 0.f, T1 = 0.f;
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) T0 = dot2(m[k], xv[k], T0);
-#pragma unroll
-                    for (int k = 8; k < 16; ++k) T1 = dot2(m[k], xv[k], T1);
-                    const float* sx = xsum + t * (K >> 4) + sb;
-                    acc[t] += a0 * (T0 - 1056.0f * sx[0]) + a1 * (T1 - 1056.0f * sx[1]);
-                }
+        for (int c = 0; c < TM; ++c) {
+            if (c < cnt) {
+                const float T = dotf<32>(qf, xs + c * xrs + xo);
+                const float* sx = iss + c * srs + (e0 >> 4);
+                part[c] += a * T - bm * (sx[0] + sx[1]);
             }
         }
+    }
 }
+
+template <int TM>
+__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q6_K>& q, int j, int p, const float* xs, int xrs,
+                                       const float* iss, int srs, int cnt, float* part) {
+    const float d = h2f((uint16_t)q.d);
+    const int h = p >> 1, g = p & 1;
+    const uint32_t la[4] = {q.la.x, q.la.y, q.la.z, q.la.w};
+    const uint32_t lb[4] = {q.lb.x, q.lb.y, q.lb.z, q.lb.w};
+    const uint32_t qh[4] = {q.qh.x, q.qh.y, q.qh.z, q.qh.w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        float qf[16];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bytes_f(q6_word(la[k], lb[k], qh[k], s), qf + 4 * k);
+        const int bi = 2 * s + g;
+        const uint32_t sw = bi < 4 ? q.sc.x : q.sc.y;
+        const float a = d * (float)(int8_t)((sw >> (8 * (bi & 3))) & 0xff);
+        const int e0 = 256 * j + 128 * h + 32 * s + 16 * g;
+        const int xo = xpos_f(e0);
+#pragma unroll
+        for (int c = 0; c < TM; ++c) {
+            if (c < cnt) {
+                const float T = dotf<16>(qf, xs + c * xrs + xo);
+                part[c] += a * (T - 32.0f * iss[c * srs + (e0 >> 4)]);
+            }
+        }
+    }
+}
+
+template <int TM>
+__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q8_0>& q, int j, int p, const float* xs, int xrs,
+                                       const float* iss, int srs, int cnt, float* part) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const float d = jj ? hi_half(q.d) : lo_half(q.d);
+        const u32x4 ca = jj ? q.c2 : q.c0, cb = jj ? q.c3 : q.c1;
+        const uint32_t w8[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+        float qf[32];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) bytes_f(w8[k] ^ 0x80808080u, qf + 4 * k);  // q + 128 per byte
+        const int e0 = 256 * j + 64 * p + 32 * jj;
+        const int xo = xpos_f(e0);
+#pragma unroll
+        for (int c = 0; c < TM; ++c) {
+            if (c < cnt) {
+                const float T = dotf<32>(qf, xs + c * xrs + xo);
+                const float* sx = iss + c * srs + (e0 >> 4);
+                part[c] += d * (T - 128.0f * (sx[0] + sx[1]));
+            }
+        }
+    }
+}
+
 
 // ---------------------------------------------------------------- down (fp32)
 // acc[t] += inter_t . w(row, block); x = global fp32 rows (stride K, wave-uniform)
@@ -332,9 +489,10 @@ __device__ __forceinline__ float kslot_sum(float v) {
 
 // ============================================================================ routing in a block
 // Decode forward: the router kernel writes logits [M][E]; every gate/up block re-derives
-// the top-k sets of the M <= 8 tokens from them (about a microsecond of register work
-// instead of a launch and its dependent global round trips), and block (0, 0) also
-// publishes a compact routing descriptor for the fused down + combine kernel:
+// the top-k sets of the M <= 8 tokens from them (wave m selects token m with scalar
+// ballot arithmetic, about half a microsecond, instead of a launch and its dependent
+// global round trips), and block (0, 0) also publishes a compact routing descriptor for
+// the fused down + combine kernel:
 //   int32 words: [0] n_active; slot a at kDescSlot + 4a = {expert, first sorted pair,
 //   pair count, 0}; sorted pair p at kDescPair + 2p = {token, weight bits}.
 // Active slots are in ascending expert id; the pairs of an expert in ascending token
@@ -350,9 +508,7 @@ struct RouteShared {
     int wp[16];                 // (token, expert) pairs in the words before q
     int mem_e[kDecTM * 16];     // the K members of token m at [m*K, m*K+K), ascending id
     float mem_w[kDecTM * 16];   // their combine weights (publishing block only)
-    int n_act, e, p_begin, count;
-    int tok[kDecTM];
-    uint64_t wbuf[4][64];       // per-wave selection scratch
+    int n_act;                  // active experts
 };
 
 // Selection key of (logit v, expert e): larger key = earlier in (logit desc, id asc).
@@ -383,12 +539,14 @@ __device__ __forceinline__ void copy_words(T* dst, const T* __restrict__ src, in
     copy_idx<U, T>(n, tid, nth, [=](int i) { return src + i; }, [=](int i) { return dst + i; });
 }
 
-// K-th largest of the distinct keys of one token held by a wave (lane l: experts l + 64r),
-// by a 41-step radix descent on the key bits (ballot counts).  Exact for any keys; used
-// when the candidate select below has too many candidates.
+// K-th largest of the distinct keys of one token held by a wave (lane l: experts l + 64r):
+// a 41-step radix descent on the key bits.  The threshold and the counts are wave-uniform
+// (scalar registers); each step is one vector compare per key word and a popcount of the
+// resulting lane mask.
 template <int RE>
 __device__ __forceinline__ uint64_t kth_key_radix(const uint64_t (&key)[RE], int K) {
     uint64_t thr = 0;
+#pragma unroll
     for (int b = 40; b >= 0; --b) {
         const uint64_t cand = thr | (1ull << b);
         int cnt = 0;
@@ -399,170 +557,131 @@ __device__ __forceinline__ uint64_t kth_key_radix(const uint64_t (&key)[RE], int
     return thr;
 }
 
-// Rank of v among n 64-bit values in LDS (number strictly greater), n even.
-__device__ __forceinline__ int lds_rank(const uint64_t* buf, int n, uint64_t v) {
-    int c = 0;
-    for (int j = 0; j < n; j += 2) {
-        const uint64_t a = buf[j], b = buf[j + 1];
-        c += a > v ? 1 : 0;
-        c += b > v ? 1 : 0;
-    }
-    return c;
-}
-
-// K-th largest key of one token (keys distinct, at least K of them nonzero; 1 <= K <= 16).
-// 1. T = the K-th largest of the 64 lane maxima.  At most K lanes have a maximum >= the
-//    K-th largest key k* (each such maximum is a distinct key >= k*), so T <= k*.
-// 2. The candidates (keys >= T) hold the K largest keys; they are ranked among
-//    themselves and the one of rank K-1 is k*.  More than 64 candidates (keys bunched in
-//    few lanes) take the radix descent instead.
-// wbuf: this wave's 64-word LDS scratch.
+// Logits of token m for lane l (experts l + 64r; -inf past E).
 template <int RE>
-__device__ __forceinline__ uint64_t kth_key(const uint64_t (&key)[RE], int K, int lane, uint64_t* wbuf) {
-    uint64_t lm = 0;
-#pragma unroll
-    for (int r = 0; r < RE; ++r) lm = key[r] > lm ? key[r] : lm;
-    wbuf[lane] = lm;
-    __builtin_amdgcn_wave_barrier();
-    const int c1 = lds_rank(wbuf, 64, lm);
-    const uint64_t b1 = __ballot(lm != 0 && c1 == K - 1);
-    const int l1 = __ffsll((unsigned long long)b1) - 1;
-    const uint64_t T = ((uint64_t)__shfl(uint32_t(lm >> 32), l1, 64) << 32) | __shfl(uint32_t(lm), l1, 64);
-    int C = 0;
-#pragma unroll
-    for (int r = 0; r < RE; ++r) C += __popcll(__ballot(key[r] >= T));
-    if (C > 64) return kth_key_radix<RE>(key, K);
-    __builtin_amdgcn_wave_barrier();
-    int base = 0;
+__device__ __forceinline__ void load_logits(const float* __restrict__ logits, int m, int E, int lane, float (&v)[RE]) {
 #pragma unroll
     for (int r = 0; r < RE; ++r) {
-        const bool in = key[r] >= T;
-        const uint64_t mk = __ballot(in);
-        if (in) wbuf[base + __popcll(mk & ((1ull << lane) - 1ull))] = key[r];
-        base += __popcll(mk);
-    }
-    if ((C & 1) && lane == C) wbuf[C] = 0;  // pad to an even count (0 is below every key)
-    __builtin_amdgcn_wave_barrier();
-    const uint64_t ci = lane < C ? wbuf[lane] : 0;
-    const int c2 = lds_rank(wbuf, (C + 1) & ~1, ci);
-    const uint64_t b2 = __ballot(lane < C && c2 == K - 1);
-    const int l2 = __ffsll((unsigned long long)b2) - 1;
-    return ((uint64_t)__shfl(uint32_t(ci >> 32), l2, 64) << 32) | __shfl(uint32_t(ci), l2, 64);
-}
-
-// Top-k membership of NT tokens handled by one wave (tokens m = wv + nw*i, i < NT; those
-// >= M are skipped).  Lane l holds the keys of experts l + 64r, r < RE; the members of a
-// token are exactly its keys at or above its K-th largest key (keys are distinct).  With
-// `weights`, also the softmax weights of the members (max-subtracted, denominator over
-// all E, optional renorm; model.py:903-907).
-template <int RE, int NT>
-__device__ __forceinline__ void route_tokens(const float* sl, int M, int E, int K, RouteShared& R, bool weights,
-                                             int norm, int wv, int nw, int lane) {
-    uint64_t key[NT][RE];
-    uint64_t thr[NT];
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-        const int m = wv + nw * i;
-#pragma unroll
-        for (int r = 0; r < RE; ++r) {
-            const int e = lane + 64 * r;
-            key[i][r] = (m < M && e < E) ? route_key(sl[m * E + e], e) : 0ull;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < NT; ++i) thr[i] = wv + nw * i < M ? kth_key<RE>(key[i], K, lane, R.wbuf[wv]) : ~0ull;
-    if (wv == 0) PG_MARK(1, 7);
-#pragma unroll
-    for (int i = 0; i < NT; ++i) {
-        const int m = wv + nw * i;
-        if (m >= M) continue;
-        float top = -INFINITY, den = 0.f;
-        if (weights) {
-#pragma unroll
-            for (int r = 0; r < RE; ++r)
-                if (lane + 64 * r < E) top = fmaxf(top, sl[m * E + lane + 64 * r]);
-#pragma unroll
-            for (int s = 32; s >= 1; s >>= 1) top = fmaxf(top, __shfl_xor(top, s, 64));
-#pragma unroll
-            for (int r = 0; r < RE; ++r)
-                if (lane + 64 * r < E) den += expf(sl[m * E + lane + 64 * r] - top);
-            den = group_sum<64>(den);
-        }
-        int base = 0;
-        float psel = 0.f;
-#pragma unroll
-        for (int r = 0; r < RE; ++r) {
-            const bool in = key[i][r] >= thr[i] && lane + 64 * r < E;
-            const uint64_t mask = __ballot(in);
-            if (lane == 0) {
-                R.pres[m][2 * r] = (uint32_t)mask;
-                R.pres[m][2 * r + 1] = (uint32_t)(mask >> 32);
-            }
-            const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
-            if (in && pos < K) {  // exactly K members unless logits hold NaNs
-                R.mem_e[m * K + pos] = lane + 64 * r;
-                if (weights) {
-                    const float p = expf(sl[m * E + lane + 64 * r] - top) / den;
-                    R.mem_w[m * K + pos] = p;
-                    psel += p;
-                }
-            }
-            base += __popcll(mask);
-        }
-        if (weights && norm) {
-            psel = group_sum<64>(psel);
-            for (int j = lane; j < K; j += 64) R.mem_w[m * K + j] = R.mem_w[m * K + j] / fmaxf(psel, 1e-20f);
-        }
-        if (lane < 16 && lane >= 2 * RE) R.pres[m][lane] = 0u;
+        const int e = lane + 64 * r;
+        v[r] = e < E ? logits[(int64_t)m * E + e] : -INFINITY;
     }
 }
 
-// Routing of the M <= 8 tokens in one block from the logits [M][E] (sl: LDS scratch of
-// M*E floats), then the per-word prefix counts: used / wc / wp / n_act.  Every thread of
-// the block calls this.  NT = tokens per wave, a compile-time bound >= ceil(M / waves).
-template <int NT>
-__device__ __forceinline__ void route_in_block(const float* __restrict__ logits, int M, int E, int K, float* sl,
-                                               RouteShared& R, bool weights, int norm) {
-    const int tid = threadIdx.x, nth = blockDim.x, lane = tid & 63, wv = tid >> 6, nw = nth >> 6;
-    copy_words<8>(sl, logits, M * E, tid, nth);
-    __syncthreads();
-    PG_MARK(1, 6);
-    if (E <= 64)
-        route_tokens<1, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
-    else if (E <= 128)
-        route_tokens<2, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
-    else if (E <= 256)
-        route_tokens<4, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
-    else
-        route_tokens<8, NT>(sl, M, E, K, R, weights, norm, wv, nw, lane);
-    __syncthreads();
-    if (wv == 0) {  // lane q: word q of the expert bitmaps; wave prefix sums over the words
-        uint32_t u = 0;
-        int pc = 0;
-        if (lane < 16) {
-            for (int m = 0; m < M; ++m) {
-                const uint32_t w = R.pres[m][lane];
-                u |= w;
-                pc += __popc(w);
-            }
-        }
-        int ca = __popc(u), cp = pc;
+// Top-k membership of token m (one wave; v = load_logits): the members are exactly the
+// keys at or above the K-th largest key (keys are distinct).  Lane 0 writes the
+// membership words R.pres[m][*]; with `weights`, also the members' ids and softmax weights
+// (max-subtracted, denominator over all E, optional renorm; model.py:903-907) in
+// ascending id order to R.mem_e / R.mem_w.
+template <int RE>
+__device__ __forceinline__ void route_token(const float (&v)[RE], int m, int E, int K, RouteShared& R, bool weights,
+                                            int norm, int lane) {
+    uint64_t key[RE];
 #pragma unroll
-        for (int s = 1; s < 16; s <<= 1) {
-            const int oa = __shfl_up(ca, s, 64), op = __shfl_up(cp, s, 64);
-            if (lane >= s) {
-                ca += oa;
-                cp += op;
-            }
-        }
-        if (lane < 16) {
-            R.used[lane] = u;
-            R.wc[lane] = ca - __popc(u);
-            R.wp[lane] = cp - pc;
-        }
-        if (lane == 15) R.n_act = ca;
+    for (int r = 0; r < RE; ++r) key[r] = lane + 64 * r < E ? route_key(v[r], lane + 64 * r) : 0ull;
+    const uint64_t thr = kth_key_radix<RE>(key, K);
+    float top = -INFINITY, den = 0.f;
+    if (weights) {
+#pragma unroll
+        for (int r = 0; r < RE; ++r) top = fmaxf(top, v[r]);
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) top = fmaxf(top, __shfl_xor(top, s, 64));
+#pragma unroll
+        for (int r = 0; r < RE; ++r)
+            if (lane + 64 * r < E) den += expf(v[r] - top);
+        den = group_sum<64>(den);
     }
-    __syncthreads();
+    int base = 0;
+    float psel = 0.f;
+#pragma unroll
+    for (int r = 0; r < RE; ++r) {
+        const bool in = key[r] >= thr && lane + 64 * r < E;
+        const uint64_t mask = __ballot(in);
+        if (lane == 0) {
+            R.pres[m][2 * r] = (uint32_t)mask;
+            R.pres[m][2 * r + 1] = (uint32_t)(mask >> 32);
+        }
+        const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
+        if (weights && in && pos < K) {  // exactly K members unless logits hold NaNs
+            const float pr = expf(v[r] - top) / den;
+            R.mem_e[m * K + pos] = lane + 64 * r;
+            R.mem_w[m * K + pos] = pr;
+            psel += pr;
+        }
+        base += __popcll(mask);
+    }
+    if (weights && norm) {
+        psel = group_sum<64>(psel);
+        for (int i = lane; i < K; i += 64) R.mem_w[m * K + i] = R.mem_w[m * K + i] / fmaxf(psel, 1e-20f);
+    }
+    if (lane < 16 && lane >= 2 * RE) R.pres[m][lane] = 0u;
+}
+
+// Active slot a of the routing in R (after the barrier that follows route_token): every
+// wave derives it on its own from the membership words (lane q < 16 holds word q of every
+// token), with DPP row scans and lane reads instead of LDS round trips, so no further
+// barrier is needed.  With store_words, the per-word prefix counts used / wc / wp and
+// n_act also go to R (for publish_route).
+struct SlotInfo {
+    int n_act, e, p_begin, count;
+    uint32_t toks;  // the count tokens of expert e, ascending, 4 bits each
+};
+
+// Inclusive prefix sum over each 16-lane DPP row.
+__device__ __forceinline__ int row_scan16(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    return v;
+}
+
+__device__ __forceinline__ SlotInfo slot_info(RouteShared& R, int M, int a, int lane, bool store_words) {
+    uint32_t wm[kDecTM];
+    uint32_t u = 0;
+    int pc = 0;
+#pragma unroll
+    for (int m = 0; m < kDecTM; ++m) {
+        wm[m] = (m < M && lane < 16) ? R.pres[m][lane & 15] : 0u;
+        u |= wm[m];
+        pc += __popc(wm[m]);
+    }
+    const int ca = row_scan16(__popc(u)), cp = row_scan16(pc);
+    const int wc = ca - __popc(u), wp = cp - pc;
+    if (store_words && lane < 16) {
+        R.used[lane] = u;
+        R.wc[lane] = wc;
+        R.wp[lane] = wp;
+    }
+    SlotInfo si;
+    si.n_act = __builtin_amdgcn_readlane(ca, 15);
+    if (store_words && lane == 0) R.n_act = si.n_act;
+    si.e = -1;
+    si.p_begin = si.count = 0;
+    si.toks = 0;
+    if (a >= si.n_act) return si;
+    const uint64_t hit = __ballot(lane < 16 && a >= wc && a < ca);
+    const int q = __ffsll((unsigned long long)hit) - 1;
+    uint32_t uq = __builtin_amdgcn_readlane(u, q);
+    const int skip = a - __builtin_amdgcn_readlane(wc, q);
+    for (int i = 0; i < skip; ++i) uq &= uq - 1u;
+    const int bit = __ffs(uq) - 1;
+    si.e = 32 * q + bit;
+    const uint32_t below = (1u << bit) - 1u;
+    int pb = __builtin_amdgcn_readlane(wp, q), c = 0;
+    uint32_t toks = 0;
+#pragma unroll
+    for (int m = 0; m < kDecTM; ++m) {
+        const uint32_t w = __builtin_amdgcn_readlane(wm[m], q);  // 0 past M
+        pb += __popc(w & below);
+        if ((w >> bit) & 1u) {
+            toks |= (uint32_t)m << (4 * c);
+            ++c;
+        }
+    }
+    si.p_begin = pb;
+    si.count = c;
+    si.toks = toks;
+    return si;
 }
 
 // Expert e's active-slot index (or -1), its first sorted pair and pair count.
@@ -587,8 +706,9 @@ struct FlatRoute {
     float* w;
 };
 
-// Publish the routing descriptor (block (0, 0) only; R holds the weights), and the flat
-// arrays when fl.offsets is set.  One thread per expert, then one per pair.
+// Publish the routing descriptor (block (0, 0) only; R holds the weights and the word
+// prefix counts), and the flat arrays when fl.offsets is set.  One thread per expert, then
+// one per pair.
 __device__ __forceinline__ void publish_route(const RouteShared& R, int M, int E, int K, int32_t* __restrict__ desc,
                                               const FlatRoute& fl) {
     const int tid = threadIdx.x, nth = blockDim.x;
@@ -633,6 +753,7 @@ __device__ __forceinline__ void publish_route(const RouteShared& R, int M, int E
     }
 }
 
+
 // ============================================================================ kernels
 // Where a decode expert kernel finds its pairs:
 //   kDispatch: offsets / perm / active / n_active of a counting-sort dispatch (stage API);
@@ -646,168 +767,295 @@ struct DecDisp {
     const int32_t *offsets, *perm, *active, *n_active;
     const float* logits;  // kRoute
     int32_t* desc;        // kRoute: published by block (0, 0)
-    int M, E, norm;       // M: tokens (kRoute, kIdent)
+    int M, E, norm;       // M: tokens (every mode)
     FlatRoute flat;       // kRoute: optional flat arrays, published by block (0, 0)
 };
 
-// Gate/up + SwiGLU.  Block = RB rows of one active expert, W waves; lane (r, ks):
-// row = RB*blockIdx.x + r, super-blocks j = ks + KS*w, + KS*W, ...  Pairs of the expert
-// are taken TM at a time.  inter / isum rows are indexed by sorted pair.
-// Dynamic LDS: max(xs [TM][K] fp16 + xs_sum [TM][K/16] f32, logits [M][E] f32 (kRoute),
-// partials [W][TM][2][RB] + SwiGLU row [TM][RB]).
-// xsum (optional): 16-element sums of x rows [M][K/16]; isum (optional output):
-// 16-element sums of inter rows [P][N/16].
-template <int QT, int RB, int W, int TM>
-__global__ __launch_bounds__(W * 64) void dec_gateup_kernel(const uint8_t* __restrict__ gbase,
-                                                            const uint8_t* __restrict__ ubase, int64_t gstride,
-                                                            int64_t ustride, int N, int K,
-                                                            const uint16_t* __restrict__ x,
-                                                            const float* __restrict__ xsum, int topk, DecDisp dp,
-                                                            float* __restrict__ inter, float* __restrict__ isum) {
-    constexpr int KS = 64 / RB;
+// Active slot a of the dispatch or identity modes (a token meets an expert at most once,
+// so count <= M <= 8).
+__device__ __forceinline__ SlotInfo slot_plain(const DecDisp& dp, int a, int topk) {
+    SlotInfo si;
+    si.e = -1;
+    si.p_begin = si.count = 0;
+    si.toks = 0;
+    if (dp.mode == kIdent) {
+        si.n_act = 1;
+        if (a > 0) return si;
+        si.e = 0;
+        si.count = dp.M;
+        for (int m = 0; m < dp.M; ++m) si.toks |= (uint32_t)m << (4 * m);
+        return si;
+    }
+    si.n_act = *dp.n_active;
+    if (a >= si.n_act) return si;
+    si.e = dp.active[a];
+    si.p_begin = dp.offsets[si.e];
+    si.count = min(dp.offsets[si.e + 1] - si.p_begin, dp.M);
+    for (int t = 0; t < si.count; ++t) si.toks |= (uint32_t)(dp.perm[si.p_begin + t] / topk) << (4 * t);
+    return si;
+}
+
+// Gate/up + SwiGLU.  Block = 16 rows of the experts of active slots blockIdx.y,
+// + gridDim.y, ...; W (even) waves: wave w owns the items it = w, w + W, ... of the
+// 2 * (K/256) (matrix = it & 1, super-block j = it >> 1), lane = (row r = lane & 15,
+// quarter p = lane >> 4).  Every token row is staged in LDS (fp16, padded units) while the
+// block routes, once for all its slots; each lane then loads the quarters of two items at
+// once and accumulates one partial per pair of the expert.  inter / isum rows are indexed
+// by sorted pair p_begin + t.
+// Dynamic LDS: xs [M][K/64][72] fp16 | xss [M][K/16] f32.
+// xsum (optional): 16-element sums of the x rows [M][K/16] (else computed from xs);
+// isum (optional output): 16-element sums of the inter rows [P][N/16].
+template <int RE, typename Issue>
+__device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteShared& R, bool pub, int lane, int w,
+                                            int nw, Issue issue) {
+    float v[RE];
+    if (w < dp.M) load_logits<RE>(dp.logits, w, dp.E, lane, v);
+    issue();  // the token-row loads go out behind the logits
+    for (int m = w; m < dp.M; m += nw) {
+        if (m != w) load_logits<RE>(dp.logits, m, dp.E, lane, v);
+        route_token<RE>(v, m, dp.E, topk, R, pub, dp.norm, lane);
+    }
+}
+
+template <int QT, int TM>
+__global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict__ gbase,
+                                                      const uint8_t* __restrict__ ubase, int64_t gstride,
+                                                      int64_t ustride, int N, int K, const uint16_t* __restrict__ x,
+                                                      const float* __restrict__ xsum, int topk, DecDisp dp,
+                                                      float* __restrict__ inter, float* __restrict__ isum) {
+    constexpr int RB = 16, XR = 4;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ RouteShared R;
-    const int a = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int MODE = dp.mode;
-    int e, p_begin, p_end;
-    PG_MARK(1, 0);
-    if (MODE == kRoute) {
-        const bool pub = blockIdx.x == 0 && a == 0;
-        // tokens per wave: sized from TM, or for kDecTM when the LDS limit made TM < M
-        if (dp.M <= ((TM + W - 1) / W) * W)
-            route_in_block<(TM + W - 1) / W>(dp.logits, dp.M, dp.E, topk, (float*)smem, R, pub, dp.norm);
-        else
-            route_in_block<(kDecTM + W - 1) / W>(dp.logits, dp.M, dp.E, topk, (float*)smem, R, pub, dp.norm);
-        PG_MARK(1, 1);
-        if (a >= R.n_act) return;  // uniform: every block computed the same n_act
-        for (int ee = tid; ee < dp.E; ee += W * 64) {  // the expert of this block's slot
-            int pb = 0, c = 0;
-            if (route_expert(R, dp.M, ee, pb, c) == a) {
-                R.e = ee;
-                R.p_begin = pb;
-                R.count = c;
-                int n = 0;
-                for (int m = 0; m < dp.M; ++m)
-                    if ((R.pres[m][ee >> 5] >> (ee & 31)) & 1u) R.tok[n++] = m;
-            }
-        }
-        __syncthreads();
-        PG_MARK(1, 2);
-        e = R.e;
-        p_begin = R.p_begin;
-        p_end = p_begin + R.count;
-    } else if (MODE == kIdent) {
-        e = 0;
-        p_begin = 0;
-        p_end = dp.M;
-    } else {
-        if (a >= *dp.n_active) return;
-        e = dp.active[a];
-        p_begin = dp.offsets[e];
-        p_end = dp.offsets[e + 1];
-    }
-    const int r = lane % RB, ks = lane / RB;
-    const int row = blockIdx.x * RB + r;  // < row_groups(N) * 64: padded tile rows are readable
-    const int nb = K >> 8;
-    const int j0 = ks + KS * w;
+    __shared__ float red[16][TM][RB];  // per-wave row partials
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nth = blockDim.x, nw = nth >> 6;
+    const int M = dp.M, MODE = dp.mode;
+    const int nb = K >> 8, xrs = (K >> 6) * kXuH, srs = K >> 4;
+    const bool pub = MODE == kRoute && blockIdx.x == 0 && blockIdx.y == 0;
     uint16_t* xs = (uint16_t*)smem;
-    float* xss = (float*)(smem + (size_t)TM * K * 2);
-    float* red = (float*)smem;           // [W][TM][2][RB] after the K loop
-    float* act = red + W * TM * 2 * RB;  // [TM][RB] SwiGLU values
-    const uint8_t* gm = gbase + (int64_t)e * gstride;
-    const uint8_t* um = ubase + (int64_t)e * ustride;
-    for (int p0 = p_begin; p0 < p_end; p0 += TM) {
-        const int me = min(TM, p_end - p0);
-        Raw<QT> rg, ru;
-        if (j0 < nb) {  // weights first: their latency overlaps the activation staging
-            load_raw<QT>(rg, gm, N, nb, row, j0);
-            load_raw<QT>(ru, um, N, nb, row, j0);
+    float* xss = (float*)(smem + (size_t)M * xrs * 2);
+    PG_MARK(1, 0);
+    // 1. token rows (and their 16-element sums) to registers, behind the logits of the
+    //    wave's token; the selection then waits for the logits only
+    const int npc = M * (K >> 3);  // 16-byte pieces of the x rows
+    const int nps = xsum ? M * (K >> 6) : 0;
+    u32x4 xr[XR];
+    floatx4 sr;
+    auto issue = [&]() {
+#pragma unroll
+        for (int k = 0; k < XR; ++k) {
+            const int i = tid + k * nth;
+            if (i < npc) xr[k] = *(const u32x4*)(x + 8 * (int64_t)i);
+        }
+        if (tid < nps) sr = *(const floatx4*)(xsum + 4 * tid);
+    };
+    if (MODE == kRoute) {
+        if (dp.E <= 64)
+            route_waves<1>(dp, topk, R, pub, lane, w, nw, issue);
+        else if (dp.E <= 128)
+            route_waves<2>(dp, topk, R, pub, lane, w, nw, issue);
+        else if (dp.E <= 256)
+            route_waves<4>(dp, topk, R, pub, lane, w, nw, issue);
+        else
+            route_waves<8>(dp, topk, R, pub, lane, w, nw, issue);
+    } else {
+        issue();
+    }
+    PG_MARK(1, 6);
+    // 2. rows to LDS (pieces past XR per thread are copied directly)
+    const int kp = K >> 3;
+#pragma unroll
+    for (int k = 0; k < XR; ++k) {
+        const int i = tid + k * nth;
+        if (i < npc) *(u32x4*)(xs + (i / kp) * xrs + xpos_h(8 * (i % kp))) = xr[k];
+    }
+    for (int i = tid + XR * nth; i < npc; i += nth)
+        *(u32x4*)(xs + (i / kp) * xrs + xpos_h(8 * (i % kp))) = *(const u32x4*)(x + 8 * (int64_t)i);
+    if (tid < nps) *(floatx4*)(xss + 4 * tid) = sr;
+    for (int i = tid + nth; i < nps; i += nth) *(floatx4*)(xss + 4 * i) = *(const floatx4*)(xsum + 4 * i);
+    __syncthreads();
+    if (!xsum) {
+        for (int i = tid; i < M * srs; i += nth) {
+            const uint16_t* pp = xs + (i / srs) * xrs + xpos_h(16 * (i % srs));
+            float sm = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) sm += h2f(pp[k]);
+            xss[i] = sm;
         }
         __syncthreads();
-        for (int i = tid; i < me * (K >> 3); i += W * 64) {
-            const int t = i / (K >> 3), c = i % (K >> 3);
-            const int tok = MODE == kRoute ? R.tok[p0 - p_begin + t] : MODE == kIdent ? p0 + t : dp.perm[p0 + t] / topk;
-            *(uint4*)(xs + t * K + 8 * c) = *(const uint4*)(x + (int64_t)tok * K + 8 * c);
-        }
-        if (xsum) {
-            for (int i = tid; i < me * (K >> 4); i += W * 64) {
-                const int t = i / (K >> 4), c = i % (K >> 4);
-                const int tok =
-                    MODE == kRoute ? R.tok[p0 - p_begin + t] : MODE == kIdent ? p0 + t : dp.perm[p0 + t] / topk;
-                xss[i] = xsum[(int64_t)tok * (K >> 4) + c];
-            }
-        }
-        __syncthreads();
-        if (!xsum) {
-            for (int i = tid; i < me * (K >> 4); i += W * 64) {
-                const uint16_t* p = xs + (i / (K >> 4)) * K + 16 * (i % (K >> 4));
-                float sm = 0.f;
+    }
+    PG_MARK(1, 1);
+    // 3. the block's active slots a = blockIdx.y, + gridDim.y, ...: expert and pairs (the
+    //    same in every wave), items, then the SwiGLU rows
+    const int r = lane & 15, p = lane >> 4;
+    const int row = blockIdx.x * RB + r;  // < row_groups(N) * 64: padded tile rows are readable
+    const int nit = 2 * nb;
+    for (int a = blockIdx.y;; a += gridDim.y) {
+        const SlotInfo si = MODE == kRoute ? slot_info(R, M, a, lane, w == 0 && pub && a == 0) : slot_plain(dp, a, topk);
+        if (si.e < 0) break;  // uniform over the block
+        PG_MARK(1, 2);
+        // items, two per wave at a time (both quarters' loads in flight together)
+        const uint8_t* mat = (w & 1) ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
+        float acc[TM];
 #pragma unroll
-                for (int k = 0; k < 16; ++k) sm += h2f(p[k]);
-                xss[i] = sm;
-            }
-            __syncthreads();
-        }
-        PG_MARK(1, 3);
-        float ag[TM], au[TM];
-#pragma unroll
-        for (int t = 0; t < TM; ++t) ag[t] = au[t] = 0.f;
-        for (int j = j0; j < nb; j += KS * W) {
-            if (j != j0) {
-                load_raw<QT>(rg, gm, N, nb, row, j);
-                load_raw<QT>(ru, um, N, nb, row, j);
-            }
-            gu_compute<TM>(rg, xs + 256 * j, xss + 16 * j, K, me, ag);
-            gu_compute<TM>(ru, xs + 256 * j, xss + 16 * j, K, me, au);
+        for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+        for (int it = w; it < nit; it += 2 * nw) {
+            const int it1 = it + nw;
+            Qtr<QT> q0, q1;
+            load_qtr<QT>(q0, mat, N, nb, row, it >> 1, p);
+            load_qtr<QT>(q1, mat, N, nb, row, min(it1, nit - 1) >> 1, p);
+            gu_qtr<TM>(q0, it >> 1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+            if (it1 < nit) gu_qtr<TM>(q1, it1 >> 1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
         }
         PG_MARK(1, 4);
+        // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
 #pragma unroll
-        for (int t = 0; t < TM; ++t) {
-            ag[t] = kslot_sum<RB>(ag[t]);
-            au[t] = kslot_sum<RB>(au[t]);
-        }
-        __syncthreads();  // xs is dead: reuse it for the cross-wave partials
-        if (ks == 0) {
+        for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+        if (p == 0) {
 #pragma unroll
             for (int t = 0; t < TM; ++t)
-                if (t < me) {
-                    red[((w * TM + t) * 2 + 0) * RB + r] = ag[t];
-                    red[((w * TM + t) * 2 + 1) * RB + r] = au[t];
-                }
+                if (t < si.count) red[w][t][r] = acc[t];
         }
         __syncthreads();
-        for (int i = tid; i < me * RB; i += W * 64) {
-            const int t = i / RB, rr = i % RB;
+        // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
+        // of a token is a shuffle reduction inside its group
+        const int cnt = si.count, p0 = si.p_begin;
+        if (tid < cnt * RB) {
+            const int t = tid >> 4, rr = tid & 15;
             float g = 0.f, u = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < W; ++ww) {
-                g += red[((ww * TM + t) * 2 + 0) * RB + rr];
-                u += red[((ww * TM + t) * 2 + 1) * RB + rr];
+            for (int ww = 0; ww < nw; ww += 2) {
+                g += red[ww][t][rr];
+                u += red[ww + 1][t][rr];
             }
             const float v = silu(g) * u;
-            act[t * RB + rr] = v;
             const int orow = blockIdx.x * RB + rr;
             if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
-        }
-        if (isum) {
-            __syncthreads();
-            for (int i = tid; i < me * (RB / 16); i += W * 64) {
-                const int t = i / (RB / 16), g16 = i % (RB / 16);
-                const int grow = blockIdx.x * RB + 16 * g16;
-                if (grow < N) {
-                    float sm = 0.f;
-#pragma unroll
-                    for (int k = 0; k < 16; ++k) sm += act[t * RB + 16 * g16 + k];
-                    isum[(int64_t)(p0 + t) * (N >> 4) + (grow >> 4)] = sm;
-                }
+            if (isum) {
+                const float sm = group_sum<16>(v);
+                if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
             }
         }
+        __syncthreads();  // red is rewritten by the next slot
     }
     // block (0, 0) publishes the routing last: its stores then stay off the block's own
     // critical path (a barrier would wait for them)
-    if (MODE == kRoute && blockIdx.x == 0 && a == 0) publish_route(R, dp.M, dp.E, topk, dp.desc, dp.flat);
+    if (pub) publish_route(R, M, dp.E, topk, dp.desc, dp.flat);
     PG_MARK(1, 5);
+}
+
+// Fused down + combine.  Block = 8 output rows for all M tokens; lane = (row r = lane & 7,
+// quarter p = (lane >> 3) & 3, u = lane >> 5); the items (active slot a, super-block j),
+// it = a * (K/256) + j, go two per wave per pass (it = 2w + u, 2w + 2W + u, then + 4W),
+// each lane accumulating w_(t,a) * (inter_(t,a) . d_a,row) per token; a fixed shuffle +
+// LDS tree sums the lanes and waves.  out[t, row] = that sum (+ shared[t, row] *
+// sigmoid(shared_logit[t])).  Inputs: the routing descriptor (P = M*K pairs) and the inter
+// / isum rows in sorted pair order, all staged in LDS at once (the host uses this kernel
+// only when they fit).  The item order depends only on the routing, so results are
+// reproducible run to run.
+// Dynamic LDS: xs [P][K/64][68] f32 | iss [P][K/16] f32.
+template <int QT, int TM>
+__device__ __forceinline__ void dc_item(const Qtr<QT>& q, bool valid, int it, int nb, int p, const float* xs, int xrs,
+                                        const float* iss, int srs, const int* d_pb, const int* d_cnt,
+                                        const int* d_tok, const float* d_w, float* acc) {
+    if (!valid) return;
+    const int a = it / nb, j = it % nb;
+    const int pb = d_pb[a], cnt = min(d_cnt[a], TM);
+    float part[TM];
+#pragma unroll
+    for (int c = 0; c < TM; ++c) part[c] = 0.f;
+    dn_qtr<TM>(q, j, p, xs + pb * xrs, xrs, iss + pb * srs, srs, cnt, part);
+#pragma unroll
+    for (int c = 0; c < TM; ++c) {
+        if (c < cnt) {
+            const int tq = d_tok[pb + c];
+            const float v = d_w[pb + c] * part[c];
+#pragma unroll
+            for (int t = 0; t < TM; ++t)
+                if (t == tq) acc[t] += v;
+        }
+    }
+}
+
+template <int QT, int TM>
+__global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict__ dbase, int64_t dstride, int N,
+                                                      int K, const float* __restrict__ inter,
+                                                      const float* __restrict__ isum, const int32_t* __restrict__ desc,
+                                                      int M, int P, const float* __restrict__ shared,
+                                                      const float* __restrict__ shared_logit,
+                                                      float* __restrict__ out) {
+    constexpr int RB = 8;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int d_pb[128], d_cnt[128], d_tok[128];
+    __shared__ float d_w[128];
+    __shared__ float red[16][TM][RB];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nth = blockDim.x, nw = nth >> 6;
+    const int nb = K >> 8, xrs = (K >> 6) * kXuF, srs = K >> 4;
+    float* xs = (float*)smem;
+    float* iss = xs + P * xrs;
+    const int r = lane & 7, p = (lane >> 3) & 3, u = lane >> 5;
+    const int row = blockIdx.x * RB + r;
+    PG_MARK(3, 0);
+    // 1. the experts of this lane's first two items straight from the descriptor, then
+    //    their weights, then the inter rows and the pair table behind them: the weights'
+    //    latency covers the staging
+    const int S = desc[0] * nb;  // items (active slot a, super-block j), it = a * nb + j
+    int it0 = 2 * w + u, it1 = it0 + 2 * nw;
+    int e0 = desc[kDescSlot + 4 * min(it0 / nb, 127)], e1 = desc[kDescSlot + 4 * min(it1 / nb, 127)];
+    Qtr<QT> q0, q1;
+    load_qtr<QT>(q0, dbase + (int64_t)(it0 < S ? e0 : 0) * dstride, N, nb, row, it0 % nb, p);
+    load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, row, it1 % nb, p);
+    for (int i = tid; i < P; i += nth) {
+        d_pb[i] = desc[kDescSlot + 4 * i + 1];
+        d_cnt[i] = desc[kDescSlot + 4 * i + 2];
+        d_tok[i] = desc[kDescPair + 2 * i];
+        d_w[i] = __builtin_bit_cast(float, desc[kDescPair + 2 * i + 1]);
+    }
+    const int kq = K >> 2;
+    copy_idx<4, u32x4>(
+        P * kq, tid, nth, [=](int i) { return (const u32x4*)(inter + 4 * (int64_t)i); },
+        [=](int i) { return (u32x4*)(xs + (i / kq) * xrs + xpos_f(4 * (i % kq))); });
+    copy_words<2>((u32x4*)iss, (const u32x4*)isum, P * (K >> 6), tid, nth);
+    __syncthreads();
+    PG_MARK(3, 1);
+    // 2. items, two per lane per pass
+    float acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+    for (;;) {
+        dc_item<QT, TM>(q0, it0 < S, it0, nb, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
+        dc_item<QT, TM>(q1, it1 < S, it1, nb, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
+        it0 += 4 * nw;
+        it1 += 4 * nw;
+        if (it0 - u >= S) break;  // wave-uniform (it0 - u is the pass's first item): no item left
+        // (rare) more items than lanes: next pass
+        e0 = desc[kDescSlot + 4 * min(it0 / nb, 127)];
+        e1 = desc[kDescSlot + 4 * min(it1 / nb, 127)];
+        load_qtr<QT>(q0, dbase + (int64_t)(it0 < S ? e0 : 0) * dstride, N, nb, row, it0 % nb, p);
+        load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, row, it1 % nb, p);
+    }
+    PG_MARK(3, 2);
+    // 3. lanes -> rows (lanes r + 8k), waves -> tokens' outputs
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+    if (lane < RB) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) red[w][t][r] = acc[t];
+    }
+    __syncthreads();
+    PG_MARK(3, 3);
+    for (int i = tid; i < M * RB; i += nth) {
+        const int t = i / RB, rr = i % RB;
+        float v = 0.f;
+        for (int ww = 0; ww < nw; ++ww) v += red[ww][t][rr];
+        const int orow = blockIdx.x * RB + rr;
+        if (orow < N) {
+            if (shared) {
+                const float g = shared_logit ? 1.0f / (1.0f + expf(-shared_logit[t])) : 1.0f;
+                v += shared[(int64_t)t * N + orow] * g;
+            }
+            out[(int64_t)t * N + orow] = v;
+        }
+    }
+    PG_MARK(3, 4);
 }
 
 // Per-expert down GEMV: partial[p, row] = w[perm[p]] * (inter_p . d_row) for the pairs of
@@ -908,124 +1156,10 @@ __global__ __launch_bounds__(W * 64) void dec_down_kernel(const uint8_t* __restr
     }
 }
 
-// Fused down + combine.  Block = RB output rows for all M tokens; its W waves x KS lane
-// groups walk the slices (active slot a, super-block j), slice s = ks + KS*w + KS*W*i, each
-// lane accumulating w_(t,a) * (inter_(t,a) . d_a,row(j)) per token, with the next slice's
-// weights loaded before the current one is computed; a fixed shuffle + LDS tree sums the
-// slices.  out[t, row] = that sum (+ shared[t, row] * sigmoid(shared_logit[t])).
-// Inputs: the routing descriptor (P = M*K pairs), inter / isum rows in sorted pair order,
-// all P rows staged in LDS together with the descriptor (the host uses this kernel only
-// when P*K*4 + P*K/16*4 fits).  The slice order depends only on the routing, so results
-// are reproducible run to run.
-// Dynamic LDS: xs [P][K] f32 | iss [P][K/16] f32.
-template <int QT, int RB, int W, int TM>
-__global__ __launch_bounds__(W * 64) void dec_down_combine_kernel(
-    const uint8_t* __restrict__ dbase, int64_t dstride, int N, int K, const float* __restrict__ inter,
-    const float* __restrict__ isum, const int32_t* __restrict__ desc, int M, int P, const float* __restrict__ shared,
-    const float* __restrict__ shared_logit, float* __restrict__ out) {
-    constexpr int KS = 64 / RB;
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int d_slot[128 * 3];
-    __shared__ int d_tok[128];
-    __shared__ float d_w[128];
-    __shared__ float red[W][TM][RB];
-    __shared__ int s_nact;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    float* xs = (float*)smem;
-    float* iss = xs + P * K;
-    PG_MARK(3, 0);
-    {
-        int v[5] = {0, 0, 0, 0, 0};
-        const bool has = tid < P;
-        if (has) {
-            v[0] = desc[kDescSlot + 4 * tid];
-            v[1] = desc[kDescSlot + 4 * tid + 1];
-            v[2] = desc[kDescSlot + 4 * tid + 2];
-            v[3] = desc[kDescPair + 2 * tid];
-            v[4] = desc[kDescPair + 2 * tid + 1];
-        }
-        const int n0 = tid == 0 ? desc[0] : 0;
-        copy_words<8>((uint4*)xs, (const uint4*)inter, P * (K >> 2), tid, W * 64);
-        copy_words<4>((uint4*)iss, (const uint4*)isum, P * (K >> 6), tid, W * 64);
-        if (has) {
-            d_slot[3 * tid] = v[0];
-            d_slot[3 * tid + 1] = v[1];
-            d_slot[3 * tid + 2] = v[2];
-            d_tok[tid] = v[3];
-            d_w[tid] = __builtin_bit_cast(float, v[4]);
-        }
-        if (tid == 0) s_nact = n0;
-    }
-    __syncthreads();
-    PG_MARK(3, 1);
-    const int nact = s_nact;
-    const int r = lane % RB, ks = lane / RB;
-    const int row = blockIdx.x * RB + r;
-    const int nb = K >> 8;
-    const int S = nact * nb;
-    float acc[TM];
-#pragma unroll
-    for (int t = 0; t < TM; ++t) acc[t] = 0.f;
-    int s = ks + KS * w;
-    Raw<QT> rw;
-    if (s < S) load_raw<QT>(rw, dbase + (int64_t)d_slot[3 * (s / nb)] * dstride, N, nb, row, s % nb);
-    while (s < S) {
-        const int sn = s + KS * W;
-        Raw<QT> rn;
-        if (sn < S) load_raw<QT>(rn, dbase + (int64_t)d_slot[3 * (sn / nb)] * dstride, N, nb, row, sn % nb);
-        const int a = s / nb, j = s % nb;
-        const int p0 = d_slot[3 * a + 1], cnt = d_slot[3 * a + 2];
-        float part[TM];
-#pragma unroll
-        for (int t = 0; t < TM; ++t) part[t] = 0.f;
-        dn_compute<TM>(rw, xs + p0 * K + 256 * j, iss + p0 * (K >> 4) + 16 * j, K, cnt, part);
-#pragma unroll
-        for (int q = 0; q < TM; ++q) {
-            if (q < cnt) {
-                const int tq = d_tok[p0 + q];
-                const float v = d_w[p0 + q] * part[q];
-#pragma unroll
-                for (int t = 0; t < TM; ++t)
-                    if (t == tq) acc[t] += v;
-            }
-        }
-        rw = rn;
-        s = sn;
-        PG_MARK(3, 2);
-    }
-    PG_MARK(3, 3);
-#pragma unroll
-    for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
-    if (ks == 0) {
-#pragma unroll
-        for (int t = 0; t < TM; ++t) red[w][t][r] = acc[t];
-    }
-    __syncthreads();
-    for (int i = tid; i < M * RB; i += W * 64) {
-        const int t = i / RB, rr = i % RB;
-        float v = 0.f;
-#pragma unroll
-        for (int ww = 0; ww < W; ++ww) v += red[ww][t][rr];
-        const int orow = blockIdx.x * RB + rr;
-        if (orow < N) {
-            if (shared) {
-                const float g = shared_logit ? 1.0f / (1.0f + expf(-shared_logit[t])) : 1.0f;
-                v += shared[(int64_t)t * N + orow] * g;
-            }
-            out[(int64_t)t * N + orow] = v;
-        }
-    }
-    PG_MARK(3, 4);
-}
-
-// LDS bytes the fused down + combine kernel stages (all P inter rows and their sums).
-inline size_t dc_stage_bytes(int P, int K) { return (size_t)P * K * 4 + (size_t)P * (K / 16) * 4; }
-constexpr size_t kDcStageMax = 52 * 1024;
-
 // ============================================================================ launch plumbing
-// Block shapes (rows per block RB, waves W <= 4 so every wave may use up to 512 VGPRs):
-// one super-block per lane when nb equals KS * W for one of them, else (16, 4) with a
-// K loop.
+// Per-expert down (stage API / shared expert): block shapes (rows per block RB, waves
+// W <= 4 so every wave may use up to 512 VGPRs): one super-block per lane when nb equals
+// KS * W for one of them, else (16, 4) with a K loop.
 struct DecShape {
     int RB, W;
 };
@@ -1037,14 +1171,6 @@ inline DecShape pick_shape(int nb) {
     return {16, 4};
 }
 
-// Token tile: the smallest power of two >= M (max 8), halved while the gate/up LDS stage
-// (TM fp16 rows of K plus their 16-element sums) would exceed 60 KB.
-inline int tile_tokens(int M, int K) {
-    int t = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-    while (t > 1 && (size_t)t * K * 2 + (size_t)t * (K / 16) * 4 > 60 * 1024) t >>= 1;
-    return t;
-}
-
 // Down: per K step, t rows of JW super-blocks staged as fp32 (1088 bytes a super-block
 // with its sums) plus the [W][t][RB] partials; t halves while that exceeds 60 KB.
 inline size_t down_lds_bytes(int t, int RB, int W) { return (size_t)t * (64 / RB) * W * 1088 + (size_t)W * t * RB * 4; }
@@ -1054,16 +1180,36 @@ inline int down_tile_tokens(int M, const DecShape& sp) {
     return t;
 }
 
-template <int QT, int RB, int W, int TM>
+// Token bound of the routed kernels: the smallest of 1, 2, 4, 8 that is >= M.
+inline int tm_bucket(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
+
+// Gate/up: waves = K/256 rounded up to even (at most two items per wave up to 16
+// super-blocks), 2..16.
+inline int gu_waves(int nb) {
+    const int w = nb + (nb & 1);
+    return w < 2 ? 2 : w > 16 ? 16 : w;
+}
+inline size_t gu_lds_bytes(int M, int K) { return (size_t)M * (K / 64) * kXuH * 2 + (size_t)M * (K / 16) * 4; }
+// Gate/up grid rows: active slots per block column, at most 16 (blocks then take several
+// slots, routing and staging the tokens once).
+inline int gu_slot_blocks(int max_active) { return max_active < 16 ? max_active : 16; }
+// Fused down + combine: two items per wave per pass, so (items + 1) / 2 waves up to 16.
+inline int dc_waves(int items) {
+    const int w = (items + 1) / 2;
+    return w < 1 ? 1 : w > 16 ? 16 : w;
+}
+inline size_t dc_lds_bytes(int P, int K) { return (size_t)P * (K / 64) * kXuF * 4 + (size_t)P * (K / 16) * 4; }
+
+// Dynamic LDS a block of the current device may take beside the kernels' static arrays.
+size_t dec_lds_limit();
+
+template <int QT, int TM>
 inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, const DecDisp& dp,
                       int max_active, float* inter, float* isum, hipStream_t st) {
-    const size_t stage = (size_t)TM * g.K * 2 + (size_t)TM * (g.K / 16) * 4;
-    const size_t tail = (size_t)W * TM * 2 * RB * 4 + (size_t)TM * RB * 4;
-    const size_t logits = dp.mode == kRoute ? (size_t)dp.M * dp.E * 4 : 0;
-    size_t sh = stage > tail ? stage : tail;
-    sh = sh > logits ? sh : logits;
-    PG_LAUNCH((dec_gateup_kernel<QT, RB, W, TM>), dim3(div_up(g.N, RB), max_active), dim3(64 * W), sh,
-                       st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, inter, isum);
+    const int W = gu_waves(g.K >> 8);
+    PG_LAUNCH((dec_gu_kernel<QT, TM>), dim3(div_up(g.N, 16), gu_slot_blocks(max_active)), dim3(64 * W),
+              gu_lds_bytes(dp.M, g.K), st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp,
+              inter, isum);
 }
 
 template <int QT, int RB, int W, int TM>
@@ -1074,12 +1220,12 @@ inline void dn_launch(const Mats& d, const float* inter, const float* isum, cons
                        st, d.base, d.stride, d.N, d.K, inter, isum, dp, topk_w, partial);
 }
 
-template <int QT, int RB, int W, int TM>
+template <int QT, int TM>
 inline void dc_launch(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
-                      const float* shared, const float* shared_logit, float* out, hipStream_t st) {
-    PG_LAUNCH((dec_down_combine_kernel<QT, RB, W, TM>), dim3(div_up(d.N, RB)), dim3(64 * W),
-                       dc_stage_bytes(P, d.K), st, d.base,
-                       d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out);
+                      int max_active, const float* shared, const float* shared_logit, float* out, hipStream_t st) {
+    const int W = dc_waves(max_active * (d.K >> 8));
+    PG_LAUNCH((dec_dc_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, d.K), st, d.base,
+              d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out);
 }
 
 #define PG_TM(F, QT, RB, W, ...)                   \
@@ -1090,7 +1236,15 @@ inline void dc_launch(const Mats& d, const float* inter, const float* isum, cons
     default: F<QT, RB, W, 8>(__VA_ARGS__); break; \
     }
 
-// Block shapes for the per-expert kernels: the shapes pick_shape returns.
+#define PG_TM2(F, QT, ...)                   \
+    switch (tm_bucket(M)) {                  \
+    case 1: F<QT, 1>(__VA_ARGS__); break;    \
+    case 2: F<QT, 2>(__VA_ARGS__); break;    \
+    case 4: F<QT, 4>(__VA_ARGS__); break;    \
+    default: F<QT, 8>(__VA_ARGS__); break;   \
+    }
+
+// Block shapes for the per-expert down kernel: the shapes pick_shape returns.
 #define PG_SHAPES(F, QT, ...)                                  \
     switch (sp.RB * 16 + sp.W) {                               \
     case 16 * 16 + 1: PG_TM(F, QT, 16, 1, __VA_ARGS__); break; \
@@ -1101,34 +1255,9 @@ inline void dc_launch(const Mats& d, const float* inter, const float* isum, cons
     default: PG_TM(F, QT, 16, 4, __VA_ARGS__); break;          \
     }
 
-// Fused down + combine: rows per block and waves chosen so the grid has >= 256 blocks
-// where the output allows it and each lane walks few slices.
-struct DcShape {
-    int RB, W;
-};
-inline DcShape pick_dc_shape(int N, int slices) {
-    const int rb = N >= 256 * 16 ? 16 : 8;
-    const int ks = 64 / rb;
-    int w = (slices + ks - 1) / ks;
-    w = w < 1 ? 1 : w > 4 ? 4 : w;
-    return {rb, w};
-}
-
-#define PG_DC_SHAPES(QT, ...)                                    \
-    switch (dsp.RB * 16 + dsp.W) {                               \
-    case 8 * 16 + 1: PG_TM(dc_launch, QT, 8, 1, __VA_ARGS__); break;  \
-    case 8 * 16 + 2: PG_TM(dc_launch, QT, 8, 2, __VA_ARGS__); break;  \
-    case 8 * 16 + 3: PG_TM(dc_launch, QT, 8, 3, __VA_ARGS__); break;  \
-    case 8 * 16 + 4: PG_TM(dc_launch, QT, 8, 4, __VA_ARGS__); break;  \
-    case 16 * 16 + 1: PG_TM(dc_launch, QT, 16, 1, __VA_ARGS__); break; \
-    case 16 * 16 + 2: PG_TM(dc_launch, QT, 16, 2, __VA_ARGS__); break; \
-    case 16 * 16 + 3: PG_TM(dc_launch, QT, 16, 3, __VA_ARGS__); break; \
-    default: PG_TM(dc_launch, QT, 16, 4, __VA_ARGS__); break;          \
-    }
-
-// Per-qtype launchers (defined in decode_q4k.hip / decode_q6k.hip / decode_q8_0.hip).
+// Per-qtype launchers (instantiated by decode_inst.hip, one object per format and stage).
 template <int QT>
-int dec_gateup_q(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M, int mode,
+int dec_gateup_q(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
                  const DecDisp& dp, int max_active, float* inter, float* isum, hipStream_t st);
 template <int QT>
 int dec_down_q(const Mats& d, const float* inter, const float* isum, int M, int mode, const DecDisp& dp,
@@ -1140,12 +1269,11 @@ int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, con
 #define PG_DEFINE_DECODE_GATEUP(QT)                                                                                  \
     template <>                                                                                                     \
     int dec_gateup_q<QT>(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,      \
-                         int mode, const DecDisp& dp, int max_active, float* inter, float* isum, hipStream_t st) {  \
-        const DecShape sp = pick_shape(g.K >> 8);                                                                   \
-        const int TM = tile_tokens(M, g.K);                                                                         \
-        if ((size_t)TM * g.K * 2 + (size_t)TM * (g.K / 16) * 4 > 64 * 1024)                                        \
-            return fail(PGMOE_E_UNSUPPORTED, "decode gate/up: %d inputs exceed the LDS stage", g.K);                \
-        PG_SHAPES(gu_launch, QT, g, u, x, xsum, topk, dp, max_active, inter, isum, st);                  \
+                         const DecDisp& dp, int max_active, float* inter, float* isum, hipStream_t st) {            \
+        if (M < 1 || M > kDecTM) return fail(PGMOE_E_UNSUPPORTED, "decode gate/up: 1..%d tokens (got %d)", kDecTM, M); \
+        if (gu_lds_bytes(M, g.K) > dec_lds_limit())                                           \
+            return fail(PGMOE_E_UNSUPPORTED, "decode gate/up: %d tokens of %d inputs exceed LDS", M, g.K);          \
+        PG_TM2(gu_launch, QT, g, u, x, xsum, topk, dp, max_active, inter, isum, st);                                 \
         return check_launch("dec_gateup");                                                                          \
     }
 
@@ -1164,11 +1292,9 @@ int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, con
     int dec_down_combine_q<QT>(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M,   \
                                int P, int max_active, const float* shared, const float* shared_logit, float* out,   \
                                hipStream_t st) {                                                                    \
-        const DcShape dsp = pick_dc_shape(d.N, max_active * (d.K >> 8));                                            \
-        const int TM = tile_tokens(M, 0);                                                                           \
-        if (dc_stage_bytes(P, d.K) > kDcStageMax)                                                                   \
+        if (P > 128 || dc_lds_bytes(P, d.K) > dec_lds_limit())                                                      \
             return fail(PGMOE_E_UNSUPPORTED, "decode down + combine: %d pairs of %d inputs exceed LDS", P, d.K);    \
-        PG_DC_SHAPES(QT, d, inter, isum, desc, M, P, shared, shared_logit, out, st);                                 \
+        PG_TM2(dc_launch, QT, d, inter, isum, desc, M, P, max_active, shared, shared_logit, out, st);               \
         return check_launch("dec_down_combine");                                                                    \
     }
 

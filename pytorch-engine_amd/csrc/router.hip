@@ -264,17 +264,23 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
 int launch_router_logits(const uint16_t* x, const float* W, const float* bias, int M, int H, int E,
                          float* logits, hipStream_t st, const float* extra_w, float* extra_out, float* xsum) {
     if (M <= 0) return PGMOE_OK;
-    const int threads = 256;
     const int rows = E + (extra_w ? 1 : 0);
+    // decode (M <= 8): one single-wave block per (all tokens, one expert), so the router
+    // read spreads over as many CUs as there are experts; prefill: 4-wave blocks
+    const int threads = M <= 8 ? 64 : 256;
     const int xblocks = xsum ? div_up(M * (H >> 4), threads) : 0;
 #define PG_ROUTER(TM_, TE_)                                                                                   \
     do {                                                                                                      \
-        const int rb = div_up(div_up(M, TM_) * div_up(rows, TE_), 4);                                        \
+        const int rb = div_up(div_up(M, TM_) * div_up(rows, TE_), threads >> 6);                             \
         PG_LAUNCH((router_logits_kernel<TM_, TE_>), dim3(rb + xblocks), dim3(threads), 0, st, x, W, bias, \
                            M, H, E, logits, extra_w, extra_out, xsum, rb);                                    \
     } while (0)
-    if (M <= 4)
-        PG_ROUTER(4, 1);  // decode: one wave per (all tokens, one expert) spreads the router read widely
+    if (M == 1)
+        PG_ROUTER(1, 1);
+    else if (M == 2)
+        PG_ROUTER(2, 1);
+    else if (M <= 4)
+        PG_ROUTER(4, 1);
     else if (M <= 8)
         PG_ROUTER(8, 1);
     else if (!extra_w && !xsum && E >= 16 && H % kRgH == 0) {

@@ -111,12 +111,12 @@ def test_qwen3_prefill_zipf():
     assert (counts == 0).sum() > 0 and counts.max() > 500
 
 
-@pytest.mark.parametrize("M", [1, 2048])
+@pytest.mark.parametrize("M", [1, 8, 2048])
 def test_mixtral(M):
     _run("mixtral_8x7b", M, 6)
 
 
-@pytest.mark.parametrize("M", [1, 512])
+@pytest.mark.parametrize("M", [1, 8, 512])
 def test_qwen2_shared_expert(M):
     _run("qwen2_57b_a14b", M, 6)
 
