@@ -79,6 +79,19 @@ __device__ __forceinline__ float scatter_sum64(float (&v)[N], int lane) {
     return v[0];
 }
 
+// K-quant 6-bit (scale, min) of sub-block s from the 12 scale bytes (words D, Mb, MD).
+__device__ __forceinline__ void kscale(uint32_t D, uint32_t Mb, uint32_t MD, int s, int& sc, int& mn) {
+    if (s < 4) {
+        sc = (D >> (8 * s)) & 63;
+        mn = (Mb >> (8 * s)) & 63;
+    } else {
+        const int j = s - 4;
+        const uint32_t md = (MD >> (8 * j)) & 0xff;
+        sc = (md & 0x0f) | (((D >> (8 * j)) >> 2) & 0x30);
+        mn = (md >> 4) | (((Mb >> (8 * j)) >> 2) & 0x30);
+    }
+}
+
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
 // Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes at g land at

@@ -39,19 +39,6 @@ __device__ __forceinline__ uint32_t magic2(uint32_t v, uint32_t sel) {
 
 __device__ __forceinline__ uint32_t ld32(const uint16_t* p) { return *(const uint32_t*)p; }
 
-// K-quant 6-bit (scale, min) of sub-block s from the 12 scale bytes (words D, Mb, MD).
-__device__ __forceinline__ void kscale(uint32_t D, uint32_t Mb, uint32_t MD, int s, int& sc, int& mn) {
-    if (s < 4) {
-        sc = (D >> (8 * s)) & 63;
-        mn = (Mb >> (8 * s)) & 63;
-    } else {
-        const int j = s - 4;
-        const uint32_t md = (MD >> (8 * j)) & 0xff;
-        sc = (md & 0x0f) | (((D >> (8 * j)) >> 2) & 0x30);
-        mn = (md >> 4) | (((Mb >> (8 * j)) >> 2) & 0x30);
-    }
-}
-
 // Q6_K 6-bit codes (0..63) of elements 128h + 32s + 4k + 0..3, one per byte.
 __device__ __forceinline__ uint32_t q6_word(uint32_t qlA, uint32_t qlB, uint32_t qh, int s) {
     const uint32_t lo = (s & 1 ? qlB : qlA) >> (4 * (s >> 1));

@@ -3,10 +3,12 @@
 // A tile is 256 sorted pairs of one expert x 256 output columns.  The block is 8 waves
 // (two per SIMD), each owning 128 rows x 64 columns as 4 x 2 v_mfma_f32_32x32x16_f16
 // tiles (128 fp32 accumulators per lane).  The K loop steps one 64-weight unit at a
-// time through two LDS stages: while the MFMAs read unit u from one stage, the block
-// writes unit u + 1 into the other (fp16 activations, and weights dequantised as
-// w = a*q - b in fp32 with one rounding to fp16), and the raw bytes of unit u + 2 are
-// already on their way into a second register set.  One barrier per unit.
+// time through a ring of three LDS stages filled by direct HBM -> LDS copies two units
+// ahead: the fp16 activation rows (16-byte slots XOR-swizzled by row) and the raw GGUF
+// bytes of the 256 weight rows (whole 1 KB chunks of the 64-row tile layout, with their
+// scale chunks).  Each wave decodes its own B fragments from the raw bytes in registers
+// (w = a * code + c in fp32, one rounding to fp16) one k16 group ahead of the MFMAs
+// that use them.  One barrier per unit.
 //   gate/up: A = x rows gathered through perm (fp16), B = 128 gate rows + 128 up rows of
 //            the same intermediate indices, arranged so every wave holds matching gate
 //            and up columns; epilogue = SwiGLU in fp32 -> inter [P][I].
@@ -25,125 +27,207 @@ namespace pgmoe {
 
 constexpr int kGM = 256;      // pair rows per tile
 constexpr int kGN = 256;      // B rows (output columns) per tile
-constexpr int kGP = 64 + 8;   // LDS pitch in halves (16-byte pad against bank conflicts)
-constexpr int kGThreads = 512;
 constexpr int kXcd = 8;
 
 typedef _Float16 gh8 __attribute__((ext_vector_type(8)));
 typedef uint32_t gu4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float gf16 __attribute__((ext_vector_type(16)));
 
-// ---------------------------------------------------------------- raw weight half rows
-// Groups h and h + 2 (h = 0 or 1) of one row in one 64-weight unit (see Fmt<QT>): the
-// groups that share their quant bytes (Q4_K: one qs chunk, low / high nibbles; Q6_K: one
-// ql chunk, low / high nibbles, plus the qh chunk; Q8_0: two chunks).  Loaded a step ahead,
-// decoded to 2 x 16 fp16 values with Fmt<QT>::group's arithmetic (fp32 math, one rounding).
-template <int QT> struct GHalf;
-template <> struct GHalf<PGMOE_Q4_K> { uint4 hdr, q; };
-template <> struct GHalf<PGMOE_Q6_K> { uint4 lo, hi; uint2 scw; uint32_t db; };
-template <> struct GHalf<PGMOE_Q8_0> { uint4 q0, q1; uint32_t dw; };
-
-template <int QT>
-__device__ __forceinline__ void gload(const uint8_t* mat, int nb, int N, int row, int u, int h, GHalf<QT>& r);
-
-template <>
-__device__ __forceinline__ void gload<PGMOE_Q4_K>(const uint8_t* mat, int nb, int N, int row, int u, int h,
-                                                   GHalf<PGMOE_Q4_K>& r) {
-    const uint8_t* t = tile_ptr<PGMOE_Q4_K>(mat, nb, row >> 6, u >> 2) + (row & 63) * 16;
-    r.hdr = *(const uint4*)t;
-    r.q = *(const uint4*)(t + (1 + 2 * (u & 3) + h) * 1024);
-}
-
-template <>
-__device__ __forceinline__ void gload<PGMOE_Q6_K>(const uint8_t* mat, int nb, int N, int row, int u, int h,
-                                                   GHalf<PGMOE_Q6_K>& r) {
-    const int rg = row >> 6, rr = row & 63, blk = u >> 2, h6 = (u & 3) >> 1, half = u & 1;
-    const uint8_t* t = tile_ptr<PGMOE_Q6_K>(mat, nb, rg, blk) + rr * 16;
-    r.lo = *(const uint4*)(t + (4 * h6 + 2 * h + half) * 1024);  // ql[64h6 + 32h + 16half ..]
-    r.hi = *(const uint4*)(t + (8 + 2 * h6 + half) * 1024);      // qh[32h6 + 16half ..]
-    r.scw = *(const uint2*)(t + 12 * 1024 + 8 * h6);             // scales 8h6 .. 8h6+7
-    const int64_t dplane = (int64_t)row_groups(N) * nb * 13 * 1024;
-    r.db = *(const uint16_t*)(mat + dplane + (((int64_t)rg * nb + blk) * 64 + rr) * 2);
-}
-
-template <>
-__device__ __forceinline__ void gload<PGMOE_Q8_0>(const uint8_t* mat, int nb, int N, int row, int u, int h,
-                                                   GHalf<PGMOE_Q8_0>& r) {
-    const uint8_t* t = tile_ptr<PGMOE_Q8_0>(mat, nb, row >> 6, u >> 2) + (row & 63) * 16;
-    r.q0 = *(const uint4*)(t + (4 * (u & 3) + h) * 1024);
-    r.q1 = *(const uint4*)(t + (4 * (u & 3) + h + 2) * 1024);
-    r.dw = *(const uint32_t*)(t + 16 * 1024 + 4 * (u & 3));
-}
-
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
-}
-
-// 4 bytes of codes v (one code per byte) -> w = a*code + nb as two fp16 pairs
-__device__ __forceinline__ void dq4(uint32_t v, float a, float nb, uint32_t* o) {
-    o[0] = pack_h2(__builtin_fmaf(a, (float)(v & 0xff), nb), __builtin_fmaf(a, (float)((v >> 8) & 0xff), nb));
-    o[1] = pack_h2(__builtin_fmaf(a, (float)((v >> 16) & 0xff), nb), __builtin_fmaf(a, (float)(v >> 24), nb));
-}
-
-// Group g = h + 2*gg (gg = 0 or 1) of the half row -> 8 packed fp16 pairs.
-template <int QT>
-__device__ __forceinline__ void gdecode(const GHalf<QT>& r, int u, int h, int gg, uint32_t out[8]);
-
-template <>
-__device__ __forceinline__ void gdecode<PGMOE_Q4_K>(const GHalf<PGMOE_Q4_K>& r, int u, int h, int gg,
-                                                     uint32_t out[8]) {
-    const int s = 2 * (u & 3) + gg;  // group h + 2gg: sub-block 2(u%4) + gg, nibble gg
-    const uint32_t D = r.hdr.y, Mb = r.hdr.z, MD = r.hdr.w;
-    int sc, mn;
-    if (s < 4) {
-        sc = (D >> (8 * s)) & 63;
-        mn = (Mb >> (8 * s)) & 63;
-    } else {
-        const int j = s - 4;
-        const uint32_t md = (MD >> (8 * j)) & 0xff;
-        sc = (md & 0x0f) | (((D >> (8 * j)) >> 2) & 0x30);
-        mn = (md >> 4) | (((Mb >> (8 * j)) >> 2) & 0x30);
+// ---------------------------------------------------------------- staged weight bytes
+// Per 64-weight unit u (see Fmt<QT>) a tile stages, for each of its four 64-row groups,
+// CH chunks of quant bytes plus the row's scale chunk (whole 1 KB tile chunks, straight
+// from the tile layout); Q6_K also stages the fp16 d of the 256 rows.
+//   Q4_K: qs chunks 1 + 2c, 2 + 2c (c = u % 4); scales: chunk 0 (d, dmin, 12 scale bytes)
+//   Q6_K: ql chunks 4h + half, 4h + 2 + half, qh chunk 8 + 2h + half ((h, half) =
+//         ((u % 4) >> 1, u & 1)); scales: chunk 12; d: 4 x 128 bytes
+//   Q8_0: chunks 4c .. 4c + 3 (the qs of Q8_0 blocks 2c, 2c + 1); scales: chunk 16
+// Group g of the unit (k = 16g .. 16g + 15) reads, for the 8 weights 8h .. 8h + 7 of a lane
+// half h, bytes 8h .. 8h + 7 of one staged chunk:
+//   Q4_K: chunk g & 1, nibble g >> 1;  Q6_K: ql chunk g & 1 (nibble g >> 1) and the qh
+//   chunk (bits 2g, 2g + 1);  Q8_0: chunk g.
+template <int QT> struct GStage;
+template <> struct GStage<PGMOE_Q4_K> {
+    static constexpr int CH = 2, HC = 0, DPL = 0;
+    __device__ static __forceinline__ int chunk(int u, int cc) { return 1 + 2 * (u & 3) + cc; }
+};
+template <> struct GStage<PGMOE_Q6_K> {
+    static constexpr int CH = 3, HC = 12, DPL = 1;
+    __device__ static __forceinline__ int chunk(int u, int cc) {
+        const int h = (u & 3) >> 1, half = u & 1;
+        return cc == 0 ? 4 * h + half : cc == 1 ? 4 * h + 2 + half : 8 + 2 * h + half;
     }
-    const float a = lo_half(r.hdr.x) * (float)sc;
-    const float nb = -(hi_half(r.hdr.x) * (float)mn);
-    const int sh = 4 * gg;
-    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) dq4((w[k] >> sh) & 0x0f0f0f0fu, a, nb, out + 2 * k);
+};
+template <> struct GStage<PGMOE_Q8_0> {
+    static constexpr int CH = 4, HC = 16, DPL = 0;
+    __device__ static __forceinline__ int chunk(int u, int cc) { return 4 * (u & 3) + cc; }
+};
+
+// LDS stage: A [256 rows][128 bytes] (16-byte slot s of row r holds k chunk s ^ (r & 7)),
+// then B: row group bg, chunk cc (cc = CH: scales) at kGA + (bg * (CH + 1) + cc) * 1024,
+// Q6_K d of row group bg at kGA + 4 * (CH + 1) * 1024 + 128 bg.
+constexpr int kGA = kGM * 128;
+// CT = 32-column B tiles per wave: the block's 256 x 256 tile is cut into 2 x (8 / CT)
+// wave tiles of 128 rows x 32 CT columns (CT = 2: 8 waves, two per SIMD; CT = 4: 4 waves,
+// accumulators in AGPRs).
+template <int QT, int CT>
+struct GLay {
+    static constexpr int CH = GStage<QT>::CH;
+    static constexpr int NW = 16 / CT;                              // waves
+    static constexpr int SLOTS = 4 * (CH + 1) + GStage<QT>::DPL;  // 1 KB copies for B
+    static constexpr int AQ = 32 / NW;                              // A copies per wave
+    static constexpr int BQ = (SLOTS + NW - 1) / NW;                // B copies per wave
+    static constexpr int STAGE = kGA + SLOTS * 1024;
+    static constexpr int VM = AQ + BQ;                              // copies per wave per unit
+};
+
+// HBM -> LDS copy of 16 bytes per lane (lane l to lds + 16 l), written as inline asm so
+// the compiler neither adds waits for it before unrelated LDS reads nor counts it in its
+// own vmcnt bookkeeping; the kernel waits for the copies itself (vm_wait) before the
+// barrier that publishes a stage.  lds is the wave-uniform LDS byte address.
+__device__ __forceinline__ void g2l(const void* g, uint32_t lds) {
+    uint32_t keep;  // m0 is reserved to the compiler: restore it around the copy
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "v"(g), "s"(lds)
+                 : "memory");
+}
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-template <>
-__device__ __forceinline__ void gdecode<PGMOE_Q6_K>(const GHalf<PGMOE_Q6_K>& r, int u, int h, int gg,
-                                                     uint32_t out[8]) {
-    const int g = h + 2 * gg, half = u & 1;
-    const int sb = 2 * g + half;  // scale byte within the 8 loaded (8h6 + sb)
-    const uint32_t sw = sb < 4 ? r.scw.x : r.scw.y;
-    const int sc = (int)(int8_t)((sw >> (8 * (sb & 3))) & 0xff);
-    const float a = h2f((uint16_t)r.db) * (float)sc;
-    const float nb = -32.0f * a;
-    const int lsh = 4 * gg, hsh = 2 * g;
-    const uint32_t lw[4] = {r.lo.x, r.lo.y, r.lo.z, r.lo.w};
-    const uint32_t hw[4] = {r.hi.x, r.hi.y, r.hi.z, r.hi.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-        dq4(((lw[k] >> lsh) & 0x0f0f0f0fu) | (((hw[k] >> hsh) & 0x03030303u) << 4), a, nb, out + 2 * k);
-}
+typedef _Float16 gh2 __attribute__((ext_vector_type(2)));
 
-template <>
-__device__ __forceinline__ void gdecode<PGMOE_Q8_0>(const GHalf<PGMOE_Q8_0>& r, int u, int h, int gg,
-                                                     uint32_t out[8]) {
-    const int g = h + 2 * gg;
-    const float a = (g < 2) ? lo_half(r.dw) : hi_half(r.dw);
-    const uint4 qv = gg ? r.q1 : r.q0;
-    const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
+// w = a * code + c2 as fp16 for 8 codes given as fp16 (1024 + code) pairs (c2 = c - 1024a
+// folded by the caller: one fp32 FMA per weight, one rounding to fp16).
+__device__ __forceinline__ gh8 deq8(const uint32_t (&m)[4], float a, float c) {
+    gh8 r;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const uint32_t v = w[k];
-        out[2 * k] = pack_h2(a * (float)(int8_t)(v & 0xff), a * (float)(int8_t)((v >> 8) & 0xff));
-        out[2 * k + 1] = pack_h2(a * (float)(int8_t)((v >> 16) & 0xff), a * (float)(int8_t)(v >> 24));
+        const gh2 h = __builtin_bit_cast(gh2, m[k]);
+        r[2 * k] = (_Float16)__builtin_fmaf((float)h.x, a, c);
+        r[2 * k + 1] = (_Float16)__builtin_fmaf((float)h.y, a, c);
     }
+    return r;
 }
+
+// SiLU with the hardware exp2 and reciprocal (about 1 ulp each; the MFMA path's inputs
+// are fp16 already).
+__device__ __forceinline__ float silu_fast(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
+}
+
+__device__ __forceinline__ void magic8(uint32_t lo, uint32_t hi, uint32_t (&m)[4]) {
+    m[0] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
+    m[1] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u);
+    m[2] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u);
+    m[3] = __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u);
+}
+
+// One B column (row of W) of one unit in a lane: its staged bytes and scales, decoded per
+// group into the MFMA B operand (8 fp16 weights k = 16g + 8h .. +8).
+template <int QT> struct GCol;
+
+// K-quant (scale, min) of sub-block s (uniform) without branches: both encodings are
+// decoded and s picks one.
+__device__ __forceinline__ void kscale_sel(uint32_t D, uint32_t Mb, uint32_t MD, int s, int& sc, int& mn) {
+    const int j = 8 * (s & 3);
+    const int sl = (D >> j) & 63, ml = (Mb >> j) & 63;
+    const uint32_t md = (MD >> j) & 0xff;
+    const int sh = (md & 0x0f) | ((D >> (j + 2)) & 0x30), mh = (md >> 4) | ((Mb >> (j + 2)) & 0x30);
+    sc = s < 4 ? sl : sh;
+    mn = s < 4 ? ml : mh;
+}
+
+template <> struct GCol<PGMOE_Q4_K> {
+    u32x2 q[2];
+    u32x4 hd;
+    float a[2], c[2];  // sub-blocks 2(u%4) (groups 0, 1), 2(u%4) + 1 (groups 2, 3)
+    __device__ __forceinline__ void fetch(const uint8_t* B, int bg, int rig, int h, int u) {
+        const uint8_t* base = B + bg * 3 * 1024 + rig * 16;
+        q[0] = *(const u32x2*)(base + 8 * h);
+        q[1] = *(const u32x2*)(base + 1024 + 8 * h);
+        hd = *(const u32x4*)(base + 2 * 1024);
+    }
+    __device__ __forceinline__ void prep(int u) {
+        const float d = lo_half(hd.x), dm = hi_half(hd.x);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            int sc, mn;
+            kscale_sel(hd.y, hd.z, hd.w, 2 * (u & 3) + t, sc, mn);
+            a[t] = d * (float)sc;
+            c[t] = -(dm * (float)mn) - 1024.0f * a[t];
+        }
+    }
+    __device__ __forceinline__ gh8 group(int g) const {
+        const u32x2 s = q[g & 1];
+        const int sh = 4 * (g >> 1);
+        uint32_t m[4];
+        magic8((s.x >> sh) & 0x0f0f0f0fu, (s.y >> sh) & 0x0f0f0f0fu, m);
+        return deq8(m, a[g >> 1], c[g >> 1]);
+    }
+};
+
+template <> struct GCol<PGMOE_Q6_K> {
+    u32x2 q[3], sw;
+    uint16_t db;
+    float a[4];
+    __device__ __forceinline__ void fetch(const uint8_t* B, int bg, int rig, int h, int u) {
+        const uint8_t* base = B + bg * 4 * 1024 + rig * 16;
+        q[0] = *(const u32x2*)(base + 8 * h);
+        q[1] = *(const u32x2*)(base + 1024 + 8 * h);
+        q[2] = *(const u32x2*)(base + 2 * 1024 + 8 * h);
+        sw = *(const u32x2*)(base + 3 * 1024 + 8 * ((u & 3) >> 1));  // scale bytes 8h6 .. +7
+        db = *(const uint16_t*)(B + 16 * 1024 + bg * 128 + rig * 2);
+    }
+    __device__ __forceinline__ void prep(int u) {
+        const int half = u & 1;
+        const float d = h2f(db);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int bi = 2 * g + half;
+            a[g] = d * (float)(int8_t)(((bi < 4 ? sw.x : sw.y) >> (8 * (bi & 3))) & 0xff);
+        }
+    }
+    __device__ __forceinline__ gh8 group(int g) const {
+        const u32x2 l = q[g & 1], hq = q[2];
+        const int sh = 4 * (g >> 1), hs = 2 * g;
+        const uint32_t c0 = ((l.x >> sh) & 0x0f0f0f0fu) | (((hq.x >> hs) & 0x03030303u) << 4);
+        const uint32_t c1 = ((l.y >> sh) & 0x0f0f0f0fu) | (((hq.y >> hs) & 0x03030303u) << 4);
+        uint32_t m[4];
+        magic8(c0, c1, m);
+        return deq8(m, a[g], -1056.0f * a[g]);  // (1024 + q6) a - 1056 a = (q6 - 32) a
+    }
+};
+
+template <> struct GCol<PGMOE_Q8_0> {
+    u32x2 q[4];
+    uint32_t dw;  // fp16 scales of Q8_0 blocks 2(u%4) (groups 0, 1), 2(u%4) + 1 (groups 2, 3)
+    float d[2];
+    __device__ __forceinline__ void fetch(const uint8_t* B, int bg, int rig, int h, int u) {
+        const uint8_t* base = B + bg * 5 * 1024 + rig * 16;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) q[cc] = *(const u32x2*)(base + cc * 1024 + 8 * h);
+        dw = *(const uint32_t*)(base + 4 * 1024 + 4 * (u & 3));
+    }
+    __device__ __forceinline__ void prep(int u) {
+        d[0] = lo_half(dw);
+        d[1] = hi_half(dw);
+    }
+    __device__ __forceinline__ gh8 group(int g) const {
+        const u32x2 s = q[g];
+        uint32_t m[4];
+        magic8(s.x ^ 0x80808080u, s.y ^ 0x80808080u, m);  // fp16 1152 + q
+        return deq8(m, d[g >> 1], -1152.0f * d[g >> 1]);
+    }
+};
 
 // ---------------------------------------------------------------- tile mapping
 // Block id -> (M tile, N tile): XCD x = id % 8 takes M tiles x, x+8, ... and runs all N
@@ -165,197 +249,227 @@ __device__ __forceinline__ int gemm_tile_expert(const int32_t* tile_off, int E, 
     return lo;
 }
 
-// ---------------------------------------------------------------- the kernel
-// k columns [ko0, ko0 + 32) of the 64-wide unit: 2 slices of 16, each 8
-// v_mfma_f32_32x32x16_f16 over the wave's 4 x 2 tiles of 32 x 32 (the f16 MFMA with the
-// full matrix-core rate on gfx950; 16x16x32 runs at half).  Operand layout: lane l holds
-// A[l%32][8(l/32) .. +8] and B[8(l/32) .. +8][l%32]; register v of D is
-// D[8(v/4) + 4(l/32) + v%4][l%32].
-// NI = the wave's 32-row slices that hold pairs (1..4); the others are skipped.
-template <int NI>
-__device__ __forceinline__ void gemm_half(const _Float16* As, const _Float16* Bs, int wm, int wn, int lane, int ko0,
-                                          gf16 (&acc)[4][2]) {
+// ---------------------------------------------------------------- one unit of MFMAs
+// Wave (wm, wn): rows 128 wm + 32 i (i < NI, the 32-row slices holding pairs), CT column
+// tiles j.  Group g = k16 slice g of the unit: A fragment lane l = row l % 32, k chunk
+// 2g + l / 32 (slot (2g + l/32) ^ (row & 7)); B fragment = the lane's column's group g,
+// weights 8(l/32) .. +8.  Register v of D is D[8(v/4) + 4(l/32) + v%4][l%32].
+// A fragments and B decodes run one group ahead of the MFMAs that use them, spread
+// between those MFMAs (a wave issues in order; each MFMA runs while the next few VALU
+// instructions issue).
+template <int QT, int NI, int CT>
+__device__ __forceinline__ void gemm_unit(const uint8_t* S, const GCol<QT> (&col)[CT], int wm, int lane,
+                                          gf16 (&acc)[4][CT]) {
+    const int h = lane >> 5;
+    gh8 af[2][NI], bf[2][CT];
+    auto stage = [&](int g, gh8 (&a)[NI], gh8 (&b)[CT]) {
+        const int kc = 2 * g + h;
 #pragma unroll
-    for (int ks = 0; ks < 32; ks += 16) {
-        const int ko = ko0 + ks + 8 * (lane >> 5);
-        gh8 af[NI];
-#pragma unroll
-        for (int i = 0; i < NI; ++i) af[i] = *(const gh8*)&As[(128 * wm + 32 * i + (lane & 31)) * kGP + ko];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const gh8 bf = *(const gh8*)&Bs[(64 * wn + 32 * j + (lane & 31)) * kGP + ko];
-#pragma unroll
-            for (int i = 0; i < NI; ++i)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf, acc[i][j], 0, 0, 0);
+        for (int i = 0; i < NI; ++i) {
+            const int r = 128 * wm + 32 * i + (lane & 31);
+            a[i] = *(const gh8*)(S + r * 128 + 16 * (kc ^ (r & 7)));
         }
+#pragma unroll
+        for (int j = 0; j < CT; ++j) b[j] = col[j].group(g);
+    };
+    stage(0, af[0], bf[0]);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        if (g < 3) stage(g + 1, af[(g + 1) & 1], bf[(g + 1) & 1]);
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int j = 0; j < CT; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[g & 1][i], bf[g & 1][j], acc[i][j], 0, 0, 0);
+        if (g < 3) {
+#pragma unroll
+            for (int k = 0; k < CT * NI; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                if (k < NI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+                __builtin_amdgcn_sched_group_barrier(0x002, (5 * CT) / NI, 0);  // VALU
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-__device__ __forceinline__ void gemm_unit(const _Float16* As, const _Float16* Bs, int wm, int wn, int lane, int ni,
-                                          gf16 (&acc)[4][2]) {
-    switch (ni) {
-    case 4:
-        gemm_half<4>(As, Bs, wm, wn, lane, 0, acc);
-        gemm_half<4>(As, Bs, wm, wn, lane, 32, acc);
-        break;
-    case 3:
-        gemm_half<3>(As, Bs, wm, wn, lane, 0, acc);
-        gemm_half<3>(As, Bs, wm, wn, lane, 32, acc);
-        break;
-    case 2:
-        gemm_half<2>(As, Bs, wm, wn, lane, 0, acc);
-        gemm_half<2>(As, Bs, wm, wn, lane, 32, acc);
-        break;
-    case 1:
-        gemm_half<1>(As, Bs, wm, wn, lane, 0, acc);
-        gemm_half<1>(As, Bs, wm, wn, lane, 32, acc);
-        break;
-    default: break;
+// The lane's CT B columns of a unit: row group bg[j], row rig[j] in it.
+template <int QT, int NI, int CT>
+__device__ __forceinline__ void gemm_unit_b(const uint8_t* S, const int (&bg)[CT], const int (&rig)[CT], int u,
+                                            int wm, int lane, gf16 (&acc)[4][CT]) {
+    if constexpr (NI > 0) {
+        // every LDS read of the columns first, one wait, then the scales
+        GCol<QT> col[CT];
+#pragma unroll
+        for (int j = 0; j < CT; ++j) col[j].fetch(S + kGA, bg[j], rig[j], lane >> 5, u);
+#pragma unroll
+        for (int j = 0; j < CT; ++j) col[j].prep(u);
+        gemm_unit<QT, NI, CT>(S, col, wm, lane, acc);
     }
 }
 
-template <int QT, bool GATEUP>
-__global__ __launch_bounds__(kGThreads) void gemm_kernel(
+// ---------------------------------------------------------------- the kernel
+template <int QT, bool GATEUP, int CT>
+__global__ __launch_bounds__(1024 / CT) void gemm_kernel(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, int64_t wstride0, int64_t wstride1,
     int N, int K, const uint16_t* __restrict__ act, int topk, int E, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm, const int32_t* __restrict__ tile_off, int n_ntiles,
     const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out) {
-    // two LDS stages: the next unit is staged into one while the other feeds the MFMAs
-    __shared__ __attribute__((aligned(16))) _Float16 A0[kGM * kGP];
-    __shared__ __attribute__((aligned(16))) _Float16 B0[kGN * kGP];
-    __shared__ __attribute__((aligned(16))) _Float16 A1[kGM * kGP];
-    __shared__ __attribute__((aligned(16))) _Float16 B1[kGN * kGP];
+    using L = GLay<QT, CT>;
+    constexpr int NW = L::NW, HW = NW / 2;
+    constexpr int CH = L::CH;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * L::STAGE];
     __shared__ int rowsrc[kGM];
+    __shared__ float rowscale[kGM];  // down: rs[p] * topk_w[perm[p]] of every tile row
     int mt, nt;
     PG_MARK(GATEUP ? 4 : 5, 0);
     if (!gemm_tile_of(blockIdx.x, n_ntiles, tile_off[E], mt, nt)) return;
     const int e = gemm_tile_expert(tile_off, E, mt);
     const int m0 = offsets[e] + (mt - tile_off[e]) * kGM;
     const int mrows = min(kGM, offsets[e + 1] - m0);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // wave tile: rows 128 wm .., B rows 64 wn .. (waves w and w + 4 share a SIMD)
-    const int wm = wave >> 2, wn = wave & 3;
-    const int units = K >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / HW, wn = wave % HW;  // waves w and w + HW: same columns
+    const int units = K >> 6, nb = K >> 8;
     // A source rows: gate/up gathers token rows of x, down reads its own pair rows.  Rows
     // past the tile's pairs repeat its last pair: they only feed accumulator rows that
     // are never stored.
     if (tid < kGM) {
         const int p = m0 + min(tid, mrows - 1);
         rowsrc[tid] = GATEUP ? perm[p] / topk : p;
+        if (!GATEUP) rowscale[tid] = rs[p] * topk_w[perm[p]];
     }
     __syncthreads();
 
-    // staging: thread t moves A chunks (rows t/8 + 64q, 16-byte chunk t%8) and groups
-    // h, h + 2 (h = t%2) of B row t/2
-    const int ar = tid >> 3, ac = tid & 7;
-    const int br = tid >> 1, bh = tid & 1;
-    const int nb = K >> 8;
-    int asrc[4];
+    // ---- copy plan.  A: wave w copies rows 8i .. 8i+7 for i = w + NW q (q < AQ); lane
+    // l takes row 8i + l/8, slot l%8 = k chunk (l%8) ^ (l/8).
+    const int akc = (lane & 7) ^ (lane >> 3);
+    const uint16_t* arow[L::AQ];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) asrc[q] = rowsrc[ar + 64 * q];
-    // B rows: gate/up tile rows, per wave column wn: 32 gate then 32 up rows of the
-    // intermediate indices nt*128 + 32wn + ..; down: output rows nt*256 + r.  Rows past N
-    // repeat row N-1: they only feed columns that are never stored.
-    const uint8_t* bmat;
-    int brow;
-    if (GATEUP) {
-        const bool up = (br >> 5) & 1;
-        bmat = up ? w1 + (int64_t)e * wstride1 : w0 + (int64_t)e * wstride0;
-        brow = nt * (kGN / 2) + 32 * (br >> 6) + (br & 31);
-    } else {
-        bmat = w0 + (int64_t)e * wstride0;
-        brow = nt * kGN + br;
+    for (int q = 0; q < L::AQ; ++q) arow[q] = act + (int64_t)rowsrc[8 * (wave + NW * q) + (lane >> 3)] * K;
+    // B row groups bg: gate/up: 0, 1 = gate rows nt*128 + 64bg, 2, 3 = the same up rows;
+    // down: rows nt*256 + 64bg.  Groups past N repeat the last one (their columns are
+    // never stored).
+    const int ngr = row_groups(N);
+    auto bmat = [&](int bg) -> const uint8_t* {
+        return GATEUP ? (bg < 2 ? w0 + (int64_t)e * wstride0 : w1 + (int64_t)e * wstride1) : w0 + (int64_t)e * wstride0;
+    };
+    auto brg = [&](int bg) { return min(GATEUP ? 2 * nt + (bg & 1) : 4 * nt + bg, ngr - 1); };
+    // B copy slots of this wave: s = wave + NW q; slot s < 4 (CH + 1): row group s / (CH + 1),
+    // chunk s % (CH + 1) (CH = the scale chunk); Q6_K slot 4 (CH + 1): the d of all four
+    // row groups; slots past SLOTS repeat slot s - SLOTS (same source, same place).
+    const uint8_t* bsrc[L::BQ];
+    int bkind[L::BQ], bcc[L::BQ];
+    uint32_t bdst[L::BQ];
+#pragma unroll
+    for (int q = 0; q < L::BQ; ++q) {
+        int s = wave + NW * q;
+        if (s >= L::SLOTS) s -= L::SLOTS;
+        bdst[q] = s * 1024;
+        if (s < 4 * (CH + 1)) {
+            const int bg = s / (CH + 1), cc = s % (CH + 1);
+            bkind[q] = 0;
+            bcc[q] = cc;
+            bsrc[q] = bmat(bg) + (int64_t)brg(bg) * nb * (Tile<QT>::CH * 1024) + lane * 16;
+        } else {  // Q6_K d plane: lanes 8g .. 8g+7 copy the 128 bytes of row group g
+            const int g = (lane >> 3) & 3;
+            bkind[q] = 1;
+            bcc[q] = 0;
+            const int64_t dpl = (int64_t)ngr * nb * 13 * 1024;
+            bsrc[q] = bmat(g) + dpl + (int64_t)brg(g) * nb * 128 + (lane & 7) * 16;
+        }
     }
-    brow = min(brow, N - 1);
+    const uint32_t sbase = lds_addr(smem);
+    // Issue every copy of unit u into stage st (u clamped: the last steps repeat it).
+    auto copy_unit = [&](int u, int st) {
+        u = min(u, units - 1);
+        const uint32_t S = sbase + st * L::STAGE;
+#pragma unroll
+        for (int q = 0; q < L::AQ; ++q)
+            g2l(arow[q] + Fmt<QT>::col(u, akc >> 1) + 8 * (akc & 1), S + (wave + NW * q) * 1024);
+#pragma unroll
+        for (int q = 0; q < L::BQ; ++q) {
+            const uint8_t* src;
+            if (bkind[q] == 0) {
+                const int ch = bcc[q] == CH ? GStage<QT>::HC : GStage<QT>::chunk(u, bcc[q]);
+                src = bsrc[q] + (int64_t)(u >> 2) * (Tile<QT>::CH * 1024) + ch * 1024;
+            } else {
+                src = bsrc[q] + (int64_t)(u >> 2) * 128;
+            }
+            g2l(src, S + kGA + bdst[q]);
+        }
+    };
 
-    gf16 acc[4][2];
+    gf16 acc[4][CT];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < CT; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
     const bool active = 128 * wm < mrows;
     const int ni = active ? min(4, (mrows - 128 * wm + 31) >> 5) : 0;  // 32-row slices with pairs
-    const bool store_first = wave >= 4;
-    // Two register sets of raw staging data and two LDS stages.  The loads are
-    // unconditional (every index is valid), so every step issues the same instructions and
-    // the waits for the previous step's loads stay exact; the last steps load a repeated
-    // unit that is never stored.
-    gu4 a0[4], a1[4];
-    GHalf<QT> b0, b1;
-#define PG_GLOAD(AR, BR, UU)                                                              \
-    do {                                                                                  \
-        const int pg_u = (UU);                                                            \
-        const int pg_col = Fmt<QT>::col(pg_u, ac >> 1) + 8 * (ac & 1);                    \
-        AR[0] = *(const gu4*)(act + (int64_t)asrc[0] * K + pg_col);                      \
-        AR[1] = *(const gu4*)(act + (int64_t)asrc[1] * K + pg_col);                      \
-        AR[2] = *(const gu4*)(act + (int64_t)asrc[2] * K + pg_col);                      \
-        AR[3] = *(const gu4*)(act + (int64_t)asrc[3] * K + pg_col);                      \
-        gload<QT>(bmat, nb, N, brow, pg_u, bh, BR);                                       \
-    } while (0)
-#define PG_GSTORE(AR, BR, UU, AS, BS)                                                     \
-    do {                                                                                  \
-        *(gu4*)&AS[(ar + 0) * kGP + 8 * ac] = AR[0];                                     \
-        *(gu4*)&AS[(ar + 64) * kGP + 8 * ac] = AR[1];                                    \
-        *(gu4*)&AS[(ar + 128) * kGP + 8 * ac] = AR[2];                                   \
-        *(gu4*)&AS[(ar + 192) * kGP + 8 * ac] = AR[3];                                   \
-        _Pragma("unroll") for (int gg = 0; gg < 2; ++gg) {                                \
-            uint32_t hv[8];                                                               \
-            gdecode<QT>(BR, (UU), bh, gg, hv);                                            \
-            uint4* pg_d = (uint4*)&BS[br * kGP + 16 * (bh + 2 * gg)];                     \
-            pg_d[0] = make_uint4(hv[0], hv[1], hv[2], hv[3]);                             \
-            pg_d[1] = make_uint4(hv[4], hv[5], hv[6], hv[7]);                             \
-        }                                                                                 \
-    } while (0)
-    PG_GLOAD(a0, b0, 0);
-    PG_GLOAD(a1, b1, min(1, units - 1));
-    PG_GSTORE(a0, b0, 0, A0, B0);
-    __syncthreads();
-    // Step u: issue the loads of unit u + 2 into the free register set, run the MFMAs of
-    // unit u (stage u & 1) and write unit u + 1 (loaded a step earlier) into the other
-    // stage; one barrier.  The two waves of a SIMD do the write at opposite ends of their
-    // MFMAs (waves 0-3 compute first, waves 4-7 write first), so one wave's dequantisation
-    // runs while the other keeps the matrix core busy.  The last steps re-store a unit that
-    // is never read.
-#define PG_GSTEP(AC, BC, AN, BN, ARN, BRN, ARF, BRF, UNEXT, ULOAD)                        \
-    do {                                                                                  \
-        PG_GLOAD(ARF, BRF, (ULOAD));                                                      \
-        if (store_first) PG_GSTORE(ARN, BRN, (UNEXT), AN, BN);                            \
-        gemm_unit(AC, BC, wm, wn, lane, ni, acc);                                         \
-        if (!store_first) PG_GSTORE(ARN, BRN, (UNEXT), AN, BN);                           \
-        __syncthreads();                                                                  \
-    } while (0)
-    for (int u = 0; u < units; u += 2) {
-        if (u == 4) PG_MARK(GATEUP ? 4 : 5, 1);
-        PG_GSTEP(A0, B0, A1, B1, a1, b1, a0, b0, min(u + 1, units - 1), min(u + 2, units - 1));
-        if (u == 4) PG_MARK(GATEUP ? 4 : 5, 2);
-        if (u + 1 >= units) break;
-        PG_GSTEP(A1, B1, A0, B0, a0, b0, a1, b1, min(u + 2, units - 1), min(u + 3, units - 1));
-        if (u == 4) PG_MARK(GATEUP ? 4 : 5, 3);
+    // the lane's CT B columns (j): gate/up: j < CT/2 gate tile column c = 16 CT wn + 32j +
+    // l%32 (rows nt*128 + c), j >= CT/2 the same up columns; down: tile column
+    // c = 32 CT wn + 32j + l%32 (rows nt*256 + c).  Row group c / 64 (+ 2 for up), row c % 64.
+    int bgj[CT], rigj[CT];
+#pragma unroll
+    for (int j = 0; j < CT; ++j) {
+        const int jj = GATEUP ? j % (CT / 2) : j;
+        const int c = (GATEUP ? 16 : 32) * CT * wn + 32 * jj + (lane & 31);
+        bgj[j] = (c >> 6) + (GATEUP && j >= CT / 2 ? 2 : 0);
+        rigj[j] = c & 63;
     }
-#undef PG_GSTEP
-#undef PG_GLOAD
-#undef PG_GSTORE
+
+    // ---- pipeline: three stages, copies two units ahead.  Step u: wait for this wave's
+    // copies of unit u (those of unit u + 1 may still fly), barrier (every wave's copies
+    // landed; every wave is done with unit u - 1's stage), copy unit u + 2 into that
+    // stage, compute unit u.
+    // The loop is instantiated per NI (a whole copy each) so the register allocation of
+    // one copy never has to merge the others'.
+    PG_MARK(GATEUP ? 4 : 5, 1);
+    copy_unit(0, 0);
+    copy_unit(1, 1);
+#define PG_GLOOP(NI_)                                                                        \
+    for (int u = 0, st = 0; u < units; ++u, st = st == 2 ? 0 : st + 1) {                    \
+        if (u == units / 4) PG_MARK(GATEUP ? 4 : 5, 2);                                      \
+        if (u == (3 * units) / 4) PG_MARK(GATEUP ? 4 : 5, 3);                                \
+        vm_wait<L::VM>();                                                                    \
+        lds_barrier();                                                                       \
+        copy_unit(u + 2, st == 0 ? 2 : st - 1);                                             \
+        gemm_unit_b<QT, NI_, CT>(smem + st * L::STAGE, bgj, rigj, u, wm, lane, acc);         \
+    }
+    switch (ni) {
+    case 4: PG_GLOOP(4) break;
+    case 3: PG_GLOOP(3) break;
+    case 2: PG_GLOOP(2) break;
+    case 1: PG_GLOOP(1) break;
+    default: PG_GLOOP(0) break;
+    }
+#undef PG_GLOOP
+    vm_wait<0>();  // the clamped copies past the last unit land before the block ends
     PG_MARK(GATEUP ? 4 : 5, 4);
     if (!active) return;
     // epilogue: register v of tile (i, j) is row 32i + 8(v/4) + 4(l/32) + v%4, column
     // 32j + l%32 of the wave tile
     if (GATEUP) {
-        // wave columns: tile 0 gate indices nt*128 + 32wn + l%32, tile 1 the matching up
-        const int col = nt * (kGN / 2) + 32 * wn + (lane & 31);
-        if (col < N) {
+        // wave columns: tiles j < CT/2 gate indices nt*128 + 16 CT wn + 32j + l%32, tile
+        // j + CT/2 the matching up
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < CT / 2; ++j) {
+            const int col = nt * (kGN / 2) + 16 * CT * wn + 32 * j + (lane & 31);
+            if (col < N) {
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int r = 128 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                    if (r < mrows) out[(int64_t)(m0 + r) * N + col] = silu(acc[i][0][v]) * acc[i][1][v];
-                }
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int r = 128 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                        if (r < mrows) out[(int64_t)(m0 + r) * N + col] = silu_fast(acc[i][j][v]) * acc[i][j + CT / 2][v];
+                    }
+            }
         }
     } else {
-        const int c0 = nt * kGN + 64 * wn + (lane & 31);
+        const int c0 = nt * kGN + 32 * CT * wn + (lane & 31);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -363,18 +477,29 @@ __global__ __launch_bounds__(kGThreads) void gemm_kernel(
                 const int r = 128 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 if (r >= mrows) continue;
                 const int p = m0 + r;
-                const float sc = rs[p] * topk_w[perm[p]];
+                const float sc = rowscale[r];
                 float* orow = out + (int64_t)p * N;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < CT; ++j) {
                     const int col = c0 + 32 * j;
                     if (col < N) orow[col] = acc[i][j][v] * sc;
                 }
             }
     }
+    PG_MARK(GATEUP ? 4 : 5, 5);
 }
 
 int gemm_tile_pairs() { return kGM; }
+
+// Column tiles per wave of each product (build-time choices; 2 = 8 waves, 4 = 4 waves).
+// Measured on the Qwen3 Zipf prefill: 8 waves is faster for both (the second wave of a
+// SIMD issues its decode VALU and LDS reads while the first one's MFMAs run).
+#ifndef PG_GU_CT
+#define PG_GU_CT 2
+#endif
+#ifndef PG_DN_CT
+#define PG_DN_CT 2
+#endif
 
 // Upper bound of 256-row tiles for P pairs over at most E experts, rounded up to whole
 // XCD groups.
@@ -389,9 +514,9 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
     const int nnt = div_up(g.N, kGN / 2);
-    const dim3 grid(gemm_max_mtiles(P, E) * nnt), block(kGThreads);
+    const dim3 grid(gemm_max_mtiles(P, E) * nnt);
 #define PG_GU(QT)                                                                                               \
-    PG_LAUNCH((gemm_kernel<QT, true>), grid, block, 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
+    PG_LAUNCH((gemm_kernel<QT, true, PG_GU_CT>), grid, dim3(64 * GLay<QT, PG_GU_CT>::NW), 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
               E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter)
     switch (g.qtype) {
     case PGMOE_Q4_K: PG_GU(PGMOE_Q4_K); break;
@@ -410,9 +535,9 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
     const int nnt = div_up(d.N, kGN);
-    const dim3 grid(gemm_max_mtiles(P, E) * nnt), block(kGThreads);
+    const dim3 grid(gemm_max_mtiles(P, E) * nnt);
 #define PG_DN(QT)                                                                                               \
-    PG_LAUNCH((gemm_kernel<QT, false>), grid, block, 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
+    PG_LAUNCH((gemm_kernel<QT, false, PG_DN_CT>), grid, dim3(64 * GLay<QT, PG_DN_CT>::NW), 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
               topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial)
     switch (d.qtype) {
     case PGMOE_Q4_K: PG_DN(PGMOE_Q4_K); break;
