@@ -26,6 +26,17 @@ __device__ int block_inclusive_scan(int v, int* buf) {
     return r;
 }
 
+// kDispBatch ids per lane of the chunk [b0, c1) (pair f = b0 + 64k + lane; -1 past c1).
+constexpr int kDispBatch = 32;
+__device__ __forceinline__ void load_batch(const int32_t* __restrict__ idx, int b0, int c1, int lane,
+                                           int (&ids)[kDispBatch]) {
+#pragma unroll
+    for (int k = 0; k < kDispBatch; ++k) {
+        const int f = b0 + 64 * k + lane;
+        ids[k] = f < c1 ? idx[f] : -1;
+    }
+}
+
 // Single workgroup.  Flat pair ids f = t*K + k are split into kDispWaves contiguous
 // chunks, one per wavefront.  Pass 1 counts ids per (wave, expert); a scan turns the
 // counts into per-(wave, expert) base positions; pass 2 walks each chunk in order,
@@ -45,10 +56,14 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
     __syncthreads();
     const int chunk = (P + kDispWaves - 1) / kDispWaves;
     const int c0 = wv * chunk, c1 = min(P, c0 + chunk);
-    // ids outside [0, E) are skipped (never written to LDS or to perm/inv)
-    for (int f = c0 + lane; f < c1; f += 64) {
-        const int id = idx[f];
-        if ((unsigned)id < (unsigned)E) atomicAdd(&cnt[wv][id], 1);
+    // ids outside [0, E) are skipped (never written to LDS or to perm/inv).  A wave reads
+    // its chunk kDispBatch ids per lane at a time, every load of a batch in flight at once.
+    for (int b0 = c0; b0 < c1; b0 += 64 * kDispBatch) {
+        int ids[kDispBatch];
+        load_batch(idx, b0, c1, lane, ids);
+#pragma unroll
+        for (int k = 0; k < kDispBatch; ++k)
+            if ((unsigned)ids[k] < (unsigned)E) atomicAdd(&cnt[wv][ids[k]], 1);
     }
     __syncthreads();
 
@@ -82,30 +97,35 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
     }
     __syncthreads();
 
-    // pass 2: stable scatter; every wave runs the same number of steps
-    const int steps = (chunk + 63) / 64;
-    for (int s = 0; s < steps; ++s) {
-        const int f = c0 + 64 * s + lane;
-        const int id = f < c1 ? idx[f] : -1;
-        const bool valid = (unsigned)id < (unsigned)E;
-        // lanes holding the same id: intersect ballots over the id's bits
-        uint64_t same = __ballot(valid);
-        if (!valid) same = 0;
-        for (int b = 0; b < 9; ++b) {  // E <= 512 -> ids < 2^9
-            const bool bit = valid && ((id >> b) & 1);
-            const uint64_t m = __ballot(bit);
-            same &= bit ? m : ~m;
+    // pass 2: stable scatter, each wave over its own chunk and its own bases (no block
+    // barrier needed), in steps of 64 ascending ids
+    for (int b0 = c0; b0 < c1; b0 += 64 * kDispBatch) {
+        int ids[kDispBatch];
+        load_batch(idx, b0, c1, lane, ids);
+#pragma unroll
+        for (int k = 0; k < kDispBatch; ++k) {
+            const int f = b0 + 64 * k + lane;
+            const int id = ids[k];
+            const bool valid = (unsigned)id < (unsigned)E;
+            // lanes holding the same id: intersect ballots over the id's bits
+            uint64_t same = __ballot(valid);
+            if (!valid) same = 0;
+#pragma unroll
+            for (int b = 0; b < 9; ++b) {  // E <= 512 -> ids < 2^9
+                const bool bit = valid && ((id >> b) & 1);
+                const uint64_t m = __ballot(bit);
+                same &= bit ? m : ~m;
+            }
+            if (valid) {
+                const uint64_t below = same & ((1ull << lane) - 1ull);
+                const int rank = __popcll(below);
+                const int pos = cnt[wv][id] + rank;
+                perm[pos] = f;
+                inv[f] = pos;
+                if ((same >> lane) == 1ull)  // highest lane of its id group advances the base
+                    cnt[wv][id] += __popcll(same);
+            }
         }
-        if (valid) {
-            const uint64_t below = same & ((1ull << lane) - 1ull);
-            const int rank = __popcll(below);
-            const int pos = cnt[wv][id] + rank;
-            perm[pos] = f;
-            inv[f] = pos;
-            if ((same >> lane) == 1ull)  // highest lane of its id group advances the base
-                cnt[wv][id] += __popcll(same);
-        }
-        __syncthreads();
     }
 }
 
