@@ -36,7 +36,7 @@ for p in (REPO, os.path.join(REPO, "pytorch-engine_amd")):
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 METRIC = "MoE layer tok/s at M=1 and M=4096 (Qwen3-30B-A3B shape); % HBM / MFMA roofline"
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_dec_gateup_qwen3_m1.json")
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_dec_gu_qwen3_m1.json")
 
 
 def log(msg: str) -> None:
@@ -348,12 +348,12 @@ def main() -> int:
                    "weight_copies": args.copies, "timing": "one forward per HIP graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "dec_gateup_kernel (routed gate/up + SwiGLU), M=1",
+                     "kernel": "dec_gu_kernel (routed gate/up + SwiGLU), M=1",
                      "algorithmic_bytes": gu_bytes, "kernel_us": gu_us,
                      "traffic_source": traffic_rec.get("source") if traffic_rec else None},
         "cpu_baseline": cpu,
         "decode": {str(k): v for k, v in decode.items()},
-        "kernels_m1": {"names": ["router_logits", "dec_gateup", "dec_down_combine"], "us": d1["kernel_us"],
+        "kernels_m1": {"names": ["router_logits", "dec_gu", "dec_dc"], "us": d1["kernel_us"],
                        "down_combine_gbs": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1),
                        "layer_active_gbs": round(layer_gbs, 1),
                        "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},

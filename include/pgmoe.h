@@ -15,14 +15,18 @@
  *   - activations are IEEE fp16 passed as uint16_t bits; outputs are fp32.
  *
  * Device weight layout (pgmoe_weights.base, matrices mat_stride bytes apart, each
- * exactly as many bytes as the GGUF blocks it holds, see pgmoe_weight_bytes):
- *   Q4_K (type 12): GGUF blocks unchanged (144 B = 9 x 16 B, already 16-B aligned).
- *   Q6_K (type 14): three planes per matrix, nb = cols/256 blocks per row:
- *       body  [rows][nb][4 units][48 B]; unit u = 2h + half holds
- *             ql[64h + 16half : +16] | ql[64h + 32 + 16half : +16] | qh[32h + 16half : +16]
- *       scale [rows][nb][4 units][4 B] = sc[8h + 2s + half] for s = 0..3
- *       d     [rows][nb] fp16
- *   Q8_0 (type 8): two planes per matrix: qs [rows][cols] int8, d [rows][cols/32] fp16.
+ * exactly as many bytes as the GGUF blocks it holds, rows padded to a multiple of 64 with
+ * zero rows, see pgmoe_weight_bytes): a matrix [N rows, K cols] (K a multiple of 256) is
+ * stored as tiles of 64 rows x one 256-weight super-block; tile (rg, b) at
+ * base + (rg * K/256 + b) * CH * 1024 holds CH 16-byte chunks per row, chunk-major:
+ * chunk c of row r at + c*1024 + r*16.  Chunk contents (same bits as the GGUF block):
+ *   Q4_K (type 12, CH 9):  c0 = d, dmin, 12 scale bytes;  c1..c8 = qs[16(c-1) .. +16]
+ *   Q6_K (type 14, CH 13): c0..c7 = ql[16c ..];  c8..c11 = qh[16(c-8) ..];  c12 = the 16
+ *                          int8 scales; the fp16 d in a plane after all tiles:
+ *                          d(rg, b, r) at base + ceil(N/64)*(K/256)*13*1024
+ *                          + ((rg*(K/256) + b)*64 + r)*2
+ *   Q8_0 (type 8, CH 17):  c0..c15 = the qs of the super-block's 8 Q8_0 blocks in order;
+ *                          c16 = their 8 fp16 d
  * pgmoe_relayout_weights() converts GGUF bytes already on the device into this layout.
  */
 #ifndef PGMOE_H

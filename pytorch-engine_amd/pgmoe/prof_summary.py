@@ -2,6 +2,7 @@
 
     python -m pgmoe.prof_summary RUN_results.db                 # kernel trace table
     python -m pgmoe.prof_summary --pmc RUN_results.db [NAME]    # counters per kernel
+    python -m pgmoe.prof_summary --traffic FETCH.db WRITE.db NAME  # HBM bytes per launch
 
 The kernel-trace mode groups dispatches by kernel name, grid and block. For each group it
 reports the number of calls, the average / min / max duration in microseconds, and the
@@ -72,8 +73,50 @@ def summarise_pmc(db: str, pattern: str = "") -> str:
     return "\n".join(lines)
 
 
+def _dispatch_values(db: str, pattern: str, counter: str) -> list:
+    """Per-dispatch totals of `counter` (summed over instances) for kernels whose name
+    contains `pattern`."""
+    c = sqlite3.connect(db)
+    rows = c.execute("select dispatch_id, name, counter_name, counter_value from pmc_events").fetchall()
+    per = collections.defaultdict(float)
+    for d, n, cn, cv in rows:
+        if cn == counter and pattern in n:
+            per[d] += cv
+    return [per[d] for d in sorted(per)]
+
+
+def traffic(fetch_db: str, write_db: str, pattern: str, copy_name: str = "copyBuffer") -> dict:
+    """HBM bytes per launch of the kernels whose name contains `pattern`, from a
+    FETCH_SIZE pass and a WRITE_SIZE pass (KiB per dispatch, summed over instances), each
+    scaled by what the same counter reads for the largest runtime device copies in the
+    same runs (bytes moved per copy = their WRITE_SIZE, which reports every byte written)."""
+    fk = _dispatch_values(fetch_db, pattern, "FETCH_SIZE")
+    wk = _dispatch_values(write_db, pattern, "WRITE_SIZE")
+    fc = _dispatch_values(fetch_db, copy_name, "FETCH_SIZE")
+    wc = _dispatch_values(write_db, copy_name, "WRITE_SIZE")
+    big_w = [v for v in wc if v >= 0.5 * max(wc)]
+    big_f = sorted(fc)[-len(big_w):]
+    moved_kib = sum(big_w) / len(big_w)
+    fetch_factor = moved_kib / (sum(big_f) / len(big_f))
+    write_factor = 1.0
+    f_kib = sum(fk) / len(fk)
+    w_kib = sum(wk) / len(wk)
+    fetch_b = f_kib * 1024 * fetch_factor
+    write_b = w_kib * 1024 * write_factor
+    return {"kernel_pattern": pattern, "bytes_per_launch": int(round(fetch_b + write_b)),
+            "fetch_bytes": int(round(fetch_b)), "write_bytes": int(round(write_b)),
+            "fetch_size_kib_raw": round(f_kib, 3), "write_size_kib_raw": round(w_kib, 3),
+            "fetch_factor": round(fetch_factor, 5), "write_factor": write_factor,
+            "dispatches": [len(fk), len(wk)],
+            "calibration": f"{len(big_w)} device copies ({copy_name}): FETCH_SIZE {sum(big_f) / len(big_f):.1f} KiB, "
+                           f"WRITE_SIZE {moved_kib:.1f} KiB per copy"}
+
+
 if __name__ == "__main__":
-    if len(sys.argv) >= 3 and sys.argv[1] == "--pmc":
+    if len(sys.argv) >= 5 and sys.argv[1] == "--traffic":
+        import json
+        print(json.dumps(traffic(sys.argv[2], sys.argv[3], sys.argv[4]), indent=1))
+    elif len(sys.argv) >= 3 and sys.argv[1] == "--pmc":
         print(summarise_pmc(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else ""))
     else:
         print(summarise(sys.argv[1]))
