@@ -283,12 +283,15 @@ def main() -> int:
                      "active_weight_bytes": base.active_weight_bytes(n_act)}
         log(f"[bench] decode M={M}: {decode[M]}")
 
-    # dominant kernel at M = 1: the routed gate/up (launch 1 of router, gate/up, down+combine)
+    # dominant kernel at M = 1: the routed gate/up, launch 0 of (gate/up with the router
+    # folded in, down + combine); its algorithmic bytes are the active experts' gate/up GGUF
+    # bytes plus the fp32 router weights it reads
     d1 = decode[1]
-    gu_us = d1["kernel_us"][1]
-    gu_bytes = d1["active_experts"] * (base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat)
+    gu_us = d1["kernel_us"][0]
+    gu_bytes = (d1["active_experts"] * (base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat)
+                + spec.n_experts * spec.hidden * 4)
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-    dn_us = d1["kernel_us"][2]
+    dn_us = d1["kernel_us"][1]
     dn_bytes = d1["active_experts"] * base.down_exps.gguf_bytes_per_mat
     layer_gbs = d1["active_weight_bytes"] / (d1["us_per_step"] * 1e-6) / 1e9
     traffic, traffic_rec = load_traffic()
@@ -348,12 +351,12 @@ def main() -> int:
                    "weight_copies": args.copies, "timing": "one forward per HIP graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "dec_gu_kernel (routed gate/up + SwiGLU), M=1",
+                     "kernel": "dec_gu_kernel (router + routing + gate/up + SwiGLU), M=1",
                      "algorithmic_bytes": gu_bytes, "kernel_us": gu_us,
                      "traffic_source": traffic_rec.get("source") if traffic_rec else None},
         "cpu_baseline": cpu,
         "decode": {str(k): v for k, v in decode.items()},
-        "kernels_m1": {"names": ["router_logits", "dec_gu", "dec_dc"], "us": d1["kernel_us"],
+        "kernels_m1": {"names": ["dec_gu", "dec_dc"], "us": d1["kernel_us"],
                        "down_combine_gbs": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1),
                        "layer_active_gbs": round(layer_gbs, 1),
                        "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},

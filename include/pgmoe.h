@@ -85,7 +85,10 @@ int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
 int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
                            void* dst, void* stream);
 
-/* Workspace bytes pgmoe_moe_forward needs for M tokens. */
+/* Workspace bytes pgmoe_moe_forward needs for M tokens.  Zero the workspace once when it
+ * is allocated: for M <= 8 it begins with the router's ready-tagged logits, which the
+ * forward leaves at zero for the next call (calls that share a workspace must not
+ * overlap, and a workspace whose forward failed part-way must be zeroed again). */
 size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M);
 
 /* One MoE layer: out[M, H] = GGUFSparseMoEMLP.forward(x[M, H]) (model.py:898-937).
@@ -98,8 +101,8 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
  * The i-th kernel the call launches (i < n_events) records start_events[i] when it begins
  * and stop_events[i] when it ends (hipEvent_t handles created by the caller; either array
  * may be NULL).  *n_launches (if not NULL) receives the number of kernels launched.
- * Launch order: decode (M <= 8): router, gate/up, [shared gate/up, shared down], down +
- * combine (or down, combine); prefill: router, top-k, dispatch, gate/up, row-scale, down,
+ * Launch order: decode (M <= 8): gate/up (router and routing folded in), [shared gate/up,
+ * shared down], down + combine (or down, combine); prefill: router, top-k, dispatch, gate/up, row-scale, down,
  * [shared: identity dispatch, gate/up, row-scale, down, shared gate], combine. */
 int pgmoe_moe_forward_timed(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
                             size_t ws_bytes, void* stream, void** start_events, void** stop_events,

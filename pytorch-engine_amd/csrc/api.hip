@@ -66,7 +66,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
-    size_t desc, xsum, isum, s_isum;
+    size_t rlog, desc, xsum, isum, s_isum;
     size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, inter, a16, rs, partial;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
@@ -84,11 +84,14 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     const size_t P = (size_t)M * K;
     const bool gemm = M > decode_tokens_max();
     size_t c = 0;
+    // first: the decode router's ready-tagged logits (zero between calls; the workspace
+    // must be zeroed once when it is allocated)
+    o.rlog = take(c, gemm ? 0 : (size_t)decode_rlog_words(M, (int)E) * 8);
     o.desc = take(c, gemm ? 0 : (size_t)decode_desc_words() * 4);
     o.xsum = take(c, gemm ? 0 : (size_t)M * (H / 16) * 4);
     o.isum = take(c, gemm ? 0 : P * (I / 16) * 4);
     o.s_isum = take(c, (gemm || !L->has_shared) ? 0 : (size_t)M * (L->sh_gate.n_rows / 16) * 4);
-    o.logits = take(c, (size_t)M * E * 4);
+    o.logits = take(c, gemm ? (size_t)M * E * 4 : 0);
     o.idx = take(c, P * 4);
     o.w = take(c, P * 4);
     o.offsets = take(c, (E + 1) * 4);
@@ -257,19 +260,18 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
     const int mode = M > decode_tokens_max() ? 1 : 0;
     const int BM = gemm_tile_rows();
     if (mode == 0) {
-        // decode: router (+ shared gate row, x sums) -> gate/up with in-block routing ->
-        // [shared gate/up -> shared down] -> down + combine
+        // decode: gate/up with the router and the routing folded in -> [shared gate/up ->
+        // shared down] -> down + combine
         const float* sgw = L->has_shared ? L->sh_inp_gate : nullptr;
-        if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st, sgw,
-                                       sgw ? WS(float, s_logit) : nullptr, WS(float, xsum))))
-            return rc;
         const int max_active = M * K < E ? M * K : E;
         const bool fused = decode_fused_down(M * K, lm.down.K);
         DecFlat flat{};
         if (!fused)
             flat = DecFlat{WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv), WS(int32_t, active),
                            WS(int32_t, nact), WS(float, w)};
-        if ((rc = launch_dec_gateup_routed(lm.gate, lm.up, x, WS(float, xsum), K, M, WS(float, logits), E,
+        if ((rc = launch_dec_gateup_routed(lm.gate, lm.up, x, K, M, L->router_w, L->router_bias, sgw,
+                                           sgw ? WS(float, s_logit) : nullptr, WS(uint64_t, rlog),
+                                           L->has_shared ? WS(float, xsum) : nullptr, E,
                                            L->norm_topk, WS(int32_t, desc), flat, max_active, WS(float, inter),
                                            WS(float, isum), st)))
             return rc;
@@ -287,12 +289,13 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
         }
         if (fused)
             return launch_dec_down_combine(lm.down, WS(float, inter), WS(float, isum), WS(int32_t, desc), M, K,
-                                           max_active, shared, shared_logit, out, st);
+                                           max_active, shared, shared_logit, out, WS(uint64_t, rlog), decode_rlog_words(M, E), st);
         if ((rc = launch_dec_down(lm.down, WS(float, inter), WS(float, isum), M, WS(int32_t, offsets),
                                   WS(int32_t, perm), WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, w),
                                   WS(float, partial), st)))
             return rc;
-        return launch_combine(WS(float, partial), WS(int32_t, inv), M, K, H, shared, shared_logit, out, st);
+        return launch_combine(WS(float, partial), WS(int32_t, inv), M, K, H, shared, shared_logit, out, st,
+                              WS(uint64_t, rlog), decode_rlog_words(M, E));
     }
     if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st))) return rc;
     if ((rc = launch_topk(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w), st))) return rc;

@@ -42,13 +42,67 @@ __device__ __forceinline__ float h2f(uint16_t b) {
 __device__ __forceinline__ float lo_half(uint32_t v) { return h2f((uint16_t)(v & 0xffffu)); }
 __device__ __forceinline__ float hi_half(uint32_t v) { return h2f((uint16_t)(v >> 16)); }
 
+// Value of lane (l ^ S) for S in {1, 2, 4, 8, 16, 32}, by VALU lane moves rather than the
+// LDS crossbar (ds_bpermute, about a hundred cycles a step): DPP quad_perm [1,0,3,2] and
+// [2,3,0,1] for 1 and 2; DPP row_ror:8 (lane (l - 8) mod 16 of its row) for 8; row_ror:4 /
+// row_ror:12 chosen by lane bit 2 for 4; v_permlane16_swap / v_permlane32_swap (gfx950:
+// swap the odd rows / the upper half of one register with the even rows / lower half of
+// another) for 16 and 32.  Every lane of the wave must be active (a DPP read of an inactive
+// lane yields 0), and every lane must call it (no divergent call sites).
+template <int S>
+__device__ __forceinline__ uint32_t xor_lane_u(uint32_t v) {
+    static_assert(S == 1 || S == 2 || S == 4 || S == 8 || S == 16 || S == 32, "lane xor distance");
+    const int lane = __lane_id();
+    if constexpr (S == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return lane < 32 ? r[1] : r[0];
+    } else if constexpr (S == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else if constexpr (S == 8) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false);
+    } else if constexpr (S == 4) {
+        // both reads in every lane (as operands of a conditional they would run under a
+        // partial EXEC mask and read inactive lanes)
+        const uint32_t a = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false);
+        const uint32_t b = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x12c, 0xf, 0xf, false);
+        return (lane & 4) ? a : b;
+    } else if constexpr (S == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4e, 0xf, 0xf, false);
+    } else {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xb1, 0xf, 0xf, false);
+    }
+}
+template <int S>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __builtin_bit_cast(float, xor_lane_u<S>(__builtin_bit_cast(uint32_t, v)));
+}
+template <int S>
+__device__ __forceinline__ int xor_lane(int v) {
+    return (int)xor_lane_u<S>((uint32_t)v);
+}
+
 // Sum over an aligned group of `G` lanes (G a power of two <= 64); every lane of the
-// group ends with the same value (pairing (l, l^G/2), (l, l^G/4), ..., (l, l^1)).
-template <int G>
+// group ends with the same value (pairing (l, l^G/2), (l, l^G/4), ..., (l, l^1)).  Whole
+// waves only (xor_lane).
+template <int G, int S = G / 2>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int s = G / 2; s >= 1; s >>= 1) v += __shfl_xor(v, s, kWave);
-    return v;
+    if constexpr (S >= 1) {
+        v += xor_lane<S>(v);
+        return group_sum<G, S / 2>(v);
+    } else {
+        return v;
+    }
+}
+
+// Maximum over the 64 lanes (every lane ends with it).
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, xor_lane<32>(v));
+    v = fmaxf(v, xor_lane<16>(v));
+    v = fmaxf(v, xor_lane<8>(v));
+    v = fmaxf(v, xor_lane<4>(v));
+    v = fmaxf(v, xor_lane<2>(v));
+    return fmaxf(v, xor_lane<1>(v));
 }
 
 // group_sum<64> of N values at once (N a power of two <= 64), as a reduce-scatter: at
@@ -56,27 +110,28 @@ __device__ __forceinline__ float group_sum(float v) {
 // bit and receives its partner's partial of that half, so lane l ends holding the total of
 // value (l mod N), after N - 1 exchanges instead of 6 N.  Every level adds the same two
 // partial sums as group_sum<64> (IEEE addition commutes), so the totals have its bits.
-template <int N>
+template <int N, int S = 32>
 __device__ __forceinline__ float scatter_sum64(float (&v)[N], int lane) {
+    if constexpr (S >= 1) {
+        if constexpr (S >= N) {  // more lanes than values: plain xor step on all of them
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) {
-        if (s >= N) {  // more lanes than values: plain xor step on all of them
-#pragma unroll
-            for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], s, kWave);
+            for (int i = 0; i < N; ++i) v[i] += xor_lane<S>(v[i]);
         } else {
             // selects by mask: a select between two array elements would become a select
             // of addresses and push the array to scratch memory
-            const uint32_t up = (lane & s) ? 0xffffffffu : 0u;
+            const uint32_t up = (lane & S) ? 0xffffffffu : 0u;
 #pragma unroll
-            for (int i = 0; i < s; ++i) {
-                const uint32_t lo = __builtin_bit_cast(uint32_t, v[i]), hi = __builtin_bit_cast(uint32_t, v[s + i]);
+            for (int i = 0; i < S; ++i) {
+                const uint32_t lo = __builtin_bit_cast(uint32_t, v[i]), hi = __builtin_bit_cast(uint32_t, v[S + i]);
                 const float send = __builtin_bit_cast(float, (lo & up) | (hi & ~up));
                 const float keep = __builtin_bit_cast(float, (hi & up) | (lo & ~up));
-                v[i] = keep + __shfl_xor(send, s, kWave);
+                v[i] = keep + xor_lane<S>(send);
             }
         }
+        return scatter_sum64<N, S / 2>(v, lane);
+    } else {
+        return v[0];
     }
-    return v[0];
 }
 
 // K-quant 6-bit (scale, min) of sub-block s from the 12 scale bytes (words D, Mb, MD).
@@ -102,6 +157,85 @@ __device__ __forceinline__ void dma16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Zero words [0, n) of p with relaxed agent-scope atomic stores, one word per thread of
+// the grid (the decode router's ready-tagged logits, cleared by the forward's last kernel).
+__device__ __forceinline__ void clear_words(uint64_t* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int step = gridDim.x * blockDim.x;
+    if (p)
+        for (int j = i; j < n; j += step) __hip_atomic_store(p + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- router tile
+// Router logits of one wave: TM tokens (m0 ..; rows past M repeat row M-1) x TE expert
+// rows (e0 ..; row E is extra_w, the shared expert's gate vector, when given; rows past
+// it repeat the last).  Lane l is "slot" l: it owns the 8-wide chunks c = l, l+64,
+// l+128, ... of the row and runs one fmaf chain over them in ascending order; the 64
+// slot sums are then combined by the xor tree (l, l^32), (l, l^16), ..., (l, l^1), and
+// every lane ends with every total.  The caller adds the bias last.  The CPU oracle
+// (or_router_logits) performs the same operations in the same order.  Chunks are
+// processed PF at a time with every load of the group issued before the first FMA (the
+// FMA order per slot is unchanged).
+template <int TM, int TE, int PF = (TM * TE <= 8 ? 4 : 2)>
+__device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, const float* __restrict__ W,
+                                            const float* __restrict__ extra_w, int M, int H, int E, int m0,
+                                            int e0, int lane, float (&acc)[TM][TE]) {
+    const int rows = E + (extra_w ? 1 : 0);
+    const int C = H >> 3;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
+    for (int c0 = lane; c0 < C; c0 += 64 * PF) {
+        uint4 xq[PF][TM];
+        float4 wq[PF][TE][2];
+#pragma unroll
+        for (int q = 0; q < PF; ++q) {
+            const int c = c0 + 64 * q;
+            if (c < C) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int m = m0 + i < M ? m0 + i : M - 1;
+                    xq[q][i] = *(const uint4*)(x + (int64_t)m * H + 8 * c);
+                }
+#pragma unroll
+                for (int j = 0; j < TE; ++j) {
+                    const int e = e0 + j < rows ? e0 + j : rows - 1;
+                    const float* wr = e < E ? W + (int64_t)e * H : extra_w;
+                    wq[q][j][0] = *(const float4*)(wr + 8 * c);
+                    wq[q][j][1] = *(const float4*)(wr + 8 * c + 4);
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < PF; ++q) {
+            if (c0 + 64 * q < C) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const uint32_t w4[4] = {xq[q][i].x, xq[q][i].y, xq[q][i].z, xq[q][i].w};
+                    float xv[8];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        xv[2 * k] = lo_half(w4[k]);
+                        xv[2 * k + 1] = hi_half(w4[k]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < TE; ++j) {
+                        const float wv[8] = {wq[q][j][0].x, wq[q][j][0].y, wq[q][j][0].z, wq[q][j][0].w,
+                                             wq[q][j][1].x, wq[q][j][1].y, wq[q][j][1].z, wq[q][j][1].w};
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) acc[i][j] = __builtin_fmaf(xv[k], wv[k], acc[i][j]);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TE; ++j) acc[i][j] = group_sum<64>(acc[i][j]);
+}
 
 // ---------------------------------------------------------------- device weight layout
 // Every matrix [N rows, K cols] (K a multiple of 256) is stored as tiles of 64 rows x one

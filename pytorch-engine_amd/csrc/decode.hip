@@ -15,20 +15,22 @@ int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const flo
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
                       int max_active, float* inter, float* isum, hipStream_t st) {
     const DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, M, g.n_mats, 0, {}};
-#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, dp, max_active, inter, isum, st)
+#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, dp, RouterIn{}, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
 }
 
-int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
-                             const float* logits, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
-                             float* inter, float* isum, hipStream_t st) {
+int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
+                             const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, float* xsum_out,
+                             int E, int norm, int32_t* desc, const DecFlat& flat, int max_active, float* inter,
+                             float* isum, hipStream_t st) {
     if (M < 1 || M > kDecTM) return fail(PGMOE_E_INVALID, "routed decode handles 1..%d tokens", kDecTM);
     if (topk > 16 || E > 512 || M * topk > 128)
         return fail(PGMOE_E_UNSUPPORTED, "routed decode: top_k <= 16, E <= 512, M*top_k <= 128");
-    const DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, logits, desc, M, E, norm,
+    const DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, rlog, desc, M, E, norm,
                      {flat.offsets, flat.perm, flat.inv, flat.active, flat.n_active, flat.w}};
-#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, dp, max_active, inter, isum, st)
+    const RouterIn rt{rw, bias, sgw, s_logit, xsum_out};
+#define CALL(QT) dec_gateup_q<QT>(g, u, x, nullptr, topk, M, dp, rt, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
 }
@@ -36,7 +38,7 @@ int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, co
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
                             float* isum, hipStream_t st) {
     const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
-#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, 1, M, dp, 1, inter, isum, st)
+#define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, 1, M, dp, RouterIn{}, 1, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
 }
@@ -59,9 +61,9 @@ int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, 
 
 int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int K,
                             int max_active, const float* shared, const float* shared_logit, float* out,
-                            hipStream_t st) {
+                            uint64_t* clear, int n_clear, hipStream_t st) {
     if (M < 1 || M > kDecTM || M * K > 128) return fail(PGMOE_E_INVALID, "down + combine: 1..%d tokens", kDecTM);
-#define CALL(QT) dec_down_combine_q<QT>(d, inter, isum, desc, M, M * K, max_active, shared, shared_logit, out, st)
+#define CALL(QT) dec_down_combine_q<QT>(d, inter, isum, desc, M, M * K, max_active, shared, shared_logit, out, clear, n_clear, st)
     PG_BY_QTYPE(d.qtype, "decode down + combine", CALL)
 #undef CALL
 }
@@ -85,5 +87,6 @@ size_t dec_lds_limit() {
 
 int decode_tokens_max() { return kDecTM; }
 int decode_desc_words() { return kDescWords; }
+int decode_rlog_words(int M, int E) { return kRlogCopies * M * E; }
 
 }  // namespace pgmoe

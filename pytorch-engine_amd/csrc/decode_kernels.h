@@ -469,17 +469,20 @@ __device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q8_0>& r, const float
 // Sum over the KS = 64/RB lanes that share a row (lanes r, r+RB, r+2RB, ...).
 template <int RB>
 __device__ __forceinline__ float kslot_sum(float v) {
-#pragma unroll
-    for (int s = RB; s < 64; s <<= 1) v += __shfl_xor(v, s, 64);
-    return v;
+    if constexpr (RB < 64) {
+        v += xor_lane<RB>(v);
+        return kslot_sum<2 * RB>(v);
+    } else {
+        return v;
+    }
 }
 
 // ============================================================================ routing in a block
-// Decode forward: the router kernel writes logits [M][E]; every gate/up block re-derives
-// the top-k sets of the M <= 8 tokens from them (wave m selects token m with scalar
-// ballot arithmetic, about half a microsecond, instead of a launch and its dependent
-// global round trips), and block (0, 0) also publishes a compact routing descriptor for
-// the fused down + combine kernel:
+// Decode forward: the lowest gate/up blocks compute the router logits [M][E] and every
+// gate/up block re-derives the top-k sets of the M <= 8 tokens from them (wave m selects
+// token m with scalar ballot arithmetic, about half a microsecond, instead of a launch and
+// its dependent global round trips), and block (0, 0) also publishes a compact routing
+// descriptor for the fused down + combine kernel:
 //   int32 words: [0] n_active; slot a at kDescSlot + 4a = {expert, first sorted pair,
 //   pair count, 0}; sorted pair p at kDescPair + 2p = {token, weight bits}.
 // Active slots are in ascending expert id; the pairs of an expert in ascending token
@@ -526,36 +529,71 @@ __device__ __forceinline__ void copy_words(T* dst, const T* __restrict__ src, in
     copy_idx<U, T>(n, tid, nth, [=](int i) { return src + i; }, [=](int i) { return dst + i; });
 }
 
-// K-th largest of the distinct keys of one token held by a wave (lane l: experts l + 64r):
-// a 41-step radix descent on the key bits.  The threshold and the counts are wave-uniform
-// (scalar registers); each step is one vector compare per key word and a popcount of the
-// resulting lane mask.
+// A threshold with exactly K of the distinct keys of one token at or above it (lane l
+// holds experts l + 64r): a radix descent on the 41 key bits that stops as soon as the
+// candidate has exactly K keys at or above it (with random logits after about a dozen
+// steps), else ends on the K-th largest key itself.  The threshold and the counts are
+// wave-uniform (scalar registers); each step is one vector compare per key word and a
+// popcount of the resulting lane mask.
 template <int RE>
 __device__ __forceinline__ uint64_t kth_key_radix(const uint64_t (&key)[RE], int K) {
     uint64_t thr = 0;
-#pragma unroll
     for (int b = 40; b >= 0; --b) {
         const uint64_t cand = thr | (1ull << b);
         int cnt = 0;
 #pragma unroll
         for (int r = 0; r < RE; ++r) cnt += __popcll(__ballot(key[r] >= cand));
-        thr = cnt >= K ? cand : thr;
+        if (cnt >= K) {
+            thr = cand;
+            if (cnt == K) break;
+        }
     }
     return thr;
 }
 
-// Logits of token m for lane l (experts l + 64r; -inf past E).
+// Ready-tagged logits: word [m][e] = (1 << 32) | float bits once the router wave of
+// expert e has stored it, 0 before (the forward's last kernel clears the words again).
+// Stores and polls are relaxed agent-scope atomics, so a consumer sees each word either
+// unwritten or final, from any XCD, with no fence and no cache invalidation.
+// kRlogCopies replicas of the words ([copy][M][E]): every block polls copy
+// (block id % kRlogCopies), so the few cache lines of one copy are not hammered by every
+// polling wave of the grid (polls go past the per-XCD L2s, to the memory side).
+constexpr int kRlogCopies = 16;
+__device__ __forceinline__ void put_logit(uint64_t* p, float v) {
+    __hip_atomic_store(p, (1ull << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kSpinMax = 1 << 20;  // polls before a waiting wave gives up (results then wrong, no hang)
+
+// Logits of token m for lane l (experts l + 64r; -inf past E): polls the tagged words
+// (a bounded spin with short sleeps) until every one of the wave's is written.
 template <int RE>
-__device__ __forceinline__ void load_logits(const float* __restrict__ logits, int m, int E, int lane, float (&v)[RE]) {
+__device__ __forceinline__ void load_logits(const uint64_t* rlog, int m, int E, int lane, float (&v)[RE]) {
+    uint64_t q[RE];
+    int n = 0;
+    for (;;) {
+        bool ready = true;
 #pragma unroll
-    for (int r = 0; r < RE; ++r) {
-        const int e = lane + 64 * r;
-        v[r] = e < E ? logits[(int64_t)m * E + e] : -INFINITY;
+        for (int r = 0; r < RE; ++r) {
+            const int e = lane + 64 * r;
+            q[r] = e < E ? __hip_atomic_load(rlog + (int64_t)m * E + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                         : 1ull << 32;
+            ready = ready && (q[r] >> 32) != 0;
+        }
+        if (__all(ready) || ++n >= kSpinMax) break;
+        __builtin_amdgcn_s_sleep(1);
     }
+#ifdef PG_TRACE
+    if (lane == 0 && m == 0 && blockIdx.y * gridDim.x + blockIdx.x < 8192)
+        pg_trace[(blockIdx.y * gridDim.x + blockIdx.x) * 8 + 1] = n;
+#endif
+#pragma unroll
+    for (int r = 0; r < RE; ++r) v[r] = lane + 64 * r < E ? __builtin_bit_cast(float, (uint32_t)q[r]) : -INFINITY;
+    if (m == 0) PG_MARK(1, 7);
 }
 
 // Top-k membership of token m (one wave; v = load_logits): the members are exactly the
-// keys at or above the K-th largest key (keys are distinct).  Lane 0 writes the
+// keys at or above the radix threshold (keys are distinct).  Lane 0 writes the
 // membership words R.pres[m][*]; with `weights`, also the members' ids and softmax weights
 // (max-subtracted, denominator over all E, optional renorm; model.py:903-907) in
 // ascending id order to R.mem_e / R.mem_w.
@@ -570,8 +608,7 @@ __device__ __forceinline__ void route_token(const float (&v)[RE], int m, int E, 
     if (weights) {
 #pragma unroll
         for (int r = 0; r < RE; ++r) top = fmaxf(top, v[r]);
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) top = fmaxf(top, __shfl_xor(top, s, 64));
+        top = wave_max(top);
 #pragma unroll
         for (int r = 0; r < RE; ++r)
             if (lane + 64 * r < E) den += expf(v[r] - top);
@@ -752,10 +789,23 @@ enum DecMode { kDispatch = 0, kRoute = 1, kIdent = 2 };
 struct DecDisp {
     int mode;  // DecMode
     const int32_t *offsets, *perm, *active, *n_active;
-    const float* logits;  // kRoute
+    const uint64_t* rlog; // kRoute: ready-tagged router logits [kRlogCopies][M][E] (put_logit)
     int32_t* desc;        // kRoute: published by block (0, 0)
     int M, E, norm;       // M: tokens (every mode)
     FlatRoute flat;       // kRoute: optional flat arrays, published by block (0, 0)
+};
+
+// Router work folded into the routed gate/up launch: with R = ceil(rows / blocks) (1
+// unless the grid is small), wave w < R of block b computes logits row b * R + w (all
+// tokens; row E is the shared expert's gate) and stores it as tagged words (put_logit);
+// every block's routing waves poll the words of their tokens.  The producers sit in the
+// lowest blocks, which are dispatched first, and never wait.
+struct RouterIn {
+    const float* W;        // [E][H] fp32 router weights; null: logits come from a router launch
+    const float* bias;     // [E] or null
+    const float* extra_w;  // shared expert gate row [H] or null
+    float* extra_out;      // [M] its logits
+    float* xsum_out;       // [M][H/16] 16-element sums of x for the shared expert's launches, or null
 };
 
 // Active slot a of the dispatch or identity modes (a token meets an expert at most once,
@@ -792,14 +842,14 @@ __device__ __forceinline__ SlotInfo slot_plain(const DecDisp& dp, int a, int top
 // Dynamic LDS: xs [M][K/64][72] fp16 | xss [M][K/16] f32.
 // xsum (optional): 16-element sums of the x rows [M][K/16] (else computed from xs);
 // isum (optional output): 16-element sums of the inter rows [P][N/16].
-template <int RE, typename Issue>
+template <int RE>
 __device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteShared& R, bool pub, int lane, int w,
-                                            int nw, Issue issue) {
+                                            int nw) {
     float v[RE];
-    if (w < dp.M) load_logits<RE>(dp.logits, w, dp.E, lane, v);
-    issue();  // the token-row loads go out behind the logits
+    const int copy = (blockIdx.y * gridDim.x + blockIdx.x) % kRlogCopies;
+    const uint64_t* rlog = dp.rlog + (int64_t)copy * dp.M * dp.E;
     for (int m = w; m < dp.M; m += nw) {
-        if (m != w) load_logits<RE>(dp.logits, m, dp.E, lane, v);
+        load_logits<RE>(rlog, m, dp.E, lane, v);
         route_token<RE>(v, m, dp.E, topk, R, pub, dp.norm, lane);
     }
 }
@@ -809,7 +859,8 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
                                                       const uint8_t* __restrict__ ubase, int64_t gstride,
                                                       int64_t ustride, int N, int K, const uint16_t* __restrict__ x,
                                                       const float* __restrict__ xsum, int topk, DecDisp dp,
-                                                      float* __restrict__ inter, float* __restrict__ isum) {
+                                                      RouterIn rt, float* __restrict__ inter,
+                                                      float* __restrict__ isum) {
     constexpr int RB = 16, XR = 4;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ RouteShared R;
@@ -821,8 +872,43 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     uint16_t* xs = (uint16_t*)smem;
     float* xss = (float*)(smem + (size_t)M * xrs * 2);
     PG_MARK(1, 0);
+    const bool fused = MODE == kRoute;  // kRoute always carries the router (rt)
+    const int rows = dp.E + (rt.extra_w ? 1 : 0);
+    // 0. folded router: logits rows spread one per block where the grid allows (the host
+    //    sizes the grid so that rows per block <= waves), producers in the lowest blocks
+    const int bid = blockIdx.y * gridDim.x + blockIdx.x;
+    const int rpb = (rows + gridDim.x * gridDim.y - 1) / (gridDim.x * gridDim.y);  // router rows per block
+    if (fused && w < rpb) {
+        const int e = bid * rpb + w;
+        if (e < rows) {
+            constexpr int PF = TM <= 2 ? 4 : TM == 4 ? 2 : 1;
+#ifdef PG_TRACE
+            if (lane == 0) pg_trace[(4 * 8192 + bid) * 8 + (w & 7)] = wall_clock64();
+#endif
+            float lg[TM][1];
+            router_tile<TM, 1, PF>(x, rt.W, rt.extra_w, M, K, dp.E, 0, e, lane, lg);
+            // every lane holds the totals: lane c stores copy c
+#pragma unroll
+            for (int t = 0; t < TM; ++t) {
+                if (t < M) {
+                    if (e < dp.E) {
+                        float v = lg[t][0];
+                        if (rt.bias) v = v + rt.bias[e];
+                        if (lane < kRlogCopies)
+                            put_logit((uint64_t*)dp.rlog + ((int64_t)lane * M + t) * dp.E + e, v);
+                    } else if (lane == 0) {
+                        rt.extra_out[t] = lg[t][0];
+                    }
+                }
+            }
+#ifdef PG_TRACE
+            if (lane == 0) pg_trace[(2 * 8192 + bid) * 8 + (w & 7)] = wall_clock64();
+#endif
+        }
+    }
     // 1. token rows (and their 16-element sums) to registers, behind the logits of the
-    //    wave's token; the selection then waits for the logits only
+    //    wave's token (or, with the folded router, while it runs); the selection then
+    //    waits for the logits only
     const int npc = M * (K >> 3);  // 16-byte pieces of the x rows
     const int nps = xsum ? M * (K >> 6) : 0;
     u32x4 xr[XR];
@@ -835,15 +921,16 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         }
         if (tid < nps) sr = *(const floatx4*)(xsum + 4 * tid);
     };
-    if (MODE == kRoute) {
+    if (fused) {
+        issue();
         if (dp.E <= 64)
-            route_waves<1>(dp, topk, R, pub, lane, w, nw, issue);
+            route_waves<1>(dp, topk, R, pub, lane, w, nw);
         else if (dp.E <= 128)
-            route_waves<2>(dp, topk, R, pub, lane, w, nw, issue);
+            route_waves<2>(dp, topk, R, pub, lane, w, nw);
         else if (dp.E <= 256)
-            route_waves<4>(dp, topk, R, pub, lane, w, nw, issue);
+            route_waves<4>(dp, topk, R, pub, lane, w, nw);
         else
-            route_waves<8>(dp, topk, R, pub, lane, w, nw, issue);
+            route_waves<8>(dp, topk, R, pub, lane, w, nw);
     } else {
         issue();
     }
@@ -871,6 +958,8 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         __syncthreads();
     }
     PG_MARK(1, 1);
+    if (rt.xsum_out && blockIdx.x == 0 && blockIdx.y == 0)
+        for (int i = tid; i < M * srs; i += nth) rt.xsum_out[i] = xss[i];
     // 3. the block's active slots a = blockIdx.y, + gridDim.y, ...: expert and pairs (the
     //    same in every wave), items, then the SwiGLU rows
     const int r = lane & 15, p = lane >> 4;
@@ -921,7 +1010,8 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
                 if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
             }
         }
-        __syncthreads();  // red is rewritten by the next slot
+        if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
+        __syncthreads();                           // red is rewritten by the next slot
     }
     // block (0, 0) publishes the routing last: its stores then stay off the block's own
     // critical path (a barrier would wait for them)
@@ -968,8 +1058,10 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
                                                       const float* __restrict__ isum, const int32_t* __restrict__ desc,
                                                       int M, int P, const float* __restrict__ shared,
                                                       const float* __restrict__ shared_logit,
-                                                      float* __restrict__ out) {
+                                                      float* __restrict__ out, uint64_t* __restrict__ clear,
+                                                      int n_clear) {
     constexpr int RB = 8;
+    clear_words(clear, n_clear);  // the gate/up launch is done with them
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int d_pb[128], d_cnt[128], d_tok[128];
     __shared__ float d_w[128];
@@ -1192,10 +1284,15 @@ size_t dec_lds_limit();
 
 template <int QT, int TM>
 inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, const DecDisp& dp,
-                      int max_active, float* inter, float* isum, hipStream_t st) {
-    const int W = gu_waves(g.K >> 8);
-    PG_LAUNCH((dec_gu_kernel<QT, TM>), dim3(div_up(g.N, 16), gu_slot_blocks(max_active)), dim3(64 * W),
-              gu_lds_bytes(dp.M, g.K), st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp,
+                      const RouterIn& rt, int max_active, float* inter, float* isum, hipStream_t st) {
+    const int W = gu_waves(g.K >> 8), gx = div_up(g.N, 16);
+    int gy = gu_slot_blocks(max_active);
+    if (dp.mode == kRoute) {  // every router row needs a wave
+        const int rows = dp.E + (rt.extra_w ? 1 : 0);
+        gy = gy > div_up(rows, gx * W) ? gy : div_up(rows, gx * W);
+    }
+    PG_LAUNCH((dec_gu_kernel<QT, TM>), dim3(gx, gy), dim3(64 * W),
+              gu_lds_bytes(dp.M, g.K), st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt,
               inter, isum);
 }
 
@@ -1209,10 +1306,11 @@ inline void dn_launch(const Mats& d, const float* inter, const float* isum, cons
 
 template <int QT, int TM>
 inline void dc_launch(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
-                      int max_active, const float* shared, const float* shared_logit, float* out, hipStream_t st) {
+                      int max_active, const float* shared, const float* shared_logit, float* out, uint64_t* clear,
+                      int n_clear, hipStream_t st) {
     const int W = dc_waves(max_active * (d.K >> 8));
     PG_LAUNCH((dec_dc_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, d.K), st, d.base,
-              d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out);
+              d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out, clear, n_clear);
 }
 
 #define PG_TM(F, QT, RB, W, ...)                   \
@@ -1245,22 +1343,24 @@ inline void dc_launch(const Mats& d, const float* inter, const float* isum, cons
 // Per-qtype launchers (instantiated by decode_inst.hip, one object per format and stage).
 template <int QT>
 int dec_gateup_q(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
-                 const DecDisp& dp, int max_active, float* inter, float* isum, hipStream_t st);
+                 const DecDisp& dp, const RouterIn& rt, int max_active, float* inter, float* isum, hipStream_t st);
 template <int QT>
 int dec_down_q(const Mats& d, const float* inter, const float* isum, int M, int mode, const DecDisp& dp,
                int max_active, const float* topk_w, float* partial, hipStream_t st);
 template <int QT>
 int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
-                       int max_active, const float* shared, const float* shared_logit, float* out, hipStream_t st);
+                       int max_active, const float* shared, const float* shared_logit, float* out, uint64_t* clear,
+                       int n_clear, hipStream_t st);
 
 #define PG_DEFINE_DECODE_GATEUP(QT)                                                                                  \
     template <>                                                                                                     \
     int dec_gateup_q<QT>(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,      \
-                         const DecDisp& dp, int max_active, float* inter, float* isum, hipStream_t st) {            \
+                         const DecDisp& dp, const RouterIn& rt, int max_active, float* inter, float* isum,          \
+                         hipStream_t st) {                                                                          \
         if (M < 1 || M > kDecTM) return fail(PGMOE_E_UNSUPPORTED, "decode gate/up: 1..%d tokens (got %d)", kDecTM, M); \
         if (gu_lds_bytes(M, g.K) > dec_lds_limit())                                           \
             return fail(PGMOE_E_UNSUPPORTED, "decode gate/up: %d tokens of %d inputs exceed LDS", M, g.K);          \
-        PG_TM2(gu_launch, QT, g, u, x, xsum, topk, dp, max_active, inter, isum, st);                                 \
+        PG_TM2(gu_launch, QT, g, u, x, xsum, topk, dp, rt, max_active, inter, isum, st);                             \
         return check_launch("dec_gateup");                                                                          \
     }
 
@@ -1278,10 +1378,11 @@ int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, con
     template <>                                                                                                     \
     int dec_down_combine_q<QT>(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M,   \
                                int P, int max_active, const float* shared, const float* shared_logit, float* out,   \
-                               hipStream_t st) {                                                                    \
+                               uint64_t* clear, int n_clear, hipStream_t st) {                                      \
         if (P > 128 || dc_lds_bytes(P, d.K) > dec_lds_limit())                                                      \
             return fail(PGMOE_E_UNSUPPORTED, "decode down + combine: %d pairs of %d inputs exceed LDS", P, d.K);    \
-        PG_TM2(dc_launch, QT, d, inter, isum, desc, M, P, max_active, shared, shared_logit, out, st);               \
+        PG_TM2(dc_launch, QT, d, inter, isum, desc, M, P, max_active, shared, shared_logit, out, clear, n_clear, \
+               st);                                                                                                 \
         return check_launch("dec_down_combine");                                                                    \
     }
 

@@ -35,8 +35,7 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const float* __restrict__
             mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
         }
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) mx = fmaxf(mx, __shfl_xor(mx, s, 64));
+    mx = wave_max(mx);
     const float sc = fmaxf(mx * (1.0f / 16384.0f), 1.0f);
     if (lane == 0) rs[p] = sc;
     uint16_t* orow = a16 + p * I;
@@ -66,7 +65,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
                                                       const int32_t* __restrict__ inv, int K, int H,
                                                       const float* __restrict__ shared,
                                                       const float* __restrict__ shared_logit,
-                                                      float* __restrict__ out) {
+                                                      float* __restrict__ out, uint64_t* __restrict__ clear,
+                                                      int n_clear) {
+    if (blockIdx.y == 0) clear_words(clear, n_clear);  // decode router logits (grid x = tokens)
     const int t = blockIdx.x;
     const int c = blockIdx.y * 256 + threadIdx.x;  // float4 column
     if (4 * c >= H) return;
@@ -144,12 +145,13 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
 }
 
 int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H, const float* shared,
-                   const float* shared_logit, float* out, hipStream_t st) {
+                   const float* shared_logit, float* out, hipStream_t st, uint64_t* clear,
+                   int n_clear) {
     if (M <= 0) return PGMOE_OK;
     if (K > 16) return fail(PGMOE_E_UNSUPPORTED, "combine supports top_k <= 16");
     if (H % 4) return fail(PGMOE_E_UNSUPPORTED, "combine: H %d is not a multiple of 4", H);
     PG_LAUNCH(combine_kernel, dim3(M, div_up(H / 4, 256)), dim3(256), 0, st, partial, inv, K, H, shared,
-              shared_logit, out);
+              shared_logit, out, clear, n_clear);
     return check_launch("combine");
 }
 

@@ -53,8 +53,10 @@ int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int to
 int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_t* offsets, const int32_t* perm,
                 const int32_t* active, const int32_t* n_active, const int32_t* tile_off, const float* topk_w,
                 int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st);
+// clear (optional): n_clear words the kernel sets to zero (the decode router's tagged logits).
 int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H, const float* shared,
-                   const float* shared_logit, float* out, hipStream_t st);
+                   const float* shared_logit, float* out, hipStream_t st, uint64_t* clear = nullptr,
+                   int n_clear = 0);
 int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, uint8_t* dst,
                     int64_t dst_stride, hipStream_t st);
 // Decode expert stages (M <= decode_tokens_max()).
@@ -69,16 +71,24 @@ struct DecFlat {
     int32_t *offsets, *perm, *inv, *active, *n_active;
     float* w;
 };
-int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
-                             const float* logits, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
-                             float* inter, float* isum, hipStream_t st);
+// The routed gate/up also computes the router logits (rw [E][H], bias, the shared
+// expert's gate row sgw -> s_logit) into `rlog` (decode_rlog_words ready-tagged words, zero on entry;
+// the forward's last kernel clears them), and, when xsum_out is set, the 16-element sums
+// of x for the shared expert's launches.
+int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
+                             const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, float* xsum_out,
+                             int E, int norm, int32_t* desc, const DecFlat& flat, int max_active, float* inter,
+                             float* isum, hipStream_t st);
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
                             float* isum, hipStream_t st);
 int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st);
+// clear (may be null): n_clear words the kernel sets to zero (the decode router's tagged logits).
 int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int K,
                             int max_active, const float* shared, const float* shared_logit, float* out,
-                            hipStream_t st);
+                            uint64_t* clear, int n_clear, hipStream_t st);
 int decode_desc_words();
+// 64-bit words of the decode router's ready-tagged logits (all copies) for M tokens.
+int decode_rlog_words(int M, int E);
 // Whether the fused down + combine kernel can stage P inter rows of K values.
 bool decode_fused_down(int P, int K);
 // Prefill grouped GEMMs (gemm.hip); tile_off counts gemm_tile_pairs()-row tiles.

@@ -45,65 +45,13 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
     const int mt = wave / n_etiles, et = wave % n_etiles;
     const int m0 = mt * TM, e0 = et * TE;
     if (m0 >= M) return;
-    const int C = H >> 3;
     float acc[TM][TE];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TE; ++j) acc[i][j] = 0.0f;
-    // Chunks are processed PF at a time with every load of the group issued before the
-    // first FMA, so each group costs one memory round trip.  The FMA order per slot is
-    // unchanged: chunks ascending, elements 0..7.
-    constexpr int PF = TM * TE <= 8 ? 4 : 2;
-    for (int c0 = lane; c0 < C; c0 += 64 * PF) {
-        uint4 xq[PF][TM];
-        float4 wq[PF][TE][2];
-#pragma unroll
-        for (int q = 0; q < PF; ++q) {
-            const int c = c0 + 64 * q;
-            if (c < C) {
-#pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const int m = m0 + i < M ? m0 + i : M - 1;
-                    xq[q][i] = *(const uint4*)(x + (int64_t)m * H + 8 * c);
-                }
-#pragma unroll
-                for (int j = 0; j < TE; ++j) {
-                    const int e = e0 + j < rows ? e0 + j : rows - 1;
-                    const float* wr = e < E ? W + (int64_t)e * H : extra_w;
-                    wq[q][j][0] = *(const float4*)(wr + 8 * c);
-                    wq[q][j][1] = *(const float4*)(wr + 8 * c + 4);
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < PF; ++q) {
-            if (c0 + 64 * q < C) {
-#pragma unroll
-                for (int i = 0; i < TM; ++i) {
-                    const uint32_t w4[4] = {xq[q][i].x, xq[q][i].y, xq[q][i].z, xq[q][i].w};
-                    float xv[8];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        xv[2 * k] = lo_half(w4[k]);
-                        xv[2 * k + 1] = hi_half(w4[k]);
-                    }
-#pragma unroll
-                    for (int j = 0; j < TE; ++j) {
-                        const float wv[8] = {wq[q][j][0].x, wq[q][j][0].y, wq[q][j][0].z, wq[q][j][0].w,
-                                             wq[q][j][1].x, wq[q][j][1].y, wq[q][j][1].z, wq[q][j][1].w};
-#pragma unroll
-                        for (int k = 0; k < 8; ++k) acc[i][j] = __builtin_fmaf(xv[k], wv[k], acc[i][j]);
-                    }
-                }
-            }
-        }
-    }
+    router_tile<TM, TE>(x, W, extra_w, M, H, E, m0, e0, lane, acc);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TE; ++j) {
-            float v = group_sum<64>(acc[i][j]);
+            float v = acc[i][j];
             const int m = m0 + i, e = e0 + j;
             if (lane == 0 && m < M && e < E) {
                 if (bias) v = v + bias[e];
@@ -228,15 +176,18 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
                 bi = e;
             }
         }
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) {
-            const float ov = __shfl_xor(bv, s, 64);
-            const int oi = __shfl_xor(bi, s, 64);
+        auto merge = [&](float ov, int oi) {
             if (oi != 0x7fffffff && (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi))) {
                 bv = ov;
                 bi = oi;
             }
-        }
+        };
+        merge(xor_lane<32>(bv), xor_lane<32>(bi));
+        merge(xor_lane<16>(bv), xor_lane<16>(bi));
+        merge(xor_lane<8>(bv), xor_lane<8>(bi));
+        merge(xor_lane<4>(bv), xor_lane<4>(bi));
+        merge(xor_lane<2>(bv), xor_lane<2>(bi));
+        merge(xor_lane<1>(bv), xor_lane<1>(bi));
 #pragma unroll
         for (int r = 0; r < R; ++r)
             if (lane + 64 * r == bi) taken[r] = true;

@@ -162,7 +162,7 @@ class HipSparseMoEMLP(nn.Module):
         ws = self._ws.get(M)
         if ws is None:
             n = self.workspace_bytes(M) + 256
-            # zeroed once: the workspace starts with self-resetting completion counters
+            # zeroed once: the workspace starts with self-resetting ready-tagged router logits
             raw = torch.zeros(n, dtype=torch.uint8, device=self.device)
             off = (-raw.data_ptr()) % 256
             ws = raw[off:]

@@ -168,7 +168,7 @@ def test_timed_forward_matches_forward_and_times_every_launch():
     from pgmoe._lib import check, lib
     lay, ol, mod = _pair("tiny")
     starts, stops = HipEvents(16), HipEvents(16)
-    for M, n_expected in ((1, 3), (16, 7)):  # decode: router, gate/up, down+combine; prefill: 7 kernels
+    for M, n_expected in ((1, 2), (16, 7)):  # decode: gate/up (router folded in), down+combine; prefill: 7
         x = torch.from_numpy(lay.draw_x(M)).to("cuda:0")
         ref = mod(x)
         out = torch.empty_like(ref)
@@ -181,6 +181,8 @@ def test_timed_forward_matches_forward_and_times_every_launch():
         torch.cuda.synchronize()
         assert n.value == n_expected
         assert torch.equal(out, ref)
+        if M <= 8:  # decode leaves the router's tagged logits (first in the workspace) at zero
+            assert int(ws[:16 * M * mod.n_experts * 8].view(torch.int32).abs().sum().item()) == 0  # 16 copies
         for i in range(n.value):
             d = starts.elapsed_ms(starts.ev[i], stops.ev[i])
             assert 0.0 < d < 50.0, (M, i, d)
