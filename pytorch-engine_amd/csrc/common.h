@@ -7,18 +7,28 @@
 #include "pgmoe.h"
 
 // Phase timestamps for profiling builds only: a build that defines PG_TRACE (relocatable
-// device code) also defines `__device__ unsigned long long pg_trace[]`, and thread 0 of
-// each block stores wall_clock64() (100 MHz) at slot [kernel][block][point].  Without
-// PG_TRACE the marks compile to nothing.
+// device code) also defines `__device__ unsigned long long pg_trace[]`.  A kernel declares
+// its marks with PG_DECL, PG_MARK(kern, point) keeps wall_clock64() (100 MHz) in a register,
+// and PG_FLUSH(kern) at the kernel's end has thread 0 of each block store them at
+// [kern][block][point] (stores at the marks themselves would lengthen the waits that
+// follow them).  Without PG_TRACE the macros compile to nothing.
 #ifdef PG_TRACE
 extern __device__ unsigned long long pg_trace[];
-#define PG_MARK(kern, pt)                                                                                  \
-    do {                                                                                                   \
-        const unsigned pg_b = blockIdx.y * gridDim.x + blockIdx.x;                                         \
-        if (threadIdx.x == 0 && pg_b < 8192) pg_trace[((kern) * 8192 + pg_b) * 8 + (pt)] = wall_clock64(); \
+#define PG_DECL unsigned long long pg_t[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define PG_MARK(kern, pt) (pg_t[(pt)] = wall_clock64())
+#define PG_SET(pt, v) (pg_t[(pt)] = (v))
+#define PG_FLUSH(kern)                                                                                      \
+    do {                                                                                                    \
+        const unsigned pg_b = blockIdx.y * gridDim.x + blockIdx.x;                                          \
+        if (threadIdx.x == 0 && pg_b < 8192)                                                                \
+            for (int pg_i = 0; pg_i < 8; ++pg_i)                                                            \
+                if (pg_t[pg_i]) pg_trace[((kern) * 8192 + pg_b) * 8 + pg_i] = pg_t[pg_i];                  \
     } while (0)
 #else
+#define PG_DECL
 #define PG_MARK(kern, pt) ((void)0)
+#define PG_SET(pt, v) ((void)0)
+#define PG_FLUSH(kern) ((void)0)
 #endif
 
 namespace pgmoe {

@@ -583,18 +583,14 @@ __device__ __forceinline__ void load_logits(const uint64_t* rlog, int m, int E, 
         if (__all(ready) || ++n >= kSpinMax) break;
         __builtin_amdgcn_s_sleep(1);
     }
-#ifdef PG_TRACE
-    if (lane == 0 && m == 0 && blockIdx.y * gridDim.x + blockIdx.x < 8192)
-        pg_trace[(blockIdx.y * gridDim.x + blockIdx.x) * 8 + 1] = n;
-#endif
 #pragma unroll
     for (int r = 0; r < RE; ++r) v[r] = lane + 64 * r < E ? __builtin_bit_cast(float, (uint32_t)q[r]) : -INFINITY;
-    if (m == 0) PG_MARK(1, 7);
 }
 
 // Top-k membership of token m (one wave; v = load_logits): the members are exactly the
 // keys at or above the radix threshold (keys are distinct).  Lane 0 writes the
-// membership words R.pres[m][*]; with `weights`, also the members' ids and softmax weights
+// membership words R.pres[m][*], the members write their ids to R.mem_e; with `weights`,
+// also their softmax weights
 // (max-subtracted, denominator over all E, optional renorm; model.py:903-907) in
 // ascending id order to R.mem_e / R.mem_w.
 template <int RE>
@@ -625,11 +621,13 @@ __device__ __forceinline__ void route_token(const float (&v)[RE], int m, int E, 
             R.pres[m][2 * r + 1] = (uint32_t)(mask >> 32);
         }
         const int pos = base + __popcll(mask & ((1ull << lane) - 1ull));
-        if (weights && in && pos < K) {  // exactly K members unless logits hold NaNs
-            const float pr = expf(v[r] - top) / den;
+        if (in && pos < K) {  // exactly K members unless logits hold NaNs
             R.mem_e[m * K + pos] = lane + 64 * r;
-            R.mem_w[m * K + pos] = pr;
-            psel += pr;
+            if (weights) {
+                const float pr = expf(v[r] - top) / den;
+                R.mem_w[m * K + pos] = pr;
+                psel += pr;
+            }
         }
         base += __popcll(mask);
     }
@@ -659,12 +657,13 @@ __device__ __forceinline__ int row_scan16(int v) {
     return v;
 }
 
+template <int TM>
 __device__ __forceinline__ SlotInfo slot_info(RouteShared& R, int M, int a, int lane, bool store_words) {
-    uint32_t wm[kDecTM];
+    uint32_t wm[TM];
     uint32_t u = 0;
     int pc = 0;
 #pragma unroll
-    for (int m = 0; m < kDecTM; ++m) {
+    for (int m = 0; m < TM; ++m) {
         wm[m] = (m < M && lane < 16) ? R.pres[m][lane & 15] : 0u;
         u |= wm[m];
         pc += __popc(wm[m]);
@@ -694,7 +693,7 @@ __device__ __forceinline__ SlotInfo slot_info(RouteShared& R, int M, int a, int 
     int pb = __builtin_amdgcn_readlane(wp, q), c = 0;
     uint32_t toks = 0;
 #pragma unroll
-    for (int m = 0; m < kDecTM; ++m) {
+    for (int m = 0; m < TM; ++m) {
         const uint32_t w = __builtin_amdgcn_readlane(wm[m], q);  // 0 past M
         pb += __popc(w & below);
         if ((w >> bit) & 1u) {
@@ -705,6 +704,18 @@ __device__ __forceinline__ SlotInfo slot_info(RouteShared& R, int M, int a, int 
     si.p_begin = pb;
     si.count = c;
     si.toks = toks;
+    return si;
+}
+
+// Active slot a of a single token's routing: its a-th member in ascending id (R.mem_e),
+// sorted pair a; the token has exactly K members.
+__device__ __forceinline__ SlotInfo slot_info1(const RouteShared& R, int a, int K) {
+    SlotInfo si;
+    si.n_act = K;
+    si.e = a < K ? R.mem_e[a] : -1;
+    si.p_begin = a;
+    si.count = 1;
+    si.toks = 0;
     return si;
 }
 
@@ -810,12 +821,13 @@ struct RouterIn {
 
 // Active slot a of the dispatch or identity modes (a token meets an expert at most once,
 // so count <= M <= 8).
+template <int MODE>
 __device__ __forceinline__ SlotInfo slot_plain(const DecDisp& dp, int a, int topk) {
     SlotInfo si;
     si.e = -1;
     si.p_begin = si.count = 0;
     si.toks = 0;
-    if (dp.mode == kIdent) {
+    if constexpr (MODE == kIdent) {
         si.n_act = 1;
         if (a > 0) return si;
         si.e = 0;
@@ -844,17 +856,22 @@ __device__ __forceinline__ SlotInfo slot_plain(const DecDisp& dp, int a, int top
 // isum (optional output): 16-element sums of the inter rows [P][N/16].
 template <int RE>
 __device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteShared& R, bool pub, int lane, int w,
-                                            int nw) {
+                                            int nw, [[maybe_unused]] unsigned long long& t_ready) {
     float v[RE];
     const int copy = (blockIdx.y * gridDim.x + blockIdx.x) % kRlogCopies;
     const uint64_t* rlog = dp.rlog + (int64_t)copy * dp.M * dp.E;
     for (int m = w; m < dp.M; m += nw) {
         load_logits<RE>(rlog, m, dp.E, lane, v);
+#ifdef PG_TRACE
+        if (m == 0) t_ready = wall_clock64();
+#endif
         route_token<RE>(v, m, dp.E, topk, R, pub, dp.norm, lane);
     }
 }
 
-template <int QT, int TM>
+// MODE: DecMode (fixed per instantiation, so each kernel holds only its own path); RE:
+// logit words per lane of the routing waves (kRoute: E <= 64 * RE).
+template <int QT, int TM, int MODE, int RE>
 __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict__ gbase,
                                                       const uint8_t* __restrict__ ubase, int64_t gstride,
                                                       int64_t ustride, int N, int K, const uint16_t* __restrict__ x,
@@ -866,13 +883,15 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     __shared__ RouteShared R;
     __shared__ float red[16][TM][RB];  // per-wave row partials
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nth = blockDim.x, nw = nth >> 6;
-    const int M = dp.M, MODE = dp.mode;
+    const int M = dp.M;
     const int nb = K >> 8, xrs = (K >> 6) * kXuH, srs = K >> 4;
     const bool pub = MODE == kRoute && blockIdx.x == 0 && blockIdx.y == 0;
     uint16_t* xs = (uint16_t*)smem;
     float* xss = (float*)(smem + (size_t)M * xrs * 2);
+    PG_DECL;
     PG_MARK(1, 0);
-    const bool fused = MODE == kRoute;  // kRoute always carries the router (rt)
+    unsigned long long t_ready = 0;  // profiling builds: when wave 0 had its token's logits
+    constexpr bool fused = MODE == kRoute;  // kRoute always carries the router (rt)
     const int rows = dp.E + (rt.extra_w ? 1 : 0);
     // 0. folded router: logits rows spread one per block where the grid allows (the host
     //    sizes the grid so that rows per block <= waves), producers in the lowest blocks
@@ -882,9 +901,6 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         const int e = bid * rpb + w;
         if (e < rows) {
             constexpr int PF = TM <= 2 ? 4 : TM == 4 ? 2 : 1;
-#ifdef PG_TRACE
-            if (lane == 0) pg_trace[(4 * 8192 + bid) * 8 + (w & 7)] = wall_clock64();
-#endif
             float lg[TM][1];
             router_tile<TM, 1, PF>(x, rt.W, rt.extra_w, M, K, dp.E, 0, e, lane, lg);
             // every lane holds the totals: lane c stores copy c
@@ -901,9 +917,7 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
                     }
                 }
             }
-#ifdef PG_TRACE
-            if (lane == 0) pg_trace[(2 * 8192 + bid) * 8 + (w & 7)] = wall_clock64();
-#endif
+            PG_MARK(1, 3);
         }
     }
     // 1. token rows (and their 16-element sums) to registers, behind the logits of the
@@ -921,21 +935,9 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         }
         if (tid < nps) sr = *(const floatx4*)(xsum + 4 * tid);
     };
-    if (fused) {
-        issue();
-        if (dp.E <= 64)
-            route_waves<1>(dp, topk, R, pub, lane, w, nw);
-        else if (dp.E <= 128)
-            route_waves<2>(dp, topk, R, pub, lane, w, nw);
-        else if (dp.E <= 256)
-            route_waves<4>(dp, topk, R, pub, lane, w, nw);
-        else
-            route_waves<8>(dp, topk, R, pub, lane, w, nw);
-    } else {
-        issue();
-    }
-    PG_MARK(1, 6);
-    // 2. rows to LDS (pieces past XR per thread are copied directly)
+    issue();
+    // 2. rows to LDS (pieces past XR per thread are copied directly), before the routing:
+    //    the copies overlap the wait for the logits
     const int kp = K >> 3;
 #pragma unroll
     for (int k = 0; k < XR; ++k) {
@@ -946,8 +948,8 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         *(u32x4*)(xs + (i / kp) * xrs + xpos_h(8 * (i % kp))) = *(const u32x4*)(x + 8 * (int64_t)i);
     if (tid < nps) *(floatx4*)(xss + 4 * tid) = sr;
     for (int i = tid + nth; i < nps; i += nth) *(floatx4*)(xss + 4 * i) = *(const floatx4*)(xsum + 4 * i);
-    __syncthreads();
     if (!xsum) {
+        __syncthreads();
         for (int i = tid; i < M * srs; i += nth) {
             const uint16_t* pp = xs + (i / srs) * xrs + xpos_h(16 * (i % srs));
             float sm = 0.f;
@@ -955,9 +957,11 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
             for (int k = 0; k < 16; ++k) sm += h2f(pp[k]);
             xss[i] = sm;
         }
-        __syncthreads();
     }
     PG_MARK(1, 1);
+    if constexpr (fused) route_waves<RE>(dp, topk, R, pub, lane, w, nw, t_ready);
+    __syncthreads();  // the rows, their sums and the routing
+    PG_MARK(1, 6);
     if (rt.xsum_out && blockIdx.x == 0 && blockIdx.y == 0)
         for (int i = tid; i < M * srs; i += nth) rt.xsum_out[i] = xss[i];
     // 3. the block's active slots a = blockIdx.y, + gridDim.y, ...: expert and pairs (the
@@ -966,7 +970,13 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     const int row = blockIdx.x * RB + r;  // < row_groups(N) * 64: padded tile rows are readable
     const int nit = 2 * nb;
     for (int a = blockIdx.y;; a += gridDim.y) {
-        const SlotInfo si = MODE == kRoute ? slot_info(R, M, a, lane, w == 0 && pub && a == 0) : slot_plain(dp, a, topk);
+        SlotInfo si;
+        if constexpr (MODE == kRoute && TM == 1)
+            si = pub ? slot_info<1>(R, M, a, lane, w == 0 && a == 0) : slot_info1(R, a, topk);
+        else if constexpr (MODE == kRoute)
+            si = slot_info<TM>(R, M, a, lane, w == 0 && pub && a == 0);
+        else
+            si = slot_plain<MODE>(dp, a, topk);
         if (si.e < 0) break;  // uniform over the block
         PG_MARK(1, 2);
         // items, two per wave at a time (both quarters' loads in flight together)
@@ -1015,8 +1025,11 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     }
     // block (0, 0) publishes the routing last: its stores then stay off the block's own
     // critical path (a barrier would wait for them)
-    if (pub) publish_route(R, M, dp.E, topk, dp.desc, dp.flat);
+    if constexpr (fused)
+        if (pub) publish_route(R, M, dp.E, topk, dp.desc, dp.flat);
     PG_MARK(1, 5);
+    PG_SET(7, t_ready);
+    PG_FLUSH(1);
 }
 
 // Fused down + combine.  Block = 8 output rows for all M tokens; lane = (row r = lane & 7,
@@ -1072,6 +1085,7 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
     float* iss = xs + P * xrs;
     const int r = lane & 7, p = (lane >> 3) & 3, u = lane >> 5;
     const int row = blockIdx.x * RB + r;
+    PG_DECL;
     PG_MARK(3, 0);
     // 1. the experts of this lane's first two items straight from the descriptor, then
     //    their weights, then the inter rows and the pair table behind them: the weights'
@@ -1135,6 +1149,7 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
         }
     }
     PG_MARK(3, 4);
+    PG_FLUSH(3);
 }
 
 // Per-expert down GEMV: partial[p, row] = w[perm[p]] * (inter_p . d_row) for the pairs of
@@ -1291,9 +1306,20 @@ inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const flo
         const int rows = dp.E + (rt.extra_w ? 1 : 0);
         gy = gy > div_up(rows, gx * W) ? gy : div_up(rows, gx * W);
     }
-    PG_LAUNCH((dec_gu_kernel<QT, TM>), dim3(gx, gy), dim3(64 * W),
-              gu_lds_bytes(dp.M, g.K), st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt,
-              inter, isum);
+#define PG_GU(MODE, RE)                                                                                       \
+    PG_LAUNCH((dec_gu_kernel<QT, TM, MODE, RE>), dim3(gx, gy), dim3(64 * W), gu_lds_bytes(dp.M, g.K), st, g.base, \
+              u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt, inter, isum)
+    if (dp.mode == kRoute) {
+        if (dp.E <= 128)
+            PG_GU(kRoute, 2);
+        else
+            PG_GU(kRoute, 8);
+    } else if (dp.mode == kIdent) {
+        PG_GU(kIdent, 1);
+    } else {
+        PG_GU(kDispatch, 1);
+    }
+#undef PG_GU
 }
 
 template <int QT, int RB, int W, int TM>

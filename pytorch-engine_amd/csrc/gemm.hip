@@ -322,6 +322,7 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
     __shared__ int rowsrc[kGM];
     __shared__ float rowscale[kGM];  // down: rs[p] * topk_w[perm[p]] of every tile row
     int mt, nt;
+    PG_DECL;
     PG_MARK(GATEUP ? 4 : 5, 0);
     if (!gemm_tile_of(blockIdx.x, n_ntiles, tile_off[E], mt, nt)) return;
     const int e = gemm_tile_expert(tile_off, E, mt);
@@ -487,6 +488,7 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
             }
     }
     PG_MARK(GATEUP ? 4 : 5, 5);
+    PG_FLUSH(GATEUP ? 4 : 5);
 }
 
 int gemm_tile_pairs() { return kGM; }

@@ -24,6 +24,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
                                                             const float* __restrict__ extra_w,
                                                             float* __restrict__ extra_out,
                                                             float* __restrict__ xsum, int rblocks) {
+    PG_DECL;
     PG_MARK(0, 0);
     if ((int)blockIdx.x >= rblocks) {
         const int i = (blockIdx.x - rblocks) * blockDim.x + threadIdx.x;
@@ -61,6 +62,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const uint16_t* __re
             }
         }
     PG_MARK(0, 1);
+    PG_FLUSH(0);
 }
 
 // Prefill logits (M > 8, no extra row): the same arithmetic as router_logits_kernel, tiled
