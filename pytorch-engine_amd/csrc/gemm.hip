@@ -1,25 +1,30 @@
 // Prefill (M > 8) grouped expert products on the MFMA cores.
 //
-// A tile is 256 sorted pairs of one expert x 256 output columns.  The block is 8 waves
-// (two per SIMD), each owning 128 rows x 64 columns as 4 x 2 v_mfma_f32_32x32x16_f16
-// tiles (128 fp32 accumulators per lane).  The K loop steps one 64-weight unit at a
-// time through a ring of three LDS stages filled by direct HBM -> LDS copies two units
+// A tile is 256 sorted pairs of one expert x 256 output columns.  The block is 4 waves
+// (one per SIMD; each owns all 256 rows x 64 columns, 256 fp32 accumulators per lane in
+// AGPRs, so every B column is decoded once) or 8 waves (two per SIMD; 128 rows x 64
+// columns each, every B column decoded by two waves), as 8 x 2 or 4 x 2
+// v_mfma_f32_32x32x16_f16 tiles per wave.  The K loop steps one 64-weight unit at a time
+// through a ring of three LDS stages filled by direct HBM -> LDS copies three units
 // ahead: the fp16 activation rows (16-byte slots XOR-swizzled by row) and the raw GGUF
 // bytes of the 256 weight rows (whole 1 KB chunks of the 64-row tile layout, with their
 // scale chunks).  Each wave decodes its own B fragments from the raw bytes in registers
-// (w = a * code + c in fp32, one rounding to fp16) one k16 group ahead of the MFMAs
-// that use them.  One barrier per unit.
+// (w = a * code + c in fp32, one rounding to fp16) one k16 group ahead of the MFMAs that
+// use them, across unit boundaries.  One barrier per unit.
 //   gate/up: A = x rows gathered through perm (fp16), B = 128 gate rows + 128 up rows of
 //            the same intermediate indices, arranged so every wave holds matching gate
 //            and up columns; epilogue = SwiGLU in fp32 -> inter [P][I].
 //   down   : A = a16 [P][I] (the row-scaled fp16 SwiGLU rows), B = 256 down rows;
 //            epilogue = partial[p][h] = w_p * rs_p * acc.
 // Tiles: the dispatch's tile_off counts 256-row tiles per expert; the last tile of an
-// expert holds the remainder (1..256 rows, waves past it skip their MFMAs).  Block ids
-// are ordered so the N tiles of one M tile run back to back on one XCD (blocks go to the
-// 8 XCDs round-robin), so its gathered A rows are shared through that XCD's L2.
+// expert holds the remainder (1..256 rows; 32-row slices past it skip their MFMAs and,
+// with 4 waves, their activation copies).  Block ids are ordered so the N tiles of one M
+// tile run back to back on one XCD (blocks go to the 8 XCDs round-robin), so its
+// gathered A rows are shared through that XCD's L2.
 // Reference: GGUFQuantMoEExperts.forward_expert (quant_kernels.py:1990-2011) ->
 // exec_w4a16_matmul / exec_w8a16_matmul (:1165-1420) and model.py:916-919.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -68,13 +73,16 @@ template <> struct GStage<PGMOE_Q8_0> {
 // then B: row group bg, chunk cc (cc = CH: scales) at kGA + (bg * (CH + 1) + cc) * 1024,
 // Q6_K d of row group bg at kGA + 4 * (CH + 1) * 1024 + 128 bg.
 constexpr int kGA = kGM * 128;
-// CT = 32-column B tiles per wave: the block's 256 x 256 tile is cut into 2 x (8 / CT)
-// wave tiles of 128 rows x 32 CT columns (CT = 2: 8 waves, two per SIMD; CT = 4: 4 waves,
-// accumulators in AGPRs).
-template <int QT, int CT>
+// CT = 32-column B tiles per wave, WM = waves along M: the block's 256 x 256 tile is cut
+// into WM x (8 / CT) wave tiles of 256 / WM rows x 32 CT columns.  WM = 2, CT = 2: 8 waves,
+// two per SIMD, each B column decoded by both waves of its column; WM = 1, CT = 2: 4 waves,
+// one per SIMD, every B column decoded once (256 accumulators per lane, in AGPRs).
+template <int QT, int CT, int WM>
 struct GLay {
     static constexpr int CH = GStage<QT>::CH;
-    static constexpr int NW = 16 / CT;                              // waves
+    static constexpr int NW = WM * 8 / CT;                          // waves
+    static constexpr int WN = 8 / CT;                               // waves along N
+    static constexpr int RS = 8 / WM;                               // 32-row slices per wave
     static constexpr int SLOTS = 4 * (CH + 1) + GStage<QT>::DPL;  // 1 KB copies for B
     static constexpr int AQ = 32 / NW;                              // A copies per wave
     static constexpr int BQ = (SLOTS + NW - 1) / NW;                // B copies per wave
@@ -249,74 +257,101 @@ __device__ __forceinline__ int gemm_tile_expert(const int32_t* tile_off, int E, 
     return lo;
 }
 
-// ---------------------------------------------------------------- one unit of MFMAs
-// Wave (wm, wn): rows 128 wm + 32 i (i < NI, the 32-row slices holding pairs), CT column
-// tiles j.  Group g = k16 slice g of the unit: A fragment lane l = row l % 32, k chunk
+// ---------------------------------------------------------------- the unit loop
+// Wave (wm, wn): rows 32 RS wm + 32 i (i < NI, the 32-row slices holding pairs), CT
+// column tiles j.  Group g = k16 slice g of a unit: A fragment lane l = row l % 32, k chunk
 // 2g + l / 32 (slot (2g + l/32) ^ (row & 7)); B fragment = the lane's column's group g,
 // weights 8(l/32) .. +8.  Register v of D is D[8(v/4) + 4(l/32) + v%4][l%32].
-// A fragments and B decodes run one group ahead of the MFMAs that use them, spread
-// between those MFMAs (a wave issues in order; each MFMA runs while the next few VALU
-// instructions issue).
-template <int QT, int NI, int CT>
-__device__ __forceinline__ void gemm_unit(const uint8_t* S, const GCol<QT> (&col)[CT], int wm, int lane,
-                                          gf16 (&acc)[4][CT]) {
+// The groups of all units form one stream: the A fragments and B decode of group q + 1 are
+// issued between the MFMAs of group q (a wave issues in order; each MFMA runs while the
+// next few VALU / LDS instructions issue).  The one barrier of a unit comes before its last
+// group's MFMAs: every read of the unit's stage has then been issued and waited for, so the
+// barrier both publishes the next unit's stage (its copies waited for by vm_wait) and
+// frees this one, which takes the copies of unit u + 3.  The next unit's scales and its
+// first group are decoded under the last group's MFMAs.
+// AC = A copies per wave per unit (the copies of empty 32-row slices are skipped when the
+// wave copies whole slices), BQ = B copies: a wave has AC + BQ copies in flight per unit.
+template <int QT, int NI, int CT, int RS, int AC, int BQ, int STAGE, class CopyF>
+__device__ __forceinline__ void gemm_loop(const uint8_t* smem, int units, const int (&bg)[CT], const int (&rig)[CT],
+                                          int wm, int lane, gf16 (&acc)[RS][CT], CopyF& copy_unit) {
+    constexpr int VM = AC + BQ;
+    constexpr int NA = NI > 0 ? NI : 1;
+    // VALU instructions (B decode) placed after each MFMA: about 16 CT + 16 per group
+    constexpr int VPM = (16 * CT + 16 + CT * NA - 1) / (CT * NA);
     const int h = lane >> 5;
-    gh8 af[2][NI], bf[2][CT];
-    auto stage = [&](int g, gh8 (&a)[NI], gh8 (&b)[CT]) {
-        const int kc = 2 * g + h;
+    // row r = 32 RS wm + 32 i + l%32 has r & 7 = l & 7: one address per group, the 32-row
+    // slices at immediate offsets 4096 i
+    const int aoff = (32 * RS * wm + (lane & 31)) * 128;
+    GCol<QT> col[CT];
+    gh8 af[2][NA], bf[2][CT];
+    auto cols = [&](const uint8_t* S, int u) {  // every LDS read of the columns, then the scales
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            const int r = 128 * wm + 32 * i + (lane & 31);
-            a[i] = *(const gh8*)(S + r * 128 + 16 * (kc ^ (r & 7)));
-        }
+        for (int j = 0; j < CT; ++j) col[j].fetch(S + kGA, bg[j], rig[j], h, u);
+#pragma unroll
+        for (int j = 0; j < CT; ++j) col[j].prep(u);
+    };
+    auto frag = [&](const uint8_t* S, int g, gh8 (&a)[NA], gh8 (&b)[CT]) {
+        const uint8_t* p = S + aoff + 16 * ((2 * g + h) ^ (lane & 7));
+#pragma unroll
+        for (int i = 0; i < NI; ++i) a[i] = *(const gh8*)(p + 4096 * i);
 #pragma unroll
         for (int j = 0; j < CT; ++j) b[j] = col[j].group(g);
     };
-    stage(0, af[0], bf[0]);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-        if (g < 3) stage(g + 1, af[(g + 1) & 1], bf[(g + 1) & 1]);
-#pragma unroll
-        for (int i = 0; i < NI; ++i)
-#pragma unroll
-            for (int j = 0; j < CT; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[g & 1][i], bf[g & 1][j], acc[i][j], 0, 0, 0);
-        if (g < 3) {
-#pragma unroll
-            for (int k = 0; k < CT * NI; ++k) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-                if (k < NI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
-                __builtin_amdgcn_sched_group_barrier(0x002, (5 * CT) / NI, 0);  // VALU
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-// The lane's CT B columns of a unit: row group bg[j], row rig[j] in it.
-template <int QT, int NI, int CT>
-__device__ __forceinline__ void gemm_unit_b(const uint8_t* S, const int (&bg)[CT], const int (&rig)[CT], int u,
-                                            int wm, int lane, gf16 (&acc)[4][CT]) {
+    const std::integral_constant<int, AC> ac;
+    copy_unit(ac, 0, 0);
+    copy_unit(ac, 1, 1);
+    copy_unit(ac, 2, 2);
+    vm_wait<2 * VM>();  // this wave's copies of unit 0 landed
+    lds_barrier();      // and every wave's
     if constexpr (NI > 0) {
-        // every LDS read of the columns first, one wait, then the scales
-        GCol<QT> col[CT];
+        cols(smem, 0);
+        frag(smem, 0, af[0], bf[0]);
+    }
+    for (int u = 0, st = 0; u < units; ++u) {
+        const int sn = st == 2 ? 0 : st + 1;
+        const uint8_t* S = smem + st * STAGE;
+        const uint8_t* Sn = smem + sn * STAGE;
 #pragma unroll
-        for (int j = 0; j < CT; ++j) col[j].fetch(S + kGA, bg[j], rig[j], lane >> 5, u);
+        for (int g = 0; g < 4; ++g) {
+            if (g == 3) {
+                vm_wait<VM>();
+                lds_barrier();
+                copy_unit(ac, u + 3, st);
+            }
+            if constexpr (NI > 0) {
+                if (g < 3) {
+                    frag(S, g + 1, af[(g + 1) & 1], bf[(g + 1) & 1]);
+                } else {  // the next unit (past the last one: unused reads of a stale stage)
+                    cols(Sn, u + 1);
+                    frag(Sn, 0, af[0], bf[0]);
+                }
 #pragma unroll
-        for (int j = 0; j < CT; ++j) col[j].prep(u);
-        gemm_unit<QT, NI, CT>(S, col, wm, lane, acc);
+                for (int i = 0; i < NI; ++i)
+#pragma unroll
+                    for (int j = 0; j < CT; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[g & 1][i], bf[g & 1][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int k = 0; k < CT * NI; ++k) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                    if (k < NI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);  // VALU
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        st = sn;
     }
 }
 
 // ---------------------------------------------------------------- the kernel
-template <int QT, bool GATEUP, int CT>
-__global__ __launch_bounds__(1024 / CT) void gemm_kernel(
+template <int QT, bool GATEUP, int CT, int WM>
+__global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, int64_t wstride0, int64_t wstride1,
     int N, int K, const uint16_t* __restrict__ act, int topk, int E, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm, const int32_t* __restrict__ tile_off, int n_ntiles,
     const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out) {
-    using L = GLay<QT, CT>;
-    constexpr int NW = L::NW, HW = NW / 2;
+    using L = GLay<QT, CT, WM>;
+    constexpr int NW = L::NW, WN = L::WN, RS = L::RS, WR = 32 * RS;  // WR rows per wave
     constexpr int CH = L::CH;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * L::STAGE];
     __shared__ int rowsrc[kGM];
@@ -324,13 +359,15 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
     int mt, nt;
     PG_DECL;
     PG_MARK(GATEUP ? 4 : 5, 0);
+    PG_SET(6, 1u + (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4));  // HW_ID (CU, SIMD, wave)
+    PG_SET(7, 1u + (uint32_t)__builtin_amdgcn_s_getreg((15 << 11) | 20));  // XCC_ID
     if (!gemm_tile_of(blockIdx.x, n_ntiles, tile_off[E], mt, nt)) return;
     const int e = gemm_tile_expert(tile_off, E, mt);
     const int m0 = offsets[e] + (mt - tile_off[e]) * kGM;
     const int mrows = min(kGM, offsets[e + 1] - m0);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / HW, wn = wave % HW;  // waves w and w + HW: same columns
+    const int wm = wave / WN, wn = wave % WN;  // waves w and w + WN: same columns
     const int units = K >> 6, nb = K >> 8;
     // A source rows: gate/up gathers token rows of x, down reads its own pair rows.  Rows
     // past the tile's pairs repeat its last pair: they only feed accumulator rows that
@@ -382,11 +419,11 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
     }
     const uint32_t sbase = lds_addr(smem);
     // Issue every copy of unit u into stage st (u clamped: the last steps repeat it).
-    auto copy_unit = [&](int u, int st) {
+    auto copy_unit = [&](auto ac, int u, int st) {  // ac: A copies (integral_constant)
         u = min(u, units - 1);
         const uint32_t S = sbase + st * L::STAGE;
 #pragma unroll
-        for (int q = 0; q < L::AQ; ++q)
+        for (int q = 0; q < decltype(ac)::value; ++q)
             g2l(arow[q] + Fmt<QT>::col(u, akc >> 1) + 8 * (akc & 1), S + (wave + NW * q) * 1024);
 #pragma unroll
         for (int q = 0; q < L::BQ; ++q) {
@@ -401,15 +438,15 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
         }
     };
 
-    gf16 acc[4][CT];
+    gf16 acc[RS][CT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RS; ++i)
 #pragma unroll
         for (int j = 0; j < CT; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-    const bool active = 128 * wm < mrows;
-    const int ni = active ? min(4, (mrows - 128 * wm + 31) >> 5) : 0;  // 32-row slices with pairs
+    const bool active = WR * wm < mrows;
+    const int ni = active ? min(RS, (mrows - WR * wm + 31) >> 5) : 0;  // 32-row slices with pairs
     // the lane's CT B columns (j): gate/up: j < CT/2 gate tile column c = 16 CT wn + 32j +
     // l%32 (rows nt*128 + c), j >= CT/2 the same up columns; down: tile column
     // c = 32 CT wn + 32j + l%32 (rows nt*256 + c).  Row group c / 64 (+ 2 for up), row c % 64.
@@ -422,25 +459,19 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
         rigj[j] = c & 63;
     }
 
-    // ---- pipeline: three stages, copies two units ahead.  Step u: wait for this wave's
-    // copies of unit u (those of unit u + 1 may still fly), barrier (every wave's copies
-    // landed; every wave is done with unit u - 1's stage), copy unit u + 2 into that
-    // stage, compute unit u.
-    // The loop is instantiated per NI (a whole copy each) so the register allocation of
-    // one copy never has to merge the others'.
+    // ---- pipeline: three stages; unit u + 3 is copied into unit u's stage once every wave
+    // is done with it (see gemm_loop).  The loop is instantiated per NI (a whole copy each)
+    // so the register allocation of one copy never has to merge the others'.
     PG_MARK(GATEUP ? 4 : 5, 1);
-    copy_unit(0, 0);
-    copy_unit(1, 1);
-#define PG_GLOOP(NI_)                                                                        \
-    for (int u = 0, st = 0; u < units; ++u, st = st == 2 ? 0 : st + 1) {                    \
-        if (u == units / 4) PG_MARK(GATEUP ? 4 : 5, 2);                                      \
-        if (u == (3 * units) / 4) PG_MARK(GATEUP ? 4 : 5, 3);                                \
-        vm_wait<L::VM>();                                                                    \
-        lds_barrier();                                                                       \
-        copy_unit(u + 2, st == 0 ? 2 : st - 1);                                             \
-        gemm_unit_b<QT, NI_, CT>(smem + st * L::STAGE, bgj, rigj, u, wm, lane, acc);         \
-    }
+    // With one wave along M (NW = 4) wave w copies row octet w of every 32-row slice q, so
+    // the slices without pairs (q >= ni) are not copied at all; with two, every slice is.
+#define PG_GLOOP(NI_) \
+    gemm_loop<QT, NI_, CT, RS, WM == 1 ? NI_ : L::AQ, L::BQ, L::STAGE>(smem, units, bgj, rigj, wm, lane, acc, copy_unit);
     switch (ni) {
+    case 8: if constexpr (RS == 8) { PG_GLOOP(8) } break;
+    case 7: if constexpr (RS == 8) { PG_GLOOP(7) } break;
+    case 6: if constexpr (RS == 8) { PG_GLOOP(6) } break;
+    case 5: if constexpr (RS == 8) { PG_GLOOP(5) } break;
     case 4: PG_GLOOP(4) break;
     case 3: PG_GLOOP(3) break;
     case 2: PG_GLOOP(2) break;
@@ -461,10 +492,10 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
             const int col = nt * (kGN / 2) + 16 * CT * wn + 32 * j + (lane & 31);
             if (col < N) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < RS; ++i)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        const int r = 128 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                        const int r = WR * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                         if (r < mrows) out[(int64_t)(m0 + r) * N + col] = silu_fast(acc[i][j][v]) * acc[i][j + CT / 2][v];
                     }
             }
@@ -472,10 +503,10 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
     } else {
         const int c0 = nt * kGN + 32 * CT * wn + (lane & 31);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RS; ++i)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int r = 128 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int r = WR * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 if (r >= mrows) continue;
                 const int p = m0 + r;
                 const float sc = rowscale[r];
@@ -493,14 +524,21 @@ __global__ __launch_bounds__(1024 / CT) void gemm_kernel(
 
 int gemm_tile_pairs() { return kGM; }
 
-// Column tiles per wave of each product (build-time choices; 2 = 8 waves, 4 = 4 waves).
-// Measured on the Qwen3 Zipf prefill: 8 waves is faster for both (the second wave of a
-// SIMD issues its decode VALU and LDS reads while the first one's MFMAs run).
+// Wave layout of each product (build-time choices): CT column tiles per wave, WM waves
+// along M.  Measured on the Qwen3 Zipf prefill (M = 4096): gate/up (K = 2048, Q4_K) is
+// fastest with 4 waves (WM = 1: half the B decode per SIMD, no copies of empty slices),
+// down (K = 768, Q6_K) with 8 (WM = 2: 231 us against 278 us with 4).
 #ifndef PG_GU_CT
 #define PG_GU_CT 2
 #endif
 #ifndef PG_DN_CT
 #define PG_DN_CT 2
+#endif
+#ifndef PG_GU_WM
+#define PG_GU_WM 1
+#endif
+#ifndef PG_DN_WM
+#define PG_DN_WM 2
 #endif
 
 // Upper bound of 256-row tiles for P pairs over at most E experts, rounded up to whole
@@ -518,7 +556,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
     const int nnt = div_up(g.N, kGN / 2);
     const dim3 grid(gemm_max_mtiles(P, E) * nnt);
 #define PG_GU(QT)                                                                                               \
-    PG_LAUNCH((gemm_kernel<QT, true, PG_GU_CT>), grid, dim3(64 * GLay<QT, PG_GU_CT>::NW), 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
+    PG_LAUNCH((gemm_kernel<QT, true, PG_GU_CT, PG_GU_WM>), grid, dim3(64 * GLay<QT, PG_GU_CT, PG_GU_WM>::NW), 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
               E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter)
     switch (g.qtype) {
     case PGMOE_Q4_K: PG_GU(PGMOE_Q4_K); break;
@@ -539,7 +577,7 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     const int nnt = div_up(d.N, kGN);
     const dim3 grid(gemm_max_mtiles(P, E) * nnt);
 #define PG_DN(QT)                                                                                               \
-    PG_LAUNCH((gemm_kernel<QT, false, PG_DN_CT>), grid, dim3(64 * GLay<QT, PG_DN_CT>::NW), 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
+    PG_LAUNCH((gemm_kernel<QT, false, PG_DN_CT, PG_DN_WM>), grid, dim3(64 * GLay<QT, PG_DN_CT, PG_DN_WM>::NW), 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
               topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial)
     switch (d.qtype) {
     case PGMOE_Q4_K: PG_DN(PGMOE_Q4_K); break;
