@@ -36,7 +36,8 @@ for p in (REPO, os.path.join(REPO, "pytorch-engine_amd")):
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 METRIC = "MoE layer tok/s at M=1 and M=4096 (Qwen3-30B-A3B shape); % HBM / MFMA roofline"
-TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_dec_gu_qwen3_m1.json")
+TRAFFIC_FILES = [os.path.join(REPO, "profiles", f) for f in ("traffic_dec_moe_qwen3_m1.json",
+                                                               "traffic_dec_gu_qwen3_m1.json")]
 
 
 def log(msg: str) -> None:
@@ -213,13 +214,17 @@ def cpu_baseline(lay, M: int, seconds: float):
                       f"F.linear, fp16 casts kept), {el:.1f} s on {cores} threads"}
 
 
-def load_traffic():
-    try:
-        with open(TRAFFIC_FILE) as f:
-            rec = json.load(f)
-        return rec.get("bytes_per_launch"), rec
-    except (OSError, ValueError):
-        return None, None
+def load_traffic(kernel: str):
+    """Counter-derived HBM bytes per launch of `kernel` (a kernel-name prefix), if profiled."""
+    for path in TRAFFIC_FILES:
+        try:
+            with open(path) as f:
+                rec = json.load(f)
+        except (OSError, ValueError):
+            continue
+        if rec.get("kernel", "").split("pgmoe::")[-1].startswith(kernel):
+            return rec.get("bytes_per_launch"), rec
+    return None, None
 
 
 def main() -> int:
@@ -283,18 +288,27 @@ def main() -> int:
                      "active_weight_bytes": base.active_weight_bytes(n_act)}
         log(f"[bench] decode M={M}: {decode[M]}")
 
-    # dominant kernel at M = 1: the routed gate/up, launch 0 of (gate/up with the router
-    # folded in, down + combine); its algorithmic bytes are the active experts' gate/up GGUF
-    # bytes plus the fp32 router weights it reads
+    # dominant kernel at M = 1: the whole layer in one launch (dec_moe_kernel: router, routing,
+    # gate/up + SwiGLU, down + combine) when the layer's formats have the fused kernel, else
+    # the routed gate/up launch of (gate/up with the router folded in, down + combine).  Its
+    # algorithmic bytes: the active experts' GGUF bytes of the matrices it reads plus the fp32
+    # router weights.
     d1 = decode[1]
-    gu_us = d1["kernel_us"][0]
-    gu_bytes = (d1["active_experts"] * (base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat)
-                + spec.n_experts * spec.hidden * 4)
-    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
-    dn_us = d1["kernel_us"][1]
-    dn_bytes = d1["active_experts"] * base.down_exps.gguf_bytes_per_mat
+    ku = d1["kernel_us"]
+    router_bytes = spec.n_experts * spec.hidden * 4
+    gu_mat = base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat
+    if len(ku) == 1:
+        dom_kernel, dom_names = "dec_moe_kernel", ["dec_moe"]
+        dom_desc = "dec_moe_kernel (router + routing + gate/up + SwiGLU + down + combine in one launch), M=1"
+        dom_bytes = d1["active_weight_bytes"] + router_bytes
+    else:
+        dom_kernel, dom_names = "dec_gu_kernel", ["dec_gu", "dec_dc"]
+        dom_desc = "dec_gu_kernel (router + routing + gate/up + SwiGLU), M=1"
+        dom_bytes = d1["active_experts"] * gu_mat + router_bytes
+    dom_us = ku[0]
+    dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
     layer_gbs = d1["active_weight_bytes"] / (d1["us_per_step"] * 1e-6) / 1e9
-    traffic, traffic_rec = load_traffic()
+    traffic, traffic_rec = load_traffic(dom_kernel)
 
     # ---- prefill M = 4096 with the Zipf router bias (config 3)
     prefill = None
@@ -349,15 +363,13 @@ def main() -> int:
         "config": {"workload": "qwen3_30b_a3b MoE layer decode, M=1 token per step (H=2048, E=128, top-8, "
                                "I=768, gate/up Q4_K, down Q6_K, fp16 activations, fp32 accumulate)",
                    "weight_copies": args.copies, "timing": "one forward per HIP graph replay"},
-        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "dec_gu_kernel (router + routing + gate/up + SwiGLU), M=1",
-                     "algorithmic_bytes": gu_bytes, "kernel_us": gu_us,
+        "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": dom_desc, "algorithmic_bytes": dom_bytes, "kernel_us": dom_us,
                      "traffic_source": traffic_rec.get("source") if traffic_rec else None},
         "cpu_baseline": cpu,
         "decode": {str(k): v for k, v in decode.items()},
-        "kernels_m1": {"names": ["dec_gu", "dec_dc"], "us": d1["kernel_us"],
-                       "down_combine_gbs": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1),
+        "kernels_m1": {"names": dom_names, "us": ku,
                        "layer_active_gbs": round(layer_gbs, 1),
                        "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "prefill": prefill,
