@@ -10,20 +10,21 @@ constexpr int kDispThreads = 1024;
 constexpr int kDispWaves = kDispThreads / 64;
 constexpr int kMaxExperts = 512;  // keeps the per-(wave, expert) counters at 32 KB of LDS
 
-// Inclusive scan of one int per thread over the block (Hillis-Steele in LDS).
+// Inclusive scan of one int per thread over the block: a shuffle scan inside each wave,
+// then the wave totals (two barriers).  buf: kDispWaves ints.
 __device__ int block_inclusive_scan(int v, int* buf) {
-    const int t = threadIdx.x;
-    buf[t] = v;
-    __syncthreads();
-    for (int off = 1; off < kDispThreads; off <<= 1) {
-        const int add = t >= off ? buf[t - off] : 0;
-        __syncthreads();
-        buf[t] += add;
-        __syncthreads();
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(v, off);
+        if (lane >= off) v += o;
     }
-    const int r = buf[t];
+    if (lane == 63) buf[wv] = v;
     __syncthreads();
-    return r;
+    int base = 0;
+    for (int w = 0; w < wv; ++w) base += buf[w];
+    __syncthreads();  // buf is reused by the next scan
+    return v + base;
 }
 
 // kDispBatch ids per lane of the chunk [b0, c1) (pair f = b0 + 64k + lane; -1 past c1).
@@ -37,10 +38,23 @@ __device__ __forceinline__ void load_batch(const int32_t* __restrict__ idx, int 
     }
 }
 
+// Lanes of the wave holding the same valid id (0 for an invalid one): the intersection of
+// ballots over the id's nbits bits.
+__device__ __forceinline__ uint64_t same_id_lanes(int id, bool valid, int nbits) {
+    uint64_t same = __ballot(valid);
+    if (!valid) same = 0;
+    for (int b = 0; b < nbits; ++b) {
+        const bool bit = valid && ((id >> b) & 1);
+        const uint64_t m = __ballot(bit);
+        same &= bit ? m : ~m;
+    }
+    return same;
+}
+
 // Single workgroup.  Flat pair ids f = t*K + k are split into kDispWaves contiguous
 // chunks, one per wavefront.  Pass 1 counts ids per (wave, expert); a scan turns the
-// counts into per-(wave, expert) base positions; pass 2 walks each chunk in order,
-// 64 ids at a time, ranking equal ids among the lanes with ballots, which keeps the sort
+// counts into per-(wave, expert) base positions; pass 2 walks each chunk
+// in order, 64 ids at a time, ranking equal ids among the lanes, which keeps the sort
 // stable (ascending f inside every expert, the order torch.where produces).
 __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* __restrict__ idx, int P, int E,
                                                                 int tile_rows, int32_t* __restrict__ offsets,
@@ -50,14 +64,17 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
                                                                 int32_t* __restrict__ n_active,
                                                                 int32_t* __restrict__ tile_off) {
     __shared__ int cnt[kDispWaves][kMaxExperts];
-    __shared__ int scan_buf[kDispThreads];
+    __shared__ int scan_buf[kDispWaves];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    int nbits = 0;  // bits of the largest id E - 1
+    while ((1 << nbits) < E) ++nbits;
     for (int i = t; i < kDispWaves * kMaxExperts; i += kDispThreads) (&cnt[0][0])[i] = 0;
     __syncthreads();
     const int chunk = (P + kDispWaves - 1) / kDispWaves;
     const int c0 = wv * chunk, c1 = min(P, c0 + chunk);
-    // ids outside [0, E) are skipped (never written to LDS or to perm/inv).  A wave reads
-    // its chunk kDispBatch ids per lane at a time, every load of a batch in flight at once.
+    // ids outside [0, E) are skipped (never counted, never written to perm/inv).  A wave
+    // reads its chunk kDispBatch ids per lane at a time, every load of a batch in flight
+    // at once.
     for (int b0 = c0; b0 < c1; b0 += 64 * kDispBatch) {
         int ids[kDispBatch];
         load_batch(idx, b0, c1, lane, ids);
@@ -90,12 +107,11 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
     if (has) active[ai - 1] = e;
     if (e == E - 1) *n_active = ai;
     const int nt = (e < E) ? (total + tile_rows - 1) / tile_rows : 0;
-    const int ti = block_inclusive_scan(nt, scan_buf);
+    const int ti = block_inclusive_scan(nt, scan_buf);  // its barriers also publish the bases
     if (e < E) {
         tile_off[e] = ti - nt;
         if (e == E - 1) tile_off[E] = ti;
     }
-    __syncthreads();
 
     // pass 2: stable scatter, each wave over its own chunk and its own bases (no block
     // barrier needed), in steps of 64 ascending ids
@@ -106,20 +122,10 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
         for (int k = 0; k < kDispBatch; ++k) {
             const int f = b0 + 64 * k + lane;
             const int id = ids[k];
-            const bool valid = (unsigned)id < (unsigned)E;
-            // lanes holding the same id: intersect ballots over the id's bits
-            uint64_t same = __ballot(valid);
-            if (!valid) same = 0;
-#pragma unroll
-            for (int b = 0; b < 9; ++b) {  // E <= 512 -> ids < 2^9
-                const bool bit = valid && ((id >> b) & 1);
-                const uint64_t m = __ballot(bit);
-                same &= bit ? m : ~m;
-            }
-            if (valid) {
+            const uint64_t same = same_id_lanes(id, (unsigned)id < (unsigned)E, nbits);
+            if (same) {
                 const uint64_t below = same & ((1ull << lane) - 1ull);
-                const int rank = __popcll(below);
-                const int pos = cnt[wv][id] + rank;
+                const int pos = cnt[wv][id] + __popcll(below);
                 perm[pos] = f;
                 inv[f] = pos;
                 if ((same >> lane) == 1ull)  // highest lane of its id group advances the base
