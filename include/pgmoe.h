@@ -28,6 +28,16 @@
  *   Q8_0 (type 8, CH 17):  c0..c15 = the qs of the super-block's 8 Q8_0 blocks in order;
  *                          c16 = their 8 fp16 d
  * pgmoe_relayout_weights() converts GGUF bytes already on the device into this layout.
+ *
+ * Scale plane (pgmoe_weights.scales, K-quants; read only by the mode-1 MFMA products):
+ * the sub-block scales of the layout above decoded once at load time, in fp32, one 1 KB
+ * chunk per (64-row group rg, super-block b, 64-weight unit c = 0..3), matrices
+ * pgmoe_scale_plane_bytes() apart: row r of chunk (rg, b, c) at
+ * scales + ((rg*(K/256) + b)*4 + c)*1024 + r*16 holds four floats
+ *   Q4_K: {a0, c0, a1, c1} of sub-blocks 2c + t: a = d*sc, c = -(dmin*m) - 1024*a
+ *   Q6_K: {a0, a1, a2, a3}: a_g = d * scale[8*(c >> 1) + 2g + (c & 1)]
+ * (the values a lane computes from the chunk bytes otherwise).  pgmoe_build_scale_plane()
+ * writes it from the device layout.
  */
 #ifndef PGMOE_H
 #define PGMOE_H
@@ -39,7 +49,7 @@
 extern "C" {
 #endif
 
-#define PGMOE_ABI_VERSION 1
+#define PGMOE_ABI_VERSION 2
 
 #define PGMOE_OK 0
 #define PGMOE_E_INVALID (-1)     /* bad argument, shape or pointer */
@@ -58,6 +68,8 @@ typedef struct pgmoe_weights {
     int32_t n_mats;     /* experts (1 for a shared expert) */
     const void* base;   /* device layout described above, 16-B aligned */
     int64_t mat_stride; /* bytes between consecutive matrices */
+    const void* scales; /* K-quants: the scale plane of the n_mats matrices (required by the
+                           mode-1 products, unused by mode 0); Q8_0: NULL */
 } pgmoe_weights;
 
 typedef struct pgmoe_layer {
@@ -84,6 +96,17 @@ int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
  * (quant_kernels.py:854-1036), keeping the GGUF bits instead of re-quantising. */
 int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
                            void* dst, void* stream);
+
+/* Bytes of one matrix's scale plane (0 for Q8_0, which has none; -1 if unsupported).  No
+ * counterpart in the reference: it sizes the buffer of pgmoe_build_scale_plane. */
+int64_t pgmoe_scale_plane_bytes(int32_t qtype, int64_t rows, int64_t cols);
+
+/* Scale plane of n_mats matrices in the device layout (src, mat_stride bytes apart) ->
+ * dst (pgmoe_scale_plane_bytes apart).  Load time, next to pgmoe_relayout_weights; no
+ * counterpart in the reference (its repack decodes the scales on the CPU instead,
+ * quant_kernels.py:854-904). */
+int pgmoe_build_scale_plane(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
+                            int64_t mat_stride, void* dst, void* stream);
 
 /* Workspace bytes pgmoe_moe_forward needs for M tokens.  Zero the workspace once when it
  * is allocated: for M <= 8 it begins with the router's ready-tagged logits, which the

@@ -55,6 +55,9 @@ int check_weights(const pgmoe_weights* w, const char* what, Mats* out) {
     out->n_mats = w->n_mats;
     out->base = (const uint8_t*)w->base;
     out->stride = w->mat_stride;
+    out->scales = (const uint8_t*)w->scales;
+    if (out->scales && ((uintptr_t)out->scales & 15))
+        return fail(PGMOE_E_INVALID, "%s: scales must be 16-byte aligned", what);
     return PGMOE_OK;
 }
 
@@ -180,6 +183,22 @@ int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64
     if ((uintptr_t)dst & 255) return fail(PGMOE_E_INVALID, "relayout: dst must be 256-byte aligned");
     return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, (uint8_t*)dst,
                            pgmoe_weight_bytes(qtype, rows, cols), as_stream(stream));
+}
+
+int64_t pgmoe_scale_plane_bytes(int32_t qtype, int64_t rows, int64_t cols) {
+    return scale_plane_bytes(qtype, rows, cols);
+}
+
+int pgmoe_build_scale_plane(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
+                            int64_t mat_stride, void* dst, void* stream) {
+    const int64_t pb = scale_plane_bytes(qtype, rows, cols);
+    if (pb <= 0) return fail(PGMOE_E_UNSUPPORTED, "scale plane: qtype %d with %lld columns", qtype, (long long)cols);
+    if (!src || !dst || n_mats < 1 || rows < 1 || ((uintptr_t)src & 15) || ((uintptr_t)dst & 15))
+        return fail(PGMOE_E_INVALID, "scale plane: bad arguments");
+    if (n_mats > 1 && mat_stride < layout_bytes(qtype, rows, cols))
+        return fail(PGMOE_E_INVALID, "scale plane: mat_stride %lld below the matrix bytes", (long long)mat_stride);
+    return launch_scale_plane(qtype, (const uint8_t*)src, n_mats, rows, cols, mat_stride, (uint8_t*)dst,
+                              as_stream(stream));
 }
 
 size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M) {

@@ -366,10 +366,22 @@ inline int div_up(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // Host-side description of one set of expert matrices, validated.
+// K-quant (scale, min) of sub-block s without branches: both
+// encodings are decoded and s picks one (Q4_K scale bytes: D = 0-3, Mb = 4-7, MD = 8-11).
+__device__ __forceinline__ void kscale_sel(uint32_t D, uint32_t Mb, uint32_t MD, int s, int& sc, int& mn) {
+    const int j = 8 * (s & 3);
+    const int sl = (D >> j) & 63, ml = (Mb >> j) & 63;
+    const uint32_t md = (MD >> j) & 0xff;
+    const int sh = (md & 0x0f) | ((D >> (j + 2)) & 0x30), mh = (md >> 4) | ((Mb >> (j + 2)) & 0x30);
+    sc = s < 4 ? sl : sh;
+    mn = s < 4 ? ml : mh;
+}
+
 struct Mats {
     int qtype, N, K, n_mats;
     const uint8_t* base;
     int64_t stride;
+    const uint8_t* scales;  // scale plane (K-quants; may be null outside the MFMA products)
 };
 int check_weights(const pgmoe_weights* w, const char* what, Mats* out);
 

@@ -39,39 +39,40 @@ typedef uint32_t gu4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float gf16 __attribute__((ext_vector_type(16)));
+typedef float gf4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- staged weight bytes
 // Per 64-weight unit u (see Fmt<QT>) a tile stages, for each of its four 64-row groups,
-// CH chunks of quant bytes plus the row's scale chunk (whole 1 KB tile chunks, straight
-// from the tile layout); Q6_K also stages the fp16 d of the 256 rows.
-//   Q4_K: qs chunks 1 + 2c, 2 + 2c (c = u % 4); scales: chunk 0 (d, dmin, 12 scale bytes)
+// CH chunks of quant bytes plus one scale chunk (whole 1 KB chunks):
+//   Q4_K: qs chunks 1 + 2c, 2 + 2c (c = u % 4); scales: chunk u of the row group's scale
+//         plane ({a, c} of sub-blocks 2c, 2c + 1 in fp32, decoded at load time)
 //   Q6_K: ql chunks 4h + half, 4h + 2 + half, qh chunk 8 + 2h + half ((h, half) =
-//         ((u % 4) >> 1, u & 1)); scales: chunk 12; d: 4 x 128 bytes
-//   Q8_0: chunks 4c .. 4c + 3 (the qs of Q8_0 blocks 2c, 2c + 1); scales: chunk 16
+//         ((u % 4) >> 1, u & 1)); scales: chunk u of the scale plane (a of its four
+//         16-weight sub-blocks)
+//   Q8_0: chunks 4c .. 4c + 3 (the qs of Q8_0 blocks 2c, 2c + 1); scales: tile chunk 16
 // Group g of the unit (k = 16g .. 16g + 15) reads, for the 8 weights 8h .. 8h + 7 of a lane
 // half h, bytes 8h .. 8h + 7 of one staged chunk:
 //   Q4_K: chunk g & 1, nibble g >> 1;  Q6_K: ql chunk g & 1 (nibble g >> 1) and the qh
 //   chunk (bits 2g, 2g + 1);  Q8_0: chunk g.
 template <int QT> struct GStage;
 template <> struct GStage<PGMOE_Q4_K> {
-    static constexpr int CH = 2, HC = 0, DPL = 0;
+    static constexpr int CH = 2, HC = -1;  // HC: tile chunk of the scales (-1: scale plane)
     __device__ static __forceinline__ int chunk(int u, int cc) { return 1 + 2 * (u & 3) + cc; }
 };
 template <> struct GStage<PGMOE_Q6_K> {
-    static constexpr int CH = 3, HC = 12, DPL = 1;
+    static constexpr int CH = 3, HC = -1;
     __device__ static __forceinline__ int chunk(int u, int cc) {
         const int h = (u & 3) >> 1, half = u & 1;
         return cc == 0 ? 4 * h + half : cc == 1 ? 4 * h + 2 + half : 8 + 2 * h + half;
     }
 };
 template <> struct GStage<PGMOE_Q8_0> {
-    static constexpr int CH = 4, HC = 16, DPL = 0;
+    static constexpr int CH = 4, HC = 16;
     __device__ static __forceinline__ int chunk(int u, int cc) { return 4 * (u & 3) + cc; }
 };
 
 // LDS stage: A [256 rows][128 bytes] (16-byte slot s of row r holds k chunk s ^ (r & 7)),
-// then B: row group bg, chunk cc (cc = CH: scales) at kGA + (bg * (CH + 1) + cc) * 1024,
-// Q6_K d of row group bg at kGA + 4 * (CH + 1) * 1024 + 128 bg.
+// then B: row group bg, chunk cc (cc = CH: scales) at kGA + (bg * (CH + 1) + cc) * 1024.
 constexpr int kGA = kGM * 128;
 // CT = 32-column B tiles per wave, WM = waves along M: the block's 256 x 256 tile is cut
 // into WM x (8 / CT) wave tiles of 256 / WM rows x 32 CT columns.  WM = 2, CT = 2: 8 waves,
@@ -83,7 +84,7 @@ struct GLay {
     static constexpr int NW = WM * 8 / CT;                          // waves
     static constexpr int WN = 8 / CT;                               // waves along N
     static constexpr int RS = 8 / WM;                               // 32-row slices per wave
-    static constexpr int SLOTS = 4 * (CH + 1) + GStage<QT>::DPL;  // 1 KB copies for B
+    static constexpr int SLOTS = 4 * (CH + 1);                      // 1 KB copies for B
     static constexpr int AQ = 32 / NW;                              // A copies per wave
     static constexpr int BQ = (SLOTS + NW - 1) / NW;                // B copies per wave
     static constexpr int STAGE = kGA + SLOTS * 1024;
@@ -143,36 +144,21 @@ __device__ __forceinline__ void magic8(uint32_t lo, uint32_t hi, uint32_t (&m)[4
 // group into the MFMA B operand (8 fp16 weights k = 16g + 8h .. +8).
 template <int QT> struct GCol;
 
-// K-quant (scale, min) of sub-block s (uniform) without branches: both encodings are
-// decoded and s picks one.
-__device__ __forceinline__ void kscale_sel(uint32_t D, uint32_t Mb, uint32_t MD, int s, int& sc, int& mn) {
-    const int j = 8 * (s & 3);
-    const int sl = (D >> j) & 63, ml = (Mb >> j) & 63;
-    const uint32_t md = (MD >> j) & 0xff;
-    const int sh = (md & 0x0f) | ((D >> (j + 2)) & 0x30), mh = (md >> 4) | ((Mb >> (j + 2)) & 0x30);
-    sc = s < 4 ? sl : sh;
-    mn = s < 4 ? ml : mh;
-}
-
 template <> struct GCol<PGMOE_Q4_K> {
     u32x2 q[2];
-    u32x4 hd;
+    gf4 sv;            // scale plane: {a, c} of sub-block 2(u%4), then of 2(u%4) + 1
     float a[2], c[2];  // sub-blocks 2(u%4) (groups 0, 1), 2(u%4) + 1 (groups 2, 3)
     __device__ __forceinline__ void fetch(const uint8_t* B, int bg, int rig, int h, int u) {
         const uint8_t* base = B + bg * 3 * 1024 + rig * 16;
         q[0] = *(const u32x2*)(base + 8 * h);
         q[1] = *(const u32x2*)(base + 1024 + 8 * h);
-        hd = *(const u32x4*)(base + 2 * 1024);
+        sv = *(const gf4*)(base + 2 * 1024);
     }
     __device__ __forceinline__ void prep(int u) {
-        const float d = lo_half(hd.x), dm = hi_half(hd.x);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            int sc, mn;
-            kscale_sel(hd.y, hd.z, hd.w, 2 * (u & 3) + t, sc, mn);
-            a[t] = d * (float)sc;
-            c[t] = -(dm * (float)mn) - 1024.0f * a[t];
-        }
+        a[0] = sv.x;
+        c[0] = sv.y;
+        a[1] = sv.z;
+        c[1] = sv.w;
     }
     __device__ __forceinline__ gh8 group(int g) const {
         const u32x2 s = q[g & 1];
@@ -184,25 +170,21 @@ template <> struct GCol<PGMOE_Q4_K> {
 };
 
 template <> struct GCol<PGMOE_Q6_K> {
-    u32x2 q[3], sw;
-    uint16_t db;
+    u32x2 q[3];
+    gf4 sv;  // scale plane: a of the unit's four sub-blocks, in group order
     float a[4];
     __device__ __forceinline__ void fetch(const uint8_t* B, int bg, int rig, int h, int u) {
         const uint8_t* base = B + bg * 4 * 1024 + rig * 16;
         q[0] = *(const u32x2*)(base + 8 * h);
         q[1] = *(const u32x2*)(base + 1024 + 8 * h);
         q[2] = *(const u32x2*)(base + 2 * 1024 + 8 * h);
-        sw = *(const u32x2*)(base + 3 * 1024 + 8 * ((u & 3) >> 1));  // scale bytes 8h6 .. +7
-        db = *(const uint16_t*)(B + 16 * 1024 + bg * 128 + rig * 2);
+        sv = *(const gf4*)(base + 3 * 1024);
     }
     __device__ __forceinline__ void prep(int u) {
-        const int half = u & 1;
-        const float d = h2f(db);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int bi = 2 * g + half;
-            a[g] = d * (float)(int8_t)(((bi < 4 ? sw.x : sw.y) >> (8 * (bi & 3))) & 0xff);
-        }
+        a[0] = sv.x;
+        a[1] = sv.y;
+        a[2] = sv.z;
+        a[3] = sv.w;
     }
     __device__ __forceinline__ gh8 group(int g) const {
         const u32x2 l = q[g & 1], hq = q[2];
@@ -349,7 +331,8 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, int64_t wstride0, int64_t wstride1,
     int N, int K, const uint16_t* __restrict__ act, int topk, int E, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm, const int32_t* __restrict__ tile_off, int n_ntiles,
-    const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out) {
+    const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out,
+    const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1) {
     using L = GLay<QT, CT, WM>;
     constexpr int NW = L::NW, WN = L::WN, RS = L::RS, WR = 32 * RS;  // WR rows per wave
     constexpr int CH = L::CH;
@@ -393,9 +376,15 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
         return GATEUP ? (bg < 2 ? w0 + (int64_t)e * wstride0 : w1 + (int64_t)e * wstride1) : w0 + (int64_t)e * wstride0;
     };
     auto brg = [&](int bg) { return min(GATEUP ? 2 * nt + (bg & 1) : 4 * nt + bg, ngr - 1); };
-    // B copy slots of this wave: s = wave + NW q; slot s < 4 (CH + 1): row group s / (CH + 1),
-    // chunk s % (CH + 1) (CH = the scale chunk); Q6_K slot 4 (CH + 1): the d of all four
-    // row groups; slots past SLOTS repeat slot s - SLOTS (same source, same place).
+    // scale plane of the row group (K-quants): nb * 4 chunks, chunk u for unit u
+    const int64_t pstride = (int64_t)ngr * nb * 4096;
+    auto bplane = [&](int bg) -> const uint8_t* {
+        const uint8_t* pm = GATEUP ? (bg < 2 ? s0 : s1) : s0;
+        return pm + (int64_t)e * pstride + (int64_t)brg(bg) * nb * 4096;
+    };
+    // B copy slots of this wave: s = wave + NW q; slot s: row group s / (CH + 1), chunk
+    // s % (CH + 1) (CH = the scales: a tile chunk, or the scale plane); slots past SLOTS
+    // repeat slot s - SLOTS (same source, same place).
     const uint8_t* bsrc[L::BQ];
     int bkind[L::BQ], bcc[L::BQ];
     uint32_t bdst[L::BQ];
@@ -404,17 +393,14 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
         int s = wave + NW * q;
         if (s >= L::SLOTS) s -= L::SLOTS;
         bdst[q] = s * 1024;
-        if (s < 4 * (CH + 1)) {
-            const int bg = s / (CH + 1), cc = s % (CH + 1);
-            bkind[q] = 0;
-            bcc[q] = cc;
-            bsrc[q] = bmat(bg) + (int64_t)brg(bg) * nb * (Tile<QT>::CH * 1024) + lane * 16;
-        } else {  // Q6_K d plane: lanes 8g .. 8g+7 copy the 128 bytes of row group g
-            const int g = (lane >> 3) & 3;
+        const int bg = s / (CH + 1), cc = s % (CH + 1);
+        bcc[q] = cc;
+        if (cc == CH && GStage<QT>::HC < 0) {  // kind 1: scale plane chunk u
             bkind[q] = 1;
-            bcc[q] = 0;
-            const int64_t dpl = (int64_t)ngr * nb * 13 * 1024;
-            bsrc[q] = bmat(g) + dpl + (int64_t)brg(g) * nb * 128 + (lane & 7) * 16;
+            bsrc[q] = bplane(bg) + lane * 16;
+        } else {  // kind 0: tile chunk of super-block u / 4
+            bkind[q] = 0;
+            bsrc[q] = bmat(bg) + (int64_t)brg(bg) * nb * (Tile<QT>::CH * 1024) + lane * 16;
         }
     }
     const uint32_t sbase = lds_addr(smem);
@@ -432,7 +418,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
                 const int ch = bcc[q] == CH ? GStage<QT>::HC : GStage<QT>::chunk(u, bcc[q]);
                 src = bsrc[q] + (int64_t)(u >> 2) * (Tile<QT>::CH * 1024) + ch * 1024;
             } else {
-                src = bsrc[q] + (int64_t)(u >> 2) * 128;
+                src = bsrc[q] + (int64_t)u * 1024;
             }
             g2l(src, S + kGA + bdst[q]);
         }
@@ -553,11 +539,13 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
+    if (g.qtype != PGMOE_Q8_0 && (!g.scales || !u.scales))
+        return fail(PGMOE_E_INVALID, "gemm gate/up: K-quant weights need their scale plane (pgmoe_build_scale_plane)");
     const int nnt = div_up(g.N, kGN / 2);
     const dim3 grid(gemm_max_mtiles(P, E) * nnt);
 #define PG_GU(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, true, PG_GU_CT, PG_GU_WM>), grid, dim3(64 * GLay<QT, PG_GU_CT, PG_GU_WM>::NW), 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
-              E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter)
+              E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter, g.scales, u.scales)
     switch (g.qtype) {
     case PGMOE_Q4_K: PG_GU(PGMOE_Q4_K); break;
     case PGMOE_Q6_K: PG_GU(PGMOE_Q6_K); break;
@@ -574,11 +562,13 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
+    if (d.qtype != PGMOE_Q8_0 && !d.scales)
+        return fail(PGMOE_E_INVALID, "gemm down: K-quant weights need their scale plane (pgmoe_build_scale_plane)");
     const int nnt = div_up(d.N, kGN);
     const dim3 grid(gemm_max_mtiles(P, E) * nnt);
 #define PG_DN(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, false, PG_DN_CT, PG_DN_WM>), grid, dim3(64 * GLay<QT, PG_DN_CT, PG_DN_WM>::NW), 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
-              topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial)
+              topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial, d.scales, d.scales)
     switch (d.qtype) {
     case PGMOE_Q4_K: PG_DN(PGMOE_Q4_K); break;
     case PGMOE_Q6_K: PG_DN(PGMOE_Q6_K); break;

@@ -99,6 +99,11 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
                      hipStream_t st);
 int gemm_tile_pairs();
 int64_t layout_bytes(int qtype, int64_t rows, int64_t cols);
+// Scale plane (relayout.hip): bytes of one matrix's plane (0 for Q8_0, -1 if unsupported)
+// and its load-time construction from the device layout.
+int64_t scale_plane_bytes(int qtype, int64_t rows, int64_t cols);
+int launch_scale_plane(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols,
+                       int64_t src_stride, uint8_t* dst, hipStream_t st);
 int gemm_tile_rows();
 int decode_tokens_max();
 

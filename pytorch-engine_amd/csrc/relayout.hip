@@ -68,6 +68,75 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
     }
 }
 
+// Scale plane: one thread per (matrix, 64-row group, super-block, 64-weight unit c, row):
+// the unit's sub-block scales decoded from the tile bytes exactly as the MFMA products
+// would decode them (same expressions, fp32), stored as one float4 per row.
+template <int QT>
+__global__ void scale_plane_kernel(const uint8_t* __restrict__ src, int64_t n_mats, int N, int nb,
+                                   int64_t src_stride, uint8_t* __restrict__ dst, int64_t dst_stride) {
+    const int ng = row_groups(N);
+    const int64_t per_mat = (int64_t)ng * nb * 4 * 64;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= per_mat * n_mats) return;
+    const int64_t mat = gid / per_mat;
+    const int64_t rem = gid % per_mat;  // ((rg * nb + b) * 4 + c) * 64 + r
+    const int r = (int)(rem & 63), c = (int)((rem >> 6) & 3);
+    const int64_t tb = rem >> 8;  // rg * nb + b
+    const uint8_t* md = src + mat * src_stride;
+    float4 v;
+    if (QT == PGMOE_Q4_K) {
+        const uint4 hd = *(const uint4*)(md + tb * (9 * 1024) + r * 16);
+        const float d = lo_half(hd.x), dm = hi_half(hd.x);
+        float a[2], cc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            int sc, mn;
+            kscale_sel(hd.y, hd.z, hd.w, 2 * c + t, sc, mn);
+            a[t] = d * (float)sc;
+            cc[t] = -(dm * (float)mn) - 1024.0f * a[t];
+        }
+        v = make_float4(a[0], cc[0], a[1], cc[1]);
+    } else {  // Q6_K: int8 scales in chunk 12, fp16 d in the plane after the tiles
+        const uint8_t* sc = md + tb * (13 * 1024) + 12 * 1024 + r * 16;
+        const uint16_t db = *(const uint16_t*)(md + (int64_t)ng * nb * 13 * 1024 + (tb * 64 + r) * 2);
+        const float d = h2f(db);
+        const int h = c >> 1, half = c & 1;
+        float a[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) a[g] = d * (float)(int8_t)sc[8 * h + 2 * g + half];
+        v = make_float4(a[0], a[1], a[2], a[3]);
+    }
+    *(float4*)(dst + mat * dst_stride + rem * 16) = v;
+}
+
+int64_t scale_plane_bytes(int qtype, int64_t rows, int64_t cols) {
+    if (layout_bytes(qtype, rows, cols) < 0) return -1;
+    if (qtype == PGMOE_Q8_0) return 0;
+    return (int64_t)row_groups((int)rows) * (cols / 256) * 4 * 1024;
+}
+
+int launch_scale_plane(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols,
+                       int64_t src_stride, uint8_t* dst, hipStream_t st) {
+    const int nb = (int)(cols / 256);
+    const int64_t n = n_mats * (int64_t)row_groups((int)rows) * nb * 4 * 64;
+    const int64_t dst_stride = scale_plane_bytes(qtype, rows, cols);
+    if (n == 0) return PGMOE_OK;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    switch (qtype) {
+    case PGMOE_Q4_K:
+        PG_LAUNCH(scale_plane_kernel<PGMOE_Q4_K>, grid, dim3(256), 0, st, src, n_mats, (int)rows, nb, src_stride,
+                  dst, dst_stride);
+        break;
+    case PGMOE_Q6_K:
+        PG_LAUNCH(scale_plane_kernel<PGMOE_Q6_K>, grid, dim3(256), 0, st, src, n_mats, (int)rows, nb, src_stride,
+                  dst, dst_stride);
+        break;
+    default:
+        return fail(PGMOE_E_UNSUPPORTED, "scale plane: qtype %d has none", qtype);
+    }
+    return check_launch("scale_plane");
+}
+
 int64_t layout_bytes(int qtype, int64_t rows, int64_t cols) {
     if (cols % 256 || rows < 1) return -1;
     const int64_t ng = (rows + 63) / 64, nb = cols / 256;

@@ -12,7 +12,7 @@ from typing import Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libpgmoe.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 Q8_0, Q4_K, Q6_K = 8, 12, 14
 SUPPORTED_QTYPES = (Q4_K, Q6_K, Q8_0)
@@ -30,6 +30,7 @@ class Weights(ctypes.Structure):
         ("n_mats", _I32),
         ("base", _P),
         ("mat_stride", _I64),
+        ("scales", _P),
     ]
 
 
@@ -72,6 +73,9 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_weight_bytes.restype = _I64
     L.pgmoe_weight_bytes.argtypes = [_I32, _I64, _I64]
     L.pgmoe_relayout_weights.argtypes = [_I32, _P, _I64, _I64, _I64, _P, _P]
+    L.pgmoe_scale_plane_bytes.restype = _I64
+    L.pgmoe_scale_plane_bytes.argtypes = [_I32, _I64, _I64]
+    L.pgmoe_build_scale_plane.argtypes = [_I32, _P, _I64, _I64, _I64, _I64, _P, _P]
     L.pgmoe_workspace_bytes.restype = ctypes.c_size_t
     L.pgmoe_workspace_bytes.argtypes = [ctypes.POINTER(Layer), _I32]
     L.pgmoe_moe_forward.argtypes = [ctypes.POINTER(Layer), _P, _I32, _P, _P, ctypes.c_size_t, _P]
@@ -85,7 +89,7 @@ def lib() -> ctypes.CDLL:
                                     _P, _P, _P, _P]
     L.pgmoe_combine.argtypes = [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P]
     for fn in ("pgmoe_moe_forward", "pgmoe_moe_forward_timed", "pgmoe_router_topk", "pgmoe_dispatch", "pgmoe_expert_gateup",
-               "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights"):
+               "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_build_scale_plane"):
         getattr(L, fn).restype = ctypes.c_int
     ver = L.pgmoe_abi_version()
     if ver != ABI_VERSION:
@@ -105,4 +109,5 @@ EXPORTS = (
     "pgmoe_abi_version", "pgmoe_last_error", "pgmoe_weight_bytes", "pgmoe_relayout_weights",
     "pgmoe_workspace_bytes", "pgmoe_moe_forward", "pgmoe_router_topk", "pgmoe_dispatch",
     "pgmoe_expert_gateup", "pgmoe_expert_down", "pgmoe_combine", "pgmoe_moe_forward_timed",
+    "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane",
 )

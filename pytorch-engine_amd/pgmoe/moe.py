@@ -69,9 +69,11 @@ class _ExpertTensor:
         raw = torch.from_numpy(np.asarray(raw_np)).to(device)  # H2D copy of the GGUF bytes
         self.buf = ops.relayout(self.qtype, raw, self.n_mats, self.rows, self.cols)
         del raw
+        # K-quants: the sub-block scales decoded once for the prefill MFMA products
+        self.plane = ops.scale_plane(self.qtype, self.buf, self.n_mats, self.rows, self.cols)
 
     def weights(self) -> Weights:
-        return ops.make_weights(self.qtype, self.buf, self.n_mats, self.rows, self.cols)
+        return ops.make_weights(self.qtype, self.buf, self.n_mats, self.rows, self.cols, self.plane)
 
     @property
     def gguf_bytes_per_mat(self) -> int:
@@ -202,6 +204,7 @@ class HipSparseMoEMLP(nn.Module):
             if t is not None:
                 c = copy.copy(t)
                 c.buf = t.buf.clone()
+                c.plane = t.plane.clone() if t.plane is not None else None
                 object.__setattr__(r, name, c)
         r._ws = {}
         r._layer = r._build_layer()

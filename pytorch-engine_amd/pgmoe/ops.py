@@ -59,8 +59,25 @@ def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int) -
     return dst
 
 
-def make_weights(qtype: int, buf: torch.Tensor, n_mats: int, rows: int, cols: int) -> Weights:
-    return Weights(qtype, rows, cols, n_mats, buf.data_ptr(), weight_stride(qtype, rows, cols))
+def scale_plane(qtype: int, buf: torch.Tensor, n_mats: int, rows: int, cols: int) -> Optional[torch.Tensor]:
+    """The fp32 scale plane the MFMA (prefill) products read, built on the device from the
+    device layout `buf` (uint8 [n_mats * plane bytes]); None for Q8_0, which has none."""
+    dev = _need_cuda(buf)
+    n = int(lib().pgmoe_scale_plane_bytes(qtype, rows, cols))
+    if n < 0:
+        raise ValueError(f"qtype {qtype} with {cols} columns is not supported by the HIP kernels")
+    if n == 0:
+        return None
+    dst = torch.empty(n_mats * n, dtype=torch.uint8, device=dev)
+    check(lib().pgmoe_build_scale_plane(qtype, buf.data_ptr(), n_mats, rows, cols, weight_stride(qtype, rows, cols),
+                                        dst.data_ptr(), _stream(dev)), "pgmoe_build_scale_plane")
+    return dst
+
+
+def make_weights(qtype: int, buf: torch.Tensor, n_mats: int, rows: int, cols: int,
+                 plane: Optional[torch.Tensor] = None) -> Weights:
+    return Weights(qtype, rows, cols, n_mats, buf.data_ptr(), weight_stride(qtype, rows, cols),
+                   plane.data_ptr() if plane is not None else None)
 
 
 def router_topk(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], k: int, norm: bool

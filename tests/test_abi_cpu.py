@@ -43,6 +43,22 @@ def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
     assert L.pgmoe_weight_bytes(8, 4, 320) == -1
 
 
+def test_scale_plane_bytes_and_argument_checks():
+    """Scale plane: one 1 KB chunk per (64-row group, super-block, 64-weight unit) for
+    K-quants, none for Q8_0; the builder rejects bad arguments before any device work."""
+    L = _lib.lib()
+    assert L.pgmoe_scale_plane_bytes(12, 100, 512) == 2 * 2 * 4 * 1024
+    assert L.pgmoe_scale_plane_bytes(14, 64, 768) == 1 * 3 * 4 * 1024
+    assert L.pgmoe_scale_plane_bytes(8, 64, 256) == 0
+    assert L.pgmoe_scale_plane_bytes(12, 4, 100) == -1
+    assert L.pgmoe_scale_plane_bytes(2, 4, 256) == -1
+    assert L.pgmoe_build_scale_plane(8, 0x1000, 1, 64, 256, 0, 0x2000, None) == -2  # Q8_0: none
+    assert L.pgmoe_build_scale_plane(12, 0, 1, 64, 256, 0, 0x2000, None) == -1      # NULL source
+    assert L.pgmoe_build_scale_plane(12, 0x1008, 1, 64, 256, 0, 0x2000, None) == -1  # misaligned
+    stride = L.pgmoe_weight_bytes(12, 64, 256)
+    assert L.pgmoe_build_scale_plane(12, 0x1000, 2, 64, 256, stride - 16, 0x2000, None) == -1
+
+
 def _fake_layer(E=8, K=2, H=1024, I=512, qt=12, shared=False):
     """A layer struct with aligned fake device pointers (validation never dereferences)."""
     W = _lib.Weights

@@ -138,6 +138,73 @@ def _dense(qtype, raw, n_mats, rows, cols):
     return oracle.dequant(qtype, raw, n_mats * rows, cols).reshape(n_mats, rows, cols).astype(np.float64)
 
 
+def _np_scale_plane(qtype, raw, n_mats, rows, cols):
+    """The scale plane of include/pgmoe.h in numpy (fp32, the kernel's expressions and
+    operation order): per (64-row group, super-block, unit c) 64 rows of four floats."""
+    nb, ng = cols // 256, (rows + 63) // 64
+    bpb = {Q4_K: 144, Q6_K: 210}[qtype]
+    sb = np.zeros((n_mats, ng * 64, nb, bpb), dtype=np.uint8)  # pad rows: zero bytes
+    sb[:, :rows] = raw.reshape(n_mats, rows, nb, bpb)
+    out = np.zeros((n_mats, ng, nb, 4, 64, 4), dtype=np.float32)
+    f32 = np.float32
+    for m in range(n_mats):
+        for r in range(ng * 64):
+            g, rr = divmod(r, 64)
+            for b in range(nb):
+                blk = sb[m, r, b]
+                for c in range(4):
+                    if qtype == Q4_K:
+                        d, dmin = blk[0:4].view(np.float16).astype(np.float32)
+                        q = blk[4:16].astype(np.int64)
+                        vals = []
+                        for s in (2 * c, 2 * c + 1):
+                            if s < 4:
+                                sc, mn = q[s] & 63, q[s + 4] & 63
+                            else:
+                                sc = (q[s + 4] & 0xF) | ((q[s - 4] >> 6) << 4)
+                                mn = (q[s + 4] >> 4) | ((q[s] >> 6) << 4)
+                            a = f32(d) * f32(sc)
+                            vals += [a, -(f32(dmin) * f32(mn)) - f32(1024.0) * a]
+                    else:
+                        d = blk[208:210].view(np.float16).astype(np.float32)[0]
+                        scl = blk[192:208].view(np.int8)
+                        h, half = c >> 1, c & 1
+                        vals = [f32(d) * f32(scl[8 * h + 2 * gg + half]) for gg in range(4)]
+                    out[m, g, b, c, rr] = vals
+    return out.reshape(n_mats, -1)
+
+
+@pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q4_K, 130, 256, 2)])
+def test_scale_plane_bits(dev, qtype, rows, cols, n_mats):
+    """The load-time scale plane equals its numpy restatement bit for bit (pad rows too)."""
+    from pgmoe import ops
+    rng = np.random.default_rng(rows + cols)
+    raw = np.concatenate([random_blocks(rng, qtype, rows, cols) for _ in range(n_mats)])
+    buf = ops.relayout(qtype, torch.from_numpy(raw).to(dev), n_mats, rows, cols)
+    plane = ops.scale_plane(qtype, buf, n_mats, rows, cols)
+    torch.cuda.synchronize()
+    got = plane.cpu().numpy().view(np.uint32).reshape(n_mats, -1)
+    ref = _np_scale_plane(qtype, raw, n_mats, rows, cols).view(np.uint32)
+    bad = np.argwhere(got != ref)
+    assert len(bad) == 0, (len(bad), bad[:4].tolist(), got[tuple(bad[0])], ref[tuple(bad[0])])
+    assert ops.scale_plane(Q8_0, buf, 1, 64, 256) is None  # Q8_0 has no plane
+
+
+def test_mfma_products_need_the_scale_plane(dev):
+    """Mode 1 (MFMA) with K-quant weights but no scale plane is an error, not a fallback."""
+    from pgmoe import ops
+    rng = np.random.default_rng(3)
+    E, I, H, K, M = 2, 64, 256, 1, 16
+    gb = ops.relayout(Q4_K, torch.from_numpy(np.concatenate([random_blocks(rng, Q4_K, I, H) for _ in range(E)])).to(dev),
+                      E, I, H)
+    W = ops.make_weights(Q4_K, gb, E, I, H)
+    idx = torch.zeros((M, K), dtype=torch.int32, device=dev)
+    disp = ops.dispatch(idx, E, 256)
+    x = torch.zeros((M, H), dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="scale plane"):
+        ops.expert_gateup(W, W, x, K, disp, 1)
+
+
 @pytest.mark.parametrize("qg,qd,H,I,E,K,M,mode", [
     (Q4_K, Q6_K, 512, 256, 8, 2, 1, 0), (Q4_K, Q6_K, 512, 256, 8, 2, 8, 0),
     (Q4_K, Q4_K, 256, 512, 4, 2, 5, 0), (Q8_0, Q8_0, 256, 512, 6, 3, 7, 0),
@@ -163,7 +230,10 @@ def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
     gb = ops.relayout(qg, torch.from_numpy(gr).to(dev), E, I, H)
     ub = ops.relayout(qg, torch.from_numpy(ur).to(dev), E, I, H)
     db = ops.relayout(qd, torch.from_numpy(dr).to(dev), E, H, I)
-    Wg, Wu, Wd = ops.make_weights(qg, gb, E, I, H), ops.make_weights(qg, ub, E, I, H), ops.make_weights(qd, db, E, H, I)
+    gp, up_, dp = (ops.scale_plane(qg, gb, E, I, H), ops.scale_plane(qg, ub, E, I, H),
+                   ops.scale_plane(qd, db, E, H, I))
+    Wg, Wu = ops.make_weights(qg, gb, E, I, H, gp), ops.make_weights(qg, ub, E, I, H, up_)
+    Wd = ops.make_weights(qd, db, E, H, I, dp)
     disp = ops.dispatch(torch.from_numpy(idx).to(dev), E, 256)  # the GEMM's tile size
     xd = torch.from_numpy(x).to(dev)
     inter = ops.expert_gateup(Wg, Wu, xd, K, disp, mode)
@@ -185,7 +255,7 @@ def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
         ref_inter[p] = gv / (1 + np.exp(-gv)) * uv
     got_inter = inter.cpu().numpy()
     tol = 1e-4 if mode == 0 else 2e-3
-    assert oracle.rel_l2(got_inter, ref_inter) < tol
+    assert oracle.rel_l2(got_inter, ref_inter) < tol, ("inter", oracle.rel_l2(got_inter, ref_inter))
     ref_part = np.empty((P, H))
     gi = got_inter.astype(np.float64)
     for p in range(P):
