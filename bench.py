@@ -325,16 +325,20 @@ def main() -> int:
         xp = torch.from_numpy(xp_np).to(dev)
         ms = eager_step_ms(torch, pmods, xp, args.prefill_steps, 2)
         kd = kernel_durations(torch, hip, pmods, xp, max(3, args.prefill_steps // 2))
-        # launches: router, top-k, dispatch, gate/up, row-scale, down, combine
+        # launches: router, top-k, dispatch (a counting pass first when it takes several
+        # workgroups), gate/up, row-scale, down, combine
+        names = (["router", "topk", "dispatch_count", "dispatch", "gemm_gateup", "rowscale", "gemm_down", "combine"]
+                 if len(kd) == 8 else ["router", "topk", "dispatch", "gemm_gateup", "rowscale", "gemm_down", "combine"])
+        i_gu, i_dn = names.index("gemm_gateup"), names.index("gemm_down")
         P = M * pspec.top_k
         fl_gu = 2.0 * P * pspec.hidden * 2 * pspec.inter
         fl_dn = 2.0 * P * pspec.inter * pspec.hidden
-        gu_tf = fl_gu / (kd[3] * 1e-3) / 1e12
-        dn_tf = fl_dn / (kd[5] * 1e-3) / 1e12
-        both_tf = (fl_gu + fl_dn) / ((kd[3] + kd[5]) * 1e-3) / 1e12
+        gu_tf = fl_gu / (kd[i_gu] * 1e-3) / 1e12
+        dn_tf = fl_dn / (kd[i_dn] * 1e-3) / 1e12
+        both_tf = (fl_gu + fl_dn) / ((kd[i_gu] + kd[i_dn]) * 1e-3) / 1e12
         prefill = {"M": M, "us_per_step": round(ms * 1e3, 2), "tok_per_s": round(M / (ms * 1e-3), 1),
                    "kernel_us": [round(v * 1e3, 2) for v in kd],
-                   "kernels": ["router", "topk", "dispatch", "gemm_gateup", "rowscale", "gemm_down", "combine"],
+                   "kernels": names,
                    "gemm_gateup_tflops": round(gu_tf, 1), "gemm_down_tflops": round(dn_tf, 1),
                    "gemm_tflops": round(both_tf, 1), "mfma_frac": round(both_tf / FP16_PEAK_TFLOPS, 4),
                    "layer_tflops": round((fl_gu + fl_dn) / (ms * 1e-3) / 1e12, 1)}

@@ -150,6 +150,15 @@ int pgmoe_dispatch(const int32_t* topk_idx, int32_t M, int32_t K, int32_t E, int
                    int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active,
                    int32_t* tile_off, void* stream);
 
+/* pgmoe_dispatch with caller scratch (ws, at least pgmoe_dispatch_ws_bytes(M, K, E)
+ * bytes): the same outputs, bit for bit, from several workgroups (a counting pass, then
+ * the scatter) instead of one.  No counterpart in the reference: it is the form the
+ * one-call forward uses, exposed so callers with scratch can take it. */
+size_t pgmoe_dispatch_ws_bytes(int32_t M, int32_t K, int32_t E);
+int pgmoe_dispatch_ws(const int32_t* topk_idx, int32_t M, int32_t K, int32_t E, int32_t tile_rows,
+                      int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active,
+                      int32_t* tile_off, void* ws, size_t ws_bytes, void* stream);
+
 /* R4+R5: inter[P, I] = silu(x_p . Wg_e^T) * (x_p . Wu_e^T) for every sorted pair position p,
  * fp32 accumulate and output (gate/up_exps.forward_expert + exec_fused_act_mul_rowscale,
  * model.py:916-918).  mode 0 = wavefront GEMV (M <= 8), 1 = MFMA grouped GEMM over

@@ -70,7 +70,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
     size_t rlog, desc, xsum, isum, s_isum;
-    size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, inter, a16, rs, partial;
+    size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, dcounts, inter, a16, rs, partial;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
 };
@@ -103,6 +103,7 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     o.active = take(c, E * 4);
     o.nact = take(c, 4);
     o.tile_off = take(c, (E + 1) * 4);
+    o.dcounts = take(c, gemm ? dispatch_ws_bytes((int64_t)P, (int)E) : 0);  // multi-block dispatch scratch
     o.inter = take(c, P * I * 4);
     o.a16 = take(c, gemm ? P * I * 2 : 0);
     o.rs = take(c, gemm ? P * 4 : 0);
@@ -230,6 +231,25 @@ int pgmoe_dispatch(const int32_t* topk_idx, int32_t M, int32_t K, int32_t E, int
                            as_stream(stream));
 }
 
+size_t pgmoe_dispatch_ws_bytes(int32_t M, int32_t K, int32_t E) {
+    if (M < 0 || K < 1 || E < 1 || E > 512) return 0;
+    return dispatch_ws_bytes((int64_t)M * K, E);
+}
+
+int pgmoe_dispatch_ws(const int32_t* topk_idx, int32_t M, int32_t K, int32_t E, int32_t tile_rows, int32_t* offsets,
+                      int32_t* perm, int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, void* ws,
+                      size_t ws_bytes, void* stream) {
+    if (M < 0 || K < 1 || E < 1 || E > 512 || tile_rows < 1)
+        return fail(PGMOE_E_INVALID, "dispatch: bad sizes M=%d K=%d E=%d tile_rows=%d", M, K, E, tile_rows);
+    if (!offsets || !perm || !inv || !active || !n_active || !tile_off || !ws || (M > 0 && !topk_idx))
+        return fail(PGMOE_E_INVALID, "dispatch: NULL pointer");
+    if (ws_bytes < dispatch_ws_bytes((int64_t)M * K, E))
+        return fail(PGMOE_E_WORKSPACE, "dispatch: scratch %zu bytes, need %zu", ws_bytes,
+                    dispatch_ws_bytes((int64_t)M * K, E));
+    return launch_dispatch(topk_idx, M, K, E, tile_rows, offsets, perm, inv, active, n_active, tile_off,
+                           as_stream(stream), (int32_t*)ws);
+}
+
 int pgmoe_expert_gateup(const pgmoe_weights* gate, const pgmoe_weights* up, const uint16_t* x, int32_t M,
                         int32_t K, const int32_t* offsets, const int32_t* perm, const int32_t* active,
                         const int32_t* n_active, const int32_t* tile_off, int32_t mode, float* inter,
@@ -319,7 +339,8 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
     if ((rc = launch_router_logits(x, L->router_w, L->router_bias, M, H, E, WS(float, logits), st))) return rc;
     if ((rc = launch_topk(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w), st))) return rc;
     if ((rc = launch_dispatch(WS(int32_t, idx), M, K, E, BM, WS(int32_t, offsets), WS(int32_t, perm),
-                              WS(int32_t, inv), WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), st)))
+                              WS(int32_t, inv), WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), st,
+                              WS(int32_t, dcounts))))
         return rc;
     if ((rc = launch_gateup(lm.gate, lm.up, x, M, K, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
                             WS(int32_t, nact), WS(int32_t, tile_off), mode, WS(float, inter), st)))

@@ -43,8 +43,11 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
                          float* logits, hipStream_t st, const float* extra_w = nullptr, float* extra_out = nullptr,
                          float* xsum = nullptr);
 int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w, hipStream_t st);
+// counts (optional scratch of dispatch_ws_bytes): several blocks instead of one.
 int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int32_t* offsets, int32_t* perm,
-                    int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st);
+                    int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st,
+                    int32_t* counts = nullptr);
+size_t dispatch_ws_bytes(int64_t P, int E);
 int launch_identity_dispatch(int M, int tile_rows, int32_t* offsets, int32_t* perm, int32_t* inv,
                              int32_t* active, int32_t* n_active, int32_t* tile_off, float* w, hipStream_t st);
 int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,

@@ -83,12 +83,16 @@ def lib() -> ctypes.CDLL:
                                           ctypes.POINTER(_P), ctypes.POINTER(_P), _I32, ctypes.POINTER(_I32)]
     L.pgmoe_router_topk.argtypes = [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P]
     L.pgmoe_dispatch.argtypes = [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P]
+    L.pgmoe_dispatch_ws_bytes.restype = ctypes.c_size_t
+    L.pgmoe_dispatch_ws_bytes.argtypes = [_I32, _I32, _I32]
+    L.pgmoe_dispatch_ws.argtypes = [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P]
     L.pgmoe_expert_gateup.argtypes = [ctypes.POINTER(Weights), ctypes.POINTER(Weights), _P, _I32, _I32,
                                       _P, _P, _P, _P, _P, _I32, _P, _P]
     L.pgmoe_expert_down.argtypes = [ctypes.POINTER(Weights), _P, _I32, _I32, _P, _P, _P, _P, _P, _P, _I32,
                                     _P, _P, _P, _P]
     L.pgmoe_combine.argtypes = [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P]
-    for fn in ("pgmoe_moe_forward", "pgmoe_moe_forward_timed", "pgmoe_router_topk", "pgmoe_dispatch", "pgmoe_expert_gateup",
+    for fn in ("pgmoe_moe_forward", "pgmoe_moe_forward_timed", "pgmoe_router_topk", "pgmoe_dispatch",
+               "pgmoe_dispatch_ws", "pgmoe_expert_gateup",
                "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_build_scale_plane"):
         getattr(L, fn).restype = ctypes.c_int
     ver = L.pgmoe_abi_version()
@@ -109,5 +113,5 @@ EXPORTS = (
     "pgmoe_abi_version", "pgmoe_last_error", "pgmoe_weight_bytes", "pgmoe_relayout_weights",
     "pgmoe_workspace_bytes", "pgmoe_moe_forward", "pgmoe_router_topk", "pgmoe_dispatch",
     "pgmoe_expert_gateup", "pgmoe_expert_down", "pgmoe_combine", "pgmoe_moe_forward_timed",
-    "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane",
+    "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane", "pgmoe_dispatch_ws_bytes", "pgmoe_dispatch_ws",
 )

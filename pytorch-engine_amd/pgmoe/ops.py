@@ -94,7 +94,8 @@ def router_topk(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], 
     return logits, idx, tw
 
 
-def dispatch(idx: torch.Tensor, n_experts: int, tile_rows: int = 256):
+def dispatch(idx: torch.Tensor, n_experts: int, tile_rows: int = 256, blocks: str = "one"):
+    """pgmoe_dispatch (blocks="one") or pgmoe_dispatch_ws with its scratch (blocks="many")."""
     dev = _need_cuda(idx)
     M, K = idx.shape
     P = M * K
@@ -105,9 +106,17 @@ def dispatch(idx: torch.Tensor, n_experts: int, tile_rows: int = 256):
     active = torch.empty(n_experts, **i32)
     n_active = torch.empty(1, **i32)
     tile_off = torch.empty(n_experts + 1, **i32)
-    check(lib().pgmoe_dispatch(idx.data_ptr(), M, K, n_experts, tile_rows, offsets.data_ptr(), perm.data_ptr(),
-                               inv.data_ptr(), active.data_ptr(), n_active.data_ptr(), tile_off.data_ptr(),
-                               _stream(dev)), "pgmoe_dispatch")
+    if blocks == "many":
+        nws = int(lib().pgmoe_dispatch_ws_bytes(M, K, n_experts))
+        ws = torch.empty(max(nws, 4), dtype=torch.uint8, device=dev)
+        check(lib().pgmoe_dispatch_ws(idx.data_ptr(), M, K, n_experts, tile_rows, offsets.data_ptr(),
+                                      perm.data_ptr(), inv.data_ptr(), active.data_ptr(), n_active.data_ptr(),
+                                      tile_off.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+              "pgmoe_dispatch_ws")
+    else:
+        check(lib().pgmoe_dispatch(idx.data_ptr(), M, K, n_experts, tile_rows, offsets.data_ptr(), perm.data_ptr(),
+                                   inv.data_ptr(), active.data_ptr(), n_active.data_ptr(), tile_off.data_ptr(),
+                                   _stream(dev)), "pgmoe_dispatch")
     return offsets, perm[:P], inv[:P], active, n_active, tile_off
 
 

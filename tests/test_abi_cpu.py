@@ -43,6 +43,18 @@ def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
     assert L.pgmoe_weight_bytes(8, 4, 320) == -1
 
 
+def test_dispatch_scratch_bytes():
+    """Multi-block dispatch scratch: one int per (workgroup, expert), about 2048 pairs per
+    workgroup and at most 64 workgroups."""
+    L = _lib.lib()
+    assert L.pgmoe_dispatch_ws_bytes(4096, 8, 128) == 16 * 128 * 4
+    assert L.pgmoe_dispatch_ws_bytes(1, 8, 128) == 1 * 128 * 4
+    assert L.pgmoe_dispatch_ws_bytes(100000, 8, 64) == 64 * 64 * 4
+    assert L.pgmoe_dispatch_ws_bytes(4, 8, 0) == 0
+    assert L.pgmoe_dispatch_ws(0x1000, 4, 8, 128, 256, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000, 0x7000, 0x8000,
+                               16, None) == -3  # scratch too small
+
+
 def test_scale_plane_bytes_and_argument_checks():
     """Scale plane: one 1 KB chunk per (64-row group, super-block, 64-weight unit) for
     K-quants, none for Q8_0; the builder rejects bad arguments before any device work."""

@@ -106,12 +106,16 @@ def test_topk_ties_lower_id_wins(dev):
     assert np.all(idx.cpu().numpy() == np.array([1, 2, 4, 6], np.int32))
 
 
+@pytest.mark.parametrize("blocks", ["one", "many"])
 @pytest.mark.parametrize("M,K,E,skew", [(1, 8, 128, None), (8, 8, 128, None), (4096, 8, 128, None),
                                         (4096, 8, 128, "one"), (16, 2, 8, None), (1000, 1, 1, None),
-                                        (512, 8, 64, "half"), (3, 16, 512, None), (0, 8, 128, None)])
-def test_dispatch_bitexact(dev, M, K, E, skew):
+                                        (512, 8, 64, "half"), (3, 16, 512, None), (0, 8, 128, None),
+                                        (20000, 8, 128, None), (300, 7, 9, "one")])
+def test_dispatch_bitexact(dev, M, K, E, skew, blocks):
+    """pgmoe_dispatch (one workgroup) and pgmoe_dispatch_ws (a counting pass, then up to 64
+    scatter workgroups; M = 20000 exceeds that cap) against a stable argsort."""
     from pgmoe import ops
-    log(f"dispatch M={M} K={K} E={E} skew={skew}")
+    log(f"dispatch M={M} K={K} E={E} skew={skew} blocks={blocks}")
     rng = np.random.default_rng(M * 7 + K)
     idx = np.array([rng.permutation(E)[:K] for _ in range(M)], dtype=np.int32).reshape(M, K)
     if skew == "one" and M:
@@ -121,7 +125,7 @@ def test_dispatch_bitexact(dev, M, K, E, skew):
             idx[t, 1:] = row
     if skew == "half" and M:
         idx = np.stack([np.sort(rng.permutation(E // 2)[:K]) for _ in range(M)]).astype(np.int32)
-    offsets, perm, inv, active, n_active, tile_off = ops.dispatch(torch.from_numpy(idx).to(dev), E, 64)
+    offsets, perm, inv, active, n_active, tile_off = ops.dispatch(torch.from_numpy(idx).to(dev), E, 64, blocks)
     r_off, r_perm, r_inv = oracle.dispatch(idx, E)
     assert np.array_equal(offsets.cpu().numpy(), r_off)
     assert np.array_equal(perm.cpu().numpy(), r_perm)
