@@ -85,6 +85,22 @@ size_t dec_lds_limit() {
     return cached[dev];
 }
 
+int resident_rows(const void* kernel, int threads, size_t lds, int gx, int gy) {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return gy;
+    if (!cus[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return gy;
+        cus[dev] = v;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess || per_cu <= 0)
+        return gy;
+    const int rows = per_cu * cus[dev] / gx;
+    return rows < 1 ? 1 : rows < gy ? rows : gy;
+}
+
 int decode_tokens_max() { return kDecTM; }
 int decode_desc_words() { return kDescWords; }
 int decode_rlog_words(int M, int E) { return kRlogCopies * M * E; }

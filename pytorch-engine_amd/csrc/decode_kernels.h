@@ -1296,19 +1296,27 @@ inline size_t dc_lds_bytes(int P, int K) { return (size_t)P * (K / 64) * kXuF * 
 
 // Dynamic LDS a block of the current device may take beside the kernels' static arrays.
 size_t dec_lds_limit();
+// Of gy slot rows of gx blocks each, how many fit in one round of resident blocks of
+// `kernel` on the current device (at least 1): a grid past that waits a whole block
+// duration for its last round.
+int resident_rows(const void* kernel, int threads, size_t lds, int gx, int gy);
 
 template <int QT, int TM>
 inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, const DecDisp& dp,
                       const RouterIn& rt, int max_active, float* inter, float* isum, hipStream_t st) {
     const int W = gu_waves(g.K >> 8), gx = div_up(g.N, 16);
-    int gy = gu_slot_blocks(max_active);
-    if (dp.mode == kRoute) {  // every router row needs a wave
-        const int rows = dp.E + (rt.extra_w ? 1 : 0);
-        gy = gy > div_up(rows, gx * W) ? gy : div_up(rows, gx * W);
-    }
-#define PG_GU(MODE, RE)                                                                                       \
-    PG_LAUNCH((dec_gu_kernel<QT, TM, MODE, RE>), dim3(gx, gy), dim3(64 * W), gu_lds_bytes(dp.M, g.K), st, g.base, \
-              u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt, inter, isum)
+    const int gy = gu_slot_blocks(max_active);
+    // every router row needs a wave
+    const int gmin = dp.mode == kRoute ? div_up(dp.E + (rt.extra_w ? 1 : 0), gx * W) : 1;
+    const size_t sh = gu_lds_bytes(dp.M, g.K);
+    // slot rows: as many as fit in one round of resident blocks (blocks loop over the rest)
+#define PG_GU(MODE, RE)                                                                                         \
+    do {                                                                                                        \
+        int gyr = resident_rows((const void*)dec_gu_kernel<QT, TM, MODE, RE>, 64 * W, sh, gx, gy);              \
+        gyr = gyr > gmin ? gyr : gmin;                                                                          \
+        PG_LAUNCH((dec_gu_kernel<QT, TM, MODE, RE>), dim3(gx, gyr), dim3(64 * W), sh, st, g.base, u.base,       \
+                  g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt, inter, isum);                            \
+    } while (0)
     if (dp.mode == kRoute) {
         if (dp.E <= 128)
             PG_GU(kRoute, 2);
