@@ -71,7 +71,9 @@ template <> struct GStage<PGMOE_Q8_0> {
     __device__ static __forceinline__ int chunk(int u, int cc) { return 4 * (u & 3) + cc; }
 };
 
-// LDS stage: A [256 rows][128 bytes] (16-byte slot s of row r holds k chunk s ^ (r & 7)),
+// LDS stage: A [256 rows][128 bytes] (16-byte slot s of row r holds k chunk s ^ key(r),
+// key(r) = (r & 7) ^ ((r >> 3) & 1): the 16 rows a 256-byte LDS pass reads then fall on 16
+// different 16-byte bank groups),
 // then B: row group bg, chunk cc (cc = CH: scales) at kGA + (bg * (CH + 1) + cc) * 1024.
 constexpr int kGA = kGM * 128;
 // CT = 32-column B tiles per wave, WM = waves along M: the block's 256 x 256 tile is cut
@@ -242,7 +244,7 @@ __device__ __forceinline__ int gemm_tile_expert(const int32_t* tile_off, int E, 
 // ---------------------------------------------------------------- the unit loop
 // Wave (wm, wn): rows 32 RS wm + 32 i (i < NI, the 32-row slices holding pairs), CT
 // column tiles j.  Group g = k16 slice g of a unit: A fragment lane l = row l % 32, k chunk
-// 2g + l / 32 (slot (2g + l/32) ^ (row & 7)); B fragment = the lane's column's group g,
+// 2g + l / 32 (slot (2g + l/32) ^ key(row)); B fragment = the lane's column's group g,
 // weights 8(l/32) .. +8.  Register v of D is D[8(v/4) + 4(l/32) + v%4][l%32].
 // The groups of all units form one stream: the A fragments and B decode of group q + 1 are
 // issued between the MFMAs of group q (a wave issues in order; each MFMA runs while the
@@ -261,8 +263,8 @@ __device__ __forceinline__ void gemm_loop(const uint8_t* smem, int units, const 
     // VALU instructions (B decode) placed after each MFMA: about 16 CT + 16 per group
     constexpr int VPM = (16 * CT + 16 + CT * NA - 1) / (CT * NA);
     const int h = lane >> 5;
-    // row r = 32 RS wm + 32 i + l%32 has r & 7 = l & 7: one address per group, the 32-row
-    // slices at immediate offsets 4096 i
+    // row r = 32 RS wm + 32 i + l%32 has key(r) = (l & 7) ^ ((l >> 3) & 1): one address per
+    // group, the 32-row slices at immediate offsets 4096 i
     const int aoff = (32 * RS * wm + (lane & 31)) * 128;
     GCol<QT> col[CT];
     gh8 af[2][NA], bf[2][CT];
@@ -273,7 +275,7 @@ __device__ __forceinline__ void gemm_loop(const uint8_t* smem, int units, const 
         for (int j = 0; j < CT; ++j) col[j].prep(u);
     };
     auto frag = [&](const uint8_t* S, int g, gh8 (&a)[NA], gh8 (&b)[CT]) {
-        const uint8_t* p = S + aoff + 16 * ((2 * g + h) ^ (lane & 7));
+        const uint8_t* p = S + aoff + 16 * ((2 * g + h) ^ (lane & 7) ^ ((lane >> 3) & 1));
 #pragma unroll
         for (int i = 0; i < NI; ++i) a[i] = *(const gh8*)(p + 4096 * i);
 #pragma unroll
@@ -363,8 +365,9 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     __syncthreads();
 
     // ---- copy plan.  A: wave w copies rows 8i .. 8i+7 for i = w + NW q (q < AQ); lane
-    // l takes row 8i + l/8, slot l%8 = k chunk (l%8) ^ (l/8).
-    const int akc = (lane & 7) ^ (lane >> 3);
+    // l takes row 8i + l/8, slot l%8 = k chunk (l%8) ^ (l/8) ^ (i & 1), and i & 1 = w & 1
+    // for every copy of the wave (NW is even).
+    const int akc = (lane & 7) ^ (lane >> 3) ^ (wave & 1);
     const uint16_t* arow[L::AQ];
 #pragma unroll
     for (int q = 0; q < L::AQ; ++q) arow[q] = act + (int64_t)rowsrc[8 * (wave + NW * q) + (lane >> 3)] * K;
