@@ -109,9 +109,11 @@ int pgmoe_build_scale_plane(int32_t qtype, const void* src, int64_t n_mats, int6
                             int64_t mat_stride, void* dst, void* stream);
 
 /* Workspace bytes pgmoe_moe_forward needs for M tokens.  Zero the workspace once when it
- * is allocated: for M <= 8 it begins with the router's ready-tagged logits, which the
- * forward leaves at zero for the next call (calls that share a workspace must not
- * overlap, and a workspace whose forward failed part-way must be zeroed again). */
+ * is allocated: for every M it begins with the decode router's ready-tagged logits (the
+ * same bytes whatever M is), which decode forwards leave at zero for the next call, so a
+ * workspace sized for the largest M may serve calls of any M in turn (calls that share a
+ * workspace must not overlap, and a workspace whose forward failed part-way must be
+ * zeroed again). */
 size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M);
 
 /* One MoE layer: out[M, H] = GGUFSparseMoEMLP.forward(x[M, H]) (model.py:898-937).

@@ -87,9 +87,11 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     const size_t P = (size_t)M * K;
     const bool gemm = M > decode_tokens_max();
     size_t c = 0;
-    // first: the decode router's ready-tagged logits (zero between calls; the workspace
-    // must be zeroed once when it is allocated)
-    o.rlog = take(c, gemm ? 0 : (size_t)decode_rlog_words(M, (int)E) * 8);
+    // first, laid out the same for every M: the decode router's ready-tagged logits.  They
+    // persist between calls (zero when the workspace is first allocated, and each decode
+    // forward leaves them at zero), so a workspace shared by calls of different M must
+    // find them at the same offset, where no other call writes
+    o.rlog = take(c, (size_t)decode_rlog_words(decode_tokens_max(), (int)E) * 8);
     o.desc = take(c, gemm ? 0 : (size_t)decode_desc_words() * 4);
     o.xsum = take(c, gemm ? 0 : (size_t)M * (H / 16) * 4);
     o.isum = take(c, gemm ? 0 : P * (I / 16) * 4);

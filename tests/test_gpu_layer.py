@@ -71,9 +71,10 @@ def test_qwen3_decode(M):
     _run("qwen3_30b_a3b", M, 8)
 
 
-def test_qwen3_realistic_scale_absolute():
+@pytest.mark.parametrize("M", [1, 4])
+def test_qwen3_realistic_scale_absolute(M):
     # decode path keeps fp32 throughout: the literal absolute bound holds
-    _run("qwen3_30b_a3b", 4, 4, scale=0.01, abs_tol=2e-2)
+    _run("qwen3_30b_a3b", M, M, scale=0.01, abs_tol=2e-2)
 
 
 def test_qwen3_realistic_scale_mfma_vs_reference_error():
@@ -123,7 +124,7 @@ def test_qwen2_shared_expert(M):
 
 def test_deterministic_repeat():
     lay, ol, mod = _pair("tiny")
-    for M in (3, 100):
+    for M in (1, 3, 100):
         xd = torch.from_numpy(lay.draw_x(M)).to("cuda:0")
         a = mod(xd).cpu().numpy()
         b = mod(xd).cpu().numpy()
@@ -191,6 +192,30 @@ def test_timed_forward_matches_forward_and_times_every_launch():
                                             ws.numel(), stream, starts.ev, None, 1, None), "forward_timed")
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
+
+
+def test_one_workspace_across_token_counts():
+    """One C-level workspace (sized for the largest M) shared by forwards of different M in
+    turn -- decode and prefill -- gives each the bits of a forward on a fresh zeroed
+    workspace: the decode router's tagged logits, which persist between forwards, sit at
+    the start of the workspace for every M, where no other call writes."""
+    from pgmoe._lib import check, lib
+    for name in ("tiny", "qwen3_30b_a3b"):
+        lay, ol, mod = _pair(name)
+        seq = (1, 2, 64, 1, 3, 1, 1)
+        nbytes = max(mod.workspace_bytes(M) for M in seq)
+        raw = torch.zeros(nbytes + 256, dtype=torch.uint8, device="cuda:0")
+        ws = raw[(-raw.data_ptr()) % 256:]
+        stream = torch.cuda.current_stream().cuda_stream
+        for i, M in enumerate(seq):
+            log(f"shared workspace {name}: call {i} M={M}")
+            x = torch.from_numpy(lay.draw_x(M + i)[i:]).to("cuda:0")
+            out = torch.empty((M, mod.hidden), dtype=torch.float32, device="cuda:0")
+            check(lib().pgmoe_moe_forward(mod._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          stream), "forward")
+            ref = mod(x)  # its own workspace for this M
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), (name, i, M)
 
 
 def test_graph_replay_equals_eager():
