@@ -52,6 +52,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--copies", type=int, default=8, help="rotated weight copies (MALL defeat)")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense FFN measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--m-list", default="1,2,4,8", help="decode token counts to time (1 is the headline)")
@@ -162,6 +163,48 @@ def graph_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
             raise RuntimeError("graph replay differs from the eager forward")
     del full, part
     return ms
+
+
+def dense_section(torch, oracle, dev, steps: int, warmup: int, prefill_steps: int) -> dict:
+    """The dense SwiGLU FFN (HipDenseMLP, the GGUFDenseMLP drop-in) on an 8B-class layer:
+    parity against the oracle (M = 1, and a token sample of M = 4096), decode M = 1 from
+    graph replays over 4 weight copies (380 MB, past the 256 MB MALL), prefill M = 4096."""
+    import numpy as np
+    from pgmoe import HipDenseMLP
+    from pgmoe.synth import DENSE_CONFIGS, SyntheticDense
+    sp = DENSE_CONFIGS["dense_8b"]
+    lay = SyntheticDense(sp, seed=0)
+    base = HipDenseMLP(lay.gguf, lay.config, 0, dev)
+    mats = []
+    for qt, proj, shp in zip(sp.qtypes, ("gate", "up", "down"),
+                             ((sp.inter, sp.hidden), (sp.inter, sp.hidden), (sp.hidden, sp.inter))):
+        mats.append((qt, shp[0], shp[1], np.ascontiguousarray(lay.tensor(f"ffn_{proj}.weight"))))
+    parity = {}
+    for M, toks in ((1, [0]), (4096, [0, 1777, 4095])):
+        x = lay.draw_x(M)
+        got = base(torch.from_numpy(x).to(dev)).cpu().numpy()[toks]
+        ref = oracle.dense_forward(x, *mats, tokens=toks)
+        parity[str(M)] = {"rel_l2": float(f"{oracle.rel_l2(got, ref):.3e}"),
+                          "max_rel": float(f"{oracle.max_rel(got, ref):.3e}")}
+    ok = all(v["rel_l2"] <= 1e-3 and v["max_rel"] <= 2e-2 for v in parity.values())
+    mods = [base] + [base.replica() for _ in range(3)]
+    x1 = torch.from_numpy(lay.draw_x(1)).to(dev)
+    ms1 = graph_step_ms(torch, mods, x1, steps, warmup)
+    xp = torch.from_numpy(lay.draw_x(4096)).to(dev)
+    msp = eager_step_ms(torch, mods[:2], xp, prefill_steps, 2)
+    wb = base.weight_bytes()
+    gbs = wb / (ms1 * 1e-3) / 1e9
+    fl = 2.0 * 4096 * 3 * sp.hidden * sp.inter
+    tf = fl / (msp * 1e-3) / 1e12
+    del mods, base
+    torch.cuda.empty_cache()
+    return {"workload": f"dense SwiGLU FFN H={sp.hidden} I={sp.inter}, gate/up Q4_K, down Q6_K",
+            "decode_m1": {"us_per_step": round(ms1 * 1e3, 3), "tok_per_s": round(1 / (ms1 * 1e-3), 1),
+                          "weight_bytes": wb, "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                          "timing": "one forward per HIP graph replay, 4 weight copies"},
+            "prefill": {"M": 4096, "us_per_step": round(msp * 1e3, 2), "tok_per_s": round(4096 / (msp * 1e-3), 1),
+                        "tflops": round(tf, 1), "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4)},
+            "parity": parity, **({} if ok else {"parity_failed": True})}
 
 
 def eager_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
@@ -346,6 +389,14 @@ def main() -> int:
         del pmods, pm
         torch.cuda.empty_cache()
 
+    dense = None
+    if not args.no_dense:
+        dense = dense_section(torch, oracle, dev, args.steps, args.warmup, args.prefill_steps)
+        log(f"[bench] dense: {dense}")
+        if dense.get("parity_failed"):
+            log("[bench] DENSE PARITY FAILED")
+            return 1
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(lay, 1, args.cpu_seconds)
@@ -377,6 +428,7 @@ def main() -> int:
                        "layer_active_gbs": round(layer_gbs, 1),
                        "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "prefill": prefill,
+        "dense": dense,
         "parity": {str(M): {k: (float(f"{v:.3e}") if isinstance(v, float) else v) for k, v in g.items()}
                    for M, g in gate.items()},
     }

@@ -85,6 +85,12 @@ typedef struct pgmoe_layer {
     const float* sh_inp_gate; /* [H] fp32 or NULL: sigmoid gate on the shared expert */
 } pgmoe_layer;
 
+/* A dense SwiGLU FFN: one matrix triple, no router (GGUFDenseMLP, model.py:778-846). */
+typedef struct pgmoe_dense {
+    int32_t hidden;               /* H */
+    pgmoe_weights gate, up, down; /* [I, H], [I, H], [H, I], n_mats = 1 */
+} pgmoe_dense;
+
 int pgmoe_abi_version(void);
 const char* pgmoe_last_error(void);
 
@@ -120,6 +126,16 @@ size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M);
  * Host-sync free and allocation free (graph-capturable with a fixed M). */
 int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
                       size_t ws_bytes, void* stream);
+
+/* Workspace bytes pgmoe_dense_forward needs for M tokens (0 for invalid arguments).  It
+ * holds no state between calls: any workspace of this size serves. */
+size_t pgmoe_dense_workspace_bytes(const pgmoe_dense* D, int32_t M);
+
+/* One dense SwiGLU FFN: out[M, H] (fp32) = GGUFDenseMLP.forward(x[M, H]) (model.py:839-846:
+ * gate||up GGUF products -> silu(gate) * up -> down).  Host-sync free and allocation free.
+ * The reference's GeGLU variant (gemma) has no kernel here. */
+int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, float* out, void* ws, size_t ws_bytes,
+                        void* stream);
 
 /* pgmoe_moe_forward with per-kernel timing.  No counterpart in the reference: it is for
  * benchmarks and profilers that want each kernel's duration from the caller's own stream.

@@ -212,6 +212,25 @@ class OracleLayer:
         return out
 
 
+def dense_forward(x: np.ndarray, gate: tuple, up: tuple, down: tuple,
+                  tokens: Optional[Sequence[int]] = None, conv: int = 0) -> np.ndarray:
+    """float64 output of a dense SwiGLU FFN (GGUFDenseMLP.forward, model.py:839-846) for
+    `tokens`: the expert FFN of or_moe_forward_tokens applied as its shared expert to a
+    layer with no routed experts.  gate / up / down: (qtype, rows, cols, GGUF bytes)."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    M, H = x.shape
+    toks = np.arange(M, dtype=np.int32) if tokens is None else np.asarray(tokens, dtype=np.int32)
+    toks = np.ascontiguousarray(toks)
+    out = np.empty((len(toks), H), dtype=np.float64)
+    keep = [gate, up, down]
+    ws = [ctypes.pointer(_Weights(t[0], t[1], t[2], t[3].ctypes.data)) for t in keep]
+    none = np.zeros(1, dtype=np.int32)
+    rc = lib().or_moe_forward_tokens(H, 0, 0, conv, None, None, None, *ws, None, _ptr(x), _ptr(none),
+                                     _ptr(none.view(np.float32)), _ptr(toks), len(toks), _ptr(out))
+    _check(rc, "moe_forward_tokens (dense)")
+    return out
+
+
 def rel_l2(a: np.ndarray, b: np.ndarray) -> float:
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)

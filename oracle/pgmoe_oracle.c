@@ -337,8 +337,8 @@ int or_moe_forward_tokens(int H, int E, int K, int conv,
     double* xt = (double*)malloc(sizeof(double) * (size_t)n_tokens * H);
     double* tmp = (double*)malloc(sizeof(double) * (size_t)n_tokens * H);
     double* xsel = (double*)malloc(sizeof(double) * (size_t)n_tokens * H);
-    int* sel = (int*)malloc(sizeof(int) * (size_t)n_tokens);
-    double* contrib = (double*)malloc(sizeof(double) * (size_t)n_tokens * K * H);
+    int* sel = (int*)malloc(sizeof(int) * (size_t)n_tokens + 1);
+    double* contrib = (double*)malloc(sizeof(double) * ((size_t)n_tokens * K * H + 1)); /* K = 0: dense */
     int rc = -2;
     if (!xt || !tmp || !xsel || !sel || !contrib) goto done;
     for (int j = 0; j < n_tokens; ++j)

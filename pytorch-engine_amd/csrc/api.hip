@@ -163,11 +163,94 @@ static int check_layer(const pgmoe_layer* L, LayerMats* lm) {
     return PGMOE_OK;
 }
 
+// ---------------------------------------------------------------- dense SwiGLU MLP
+// The same kernels with one matrix triple applied to every token with weight 1 (the
+// shared expert's launches without a router).
+struct DenseLayout {
+    size_t offsets, perm, inv, active, nact, tile_off, w, inter, isum, a16, rs, total;
+};
+
+static DenseLayout dense_layout(int M, int I) {
+    DenseLayout o{};
+    const bool gemm = M > decode_tokens_max();
+    size_t c = 0;
+    o.offsets = take(c, gemm ? 2 * 4 : 0);
+    o.perm = take(c, gemm ? (size_t)M * 4 : 0);
+    o.inv = take(c, gemm ? (size_t)M * 4 : 0);
+    o.active = take(c, gemm ? 4 : 0);
+    o.nact = take(c, gemm ? 4 : 0);
+    o.tile_off = take(c, gemm ? 2 * 4 : 0);
+    o.w = take(c, gemm ? (size_t)M * 4 : 0);
+    o.inter = take(c, (size_t)M * I * 4);
+    o.isum = take(c, gemm ? 0 : (size_t)M * (I / 16) * 4);
+    o.a16 = take(c, gemm ? (size_t)M * I * 2 : 0);
+    o.rs = take(c, gemm ? (size_t)M * 4 : 0);
+    o.total = c;
+    return o;
+}
+
+static int check_dense(const pgmoe_dense* D, Mats* g, Mats* u, Mats* d) {
+    if (!D) return fail(PGMOE_E_INVALID, "NULL dense layer");
+    if (D->hidden <= 0 || D->hidden % 256 || D->hidden > 65536)
+        return fail(PGMOE_E_UNSUPPORTED, "hidden size %d must be a positive multiple of 256 (<= 65536)", D->hidden);
+    int rc;
+    if ((rc = check_weights(&D->gate, "dense gate", g)) || (rc = check_weights(&D->up, "dense up", u)) ||
+        (rc = check_weights(&D->down, "dense down", d)) || (rc = check_pair(*g, *u, "dense")))
+        return rc;
+    if (g->n_mats != 1 || d->n_mats != 1 || g->K != D->hidden || d->N != D->hidden || d->K != g->N)
+        return fail(PGMOE_E_INVALID, "dense shapes do not match H=%d (gate [%d,%d,%d], down [%d,%d,%d])", D->hidden,
+                    g->n_mats, g->N, g->K, d->n_mats, d->N, d->K);
+    return PGMOE_OK;
+}
+
 }  // namespace pgmoe
 
 using namespace pgmoe;
 
 extern "C" {
+
+size_t pgmoe_dense_workspace_bytes(const pgmoe_dense* D, int32_t M) {
+    Mats g, u, d;
+    if (M < 0 || check_dense(D, &g, &u, &d)) return 0;
+    return dense_layout(M, g.N).total;
+}
+
+int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, float* out, void* ws, size_t ws_bytes,
+                        void* stream) {
+    Mats g, u, d;
+    int rc = check_dense(D, &g, &u, &d);
+    if (rc) return rc;
+    if (M < 0) return fail(PGMOE_E_INVALID, "negative token count");
+    if (M == 0) return PGMOE_OK;
+    if (!x || !out || !ws) return fail(PGMOE_E_INVALID, "dense_forward: NULL pointer");
+    if ((uintptr_t)ws & 255) return fail(PGMOE_E_INVALID, "workspace must be 256-byte aligned");
+    const DenseLayout o = dense_layout(M, g.N);
+    if (ws_bytes < o.total) return fail(PGMOE_E_WORKSPACE, "workspace %zu bytes, need %zu", ws_bytes, o.total);
+    uint8_t* b = (uint8_t*)ws;
+#define WS(T, f) reinterpret_cast<T*>(b + o.f)
+    const hipStream_t st = as_stream(stream);
+    if (M <= decode_tokens_max()) {  // gate/up + SwiGLU, then down straight into out
+        if ((rc = launch_dec_gateup_ident(g, u, x, nullptr, M, WS(float, inter), WS(float, isum), st))) return rc;
+        // the 8-row, 16-wave down blocks when the SwiGLU rows fit in LDS, else the per-expert one
+        if (decode_fused_down(M, g.N))
+            return launch_dec_down_combine(d, WS(float, inter), WS(float, isum), nullptr, M, 1, 1, nullptr, nullptr,
+                                           out, nullptr, 0, st);
+        return launch_dec_down_ident(d, WS(float, inter), WS(float, isum), M, out, st);
+    }
+    const int BM = gemm_tile_rows();
+    if ((rc = launch_identity_dispatch(M, BM, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, inv),
+                                       WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), WS(float, w),
+                                       st)))
+        return rc;
+    if ((rc = launch_gateup(g, u, x, M, 1, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
+                            WS(int32_t, nact), WS(int32_t, tile_off), 1, WS(float, inter), st)))
+        return rc;
+    // identity order: sorted pair p is token p, so the down rows are the output rows
+    return launch_down(d, WS(float, inter), M, 1, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
+                       WS(int32_t, nact), WS(int32_t, tile_off), WS(float, w), 1, WS(uint16_t, a16), WS(float, rs),
+                       out, st);
+#undef WS
+}
 
 int pgmoe_abi_version(void) { return PGMOE_ABI_VERSION; }
 
@@ -322,9 +405,12 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
             if ((rc = launch_dec_gateup_ident(lm.sg, lm.su, x, WS(float, xsum), M, WS(float, s_inter),
                                               WS(float, s_isum), st)))
                 return rc;
-            if ((rc = launch_dec_down_ident(lm.sd, WS(float, s_inter), WS(float, s_isum), M, WS(float, s_partial),
-                                            st)))
-                return rc;
+            if (decode_fused_down(M, lm.sd.K))
+                rc = launch_dec_down_combine(lm.sd, WS(float, s_inter), WS(float, s_isum), nullptr, M, 1, 1, nullptr,
+                                             nullptr, WS(float, s_partial), nullptr, 0, st);
+            else
+                rc = launch_dec_down_ident(lm.sd, WS(float, s_inter), WS(float, s_isum), M, WS(float, s_partial), st);
+            if (rc) return rc;
             shared = WS(float, s_partial);
             if (sgw) shared_logit = WS(float, s_logit);
         }

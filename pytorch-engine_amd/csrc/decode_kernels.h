@@ -1039,8 +1039,9 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
 // LDS tree sums the lanes and waves.  out[t, row] = that sum (+ shared[t, row] *
 // sigmoid(shared_logit[t])).  Inputs: the routing descriptor (P = M*K pairs) and the inter
 // / isum rows in sorted pair order, all staged in LDS at once (the host uses this kernel
-// only when they fit).  The item order depends only on the routing, so results are
-// reproducible run to run.
+// only when they fit).  A null descriptor is the identity: one slot, matrix 0, pair p =
+// token p with weight 1 (a dense FFN or the shared expert alone, P = M).  The item order
+// depends only on the routing, so results are reproducible run to run.
 // Dynamic LDS: xs [P][K/64][68] f32 | iss [P][K/16] f32.
 template <int QT, int TM>
 __device__ __forceinline__ void dc_item(const Qtr<QT>& q, bool valid, int it, int nb, int p, const float* xs, int xrs,
@@ -1090,17 +1091,19 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
     // 1. the experts of this lane's first two items straight from the descriptor, then
     //    their weights, then the inter rows and the pair table behind them: the weights'
     //    latency covers the staging
-    const int S = desc[0] * nb;  // items (active slot a, super-block j), it = a * nb + j
+    const bool ident = desc == nullptr;
+    const int S = (ident ? 1 : desc[0]) * nb;  // items (active slot a, super-block j), it = a * nb + j
     int it0 = 2 * w + u, it1 = it0 + 2 * nw;
-    int e0 = desc[kDescSlot + 4 * min(it0 / nb, 127)], e1 = desc[kDescSlot + 4 * min(it1 / nb, 127)];
+    int e0 = ident ? 0 : desc[kDescSlot + 4 * min(it0 / nb, 127)];
+    int e1 = ident ? 0 : desc[kDescSlot + 4 * min(it1 / nb, 127)];
     Qtr<QT> q0, q1;
     load_qtr<QT>(q0, dbase + (int64_t)(it0 < S ? e0 : 0) * dstride, N, nb, row, it0 % nb, p);
     load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, row, it1 % nb, p);
     for (int i = tid; i < P; i += nth) {
-        d_pb[i] = desc[kDescSlot + 4 * i + 1];
-        d_cnt[i] = desc[kDescSlot + 4 * i + 2];
-        d_tok[i] = desc[kDescPair + 2 * i];
-        d_w[i] = __builtin_bit_cast(float, desc[kDescPair + 2 * i + 1]);
+        d_pb[i] = ident ? 0 : desc[kDescSlot + 4 * i + 1];
+        d_cnt[i] = ident ? P : desc[kDescSlot + 4 * i + 2];
+        d_tok[i] = ident ? i : desc[kDescPair + 2 * i];
+        d_w[i] = ident ? 1.0f : __builtin_bit_cast(float, desc[kDescPair + 2 * i + 1]);
     }
     const int kq = K >> 2;
     copy_idx<4, u32x4>(
@@ -1120,8 +1123,8 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
         it1 += 4 * nw;
         if (it0 - u >= S) break;  // wave-uniform (it0 - u is the pass's first item): no item left
         // (rare) more items than lanes: next pass
-        e0 = desc[kDescSlot + 4 * min(it0 / nb, 127)];
-        e1 = desc[kDescSlot + 4 * min(it1 / nb, 127)];
+        e0 = ident ? 0 : desc[kDescSlot + 4 * min(it0 / nb, 127)];
+        e1 = ident ? 0 : desc[kDescSlot + 4 * min(it1 / nb, 127)];
         load_qtr<QT>(q0, dbase + (int64_t)(it0 < S ? e0 : 0) * dstride, N, nb, row, it0 % nb, p);
         load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, row, it1 % nb, p);
     }

@@ -86,6 +86,7 @@ int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, con
                             float* isum, hipStream_t st);
 int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st);
 // clear (may be null): n_clear words the kernel sets to zero (the decode router's tagged logits).
+// desc null: the identity (matrix 0 applied to every token with weight 1; P = M, K = 1).
 int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int K,
                             int max_active, const float* shared, const float* shared_logit, float* out,
                             uint64_t* clear, int n_clear, hipStream_t st);

@@ -1,14 +1,17 @@
 """pgmoe: MI355X-native quantized MoE FFN layer for GGUF models.
 
 ``HipSparseMoEMLP`` is a drop-in for PyGGUF's ``GGUFSparseMoEMLP``
-(pygguf_engine/model.py:849-937); ``pgmoe.ops`` exposes the C-ABI stages.
+(pygguf_engine/model.py:849-937) and ``HipDenseMLP`` for its ``GGUFDenseMLP``
+(model.py:778-846) on the same kernels; ``pgmoe.ops`` exposes the C-ABI stages.
 """
 
 from .gguf import GGMLType, GGUFFile, GGUFWriter, InMemoryGGUF, MoEConfig
+from .dense import HipDenseMLP
 from .moe import HipSparseMoEMLP
 
-# The reference's class name, so `from pgmoe import GGUFSparseMoEMLP` swaps the block in.
+# The reference's class names, so `from pgmoe import GGUFSparseMoEMLP` swaps the block in.
 GGUFSparseMoEMLP = HipSparseMoEMLP
+GGUFDenseMLP = HipDenseMLP
 
 __all__ = ["GGMLType", "GGUFFile", "GGUFWriter", "InMemoryGGUF", "MoEConfig", "HipSparseMoEMLP",
-           "GGUFSparseMoEMLP"]
+           "GGUFSparseMoEMLP", "HipDenseMLP", "GGUFDenseMLP"]

@@ -53,6 +53,15 @@ class Layer(ctypes.Structure):
     ]
 
 
+class Dense(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _I32),
+        ("gate", Weights),
+        ("up", Weights),
+        ("down", Weights),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -79,6 +88,9 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_workspace_bytes.restype = ctypes.c_size_t
     L.pgmoe_workspace_bytes.argtypes = [ctypes.POINTER(Layer), _I32]
     L.pgmoe_moe_forward.argtypes = [ctypes.POINTER(Layer), _P, _I32, _P, _P, ctypes.c_size_t, _P]
+    L.pgmoe_dense_workspace_bytes.restype = ctypes.c_size_t
+    L.pgmoe_dense_workspace_bytes.argtypes = [ctypes.POINTER(Dense), _I32]
+    L.pgmoe_dense_forward.argtypes = [ctypes.POINTER(Dense), _P, _I32, _P, _P, ctypes.c_size_t, _P]
     L.pgmoe_moe_forward_timed.argtypes = [ctypes.POINTER(Layer), _P, _I32, _P, _P, ctypes.c_size_t, _P,
                                           ctypes.POINTER(_P), ctypes.POINTER(_P), _I32, ctypes.POINTER(_I32)]
     L.pgmoe_router_topk.argtypes = [_P, _P, _P, _I32, _I32, _I32, _I32, _I32, _P, _P, _P, _P]
@@ -93,7 +105,8 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_combine.argtypes = [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P]
     for fn in ("pgmoe_moe_forward", "pgmoe_moe_forward_timed", "pgmoe_router_topk", "pgmoe_dispatch",
                "pgmoe_dispatch_ws", "pgmoe_expert_gateup",
-               "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_build_scale_plane"):
+               "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_build_scale_plane",
+               "pgmoe_dense_forward"):
         getattr(L, fn).restype = ctypes.c_int
     ver = L.pgmoe_abi_version()
     if ver != ABI_VERSION:
@@ -114,4 +127,5 @@ EXPORTS = (
     "pgmoe_workspace_bytes", "pgmoe_moe_forward", "pgmoe_router_topk", "pgmoe_dispatch",
     "pgmoe_expert_gateup", "pgmoe_expert_down", "pgmoe_combine", "pgmoe_moe_forward_timed",
     "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane", "pgmoe_dispatch_ws_bytes", "pgmoe_dispatch_ws",
+    "pgmoe_dense_workspace_bytes", "pgmoe_dense_forward",
 )

@@ -25,7 +25,8 @@ from .gguf import GGMLType, InMemoryGGUF, MoEConfig
 
 Q4_K, Q6_K, Q8_0 = GGMLType.Q4_K, GGMLType.Q6_K, GGMLType.Q8_0
 
-__all__ = ["LayerSpec", "CONFIGS", "SyntheticLayer", "random_blocks", "zipf_bias"]
+__all__ = ["LayerSpec", "CONFIGS", "SyntheticLayer", "DenseSpec", "DENSE_CONFIGS", "SyntheticDense",
+           "random_blocks", "zipf_bias"]
 
 
 @dataclass(frozen=True)
@@ -166,3 +167,59 @@ class SyntheticLayer:
 def with_shape(spec: LayerSpec, **kw) -> LayerSpec:
     """A copy of ``spec`` with some fields replaced (smaller test layers)."""
     return replace(spec, **kw)
+
+
+# ---------------------------------------------------------------- dense SwiGLU FFN
+@dataclass(frozen=True)
+class DenseSpec:
+    name: str
+    hidden: int
+    inter: int
+    qtypes: Tuple[int, int, int]  # gate, up, down
+    arch: str = "qwen3"
+
+    def weight_bytes(self) -> int:
+        from .gguf import tensor_nbytes
+        n = self.inter * self.hidden
+        return sum(tensor_nbytes(q, n) for q in self.qtypes)
+
+
+# Dense FFN shapes (the reference's GGUFDenseMLP, model.py:778-846): a small one for tests,
+# an 8B-class Q4_K_M layer (gate/up Q4_K, down Q6_K) and an all-Q8_0 one.
+DENSE_CONFIGS: Dict[str, DenseSpec] = {
+    "dense_tiny": DenseSpec("dense_tiny", 1024, 2816, (Q4_K, Q4_K, Q6_K)),
+    "dense_q8": DenseSpec("dense_q8", 2048, 5632, (Q8_0, Q8_0, Q8_0), arch="llama"),
+    "dense_8b": DenseSpec("dense_8b", 4096, 12288, (Q4_K, Q4_K, Q6_K)),
+}
+
+
+@dataclass
+class SyntheticDense:
+    """One seeded dense FFN (blk.0.ffn_{gate,up,down}.weight) through the GGUF reader surface."""
+
+    spec: DenseSpec
+    seed: int = 0
+    scale: float = 1.0
+    gguf: InMemoryGGUF = field(init=False)
+    config: MoEConfig = field(init=False)
+
+    def __post_init__(self) -> None:
+        sp = self.spec
+        rng = np.random.default_rng([self.seed, 7])
+        g = InMemoryGGUF({"general.architecture": sp.arch, f"{sp.arch}.embedding_length": sp.hidden,
+                          f"{sp.arch}.feed_forward_length": sp.inter})
+        H, I = sp.hidden, sp.inter
+        shapes = {"gate": (I, H), "up": (I, H), "down": (H, I)}
+        for qt, proj in zip(sp.qtypes, ("gate", "up", "down")):
+            n, k = shapes[proj]
+            g.add_tensor(f"blk.0.ffn_{proj}.weight", (n, k), qt, random_blocks(rng, qt, n, k, self.scale))
+        self.gguf = g
+        self.config = g.build_model_config()
+
+    def draw_x(self, M: int) -> np.ndarray:
+        """fp16 activations [M, hidden] ~ N(0, 1)."""
+        rng = np.random.default_rng([self.seed, M, 7])
+        return rng.standard_normal((M, self.spec.hidden), dtype=np.float32).astype(np.float16)
+
+    def tensor(self, name: str) -> np.ndarray:
+        return self.gguf.get_tensor_bytes(f"blk.0.{name}")
