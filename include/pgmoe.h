@@ -57,6 +57,7 @@ extern "C" {
 #define PGMOE_E_WORKSPACE (-3)   /* workspace too small */
 #define PGMOE_E_HIP (-4)         /* HIP runtime error (launch or query) */
 
+#define PGMOE_Q4_0 2  /* source format only: relaid out as PGMOE_Q8_0 (exact values) */
 #define PGMOE_Q8_0 8
 #define PGMOE_Q4_K 12
 #define PGMOE_Q6_K 14
@@ -94,12 +95,15 @@ typedef struct pgmoe_dense {
 int pgmoe_abi_version(void);
 const char* pgmoe_last_error(void);
 
-/* Bytes of one matrix in the device layout (== GGUF bytes); -1 if unsupported. */
+/* Bytes of one matrix in the device layout (== GGUF bytes; Q4_0: the Q8_0 layout it is
+ * converted to); -1 if unsupported. */
 int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
 
 /* GGUF blocks (device, n_mats matrices back to back) -> device layout.
  * Load-time replacement of repack_gguf_to_w4a16 / repack_gguf_to_w8a16
- * (quant_kernels.py:854-1036), keeping the GGUF bits instead of re-quantising. */
+ * (quant_kernels.py:854-1036), keeping the GGUF bits instead of re-quantising.  A Q4_0
+ * source is written in the Q8_0 layout with qs = q - 8 and the same d (every value
+ * kept exactly); pass the result as PGMOE_Q8_0 weights. */
 int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
                            void* dst, void* stream);
 

@@ -23,6 +23,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#define QT_Q4_0 2
 #define QT_Q8_0 8
 #define QT_Q4_K 12
 #define QT_Q6_K 14
@@ -147,8 +148,19 @@ static void decode_q8_0_block(const uint8_t* b, float* out) {
     for (int l = 0; l < 32; ++l) out[l] = d * (float)q[l];
 }
 
+/* Q4_0: [d f16][16 bytes: weight l in the low nibble of byte l, weight 16 + l in the
+ * high nibble]; value d * (nibble - 8) (ggml dequantize_row_q4_0). */
+static void decode_q4_0_block(const uint8_t* b, float* out) {
+    float d = or_half_to_float(rd16(b));
+    for (int l = 0; l < 16; ++l) {
+        out[l] = d * (float)((int)(b[2 + l] & 15) - 8);
+        out[16 + l] = d * (float)((int)(b[2 + l] >> 4) - 8);
+    }
+}
+
 int or_block_geometry(int qtype, int* per_block, int* block_bytes) {
     switch (qtype) {
+    case QT_Q4_0: *per_block = 32; *block_bytes = 18; return 0;
     case QT_Q4_K: *per_block = 256; *block_bytes = 144; return 0;
     case QT_Q6_K: *per_block = 256; *block_bytes = 210; return 0;
     case QT_Q8_0: *per_block = 32; *block_bytes = 34; return 0;
@@ -166,6 +178,7 @@ int or_dequant_rows(int qtype, int conv, const uint8_t* blocks, int64_t rows, in
         float* o = out + i * pb;
         if (qtype == QT_Q4_K) decode_q4k_block(b, conv, o);
         else if (qtype == QT_Q6_K) decode_q6k_block(b, conv, o);
+        else if (qtype == QT_Q4_0) decode_q4_0_block(b, o);
         else decode_q8_0_block(b, o);
     }
     return 0;

@@ -58,8 +58,9 @@ class _ExpertTensor:
         if not three_d and len(shape) != 2:
             raise ValueError(f"Expected 2D tensor for {name}, got shape={shape}")
         self.n_mats, self.rows, self.cols = (shape if three_d else (1,) + shape)
-        self.qtype = int(info.qtype)
-        if self.qtype not in SUPPORTED_QTYPES:
+        self.gguf_qtype = int(info.qtype)
+        self.qtype = ops.device_qtype(self.gguf_qtype)  # format of the device layout
+        if self.gguf_qtype not in SUPPORTED_QTYPES:
             raise NotImplementedError(
                 f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
                 "has no HIP kernel (supported: Q4_K, Q6_K, Q8_0)")
@@ -67,7 +68,7 @@ class _ExpertTensor:
             raise ValueError(f"{name}: {self.cols} input features is not a multiple of 256")
         raw_np = gguf_file.get_tensor_bytes(name)
         raw = torch.from_numpy(np.asarray(raw_np)).to(device)  # H2D copy of the GGUF bytes
-        self.buf = ops.relayout(self.qtype, raw, self.n_mats, self.rows, self.cols)
+        self.buf = ops.relayout(self.gguf_qtype, raw, self.n_mats, self.rows, self.cols)
         del raw
         # K-quants: the sub-block scales decoded once for the prefill MFMA products
         self.plane = ops.scale_plane(self.qtype, self.buf, self.n_mats, self.rows, self.cols)
@@ -77,7 +78,7 @@ class _ExpertTensor:
 
     @property
     def gguf_bytes_per_mat(self) -> int:
-        per, bb = ops.GGUF_BLOCK[self.qtype]
+        per, bb = ops.GGUF_BLOCK[self.gguf_qtype]
         return self.rows * (self.cols // per) * bb
 
 

@@ -12,9 +12,15 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import Q4_K, Q6_K, Q8_0, Weights, check, lib
+from ._lib import Q4_0, Q4_K, Q6_K, Q8_0, Weights, check, lib
 
-GGUF_BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34)}
+GGUF_BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18)}
+
+
+def device_qtype(qtype: int) -> int:
+    """Format of the device layout the relayout of GGUF `qtype` produces: Q4_0 becomes Q8_0
+    (d * (q - 8) is the Q8_0 value d * qs with qs = q - 8), the others keep theirs."""
+    return Q8_0 if qtype == Q4_0 else qtype
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -47,7 +53,8 @@ def weight_stride(qtype: int, rows: int, cols: int) -> int:
 
 
 def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int) -> torch.Tensor:
-    """GGUF bytes on the device -> pgmoe device layout (uint8 [n_mats * stride])."""
+    """GGUF bytes on the device -> pgmoe device layout (uint8 [n_mats * stride]) of format
+    device_qtype(qtype)."""
     dev = _need_cuda(raw)
     stride = weight_stride(qtype, rows, cols)
     per, bb = GGUF_BLOCK[qtype]

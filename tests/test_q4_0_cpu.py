@@ -1,0 +1,45 @@
+"""Q4_0 experts (the format of the reference's synthetic qwen35moe test model,
+tests/test_pygguf_engine.py:424-440): the oracle's Q4_0 decoder pinned by reduction to
+the golden-pinned Q8_0 decoder, and the C-ABI sizes (Q4_0 is stored as Q8_0)."""
+
+import numpy as np
+
+import oracle
+from pgmoe.synth import random_blocks
+
+Q4_0, Q8_0 = 2, 8
+
+
+def q4_0_as_q8_0(raw: np.ndarray) -> np.ndarray:
+    """Q4_0 blocks -> the Q8_0 blocks of the same values: same d, qs = nibble - 8 (weight l
+    from the low nibble of byte l, weight 16 + l from its high nibble)."""
+    b = raw.reshape(-1, 18)
+    out = np.empty((b.shape[0], 34), dtype=np.uint8)
+    out[:, 0:2] = b[:, 0:2]
+    q = b[:, 2:18]
+    out[:, 2:18] = ((q & 15).astype(np.int16) - 8).astype(np.int8).view(np.uint8)
+    out[:, 18:34] = ((q >> 4).astype(np.int16) - 8).astype(np.int8).view(np.uint8)
+    return out.reshape(-1)
+
+
+def test_q4_0_decoder_equals_q8_0_of_the_same_values():
+    rng = np.random.default_rng(5)
+    raw = random_blocks(rng, Q4_0, 6, 256)
+    a = oracle.dequant(Q4_0, raw, 6, 256)
+    b = oracle.dequant(Q8_0, q4_0_as_q8_0(raw), 6, 256)
+    np.testing.assert_array_equal(a, b)
+    # closed form on one block: d * (q - 8), low nibbles first
+    blk = np.zeros(18, dtype=np.uint8)
+    blk[0:2] = np.array([0.5], dtype=np.float16).view(np.uint8)
+    blk[2:18] = np.arange(16, dtype=np.uint8) | (np.uint8(15) << 4)
+    v = oracle.dequant(Q4_0, blk, 1, 32)
+    np.testing.assert_array_equal(v[0, :16], 0.5 * (np.arange(16) - 8))
+    np.testing.assert_array_equal(v[0, 16:], np.full(16, 0.5 * 7))
+
+
+def test_q4_0_sizes_are_q8_0_sizes():
+    from pgmoe._lib import lib
+    L = lib()
+    for rows, cols in ((64, 256), (100, 2048), (768, 2048)):
+        assert L.pgmoe_weight_bytes(Q4_0, rows, cols) == L.pgmoe_weight_bytes(Q8_0, rows, cols) > 0
+        assert L.pgmoe_scale_plane_bytes(Q8_0, rows, cols) == 0
