@@ -58,6 +58,7 @@ extern "C" {
 #define PGMOE_E_HIP (-4)         /* HIP runtime error (launch or query) */
 
 #define PGMOE_Q4_0 2  /* source format only: relaid out as PGMOE_Q8_0 (exact values) */
+#define PGMOE_Q5_0 6  /* source format only: relaid out as PGMOE_Q8_0 (exact values) */
 #define PGMOE_Q8_0 8
 #define PGMOE_Q4_K 12
 #define PGMOE_Q6_K 14
@@ -102,8 +103,8 @@ int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
 /* GGUF blocks (device, n_mats matrices back to back) -> device layout.
  * Load-time replacement of repack_gguf_to_w4a16 / repack_gguf_to_w8a16
  * (quant_kernels.py:854-1036), keeping the GGUF bits instead of re-quantising.  A Q4_0
- * source is written in the Q8_0 layout with qs = q - 8 and the same d (every value
- * kept exactly); pass the result as PGMOE_Q8_0 weights. */
+ * (Q5_0) source is written in the Q8_0 layout with qs = q - 8 (q - 16) and the same d
+ * (every value kept exactly); pass the result as PGMOE_Q8_0 weights. */
 int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
                            void* dst, void* stream);
 

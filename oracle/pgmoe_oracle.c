@@ -24,6 +24,7 @@
 #include <string.h>
 
 #define QT_Q4_0 2
+#define QT_Q5_0 6
 #define QT_Q8_0 8
 #define QT_Q4_K 12
 #define QT_Q6_K 14
@@ -158,9 +159,22 @@ static void decode_q4_0_block(const uint8_t* b, float* out) {
     }
 }
 
+/* Q5_0: [d f16][qh u32 LE: bit l = 5th bit of weight l][16 bytes: weight l in the low
+ * nibble of byte l, weight 16 + l in the high nibble]; value d * (q - 16)
+ * (ggml dequantize_row_q5_0). */
+static void decode_q5_0_block(const uint8_t* b, float* out) {
+    float d = or_half_to_float(rd16(b));
+    uint32_t qh = (uint32_t)b[2] | ((uint32_t)b[3] << 8) | ((uint32_t)b[4] << 16) | ((uint32_t)b[5] << 24);
+    for (int l = 0; l < 16; ++l) {
+        out[l] = d * (float)((int)((b[6 + l] & 15) | (((qh >> l) & 1) << 4)) - 16);
+        out[16 + l] = d * (float)((int)((b[6 + l] >> 4) | (((qh >> (16 + l)) & 1) << 4)) - 16);
+    }
+}
+
 int or_block_geometry(int qtype, int* per_block, int* block_bytes) {
     switch (qtype) {
     case QT_Q4_0: *per_block = 32; *block_bytes = 18; return 0;
+    case QT_Q5_0: *per_block = 32; *block_bytes = 22; return 0;
     case QT_Q4_K: *per_block = 256; *block_bytes = 144; return 0;
     case QT_Q6_K: *per_block = 256; *block_bytes = 210; return 0;
     case QT_Q8_0: *per_block = 32; *block_bytes = 34; return 0;
@@ -179,6 +193,7 @@ int or_dequant_rows(int qtype, int conv, const uint8_t* blocks, int64_t rows, in
         if (qtype == QT_Q4_K) decode_q4k_block(b, conv, o);
         else if (qtype == QT_Q6_K) decode_q6k_block(b, conv, o);
         else if (qtype == QT_Q4_0) decode_q4_0_block(b, o);
+        else if (qtype == QT_Q5_0) decode_q5_0_block(b, o);
         else decode_q8_0_block(b, o);
     }
     return 0;

@@ -11,6 +11,7 @@ template <> struct Gguf<PGMOE_Q4_K> { static constexpr int per = 256, bytes = 14
 template <> struct Gguf<PGMOE_Q6_K> { static constexpr int per = 256, bytes = 210; };
 template <> struct Gguf<PGMOE_Q8_0> { static constexpr int per = 32, bytes = 34; };
 template <> struct Gguf<PGMOE_Q4_0> { static constexpr int per = 32, bytes = 18; };
+template <> struct Gguf<PGMOE_Q5_0> { static constexpr int per = 32, bytes = 22; };
 
 __device__ __forceinline__ void copy16(uint8_t* d, const uint8_t* s) {
 #pragma unroll
@@ -22,9 +23,9 @@ __device__ __forceinline__ void zero16(uint8_t* d) {
     for (int i = 0; i < 16; ++i) d[i] = 0;
 }
 
-// One thread per (matrix, padded row, 256-weight block).  Q4_0 sources are written as
-// Q8_0 tiles: d * (q - 8) is the Q8_0 value d * qs with qs = q - 8 (same d, same 32-weight
-// blocks), so every value is kept exactly.
+// One thread per (matrix, padded row, 256-weight block).  Q4_0 and Q5_0 sources are
+// written as Q8_0 tiles: d * (q - 8) and d * (q - 16) (5-bit q) are the Q8_0 values d * qs
+// with qs = q - 8 / q - 16 (same d, same 32-weight blocks), so every value is kept exactly.
 template <int QT>
 __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats, int N, int nb,
                                 uint8_t* __restrict__ dst, int64_t dst_stride) {
@@ -36,7 +37,7 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
     const int64_t rem = gid % per_mat;
     const int row = (int)(rem / nb), b = (int)(rem % nb);
     const int rg = row >> 6, r = row & 63;
-    constexpr int DT = QT == PGMOE_Q4_0 ? PGMOE_Q8_0 : QT;  // device layout
+    constexpr int DT = (QT == PGMOE_Q4_0 || QT == PGMOE_Q5_0) ? PGMOE_Q8_0 : QT;  // device layout
     constexpr int CH = Tile<DT>::CH;
     uint8_t* md = dst + mat * dst_stride;
     uint8_t* t = md + ((int64_t)rg * nb + b) * (CH * 1024) + r * 16;
@@ -53,6 +54,24 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
             uint8_t* d = md + (int64_t)ng * nb * CH * 1024 + (((int64_t)rg * nb + b) * 64 + r) * 2;
             d[0] = real ? s[208] : 0;
             d[1] = real ? s[209] : 0;
+        }
+    } else if (QT == PGMOE_Q5_0) {  // eight 22-byte blocks per 256 weights -> Q8_0 tiles
+        for (int j = 0; j < 8; ++j) {
+            const uint8_t* bj = s + 22 * j;
+            const uint32_t qh = real ? (uint32_t)bj[2] | ((uint32_t)bj[3] << 8) | ((uint32_t)bj[4] << 16) |
+                                           ((uint32_t)bj[5] << 24)
+                                     : 0xffffffffu;  // pad rows: q = 16 -> 0
+            uint8_t lo[16], hi[16];
+#pragma unroll
+            for (int l = 0; l < 16; ++l) {
+                const int q = real ? bj[6 + l] : 0;
+                lo[l] = (uint8_t)(int8_t)(((q & 15) | (int)(((qh >> l) & 1) << 4)) - 16);
+                hi[l] = (uint8_t)(int8_t)(((q >> 4) | (int)(((qh >> (16 + l)) & 1) << 4)) - 16);
+            }
+            copy16(t + (2 * j) * 1024, lo);
+            copy16(t + (2 * j + 1) * 1024, hi);
+            t[16 * 1024 + 2 * j] = real ? bj[0] : 0;
+            t[16 * 1024 + 2 * j + 1] = real ? bj[1] : 0;
         }
     } else if (QT == PGMOE_Q4_0) {  // eight 18-byte blocks per 256 weights -> Q8_0 tiles
         for (int j = 0; j < 8; ++j) {
@@ -129,7 +148,8 @@ __global__ void scale_plane_kernel(const uint8_t* __restrict__ src, int64_t n_ma
 }
 
 int64_t scale_plane_bytes(int qtype, int64_t rows, int64_t cols) {
-    if (qtype == PGMOE_Q4_0 || layout_bytes(qtype, rows, cols) < 0) return -1;  // Q4_0: a source format
+    if (qtype == PGMOE_Q4_0 || qtype == PGMOE_Q5_0 || layout_bytes(qtype, rows, cols) < 0)
+        return -1;  // Q4_0 / Q5_0: source formats
     if (qtype == PGMOE_Q8_0) return 0;
     return (int64_t)row_groups((int)rows) * (cols / 256) * 4 * 1024;
 }
@@ -163,7 +183,8 @@ int64_t layout_bytes(int qtype, int64_t rows, int64_t cols) {
     case PGMOE_Q4_K: return ng * nb * 9 * 1024;
     case PGMOE_Q6_K: return ng * nb * (13 * 1024 + 128);
     case PGMOE_Q8_0:
-    case PGMOE_Q4_0: return ng * nb * 17 * 1024;  // Q4_0 is stored as Q8_0
+    case PGMOE_Q4_0:
+    case PGMOE_Q5_0: return ng * nb * 17 * 1024;  // Q4_0 / Q5_0 are stored as Q8_0
     default: return -1;
     }
 }
@@ -187,6 +208,9 @@ int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows,
         break;
     case PGMOE_Q4_0:
         PG_LAUNCH(relayout_kernel<PGMOE_Q4_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        break;
+    case PGMOE_Q5_0:
+        PG_LAUNCH(relayout_kernel<PGMOE_Q5_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
         break;
     default:
         return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d", qtype);

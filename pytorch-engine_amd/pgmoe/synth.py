@@ -23,7 +23,7 @@ import numpy as np
 
 from .gguf import GGMLType, InMemoryGGUF, MoEConfig
 
-Q4_0, Q4_K, Q6_K, Q8_0 = GGMLType.Q4_0, GGMLType.Q4_K, GGMLType.Q6_K, GGMLType.Q8_0
+Q4_0, Q5_0, Q4_K, Q6_K, Q8_0 = GGMLType.Q4_0, GGMLType.Q5_0, GGMLType.Q4_K, GGMLType.Q6_K, GGMLType.Q8_0
 
 __all__ = ["LayerSpec", "CONFIGS", "SyntheticLayer", "DenseSpec", "DENSE_CONFIGS", "SyntheticDense",
            "random_blocks", "zipf_bias"]
@@ -88,6 +88,11 @@ def random_blocks(rng: np.random.Generator, qtype: int, rows: int, cols: int,
         raw = rng.integers(0, 256, size=(nb, 210), dtype=np.uint8)
         d = (np.abs(rng.standard_normal(nb)) * (0.02 * scale)).astype(np.float16)
         raw[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    elif qtype == Q5_0:
+        nb = rows * (cols // 32)
+        raw = rng.integers(0, 256, size=(nb, 22), dtype=np.uint8)
+        d = (np.abs(rng.standard_normal(nb)) * (0.02 * scale)).astype(np.float16)
+        raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
     elif qtype == Q4_0:
         nb = rows * (cols // 32)
         raw = rng.integers(0, 256, size=(nb, 18), dtype=np.uint8)

@@ -40,6 +40,7 @@ def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
     assert L.pgmoe_weight_bytes(12, 4, 100) == -1  # not a whole K-quant block row
     assert L.pgmoe_weight_bytes(3, 4, 256) == -1   # Q4_1 has no kernel
     assert L.pgmoe_weight_bytes(13, 4, 256) == -1  # nor Q5_K
+    assert L.pgmoe_weight_bytes(6, 4, 256) == L.pgmoe_weight_bytes(8, 4, 256)  # Q5_0 is stored as Q8_0
     assert L.pgmoe_weight_bytes(8, 4, 96) == -1    # rows must be whole 256-weight tiles
     assert L.pgmoe_weight_bytes(8, 4, 320) == -1
 

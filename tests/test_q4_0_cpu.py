@@ -43,3 +43,37 @@ def test_q4_0_sizes_are_q8_0_sizes():
     for rows, cols in ((64, 256), (100, 2048), (768, 2048)):
         assert L.pgmoe_weight_bytes(Q4_0, rows, cols) == L.pgmoe_weight_bytes(Q8_0, rows, cols) > 0
         assert L.pgmoe_scale_plane_bytes(Q8_0, rows, cols) == 0
+
+
+Q5_0 = 6
+
+
+def q5_0_as_q8_0(raw: np.ndarray) -> np.ndarray:
+    """Q5_0 blocks -> the Q8_0 blocks of the same values: same d, qs = q - 16 with q the
+    nibble plus bit l (bit 16 + l for the high nibbles) of the little-endian qh word."""
+    b = raw.reshape(-1, 22)
+    out = np.empty((b.shape[0], 34), dtype=np.uint8)
+    out[:, 0:2] = b[:, 0:2]
+    qh = b[:, 2:6].copy().view("<u4").reshape(-1, 1).astype(np.int64)
+    q = b[:, 6:22].astype(np.int64)
+    l = np.arange(16)
+    lo = (q & 15) | (((qh >> l) & 1) << 4)
+    hi = (q >> 4) | (((qh >> (16 + l)) & 1) << 4)
+    out[:, 2:18] = (lo - 16).astype(np.int8).view(np.uint8)
+    out[:, 18:34] = (hi - 16).astype(np.int8).view(np.uint8)
+    return out.reshape(-1)
+
+
+def test_q5_0_decoder_equals_q8_0_of_the_same_values():
+    rng = np.random.default_rng(6)
+    raw = random_blocks(rng, Q5_0, 5, 512)
+    np.testing.assert_array_equal(oracle.dequant(Q5_0, raw, 5, 512), oracle.dequant(Q8_0, q5_0_as_q8_0(raw), 5, 512))
+    # closed form: qh bit l lifts weight l by 16, bit 16 + l weight 16 + l
+    blk = np.zeros(22, dtype=np.uint8)
+    blk[0:2] = np.array([0.25], dtype=np.float16).view(np.uint8)
+    blk[2:6] = np.array([0x0001_8000 | 1], dtype="<u4").view(np.uint8)  # bits 0, 15, 16
+    blk[6:22] = 3 | (5 << 4)
+    v = oracle.dequant(Q5_0, blk, 1, 32)[0]
+    expect = np.array([3 - 16 + (16 if l in (0, 15) else 0) for l in range(16)] +
+                      [5 - 16 + (16 if l == 0 else 0) for l in range(16)], dtype=np.float32) * 0.25
+    np.testing.assert_array_equal(v, expect)
