@@ -132,6 +132,27 @@ size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M);
 int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
                       size_t ws_bytes, void* stream);
 
+/* The routing the last pgmoe_moe_forward of M tokens on this workspace produced, read back
+ * in sorted pair order (ascending expert id, then ascending token: the order of the
+ * reference's expert loop and torch.where, model.py:911-914): offsets[E+1] (pairs of the
+ * experts below e), and for each sorted pair p < M*K its expert, token and top-k weight
+ * (softmax, renormalised when norm_topk; model.py:903-907).  For M <= 8 this decodes the
+ * routing descriptor the routed gate/up launch itself published (the routing the timed
+ * decode path computed), for larger M the top-k / dispatch arrays.  Enqueued on stream
+ * after the forward; no host sync.  No counterpart in the reference (its routing is
+ * Python-visible tensors): it lets tests and benchmarks pin the forward's own routing. */
+int pgmoe_moe_routing(const pgmoe_layer* L, int32_t M, const void* ws, size_t ws_bytes, int32_t* offsets,
+                      int32_t* pair_expert, int32_t* pair_token, float* pair_w, void* stream);
+
+/* Status word of a MoE workspace: 0, or PGMOE_STATUS_* bits set by kernels of an earlier
+ * forward (PGMOE_STATUS_SPIN_TIMEOUT: a decode wave's bounded wait for the router logits
+ * gave up, so that forward's output is wrong).  Synchronises `stream`, writes the word to
+ * *status (host) and, with clear != 0, resets it.  No counterpart in the reference (its
+ * PyTorch path has no device-side waits). */
+#define PGMOE_STATUS_SPIN_TIMEOUT 1
+int pgmoe_moe_status(const pgmoe_layer* L, void* ws, size_t ws_bytes, int32_t* status, int32_t clear,
+                     void* stream);
+
 /* Workspace bytes pgmoe_dense_forward needs for M tokens (0 for invalid arguments).  It
  * holds no state between calls: any workspace of this size serves. */
 size_t pgmoe_dense_workspace_bytes(const pgmoe_dense* D, int32_t M);

@@ -71,7 +71,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
-    size_t rlog, desc, xsum, isum, s_isum;
+    size_t rlog, status, desc, xsum, isum, s_isum;
     size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, dcounts, inter, a16, rs, partial;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
@@ -94,6 +94,9 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     // forward leaves them at zero), so a workspace shared by calls of different M must
     // find them at the same offset, where no other call writes
     o.rlog = take(c, (size_t)decode_rlog_words(decode_tokens_max(), (int)E) * 8);
+    // then the status word (also at the same offset for every M, zero until a wave's
+    // bounded wait gives up; pgmoe_moe_status reads and clears it)
+    o.status = take(c, 4);
     o.desc = take(c, gemm ? 0 : (size_t)decode_desc_words() * 4);
     o.xsum = take(c, gemm ? 0 : (size_t)M * (H / 16) * 4);
     o.isum = take(c, gemm ? 0 : P * (I / 16) * 4);
@@ -397,7 +400,7 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
                            WS(int32_t, nact), WS(float, w)};
         if ((rc = launch_dec_gateup_routed(lm.gate, lm.up, x, K, M, L->router_w, L->router_bias, sgw,
                                            sgw ? WS(float, s_logit) : nullptr, WS(uint64_t, rlog),
-                                           L->has_shared ? WS(float, xsum) : nullptr, E,
+                                           WS(int32_t, status), L->has_shared ? WS(float, xsum) : nullptr, E,
                                            L->norm_topk, WS(int32_t, desc), flat, max_active, WS(float, inter),
                                            WS(float, isum), st)))
             return rc;
@@ -462,6 +465,54 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
     }
     return launch_combine(WS(float, partial), WS(int32_t, inv), M, K, H, shared, shared_logit, out, st);
 #undef WS
+}
+
+int pgmoe_moe_routing(const pgmoe_layer* L, int32_t M, const void* ws, size_t ws_bytes, int32_t* offsets,
+                      int32_t* pair_expert, int32_t* pair_token, float* pair_w, void* stream) {
+    LayerMats lm;
+    int rc = check_layer(L, &lm);
+    if (rc) return rc;
+    if (M < 0) return fail(PGMOE_E_INVALID, "negative token count");
+    if (!ws || !offsets || (M > 0 && (!pair_expert || !pair_token || !pair_w)))
+        return fail(PGMOE_E_INVALID, "moe_routing: NULL pointer");
+    if ((uintptr_t)ws & 255) return fail(PGMOE_E_INVALID, "workspace must be 256-byte aligned");
+    const Layout o = layout_for(L, M);
+    if (ws_bytes < o.total) return fail(PGMOE_E_WORKSPACE, "workspace %zu bytes, need %zu", ws_bytes, o.total);
+    const uint8_t* b = (const uint8_t*)ws;
+#define WS(T, f) reinterpret_cast<const T*>(b + o.f)
+    const hipStream_t st = as_stream(stream);
+    if (M == 0) {
+        if (hipMemsetAsync(offsets, 0, sizeof(int32_t) * (L->n_experts + 1), st) != hipSuccess)
+            return fail(PGMOE_E_HIP, "moe_routing: memset failed");
+        return PGMOE_OK;
+    }
+    const int decode = M <= decode_tokens_max() ? 1 : 0;
+    return launch_route_readback(decode, WS(int32_t, desc), WS(int32_t, idx), WS(float, w), WS(int32_t, offsets),
+                                 WS(int32_t, perm), M, L->top_k, L->n_experts, offsets, pair_expert, pair_token,
+                                 pair_w, st);
+#undef WS
+}
+
+int pgmoe_moe_status(const pgmoe_layer* L, void* ws, size_t ws_bytes, int32_t* status, int32_t clear,
+                     void* stream) {
+    LayerMats lm;
+    int rc = check_layer(L, &lm);
+    if (rc) return rc;
+    if (!ws || !status) return fail(PGMOE_E_INVALID, "moe_status: NULL pointer");
+    if ((uintptr_t)ws & 255) return fail(PGMOE_E_INVALID, "workspace must be 256-byte aligned");
+    const Layout o = layout_for(L, 1);  // the status word sits at the same offset for every M
+    if (ws_bytes < o.status + 4) return fail(PGMOE_E_WORKSPACE, "workspace %zu bytes too small", ws_bytes);
+    const hipStream_t st = as_stream(stream);
+    int32_t* word = reinterpret_cast<int32_t*>((uint8_t*)ws + o.status);
+    int32_t v = 0;
+    if (hipMemcpyAsync(&v, word, 4, hipMemcpyDeviceToHost, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+        return fail(PGMOE_E_HIP, "moe_status: reading the status word failed");
+    if (clear && v) {
+        if (hipMemsetAsync(word, 0, 4, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)
+            return fail(PGMOE_E_HIP, "moe_status: clearing the status word failed");
+    }
+    *status = v;
+    return PGMOE_OK;
 }
 
 int pgmoe_moe_forward_timed(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,

@@ -14,20 +14,20 @@ namespace pgmoe {
 int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
                       int max_active, float* inter, float* isum, hipStream_t st) {
-    const DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, M, g.n_mats, 0, {}};
+    const DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, nullptr, M, g.n_mats, 0, {}};
 #define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, dp, RouterIn{}, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
 }
 
 int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
-                             const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, float* xsum_out,
-                             int E, int norm, int32_t* desc, const DecFlat& flat, int max_active, float* inter,
-                             float* isum, hipStream_t st) {
+                             const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, int32_t* status,
+                             float* xsum_out, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
+                             float* inter, float* isum, hipStream_t st) {
     if (M < 1 || M > kDecTM) return fail(PGMOE_E_INVALID, "routed decode handles 1..%d tokens", kDecTM);
     if (topk > 16 || E > 512 || M * topk > 128)
         return fail(PGMOE_E_UNSUPPORTED, "routed decode: top_k <= 16, E <= 512, M*top_k <= 128");
-    const DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, rlog, desc, M, E, norm,
+    const DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, rlog, desc, status, M, E, norm,
                      {flat.offsets, flat.perm, flat.inv, flat.active, flat.n_active, flat.w}};
     const RouterIn rt{rw, bias, sgw, s_logit, xsum_out};
 #define CALL(QT) dec_gateup_q<QT>(g, u, x, nullptr, topk, M, dp, rt, max_active, inter, isum, st)
@@ -37,7 +37,7 @@ int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, in
 
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
                             float* isum, hipStream_t st) {
-    const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
+    const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
 #define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, 1, M, dp, RouterIn{}, 1, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
@@ -46,14 +46,14 @@ int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, con
 int launch_dec_down(const Mats& d, const float* inter, const float* isum, int M, const int32_t* offsets,
                     const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
                     const float* topk_w, float* partial, hipStream_t st) {
-    const DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, M, d.n_mats, 0, {}};
+    const DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, nullptr, M, d.n_mats, 0, {}};
 #define CALL(QT) dec_down_q<QT>(d, inter, isum, M, kDispatch, dp, max_active, topk_w, partial, st)
     PG_BY_QTYPE(d.qtype, "decode down", CALL)
 #undef CALL
 }
 
 int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st) {
-    const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
+    const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
 #define CALL(QT) dec_down_q<QT>(d, inter, isum, M, kIdent, dp, 1, nullptr, out, st)
     PG_BY_QTYPE(d.qtype, "decode down", CALL)
 #undef CALL
@@ -99,6 +99,60 @@ int resident_rows(const void* kernel, int threads, size_t lds, int gx, int gy) {
         return gy;
     const int rows = per_cu * cus[dev] / gx;
     return rows < 1 ? 1 : rows < gy ? rows : gy;
+}
+
+// Routing of a finished forward in sorted pair order (ascending expert, then ascending
+// token): one block.  decode: from the routing descriptor the routed gate/up launch
+// published (slot a = {expert, first pair, count}, pair p = {token, weight bits});
+// prefill: from the top-k and dispatch arrays (pair p = flat id perm[p] = token * K + k).
+__global__ __launch_bounds__(256) void route_readback_kernel(int decode, const int32_t* __restrict__ desc,
+                                                             const int32_t* __restrict__ idx,
+                                                             const float* __restrict__ w,
+                                                             const int32_t* __restrict__ offsets_in,
+                                                             const int32_t* __restrict__ perm, int M, int K, int E,
+                                                             int32_t* __restrict__ offsets,
+                                                             int32_t* __restrict__ pair_expert,
+                                                             int32_t* __restrict__ pair_token,
+                                                             float* __restrict__ pair_w) {
+    const int P = M * K;
+    if (decode) {
+        const int n_act = desc[0];
+        for (int e = threadIdx.x; e <= E; e += blockDim.x) {  // pairs of the experts below e
+            int o = 0;
+            for (int a = 0; a < n_act; ++a)
+                if (desc[kDescSlot + 4 * a] < e) o += desc[kDescSlot + 4 * a + 2];
+            offsets[e] = o;
+        }
+        for (int a = 0; a < n_act; ++a) {
+            const int e = desc[kDescSlot + 4 * a], pb = desc[kDescSlot + 4 * a + 1];
+            const int c = desc[kDescSlot + 4 * a + 2];
+            for (int i = threadIdx.x; i < c; i += blockDim.x) {
+                const int p = pb + i;
+                if (p < P) pair_expert[p] = e;
+            }
+        }
+        for (int p = threadIdx.x; p < P; p += blockDim.x) {
+            pair_token[p] = desc[kDescPair + 2 * p];
+            pair_w[p] = __builtin_bit_cast(float, desc[kDescPair + 2 * p + 1]);
+        }
+        return;
+    }
+    for (int e = threadIdx.x; e <= E; e += blockDim.x) offsets[e] = offsets_in[e];
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+        const int f = perm[p];
+        pair_expert[p] = idx[f];
+        pair_token[p] = f / K;
+        pair_w[p] = w[f];
+    }
+}
+
+int launch_route_readback(int decode, const int32_t* desc, const int32_t* idx, const float* w,
+                          const int32_t* offsets_in, const int32_t* perm, int M, int K, int E, int32_t* offsets,
+                          int32_t* pair_expert, int32_t* pair_token, float* pair_w, hipStream_t st) {
+    if (decode && (M > kDecTM || M * K > 128)) return fail(PGMOE_E_INVALID, "route readback: decode M=%d", M);
+    PG_LAUNCH(route_readback_kernel, dim3(1), dim3(256), 0, st, decode, desc, idx, w, offsets_in, perm, M, K, E,
+              offsets, pair_expert, pair_token, pair_w);
+    return check_launch("route readback");
 }
 
 int decode_tokens_max() { return kDecTM; }

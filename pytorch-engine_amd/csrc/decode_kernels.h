@@ -563,12 +563,17 @@ __device__ __forceinline__ void put_logit(uint64_t* p, float v) {
     __hip_atomic_store(p, (1ull << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
 }
-constexpr int kSpinMax = 1 << 20;  // polls before a waiting wave gives up (results then wrong, no hang)
+constexpr int kSpinMax = 1 << 20;  // polls before a waiting wave gives up (no hang; see below)
+// Bit of the workspace status word set by a wave whose bounded wait gave up: the layer's
+// output is then wrong, and pgmoe_moe_status reports it to the host.
+constexpr int32_t kStatusSpinTimeout = PGMOE_STATUS_SPIN_TIMEOUT;
 
 // Logits of token m for lane l (experts l + 64r; -inf past E): polls the tagged words
-// (a bounded spin with short sleeps) until every one of the wave's is written.
+// (a bounded spin with short sleeps) until every one of the wave's is written.  A wave that
+// gives up after kSpinMax polls sets kStatusSpinTimeout in *status (vector atomic OR).
 template <int RE>
-__device__ __forceinline__ void load_logits(const uint64_t* rlog, int m, int E, int lane, float (&v)[RE]) {
+__device__ __forceinline__ void load_logits(const uint64_t* rlog, int m, int E, int lane, float (&v)[RE],
+                                            int32_t* status) {
     uint64_t q[RE];
     int n = 0;
     for (;;) {
@@ -580,7 +585,12 @@ __device__ __forceinline__ void load_logits(const uint64_t* rlog, int m, int E, 
                          : 1ull << 32;
             ready = ready && (q[r] >> 32) != 0;
         }
-        if (__all(ready) || ++n >= kSpinMax) break;
+        if (__all(ready)) break;
+        if (++n >= kSpinMax) {
+            if (lane == 0 && status) __hip_atomic_fetch_or(status, kStatusSpinTimeout, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
         __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
@@ -802,6 +812,7 @@ struct DecDisp {
     const int32_t *offsets, *perm, *active, *n_active;
     const uint64_t* rlog; // kRoute: ready-tagged router logits [kRlogCopies][M][E] (put_logit)
     int32_t* desc;        // kRoute: published by block (0, 0)
+    int32_t* status;      // kRoute: workspace status word (kStatusSpinTimeout), or null
     int M, E, norm;       // M: tokens (every mode)
     FlatRoute flat;       // kRoute: optional flat arrays, published by block (0, 0)
 };
@@ -861,7 +872,7 @@ __device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteSh
     const int copy = (blockIdx.y * gridDim.x + blockIdx.x) % kRlogCopies;
     const uint64_t* rlog = dp.rlog + (int64_t)copy * dp.M * dp.E;
     for (int m = w; m < dp.M; m += nw) {
-        load_logits<RE>(rlog, m, dp.E, lane, v);
+        load_logits<RE>(rlog, m, dp.E, lane, v, dp.status);
 #ifdef PG_TRACE
         if (m == 0) t_ready = wall_clock64();
 #endif

@@ -78,10 +78,17 @@ struct DecFlat {
 // expert's gate row sgw -> s_logit) into `rlog` (decode_rlog_words ready-tagged words, zero on entry;
 // the forward's last kernel clears them), and, when xsum_out is set, the 16-element sums
 // of x for the shared expert's launches.
+// status: the workspace status word a wave whose bounded wait for the logits gave up
+// marks (kStatusSpinTimeout), or null.
 int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
-                             const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, float* xsum_out,
-                             int E, int norm, int32_t* desc, const DecFlat& flat, int max_active, float* inter,
-                             float* isum, hipStream_t st);
+                             const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, int32_t* status,
+                             float* xsum_out, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
+                             float* inter, float* isum, hipStream_t st);
+// Routing a forward produced, read back from its workspace in sorted pair order (decode:
+// from the descriptor at desc; prefill: from the flat arrays).  offsets [E+1]; pair_*[P].
+int launch_route_readback(int decode, const int32_t* desc, const int32_t* idx, const float* w,
+                          const int32_t* offsets_in, const int32_t* perm, int M, int K, int E, int32_t* offsets,
+                          int32_t* pair_expert, int32_t* pair_token, float* pair_w, hipStream_t st);
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
                             float* isum, hipStream_t st);
 int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st);

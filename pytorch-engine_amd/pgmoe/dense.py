@@ -15,13 +15,14 @@ raises NotImplementedError, as HipSparseMoEMLP does.
 
 from __future__ import annotations
 
-from typing import Any, Dict, Optional
+from typing import Any, Optional
 
 import torch
 import torch.nn as nn
 
 from ._lib import Dense, check, lib
 from .moe import _ExpertTensor, _load_lock
+from .workspace import WorkspacePool
 
 
 class HipDenseMLP(nn.Module):
@@ -51,7 +52,7 @@ class HipDenseMLP(nn.Module):
             raise ValueError(f"{prefix}: gate {g.rows}x{g.cols}, up {u.rows}x{u.cols} and down "
                              f"{d.rows}x{d.cols} do not form an [I, H] / [H, I] FFN")
         self.hidden, self.inter = g.cols, g.rows
-        self._ws: Dict[int, torch.Tensor] = {}
+        self._ws = WorkspacePool(device, zeroed=False)  # the dense workspace keeps no state
         self._dense = self._build()
 
     @classmethod
@@ -75,13 +76,13 @@ class HipDenseMLP(nn.Module):
         return int(n)
 
     def _workspace(self, M: int) -> torch.Tensor:
-        ws = self._ws.get(M)
-        if ws is None:
-            n = self.workspace_bytes(M) + 256
-            raw = torch.empty(n, dtype=torch.uint8, device=self.device)
-            ws = raw[(-raw.data_ptr()) % 256:]
-            self._ws = {M: ws}
-        return ws
+        """The current stream's grow-only workspace (never freed while a graph may hold it;
+        see pgmoe.workspace)."""
+        return self._ws.get(self.workspace_bytes(M), torch.cuda.current_stream(self.device).cuda_stream)
+
+    def release_workspaces(self) -> None:
+        """Free the workspaces (only when no captured graph replays this layer any more)."""
+        self._ws.release()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         orig_shape = x.shape
@@ -115,7 +116,7 @@ class HipDenseMLP(nn.Module):
             c.buf = t.buf.clone()
             c.plane = t.plane.clone() if t.plane is not None else None
             object.__setattr__(r, name, c)
-        r._ws = {}
+        r._ws = self._ws.clone_empty()
         r._dense = r._build()
         return r
 

@@ -16,15 +16,17 @@ enqueues router, top-k, dispatch, expert products and combine without a host syn
 
 from __future__ import annotations
 
+import ctypes
 import threading
-from typing import Any, Dict, Optional
+from typing import Any, Optional
 
 import numpy as np
 import torch
 import torch.nn as nn
 
 from . import ops
-from ._lib import SUPPORTED_QTYPES, Layer, Weights, check, lib
+from ._lib import STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES, Layer, Weights, check, lib
+from .workspace import WorkspacePool
 
 _F32, _F16, _BF16 = 0, 1, 30
 _load_lock = threading.Lock()
@@ -63,7 +65,7 @@ class _ExpertTensor:
         if self.gguf_qtype not in SUPPORTED_QTYPES:
             raise NotImplementedError(
                 f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
-                "has no HIP kernel (supported: Q4_K, Q6_K, Q8_0)")
+                "has no HIP kernel (supported: Q4_K, Q6_K, Q8_0, and Q4_0 / Q5_0 relaid out as Q8_0)")
         if self.cols % 256:
             raise ValueError(f"{name}: {self.cols} input features is not a multiple of 256")
         raw_np = gguf_file.get_tensor_bytes(name)
@@ -123,7 +125,7 @@ class HipSparseMoEMLP(nn.Module):
         self.hidden = int(self.router_weight.shape[1])
         if self.router_weight.shape[0] != self.n_experts:
             raise ValueError(f"router has {self.router_weight.shape[0]} rows, config says {self.n_experts} experts")
-        self._ws: Dict[int, torch.Tensor] = {}
+        self._ws = WorkspacePool(device, zeroed=True)
         self._layer = self._build_layer()
 
     # ------------------------------------------------------------------ plumbing
@@ -161,16 +163,50 @@ class HipSparseMoEMLP(nn.Module):
             check(-1, "pgmoe_workspace_bytes")
         return int(n)
 
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
     def _workspace(self, M: int) -> torch.Tensor:
-        ws = self._ws.get(M)
+        """The current stream's workspace, grown (zero-filled) if M needs more bytes than it
+        has.  It starts with the decode router's self-resetting ready-tagged logits and the
+        status word, which must be zero when a buffer is new; see pgmoe.workspace."""
+        return self._ws.get(self.workspace_bytes(M), self._stream())
+
+    def release_workspaces(self) -> None:
+        """Free the workspaces (only when no captured graph replays this layer any more)."""
+        self._ws.release()
+
+    def check_status(self, clear: bool = True) -> None:
+        """Raise RuntimeError if a kernel of an earlier forward on the current stream flagged
+        its output as wrong (a decode wave's bounded wait for the router logits gave up).
+        Synchronises the stream; meant for health checks, not for every step."""
+        bufs = self._ws.buffers()
+        ws = bufs.get(self._stream())
         if ws is None:
-            n = self.workspace_bytes(M) + 256
-            # zeroed once: the workspace starts with self-resetting ready-tagged router logits
-            raw = torch.zeros(n, dtype=torch.uint8, device=self.device)
-            off = (-raw.data_ptr()) % 256
-            ws = raw[off:]
-            self._ws = {M: ws}  # keep one size: callers alternate between few M values
-        return ws
+            return
+        st = ctypes.c_int32()
+        check(lib().pgmoe_moe_status(self._layer, ws.data_ptr(), ws.numel(), ctypes.byref(st), int(clear),
+                                     self._stream()), "pgmoe_moe_status")
+        if st.value & STATUS_SPIN_TIMEOUT:
+            raise RuntimeError("a decode forward's wait for the router logits timed out: its output was wrong")
+        if st.value:
+            raise RuntimeError(f"pgmoe workspace status {st.value:#x}")
+
+    def routing(self, M: int):
+        """The routing the last forward of M tokens on the current stream produced, in sorted
+        pair order: (offsets [E+1], expert [M*K], token [M*K], weight [M*K]) device tensors,
+        read back from that forward's own workspace (pgmoe_moe_routing)."""
+        ws = self._workspace(M)
+        i32 = dict(dtype=torch.int32, device=self.device)
+        P = M * self.top_k
+        offsets = torch.empty(self.n_experts + 1, **i32)
+        pe = torch.empty(max(P, 1), **i32)
+        pt = torch.empty(max(P, 1), **i32)
+        pw = torch.empty(max(P, 1), dtype=torch.float32, device=self.device)
+        check(lib().pgmoe_moe_routing(self._layer, M, ws.data_ptr(), ws.numel(), offsets.data_ptr(),
+                                      pe.data_ptr(), pt.data_ptr(), pw.data_ptr(), self._stream()),
+              "pgmoe_moe_routing")
+        return offsets, pe[:P], pt[:P], pw[:P]
 
     # ------------------------------------------------------------------ forward
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -187,9 +223,14 @@ class HipSparseMoEMLP(nn.Module):
         out = torch.empty((M, self.hidden), dtype=torch.float32, device=self.device)
         if M:
             ws = self._workspace(M)
-            stream = torch.cuda.current_stream(self.device).cuda_stream
-            check(lib().pgmoe_moe_forward(self._layer, x_2d.data_ptr(), M, out.data_ptr(), ws.data_ptr(),
-                                          ws.numel(), stream), "pgmoe_moe_forward")
+            stream = self._stream()
+            rc = lib().pgmoe_moe_forward(self._layer, x_2d.data_ptr(), M, out.data_ptr(), ws.data_ptr(),
+                                         ws.numel(), stream)
+            if rc:
+                # a forward that stopped part-way may leave tagged router words set: the
+                # workspace must be zero again before the next call
+                self._ws.zero(stream)
+                check(rc, "pgmoe_moe_forward")
         return out.reshape(orig_shape)
 
     def replica(self) -> "HipSparseMoEMLP":
@@ -207,7 +248,7 @@ class HipSparseMoEMLP(nn.Module):
                 c.buf = t.buf.clone()
                 c.plane = t.plane.clone() if t.plane is not None else None
                 object.__setattr__(r, name, c)
-        r._ws = {}
+        r._ws = self._ws.clone_empty()
         r._layer = r._build_layer()
         return r
 
