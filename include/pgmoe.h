@@ -132,6 +132,22 @@ size_t pgmoe_workspace_bytes(const pgmoe_layer* L, int32_t M);
 int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
                       size_t ws_bytes, void* stream);
 
+/* pgmoe_moe_forward without a caller workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The workspace is a fixed 32 MiB device
+ * array inside the library, one per GPU, held until the process ends; the call allocates
+ * nothing.  Same kernels and results as pgmoe_moe_forward.  Limits and rules:
+ *   - M must fit the 32 MiB (laid out as pgmoe_workspace_bytes with the decode router's
+ *     region reserved for 512 experts): every decode M (<= 8) of the BASELINE layers and
+ *     small prefill batches; larger M returns PGMOE_E_WORKSPACE;
+ *   - every call on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ *     streams or threads) race and give wrong results;
+ *   - the first call on a device, and the first after a failed call, clears the array's
+ *     state words with a kernel and so must not run under graph capture
+ *     (PGMOE_E_INVALID otherwise);
+ *   - pgmoe_moe_status and pgmoe_moe_routing cannot reach this workspace. */
+int pgmoe_moe_forward_noalloc(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* stream);
+
 /* The routing the last pgmoe_moe_forward of M tokens on this workspace produced, read back
  * in sorted pair order (ascending expert id, then ascending token: the order of the
  * reference's expert loop and torch.where, model.py:911-914): offsets[E+1] (pairs of the

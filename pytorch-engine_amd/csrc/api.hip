@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 
@@ -83,7 +85,10 @@ static size_t take(size_t& cur, size_t bytes) {
     return at;
 }
 
-static Layout layout_for(const pgmoe_layer* L, int M) {
+// rlog_experts: the expert count the decode router's tagged-logit region is sized for
+// (the layer's own E; the allocation-free entry point reserves it for kMaxRlogExperts so
+// that layers of different E sharing its scratch all find the region at the same place).
+static Layout layout_for(const pgmoe_layer* L, int M, int rlog_experts = 0) {
     Layout o{};
     const size_t E = L->n_experts, K = L->top_k, H = L->hidden, I = L->gate.n_rows;
     const size_t P = (size_t)M * K;
@@ -93,7 +98,7 @@ static Layout layout_for(const pgmoe_layer* L, int M) {
     // persist between calls (zero when the workspace is first allocated, and each decode
     // forward leaves them at zero), so a workspace shared by calls of different M must
     // find them at the same offset, where no other call writes
-    o.rlog = take(c, (size_t)decode_rlog_words(decode_tokens_max(), (int)E) * 8);
+    o.rlog = take(c, (size_t)decode_rlog_words(decode_tokens_max(), rlog_experts > 0 ? rlog_experts : (int)E) * 8);
     // then the status word (also at the same offset for every M, zero until a wave's
     // bounded wait gives up; pgmoe_moe_status reads and clears it)
     o.status = take(c, 4);
@@ -370,21 +375,15 @@ int pgmoe_combine(const float* partial, const int32_t* inv, int32_t M, int32_t K
     return launch_combine(partial, inv, M, K, H, shared, shared_logit, out, as_stream(stream));
 }
 
-int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws, size_t ws_bytes,
-                      void* stream) {
-    LayerMats lm;
-    int rc = check_layer(L, &lm);
-    if (rc) return rc;
-    if (M < 0) return fail(PGMOE_E_INVALID, "negative token count");
-    if (M == 0) return PGMOE_OK;
-    if (!x || !out || !ws) return fail(PGMOE_E_INVALID, "moe_forward: NULL pointer");
-    if ((uintptr_t)ws & 255) return fail(PGMOE_E_INVALID, "workspace must be 256-byte aligned");
-    const Layout o = layout_for(L, M);
-    if (ws_bytes < o.total)
-        return fail(PGMOE_E_WORKSPACE, "workspace %zu bytes, need %zu", ws_bytes, o.total);
-    uint8_t* b = (uint8_t*)ws;
+}  // extern "C"
+
+namespace pgmoe {
+
+// The layer's kernels on a validated layer and workspace b laid out as o.
+static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Layout& o, uint8_t* b,
+                            const uint16_t* x, int M, float* out, hipStream_t st) {
+    int rc;
 #define WS(T, f) reinterpret_cast<T*>(b + o.f)
-    const hipStream_t st = as_stream(stream);
     const int E = L->n_experts, K = L->top_k, H = L->hidden;
     const int mode = M > decode_tokens_max() ? 1 : 0;
     const int BM = gemm_tile_rows();
@@ -467,6 +466,25 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
 #undef WS
 }
 
+}  // namespace pgmoe
+
+extern "C" {
+
+int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws, size_t ws_bytes,
+                      void* stream) {
+    LayerMats lm;
+    int rc = check_layer(L, &lm);
+    if (rc) return rc;
+    if (M < 0) return fail(PGMOE_E_INVALID, "negative token count");
+    if (M == 0) return PGMOE_OK;
+    if (!x || !out || !ws) return fail(PGMOE_E_INVALID, "moe_forward: NULL pointer");
+    if ((uintptr_t)ws & 255) return fail(PGMOE_E_INVALID, "workspace must be 256-byte aligned");
+    const Layout o = layout_for(L, M);
+    if (ws_bytes < o.total)
+        return fail(PGMOE_E_WORKSPACE, "workspace %zu bytes, need %zu", ws_bytes, o.total);
+    return moe_forward_impl(L, lm, o, (uint8_t*)ws, x, M, out, as_stream(stream));
+}
+
 int pgmoe_moe_routing(const pgmoe_layer* L, int32_t M, const void* ws, size_t ws_bytes, int32_t* offsets,
                       int32_t* pair_expert, int32_t* pair_token, float* pair_w, void* stream) {
     LayerMats lm;
@@ -524,6 +542,88 @@ int pgmoe_moe_forward_timed(const pgmoe_layer* L, const uint16_t* x, int32_t M, 
     const int rc = pgmoe_moe_forward(L, x, M, out, ws, ws_bytes, stream);
     launch_timing() = nullptr;
     if (n_launches) *n_launches = t.next;
+    return rc;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free forward
+// pgmoe_moe_forward_noalloc keeps its workspace in `scratch`, a file-scope device array of
+// which every GPU holds its own copy.  Host code never uses the array's name as an
+// address (on the host it is only a stand-in for the symbol): once per device, with that
+// device current, hipGetSymbolAddress gives the device address, kept in g_noalloc[dev].
+namespace pgmoe {
+
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+constexpr int kMaxRlogExperts = 512;  // check_layer's bound on n_experts
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+struct NoAllocState {
+    uint8_t* ptr;      // device address of this device's scratch (null until resolved)
+    bool need_clear;   // the state words (tagged logits, status) must be zeroed before use
+};
+static NoAllocState g_noalloc[kMaxDevices];
+static std::mutex g_noalloc_mu;
+
+__global__ __launch_bounds__(256) void zero_kernel(uint4* __restrict__ p, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+}  // namespace pgmoe
+
+extern "C" {
+
+int pgmoe_moe_forward_noalloc(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* stream) {
+    LayerMats lm;
+    int rc = check_layer(L, &lm);
+    if (rc) return rc;
+    if (M < 0) return fail(PGMOE_E_INVALID, "negative token count");
+    if (M == 0) return PGMOE_OK;
+    if (!x || !out) return fail(PGMOE_E_INVALID, "moe_forward_noalloc: NULL pointer");
+    const Layout o = layout_for(L, M, kMaxRlogExperts);
+    if (o.total > kNoAllocScratchBytes)
+        return fail(PGMOE_E_WORKSPACE,
+                    "moe_forward_noalloc: %d tokens need %zu bytes of scratch, above its fixed %zu bytes "
+                    "(use pgmoe_moe_forward with a caller workspace)",
+                    M, o.total, kNoAllocScratchBytes);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return fail(PGMOE_E_HIP, "moe_forward_noalloc: no usable current device");
+    const hipStream_t st = as_stream(stream);
+    uint8_t* b;
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        NoAllocState& S = g_noalloc[dev];
+        if (!S.ptr) {
+            void* p = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !p)
+                return fail(PGMOE_E_HIP, "moe_forward_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+            S.ptr = (uint8_t*)p;
+            S.need_clear = true;
+        }
+        if (S.need_clear) {
+            // tagged logits + status word; later forwards leave them at zero themselves.  A
+            // captured clear would only run when its graph replays, so it must be eager.
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+                return fail(PGMOE_E_INVALID, "moe_forward_noalloc: the first call on a device (and the first after "
+                                             "a failed call) must run outside graph capture, to clear its scratch");
+            const int64_t n16 = (int64_t)(o.status + 256) / 16;
+            hipLaunchKernelGGL(zero_kernel, dim3(64), dim3(256), 0, st, (uint4*)S.ptr, n16);
+            if ((rc = check_launch("noalloc scratch clear"))) return rc;
+            S.need_clear = false;
+        }
+        b = S.ptr;
+    }
+    rc = moe_forward_impl(L, lm, o, b, x, M, out, st);
+    if (rc) {  // a forward stopped part-way may leave tagged words set
+        std::lock_guard<std::mutex> lock(g_noalloc_mu);
+        g_noalloc[dev].need_clear = true;
+    }
     return rc;
 }
 
