@@ -179,6 +179,44 @@ size_t pgmoe_dense_workspace_bytes(const pgmoe_dense* D, int32_t M);
 int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, float* out, void* ws, size_t ws_bytes,
                         void* stream);
 
+/* Element types of pgmoe_add_rmsnorm's tensors (ggml type numbers). */
+#define PGMOE_DT_F32 0
+#define PGMOE_DT_F16 1
+#define PGMOE_DT_BF16 30
+
+/* Residual add + RMSNorm over `rows` rows of `dim` elements (dim a multiple of 4):
+ *   h[r]   = f32(x[r]) + f32(delta[r])                       (fp32, written when h_out != NULL)
+ *   out[r] = (h[r] * (1 / sqrt(sum(h[r]^2) / dim + eps))) * weight    (out_dtype F32 or F16)
+ * exec_fused_add_rmsnorm (quant_kernels.py:1552-1597: returns (h, normed)), and with
+ * delta == NULL exec_fused_rmsnorm (:1510-1549: h = f32(x)); the pre-FFN norm whose fp16
+ * output is the MoE block's input (model.py:1037).  x / delta: F32, F16 or BF16; weight:
+ * fp32 [dim].  Bit-identical to the CPU oracle's fixed summation order. */
+int pgmoe_add_rmsnorm(const void* x, int32_t x_dtype, const void* delta, int32_t delta_dtype, const float* weight,
+                      int32_t rows, int32_t dim, float eps, float* h_out, void* out, int32_t out_dtype, void* stream);
+
+/* Workspace bytes pgmoe_linear_forward needs for M tokens (0: none, or invalid arguments):
+ * nothing when it runs the GEMV (M <= 8), the identity dispatch of the GEMM otherwise, plus
+ * M x N fp32 product rows when there is a bias or the output is fp16.  No state between
+ * calls. */
+size_t pgmoe_linear_workspace_bytes(const pgmoe_weights* W, int32_t M, int32_t has_bias, int32_t out_dtype);
+
+/* The quantized linear: out[M, N] = x[M, K] . W^T (+ bias[N]) with W one matrix
+ * (n_mats = 1) in the device layout, fp32 accumulate, out PGMOE_DT_F32 or PGMOE_DT_F16
+ * (round to nearest even).  GGUFQuantLinear.forward (quant_kernels.py:1826-1837 ->
+ * exec_w4a16_matmul / exec_w8a16_matmul, :1165-1420) and
+ * FusedLinearPack.forward_single_concat (:1895-1898): attention projections, lm_head, the
+ * shared expert's fused gate||up.  M <= 8: wavefront GEMV; else the MFMA GEMM (K-quant
+ * weights then need their scale plane).  bias: fp32 [N] or NULL.  Host-sync free. */
+int pgmoe_linear_forward(const pgmoe_weights* W, const float* bias, const uint16_t* x, int32_t M, void* out,
+                         int32_t out_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/* Rows rows[0..n) of W dequantised: out[n, K] (PGMOE_DT_F32 or PGMOE_DT_F16); values as
+ * the ggml block definitions give them with fp32 products; an id outside [0, N) gives a
+ * row of NaN (nothing is read for it).  GGUFQuantLinear.embed_lookup
+ * (quant_kernels.py:1839-1863): the token-embedding lookup from a quantised table. */
+int pgmoe_dequant_rows(const pgmoe_weights* W, const int32_t* rows, int32_t n, void* out, int32_t out_dtype,
+                       void* stream);
+
 /* pgmoe_moe_forward with per-kernel timing.  No counterpart in the reference: it is for
  * benchmarks and profilers that want each kernel's duration from the caller's own stream.
  * The i-th kernel the call launches (i < n_events) records start_events[i] when it begins

@@ -59,6 +59,7 @@ def lib() -> ctypes.CDLL:
         L.or_dispatch.argtypes = [_P, _I, _I, _I, _P, _P, _P]
         L.or_act_rowscale.argtypes = [_P, _P, _I, _I, _P, _P]
         L.or_act_rowscale.restype = None
+        L.or_add_rmsnorm.argtypes = [_P, _I, _P, _I, _P, _I, _I, ctypes.c_float, _P, _P, _I]
         L.or_moe_forward_tokens.argtypes = [_I, _I, _I, _I] + [ctypes.POINTER(_Weights)] * 6 + [
             _P, _P, _P, _P, _P, _I, _P]
         _lib = L
@@ -126,6 +127,30 @@ def act_rowscale(g: np.ndarray, u: np.ndarray):
     rs = np.empty((M, 1), dtype=np.float32)
     lib().or_act_rowscale(_ptr(g), _ptr(u), M, I, _ptr(down_in), _ptr(rs))
     return down_in, rs
+
+
+# ---------------------------------------------------------------- residual add + RMSNorm
+_DT = {np.dtype(np.float32): 0, np.dtype(np.float16): 1}
+
+
+def add_rmsnorm(x: np.ndarray, delta: Optional[np.ndarray], w: np.ndarray, eps: float,
+                out_dtype=np.float16, bf16: Sequence[bool] = (False, False)):
+    """(h fp32, out) of exec_fused_add_rmsnorm (delta None: exec_fused_rmsnorm, h = f32(x)) in
+    the GPU kernel's fixed summation order.  x / delta: fp32 or fp16 arrays, or uint16 bf16
+    bits with bf16[i] set."""
+    x = np.ascontiguousarray(x)
+    R, D = x.shape
+    xdt = 30 if bf16[0] else _DT[x.dtype]
+    ddt = 0
+    if delta is not None:
+        delta = np.ascontiguousarray(delta)
+        ddt = 30 if bf16[1] else _DT[delta.dtype]
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    h = np.empty((R, D), dtype=np.float32)
+    out = np.empty((R, D), dtype=out_dtype)
+    _check(lib().or_add_rmsnorm(_ptr(x), xdt, _ptr(delta), ddt, _ptr(w), R, D, float(eps), _ptr(h), _ptr(out),
+                                _DT[np.dtype(out_dtype)]), "add_rmsnorm")
+    return h, out
 
 
 # ---------------------------------------------------------------- layer

@@ -445,3 +445,60 @@ void or_act_rowscale(const float* g, const float* u, int M, int I, uint16_t* dow
         }
     }
 }
+
+/* ---------------- residual add + RMSNorm (the MoE block's input) --------------- */
+/* exec_fused_add_rmsnorm (quant_kernels.py:1552-1597; CPU branch: h = x.float() +
+ * delta.float(), normed = F.rms_norm(h, (D,), w, eps).to(out_dtype)) and, with delta NULL,
+ * exec_fused_rmsnorm (:1510-1549).  dtypes: 0 F32, 1 F16, 30 BF16 (inputs), 0 / 1 (out).
+ * The sum of squares follows the GPU kernel's fixed order: 256 slots t, slot t owning the
+ * 4-element chunks t, t + 256, ... and adding their squares in element order; slots
+ * 64w .. 64w + 63 meet by the halving tree (s, s + 32), ..., (s, s + 1); the four group
+ * sums are added left to right.  r = 1 / sqrt(sum / D + eps); out = (h * r) * w. */
+static float ld_elem(const void* p, int dt, int64_t i) {
+    if (dt == 0) return ((const float*)p)[i];
+    uint16_t b = ((const uint16_t*)p)[i];
+    if (dt == 1) return or_half_to_float(b);
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+int or_add_rmsnorm(const void* x, int xdt, const void* delta, int ddt, const float* w, int R, int D, float eps,
+                   float* h_out, void* out, int odt) {
+    if (D <= 0 || D % 4) return -1;
+    float* h = (float*)malloc(sizeof(float) * (size_t)D);
+    if (!h) return -2;
+    const int n4 = D / 4;
+    for (int r = 0; r < R; ++r) {
+        const int64_t base = (int64_t)r * D;
+        for (int i = 0; i < D; ++i) {
+            float v = ld_elem(x, xdt, base + i);
+            if (delta) v = v + ld_elem(delta, ddt, base + i);
+            h[i] = v;
+            if (h_out) h_out[base + i] = v;
+        }
+        float slot[256];
+        for (int t = 0; t < 256; ++t) {
+            float acc = 0.0f;
+            for (int c = t; c < n4; c += 256)
+                for (int i = 0; i < 4; ++i) acc = acc + h[4 * c + i] * h[4 * c + i];
+            slot[t] = acc;
+        }
+        float tot = 0.0f;
+        for (int wv = 0; wv < 4; ++wv) {
+            float* p = slot + 64 * wv;
+            for (int stride = 32; stride >= 1; stride >>= 1)
+                for (int s = 0; s < stride; ++s) p[s] = p[s] + p[s + stride];
+            tot = wv == 0 ? p[0] : tot + p[0];
+        }
+        const float rr = 1.0f / sqrtf(tot / (float)D + eps);
+        for (int i = 0; i < D; ++i) {
+            const float v = (h[i] * rr) * w[i];
+            if (odt == 0) ((float*)out)[base + i] = v;
+            else ((uint16_t*)out)[base + i] = or_float_to_half(v);
+        }
+    }
+    free(h);
+    return 0;
+}

@@ -485,6 +485,63 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
     return moe_forward_impl(L, lm, o, (uint8_t*)ws, x, M, out, as_stream(stream));
 }
 
+size_t pgmoe_linear_workspace_bytes(const pgmoe_weights* W, int32_t M, int32_t has_bias, int32_t out_dtype) {
+    Mats w;
+    if (M < 0 || check_weights(W, "linear", &w) || w.n_mats != 1) return 0;
+    return linear_ws_bytes(w, M, has_bias || out_dtype == PGMOE_DT_F16);
+}
+
+int pgmoe_linear_forward(const pgmoe_weights* W, const float* bias, const uint16_t* x, int32_t M, void* out,
+                         int32_t out_dtype, void* ws, size_t ws_bytes, void* stream) {
+    Mats w;
+    int rc = check_weights(W, "linear", &w);
+    if (rc) return rc;
+    if (w.n_mats != 1) return fail(PGMOE_E_INVALID, "linear: one matrix (n_mats = 1), got %d", w.n_mats);
+    if (M < 0) return fail(PGMOE_E_INVALID, "negative token count");
+    if (out_dtype != PGMOE_DT_F32 && out_dtype != PGMOE_DT_F16)
+        return fail(PGMOE_E_UNSUPPORTED, "linear: output dtype %d (F32=0, F16=1)", out_dtype);
+    if (M == 0) return PGMOE_OK;
+    if (!x || !out) return fail(PGMOE_E_INVALID, "linear: NULL pointer");
+    if (((uintptr_t)x & 15) || ((uintptr_t)ws & 255) || ((uintptr_t)out & 3))
+        return fail(PGMOE_E_INVALID, "linear: x must be 16-byte, ws 256-byte, out 4-byte aligned");
+    if (w.qtype != PGMOE_Q8_0 && !w.scales && !linear_gemv_fits(M, w.K))
+        return fail(PGMOE_E_INVALID, "linear: K-quant weights need their scale plane for %d tokens", M);
+    return launch_linear(w, bias, x, M, out, out_dtype == PGMOE_DT_F16, (uint8_t*)ws, ws_bytes, as_stream(stream));
+}
+
+int pgmoe_dequant_rows(const pgmoe_weights* W, const int32_t* rows, int32_t n, void* out, int32_t out_dtype,
+                       void* stream) {
+    Mats w;
+    int rc = check_weights(W, "dequant rows", &w);
+    if (rc) return rc;
+    if (w.n_mats != 1) return fail(PGMOE_E_INVALID, "dequant rows: one matrix (n_mats = 1), got %d", w.n_mats);
+    if (n < 0 || (out_dtype != PGMOE_DT_F32 && out_dtype != PGMOE_DT_F16))
+        return fail(PGMOE_E_INVALID, "dequant rows: n %d, output dtype %d", n, out_dtype);
+    if (n == 0) return PGMOE_OK;
+    if (!rows || !out) return fail(PGMOE_E_INVALID, "dequant rows: NULL pointer");
+    return launch_dequant_rows(w, rows, n, out, out_dtype == PGMOE_DT_F16, as_stream(stream));
+}
+
+int pgmoe_add_rmsnorm(const void* x, int32_t x_dtype, const void* delta, int32_t delta_dtype, const float* weight,
+                      int32_t rows, int32_t dim, float eps, float* h_out, void* out, int32_t out_dtype, void* stream) {
+    auto dt_ok = [](int d) { return d == PGMOE_DT_F32 || d == PGMOE_DT_F16 || d == PGMOE_DT_BF16; };
+    if (rows < 0 || dim <= 0 || dim % 4) return fail(PGMOE_E_INVALID, "add_rmsnorm: rows %d, dim %d (a multiple of 4)", rows, dim);
+    if (!dt_ok(x_dtype) || (delta && !dt_ok(delta_dtype)) || (out_dtype != PGMOE_DT_F32 && out_dtype != PGMOE_DT_F16))
+        return fail(PGMOE_E_UNSUPPORTED, "add_rmsnorm: dtypes x %d, delta %d, out %d (F32=0, F16=1, BF16=30; out F32/F16)",
+                    x_dtype, delta_dtype, out_dtype);
+    if (!(eps >= 0.0f)) return fail(PGMOE_E_INVALID, "add_rmsnorm: eps must be >= 0");
+    if (rows == 0) return PGMOE_OK;
+    if (!x || !weight || !out) return fail(PGMOE_E_INVALID, "add_rmsnorm: NULL pointer");
+    const uintptr_t al = (uintptr_t)x | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)delta | (uintptr_t)h_out;
+    if (al & 7) return fail(PGMOE_E_INVALID, "add_rmsnorm: pointers must be 8-byte aligned");
+    if ((((uintptr_t)weight | (uintptr_t)h_out) & 15) || (x_dtype == PGMOE_DT_F32 && ((uintptr_t)x & 15)) ||
+        (delta && delta_dtype == PGMOE_DT_F32 && ((uintptr_t)delta & 15)) ||
+        (out_dtype == PGMOE_DT_F32 && ((uintptr_t)out & 15)))
+        return fail(PGMOE_E_INVALID, "add_rmsnorm: fp32 tensors must be 16-byte aligned");
+    return launch_add_rmsnorm(x, x_dtype, delta, delta_dtype, weight, rows, dim, eps, h_out, out, out_dtype,
+                              as_stream(stream));
+}
+
 int pgmoe_moe_routing(const pgmoe_layer* L, int32_t M, const void* ws, size_t ws_bytes, int32_t* offsets,
                       int32_t* pair_expert, int32_t* pair_token, float* pair_w, void* stream) {
     LayerMats lm;

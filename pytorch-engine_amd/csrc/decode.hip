@@ -35,6 +35,16 @@ int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, in
 #undef CALL
 }
 
+int launch_dec_linear(const Mats& w, const uint16_t* x, int M, const float* bias, void* out, int out_f16,
+                      hipStream_t st) {
+    DecDisp dp{kLinear, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
+    dp.bias = bias;
+    dp.out_f16 = out_f16;
+#define CALL(QT) dec_gateup_q<QT>(w, w, x, nullptr, 1, M, dp, RouterIn{}, 1, (float*)out, nullptr, st)
+    PG_BY_QTYPE(w.qtype, "decode linear", CALL)
+#undef CALL
+}
+
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
                             float* isum, hipStream_t st) {
     const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
@@ -154,6 +164,8 @@ int launch_route_readback(int decode, const int32_t* desc, const int32_t* idx, c
               offsets, pair_expert, pair_token, pair_w);
     return check_launch("route readback");
 }
+
+bool linear_gemv_fits(int M, int K) { return M >= 1 && M <= kDecTM && gu_lds_bytes(M, K) <= dec_lds_limit(); }
 
 int decode_tokens_max() { return kDecTM; }
 int decode_desc_words() { return kDescWords; }

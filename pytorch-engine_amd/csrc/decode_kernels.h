@@ -804,8 +804,10 @@ __device__ __forceinline__ void publish_route(const RouteShared& R, int M, int E
 //   kDispatch: offsets / perm / active / n_active of a counting-sort dispatch (stage API);
 //   kRoute   : derived in the block from the router logits (decode forward; block (0, 0)
 //              also publishes the routing descriptor);
-//   kIdent   : one expert (matrix 0) applied to every token with weight 1 (shared expert).
-enum DecMode { kDispatch = 0, kRoute = 1, kIdent = 2 };
+//   kIdent   : one expert (matrix 0) applied to every token with weight 1 (shared expert);
+//   kLinear  : kIdent with a single matrix (gate/up launch only): y = x . W^T (+ bias),
+//              the quantized linear (GGUFQuantLinear.forward, quant_kernels.py:1826).
+enum DecMode { kDispatch = 0, kRoute = 1, kIdent = 2, kLinear = 3 };
 
 struct DecDisp {
     int mode;  // DecMode
@@ -815,6 +817,8 @@ struct DecDisp {
     int32_t* status;      // kRoute: workspace status word (kStatusSpinTimeout), or null
     int M, E, norm;       // M: tokens (every mode)
     FlatRoute flat;       // kRoute: optional flat arrays, published by block (0, 0)
+    const float* bias;    // kLinear: [N] added to the outputs, or null
+    int out_f16;          // kLinear: outputs as fp16 (round to nearest even) instead of fp32
 };
 
 // Router work folded into the routed gate/up launch: with R = ceil(rows / blocks) (1
@@ -838,7 +842,7 @@ __device__ __forceinline__ SlotInfo slot_plain(const DecDisp& dp, int a, int top
     si.e = -1;
     si.p_begin = si.count = 0;
     si.toks = 0;
-    if constexpr (MODE == kIdent) {
+    if constexpr (MODE == kIdent || MODE == kLinear) {
         si.n_act = 1;
         if (a > 0) return si;
         si.e = 0;
@@ -979,7 +983,8 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     //    same in every wave), items, then the SwiGLU rows
     const int r = lane & 15, p = lane >> 4;
     const int row = blockIdx.x * RB + r;  // < row_groups(N) * 64: padded tile rows are readable
-    const int nit = 2 * nb;
+    constexpr bool lin = MODE == kLinear;  // one matrix: item = super-block, every wave on it
+    const int nit = lin ? nb : 2 * nb;
     for (int a = blockIdx.y;; a += gridDim.y) {
         SlotInfo si;
         if constexpr (MODE == kRoute && TM == 1)
@@ -991,17 +996,18 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         if (si.e < 0) break;  // uniform over the block
         PG_MARK(1, 2);
         // items, two per wave at a time (both quarters' loads in flight together)
-        const uint8_t* mat = (w & 1) ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
+        const uint8_t* mat = (!lin && (w & 1)) ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
         float acc[TM];
 #pragma unroll
         for (int t = 0; t < TM; ++t) acc[t] = 0.f;
         for (int it = w; it < nit; it += 2 * nw) {
             const int it1 = it + nw;
             Qtr<QT> q0, q1;
-            load_qtr<QT>(q0, mat, N, nb, row, it >> 1, p);
-            load_qtr<QT>(q1, mat, N, nb, row, min(it1, nit - 1) >> 1, p);
-            gu_qtr<TM>(q0, it >> 1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-            if (it1 < nit) gu_qtr<TM>(q1, it1 >> 1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+            const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
+            load_qtr<QT>(q0, mat, N, nb, row, j0, p);
+            load_qtr<QT>(q1, mat, N, nb, row, j1, p);
+            gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+            if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
         }
         PG_MARK(1, 4);
         // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
@@ -1016,7 +1022,19 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
         // of a token is a shuffle reduction inside its group
         const int cnt = si.count, p0 = si.p_begin;
-        if (tid < cnt * RB) {
+        if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
+            const int t = tid >> 4, rr = tid & 15;
+            const int orow = blockIdx.x * RB + rr;
+            float v = red[0][t][rr];
+            for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
+            if (orow < N) {
+                if (dp.bias) v = v + dp.bias[orow];
+                if (dp.out_f16)
+                    ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
+                else
+                    inter[(int64_t)(p0 + t) * N + orow] = v;
+            }
+        } else if (tid < cnt * RB) {
             const int t = tid >> 4, rr = tid & 15;
             float g = 0.f, u = 0.f;
             for (int ww = 0; ww < nw; ww += 2) {
@@ -1318,7 +1336,8 @@ int resident_rows(const void* kernel, int threads, size_t lds, int gx, int gy);
 template <int QT, int TM>
 inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, const DecDisp& dp,
                       const RouterIn& rt, int max_active, float* inter, float* isum, hipStream_t st) {
-    const int W = gu_waves(g.K >> 8), gx = div_up(g.N, 16);
+    // a linear has half the items of a gate/up pair: two per wave as well
+    const int W = gu_waves(dp.mode == kLinear ? ((g.K >> 8) + 1) / 2 : g.K >> 8), gx = div_up(g.N, 16);
     const int gy = gu_slot_blocks(max_active);
     // every router row needs a wave
     const int gmin = dp.mode == kRoute ? div_up(dp.E + (rt.extra_w ? 1 : 0), gx * W) : 1;
@@ -1338,6 +1357,8 @@ inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const flo
             PG_GU(kRoute, 8);
     } else if (dp.mode == kIdent) {
         PG_GU(kIdent, 1);
+    } else if (dp.mode == kLinear) {
+        PG_GU(kLinear, 1);
     } else {
         PG_GU(kDispatch, 1);
     }

@@ -89,6 +89,19 @@ int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, in
 int launch_route_readback(int decode, const int32_t* desc, const int32_t* idx, const float* w,
                           const int32_t* offsets_in, const int32_t* perm, int M, int K, int E, int32_t* offsets,
                           int32_t* pair_expert, int32_t* pair_token, float* pair_w, hipStream_t st);
+// y[M, N] = x . W^T (+ bias[N]) on the decode GEMV (M <= decode_tokens_max()); out fp32, or
+// fp16 with out_f16.
+int launch_dec_linear(const Mats& w, const uint16_t* x, int M, const float* bias, void* out, int out_f16,
+                      hipStream_t st);
+// Whether the decode GEMV can stage M rows of K inputs (the linear's M <= 8 path).
+bool linear_gemv_fits(int M, int K);
+// The quantized linear (linear.hip): out[M, N] = x . W^T (+ bias), fp32 or fp16; ws of
+// linear_ws_bytes(w, M, bias || out_f16) bytes (none on the GEMV path).
+size_t linear_ws_bytes(const Mats& w, int M, bool staged);
+int launch_linear(const Mats& w, const float* bias, const uint16_t* x, int M, void* out, int out_f16, uint8_t* ws,
+                  size_t ws_bytes, hipStream_t st);
+// Rows rows[0..n) of w decoded to out [n, K] (fp32, or fp16 with out_f16).
+int launch_dequant_rows(const Mats& w, const int32_t* rows, int n, void* out, int out_f16, hipStream_t st);
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
                             float* isum, hipStream_t st);
 int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st);
@@ -116,6 +129,9 @@ int64_t scale_plane_bytes(int qtype, int64_t rows, int64_t cols);
 int launch_scale_plane(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols,
                        int64_t src_stride, uint8_t* dst, hipStream_t st);
 int gemm_tile_rows();
+// Residual add + RMSNorm (norm.hip): dtypes PGMOE_DT_*; delta and h_out may be null.
+int launch_add_rmsnorm(const void* x, int xdt, const void* delta, int ddt, const float* w, int R, int D, float eps,
+                       float* h_out, void* out, int odt, hipStream_t st);
 int decode_tokens_max();
 
 }  // namespace pgmoe

@@ -7,11 +7,15 @@
 
 from .gguf import GGMLType, GGUFFile, GGUFWriter, InMemoryGGUF, MoEConfig
 from .dense import HipDenseMLP
+from .linear import FusedLinearPack, GGUFQuantLinear, HipQuantLinear
 from .moe import HipSparseMoEMLP
+from .norm import GGUFRMSNorm, HipRMSNorm, exec_fused_add_rmsnorm, exec_fused_rmsnorm
 
 # The reference's class names, so `from pgmoe import GGUFSparseMoEMLP` swaps the block in.
 GGUFSparseMoEMLP = HipSparseMoEMLP
 GGUFDenseMLP = HipDenseMLP
 
 __all__ = ["GGMLType", "GGUFFile", "GGUFWriter", "InMemoryGGUF", "MoEConfig", "HipSparseMoEMLP",
-           "GGUFSparseMoEMLP", "HipDenseMLP", "GGUFDenseMLP"]
+           "GGUFSparseMoEMLP", "HipDenseMLP", "GGUFDenseMLP", "GGUFRMSNorm", "HipRMSNorm",
+           "exec_fused_add_rmsnorm", "exec_fused_rmsnorm", "GGUFQuantLinear", "HipQuantLinear",
+           "FusedLinearPack"]

@@ -94,6 +94,11 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_dense_forward.argtypes = [ctypes.POINTER(Dense), _P, _I32, _P, _P, ctypes.c_size_t, _P]
     L.pgmoe_moe_forward_timed.argtypes = [ctypes.POINTER(Layer), _P, _I32, _P, _P, ctypes.c_size_t, _P,
                                           ctypes.POINTER(_P), ctypes.POINTER(_P), _I32, ctypes.POINTER(_I32)]
+    L.pgmoe_linear_workspace_bytes.restype = ctypes.c_size_t
+    L.pgmoe_linear_workspace_bytes.argtypes = [ctypes.POINTER(Weights), _I32, _I32, _I32]
+    L.pgmoe_linear_forward.argtypes = [ctypes.POINTER(Weights), _P, _P, _I32, _P, _I32, _P, ctypes.c_size_t, _P]
+    L.pgmoe_dequant_rows.argtypes = [ctypes.POINTER(Weights), _P, _I32, _P, _I32, _P]
+    L.pgmoe_add_rmsnorm.argtypes = [_P, _I32, _P, _I32, _P, _I32, _I32, ctypes.c_float, _P, _P, _I32, _P]
     L.pgmoe_moe_forward_noalloc.argtypes = [ctypes.POINTER(Layer), _P, _I32, _P, _P]
     L.pgmoe_moe_routing.argtypes = [ctypes.POINTER(Layer), _I32, _P, ctypes.c_size_t, _P, _P, _P, _P, _P]
     L.pgmoe_moe_status.argtypes = [ctypes.POINTER(Layer), _P, ctypes.c_size_t, ctypes.POINTER(_I32), _I32, _P]
@@ -110,7 +115,8 @@ def lib() -> ctypes.CDLL:
     for fn in ("pgmoe_moe_forward", "pgmoe_moe_forward_timed", "pgmoe_router_topk", "pgmoe_dispatch",
                "pgmoe_dispatch_ws", "pgmoe_expert_gateup",
                "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_build_scale_plane",
-               "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status", "pgmoe_moe_forward_noalloc"):
+               "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status", "pgmoe_moe_forward_noalloc",
+               "pgmoe_add_rmsnorm", "pgmoe_linear_forward", "pgmoe_dequant_rows"):
         getattr(L, fn).restype = ctypes.c_int
     ver = L.pgmoe_abi_version()
     if ver != ABI_VERSION:
@@ -132,7 +138,8 @@ EXPORTS = (
     "pgmoe_expert_gateup", "pgmoe_expert_down", "pgmoe_combine", "pgmoe_moe_forward_timed",
     "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane", "pgmoe_dispatch_ws_bytes", "pgmoe_dispatch_ws",
     "pgmoe_dense_workspace_bytes", "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status",
-    "pgmoe_moe_forward_noalloc",
+    "pgmoe_moe_forward_noalloc", "pgmoe_add_rmsnorm", "pgmoe_linear_workspace_bytes", "pgmoe_linear_forward",
+    "pgmoe_dequant_rows",
 )
 
 STATUS_SPIN_TIMEOUT = 1  # PGMOE_STATUS_SPIN_TIMEOUT

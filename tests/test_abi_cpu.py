@@ -217,3 +217,30 @@ def test_zipf_bias_skews_loads():
     _, idx, _ = ol.route(x)
     counts = np.bincount(idx.reshape(-1), minlength=128)
     assert counts.max() > 8 * counts.mean()
+
+
+def test_add_rmsnorm_argument_checks():
+    """pgmoe_add_rmsnorm validates before any device work."""
+    L = _lib.lib()
+    ok = (0x1000, 0, 0x2000, 0, 0x3000)
+    assert L.pgmoe_add_rmsnorm(*ok, 0, 256, 1e-6, None, 0x4000, 1, None) == 0      # no rows: nothing to do
+    assert L.pgmoe_add_rmsnorm(*ok, 2, 102, 1e-6, None, 0x4000, 1, None) == -1     # dim not a multiple of 4
+    assert L.pgmoe_add_rmsnorm(0x1000, 7, 0x2000, 0, 0x3000, 2, 256, 1e-6, None, 0x4000, 1, None) == -2  # x dtype
+    assert L.pgmoe_add_rmsnorm(*ok, 2, 256, 1e-6, None, 0x4000, 30, None) == -2    # bf16 output
+    assert L.pgmoe_add_rmsnorm(*ok, 2, 256, -1.0, None, 0x4000, 1, None) == -1     # negative eps
+    assert L.pgmoe_add_rmsnorm(None, 0, None, 0, 0x3000, 2, 256, 1e-6, None, 0x4000, 1, None) == -1  # NULL x
+    assert L.pgmoe_add_rmsnorm(0x1004, 0, None, 0, 0x3000, 2, 256, 1e-6, None, 0x4000, 1, None) == -1  # misaligned
+
+
+def test_noalloc_and_routing_argument_checks():
+    L = _lib.lib()
+    lay = _fake_layer()
+    assert L.pgmoe_moe_forward_noalloc(lay, 0x1000, 0, 0x2000, None) == 0           # no tokens
+    assert L.pgmoe_moe_forward_noalloc(lay, 0x1000, -1, 0x2000, None) == -1
+    assert L.pgmoe_moe_forward_noalloc(lay, None, 4, 0x2000, None) == -1
+    assert L.pgmoe_moe_forward_noalloc(lay, 0x1000, 100000, 0x2000, None) == -3     # beyond the fixed scratch
+    n = L.pgmoe_workspace_bytes(lay, 4)
+    assert L.pgmoe_moe_routing(lay, 4, 0x1000, n - 256, 0x2000, 0x3000, 0x4000, 0x5000, None) == -3
+    assert L.pgmoe_moe_routing(lay, 4, 0x1008, n, 0x2000, 0x3000, 0x4000, 0x5000, None) == -1
+    st = ctypes.c_int32()
+    assert L.pgmoe_moe_status(lay, 0x1000, 16, ctypes.byref(st), 0, None) == -3
