@@ -53,8 +53,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense FFN measurement")
+    ap.add_argument("--no-configs", action="store_true", help="skip the Mixtral and Qwen2 + shared configs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--m-list", default="1,2,4,8", help="decode token counts to time (1 is the headline)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 256 MiB device copy (calibrates FETCH/WRITE_SIZE counters)")
@@ -233,28 +234,38 @@ def copy_probe(torch) -> None:
     log(f"[bench] copy probe: 4 x {n} byte device copies")
 
 
-def cpu_baseline(lay, M: int, seconds: float):
+def cpu_baseline(lay, M: int, seconds: float, threads: int = 0, max_forwards: int = 400):
+    """The torch-CPU restatement of the reference path (oracle/torch_port.py, fp16 casts
+    kept) timed on this host for a bounded sample: forwards of M tokens until `seconds`
+    have passed (after one warm-up forward), at most max_forwards."""
     import torch
     import oracle
     from oracle import torch_port
 
     cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config, router_bias=lay.router_bias)
-    port = torch_port.PortMoE(ol)
-    x = torch.from_numpy(lay.draw_x(64))
-    port.forward(x[0:M], faithful=True)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        port.forward(x[(n * M) % 64:(n * M) % 64 + M], faithful=True)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or n >= 400:
-            break
-    return {"value": round(n * M / el, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n} forwards of M={M} token(s) of the benchmarked layer: oracle/torch_port.py, the "
+    nthr = threads or cores
+    prev = torch.get_num_threads()
+    torch.set_num_threads(nthr)
+    try:
+        ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config, router_bias=lay.router_bias)
+        port = torch_port.PortMoE(ol)
+        pool = max(M, 64)
+        x = torch.from_numpy(lay.draw_x(pool))
+        port.forward(x[0:M], faithful=True)  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while True:
+            o = (n * M) % (pool - M + 1)
+            port.forward(x[o:o + M], faithful=True)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= max_forwards:
+                break
+    finally:
+        torch.set_num_threads(prev)
+    return {"value": round(n * M / el, 3), "unit": "tok/s", "cores": nthr, "kind": "port",
+            "sample": f"{n} forward(s) of M={M} token(s) of the {lay.spec.name} layer: oracle/torch_port.py, the "
                       f"torch-CPU restatement of the reference CPU path (repacked W4/W8, chunked fp32 dequant + "
-                      f"F.linear, fp16 casts kept), {el:.1f} s on {cores} threads"}
+                      f"F.linear, fp16 casts kept), {el:.1f} s on {nthr} of {cores} host threads"}
 
 
 def routing_bit_exact(mod, M: int, idx, oracle) -> bool:
@@ -279,6 +290,103 @@ def load_traffic(kernel: str):
         if rec.get("kernel", "").split("pgmoe::")[-1].startswith(kernel):
             return rec.get("bytes_per_launch"), rec
     return None, None
+
+
+def prefill_names(n: int, shared: bool):
+    """Kernel names of a prefill forward's launches, in launch order (pgmoe.h)."""
+    head = ["router", "topk"] + (["dispatch_count"] if n - (12 if shared else 7) == 1 else []) + ["dispatch"]
+    names = head + ["gemm_gateup", "rowscale", "gemm_down"]
+    if shared:
+        names += ["sh_dispatch", "sh_gemm_gateup", "sh_rowscale", "sh_gemm_down", "sh_gate"]
+    return names + ["combine"]
+
+
+def layer_flops(spec, M: int, pairs: int) -> float:
+    f = 2.0 * pairs * 3 * spec.hidden * spec.inter
+    if spec.shared_inter:
+        f += 2.0 * M * 3 * spec.hidden * spec.shared_inter
+    return f
+
+
+def config_section(torch, oracle, hip, dev, name: str, m_dec: int, m_pf: int, steps: int, warmup: int,
+                   pf_steps: int, cpu_seconds: float, copies: int = 2) -> dict:
+    """One BASELINE config: parity gate, decode M = m_dec from graph replays over `copies`
+    weight copies (HBM fraction of the active GGUF bytes), prefill M = m_pf eager (MFMA
+    fraction of the grouped GEMMs and of the layer; for a shared expert also the HBM
+    fraction of every byte the step reads), and the CPU baseline at M = m_dec."""
+    import numpy as np
+    from pgmoe import HipSparseMoEMLP
+    from pgmoe.synth import CONFIGS, SyntheticLayer
+    spec = CONFIGS[name]
+    lay = SyntheticLayer(spec, seed=0)
+    base = HipSparseMoEMLP(lay.gguf, lay.config, 0, dev)
+    mods = [base] + [base.replica() for _ in range(copies - 1)]
+    ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config)
+    out = {"workload": f"{name}: H={spec.hidden} E={spec.n_experts} top-{spec.top_k} I={spec.inter}"
+                       + (f" + shared I={spec.shared_inter}" if spec.shared_inter else "")
+                       + f", GGUF types {list(spec.qtypes)}", "weight_copies": copies}
+    parity = {}
+    for M, toks in ((m_dec, None), (m_pf, [0, m_pf // 2, m_pf - 1])):
+        xg = lay.draw_x(M)
+        got = base(torch.from_numpy(xg).to(dev)).cpu().numpy()
+        logits, idx, w = ol.route(xg)
+        tk = np.arange(M) if toks is None else np.array(toks)
+        ref = ol.forward_tokens(xg, idx, w, tokens=tk)
+        parity[str(M)] = {"rel_l2": float(f"{oracle.rel_l2(got[tk], ref):.3e}"),
+                          "max_rel": float(f"{oracle.max_rel(got[tk], ref):.3e}"),
+                          "routing_bit_exact": routing_bit_exact(base, M, idx, oracle), "rows_checked": len(tk)}
+    out["parity"] = parity
+    ok = all(v["rel_l2"] <= 1e-3 and v["max_rel"] <= 2e-2 and v["routing_bit_exact"] for v in parity.values())
+    # decode
+    x = torch.from_numpy(lay.draw_x(m_dec)).to(dev)
+    ms = graph_step_ms(torch, mods, x, steps, warmup)
+    _, idx, _ = ol.route(lay.draw_x(m_dec))
+    n_act = len(np.unique(idx))
+    wb = base.active_weight_bytes(n_act) + base.shared_weight_bytes()
+    kd = kernel_durations(torch, hip, mods, x, 20)
+    gbs = wb / (ms * 1e-3) / 1e9
+    out["decode"] = {"M": m_dec, "us_per_step": round(ms * 1e3, 3), "tok_per_s": round(m_dec / (ms * 1e-3), 1),
+                     "active_experts": n_act, "weight_bytes": wb, "hbm_gbs": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "kernel_us": [round(v * 1e3, 3) for v in kd],
+                     "timing": f"one forward per HIP graph replay, {copies} weight copies"}
+    # prefill
+    xp_np = lay.draw_x(m_pf)
+    xp = torch.from_numpy(xp_np).to(dev)
+    msp = eager_step_ms(torch, mods, xp, pf_steps, 2)
+    kd = kernel_durations(torch, hip, mods, xp, max(3, pf_steps // 2))
+    names = prefill_names(len(kd), bool(spec.shared_inter))
+    _, idxp, _ = ol.route(xp_np)
+    n_act_p = len(np.unique(idxp))
+    fl = layer_flops(spec, m_pf, m_pf * spec.top_k)
+    gemm_ms = sum(v for n, v in zip(names, kd) if "gemm" in n)
+    wbp = base.active_weight_bytes(n_act_p) + base.shared_weight_bytes()
+    out["prefill"] = {"M": m_pf, "us_per_step": round(msp * 1e3, 2), "tok_per_s": round(m_pf / (msp * 1e-3), 1),
+                      "kernels": names, "kernel_us": [round(v * 1e3, 2) for v in kd], "flops": fl,
+                      "gemm_mfma_frac": round(fl / (gemm_ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+                      "layer_mfma_frac": round(fl / (msp * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+                      "active_experts": n_act_p, "weight_bytes": wbp,
+                      "layer_hbm_frac": round(wbp / (msp * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del mods, base
+    torch.cuda.empty_cache()
+    if cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline(lay, m_dec, cpu_seconds, max_forwards=50)
+    if not ok:
+        out["parity_failed"] = True
+    return out
+
+
+def load_trace_avg(kernel: str):
+    """Average duration (us) of `kernel` (a name prefix) in the committed kernel-trace
+    summary of this benchmark, if one is there."""
+    try:
+        with open(os.path.join(REPO, "profiles", "trace_bench.json")) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for k, v in rec.get("kernels", {}).items():
+        if k.split("pgmoe::")[-1].startswith(kernel):
+            return v.get("avg_us")
+    return None
 
 
 def main() -> int:
@@ -307,7 +415,8 @@ def main() -> int:
     mods = [base] + [base.replica() for _ in range(max(0, args.copies - 1))]
     ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config)
 
-    # ---- correctness gate on the benchmarked layer (M = 1 and M = 8)
+    # ---- correctness gate on the benchmarked layer (M = 1 and M = 8), the routing read
+    # back from the timed forward's own workspace
     gate = {}
     for M in (1, 8):
         xg = lay.draw_x(M)
@@ -335,31 +444,27 @@ def main() -> int:
         _, idx, _ = ol.route(lay.draw_x(M))
         n_act = len(np.unique(idx))
         kd = kernel_durations(torch, hip, mods, x, 50)
+        ab = base.active_weight_bytes(n_act)
         decode[M] = {"us_per_step": round(ms * 1e3, 3), "tok_per_s": round(M / (ms * 1e-3), 1),
                      "steps": steps, "eager_us_per_step": round(ms_eager * 1e3, 3),
                      "active_experts": n_act, "kernel_us": [round(v * 1e3, 3) for v in kd],
-                     "active_weight_bytes": base.active_weight_bytes(n_act)}
+                     "active_weight_bytes": ab,
+                     "layer_hbm_frac": round(ab / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"[bench] decode M={M}: {decode[M]}")
 
-    # dominant kernel at M = 1: the whole layer in one launch (dec_moe_kernel: router, routing,
-    # gate/up + SwiGLU, down + combine) when the layer's formats have the fused kernel, else
-    # the routed gate/up launch of (gate/up with the router folded in, down + combine).  Its
-    # algorithmic bytes: the active experts' GGUF bytes of the matrices it reads plus the fp32
-    # router weights.
+    # dominant kernel at M = 1: the routed gate/up launch (router folded in, routing, gate/up
+    # + SwiGLU).  Its algorithmic bytes are the active experts' gate and up GGUF bytes (the
+    # 1 MiB fp32 router weights it also reads are reported beside them, not counted).
     d1 = decode[1]
     ku = d1["kernel_us"]
     router_bytes = spec.n_experts * spec.hidden * 4
     gu_mat = base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat
-    if len(ku) == 1:
-        dom_kernel, dom_names = "dec_moe_kernel", ["dec_moe"]
-        dom_desc = "dec_moe_kernel (router + routing + gate/up + SwiGLU + down + combine in one launch), M=1"
-        dom_bytes = d1["active_weight_bytes"] + router_bytes
-    else:
-        dom_kernel, dom_names = "dec_gu_kernel", ["dec_gu", "dec_dc"]
-        dom_desc = "dec_gu_kernel (router + routing + gate/up + SwiGLU), M=1"
-        dom_bytes = d1["active_experts"] * gu_mat + router_bytes
+    dom_kernel, dom_names = "dec_gu_kernel", ["dec_gu", "dec_dc"]
+    dom_desc = "dec_gu_kernel (router + routing + gate/up + SwiGLU), M=1"
+    dom_bytes = d1["active_experts"] * gu_mat
     dom_us = ku[0]
     dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
+    trace_us = load_trace_avg("dec_gu_kernel<12, 1, 1, 2>")
     layer_gbs = d1["active_weight_bytes"] / (d1["us_per_step"] * 1e-6) / 1e9
     traffic, traffic_rec = load_traffic(dom_kernel)
 
@@ -376,12 +481,16 @@ def main() -> int:
         M = 4096
         xp_np = play.draw_x(M)
         xp = torch.from_numpy(xp_np).to(dev)
+        got = pm(xp)
+        pol = oracle.OracleLayer.from_gguf(play.gguf, play.config, router_bias=play.router_bias)
+        _, pidx, pw = pol.route(xp_np)
+        prouting = routing_bit_exact(pm, M, pidx, oracle)
+        ptoks = np.array([0, 2047, 4095])
+        pref = pol.forward_tokens(xp_np, pidx, pw, tokens=ptoks)
+        pgot = got.cpu().numpy()[ptoks]
         ms = eager_step_ms(torch, pmods, xp, args.prefill_steps, 2)
         kd = kernel_durations(torch, hip, pmods, xp, max(3, args.prefill_steps // 2))
-        # launches: router, top-k, dispatch (a counting pass first when it takes several
-        # workgroups), gate/up, row-scale, down, combine
-        names = (["router", "topk", "dispatch_count", "dispatch", "gemm_gateup", "rowscale", "gemm_down", "combine"]
-                 if len(kd) == 8 else ["router", "topk", "dispatch", "gemm_gateup", "rowscale", "gemm_down", "combine"])
+        names = prefill_names(len(kd), False)
         i_gu, i_dn = names.index("gemm_gateup"), names.index("gemm_down")
         P = M * pspec.top_k
         fl_gu = 2.0 * P * pspec.hidden * 2 * pspec.inter
@@ -389,15 +498,34 @@ def main() -> int:
         gu_tf = fl_gu / (kd[i_gu] * 1e-3) / 1e12
         dn_tf = fl_dn / (kd[i_dn] * 1e-3) / 1e12
         both_tf = (fl_gu + fl_dn) / ((kd[i_gu] + kd[i_dn]) * 1e-3) / 1e12
+        side_us = sum(v for n, v in zip(names, kd) if "gemm" not in n) * 1e3
         prefill = {"M": M, "us_per_step": round(ms * 1e3, 2), "tok_per_s": round(M / (ms * 1e-3), 1),
-                   "kernel_us": [round(v * 1e3, 2) for v in kd],
-                   "kernels": names,
+                   "kernel_us": [round(v * 1e3, 2) for v in kd], "kernels": names,
                    "gemm_gateup_tflops": round(gu_tf, 1), "gemm_down_tflops": round(dn_tf, 1),
                    "gemm_tflops": round(both_tf, 1), "mfma_frac": round(both_tf / FP16_PEAK_TFLOPS, 4),
-                   "layer_tflops": round((fl_gu + fl_dn) / (ms * 1e-3) / 1e12, 1)}
+                   "layer_tflops": round((fl_gu + fl_dn) / (ms * 1e-3) / 1e12, 1),
+                   "layer_mfma_frac": round((fl_gu + fl_dn) / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4),
+                   "side_kernels_us": round(side_us, 2),
+                   "parity": {"rel_l2": float(f"{oracle.rel_l2(pgot, pref):.3e}"),
+                              "max_rel": float(f"{oracle.max_rel(pgot, pref):.3e}"),
+                              "routing_bit_exact": prouting, "rows_checked": len(ptoks)}}
         log(f"[bench] prefill M=4096: {prefill}")
-        del pmods, pm
+        del pmods, pm, got
         torch.cuda.empty_cache()
+        if not (prouting and prefill["parity"]["rel_l2"] <= 1e-3 and prefill["parity"]["max_rel"] <= 2e-2):
+            log("[bench] PREFILL PARITY FAILED")
+            return 1
+
+    configs = {}
+    if not args.no_configs:
+        for cname, m_dec, m_pf in (("mixtral_8x7b", 1, 2048), ("qwen2_57b_a14b", 1, 512)):
+            configs[cname] = config_section(torch, oracle, hip, dev, cname, m_dec, m_pf, max(50, args.steps // 4),
+                                            10, args.prefill_steps,
+                                            0.0 if args.no_cpu_baseline else args.cpu_seconds / 2)
+            log(f"[bench] {cname}: {configs[cname]}")
+            if configs[cname].get("parity_failed"):
+                log(f"[bench] {cname} PARITY FAILED")
+                return 1
 
     dense = None
     if not args.no_dense:
@@ -408,9 +536,14 @@ def main() -> int:
             return 1
 
     cpu = None
+    cpu_more = {}
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(lay, 1, args.cpu_seconds)
         log(f"[bench] cpu baseline: {cpu}")
+        cpu_more["qwen3_m1_1thread"] = cpu_baseline(lay, 1, args.cpu_seconds / 2, threads=1)
+        if not args.no_prefill:
+            cpu_more["qwen3_zipf_prefill_m4096"] = cpu_baseline(play, 4096, 1.0, max_forwards=1)
+        log(f"[bench] cpu baselines: {cpu_more}")
 
     rec = {
         "metric": METRIC,
@@ -430,14 +563,25 @@ def main() -> int:
                    "weight_copies": args.copies, "timing": "one forward per HIP graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": dom_desc, "algorithmic_bytes": dom_bytes, "kernel_us": dom_us,
+                     "kernel": dom_desc, "algorithmic_bytes": dom_bytes,
+                     "algorithmic_bytes_note": f"{d1['active_experts']} active experts x ({gu_mat:,} gate + up GGUF "
+                                               "bytes); the launch also reads the fp32 router weights "
+                                               f"({router_bytes:,} B), not counted",
+                     "kernel_us": dom_us, "kernel_us_source": "HIP events the kernel records at its own begin / "
+                                                             "end, average over 50 forwards",
+                     "trace_avg_us": trace_us,
+                     "frac_from_trace": (round(dom_bytes / (trace_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                                         if trace_us else None),
+                     "router_inclusive_gbs": round((dom_bytes + router_bytes) / (dom_us * 1e-6) / 1e9, 1),
                      "traffic_source": traffic_rec.get("source") if traffic_rec else None},
         "cpu_baseline": cpu,
+        "cpu_baselines_more": cpu_more or None,
         "decode": {str(k): v for k, v in decode.items()},
         "kernels_m1": {"names": dom_names, "us": ku,
                        "layer_active_gbs": round(layer_gbs, 1),
                        "layer_hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
         "prefill": prefill,
+        "configs": configs or None,
         "dense": dense,
         "parity": {str(M): {k: (float(f"{v:.3e}") if isinstance(v, float) else v) for k, v in g.items()}
                    for M, g in gate.items()},

@@ -3,6 +3,7 @@
     python -m pgmoe.prof_summary RUN_results.db                 # kernel trace table
     python -m pgmoe.prof_summary --pmc RUN_results.db [NAME]    # counters per kernel
     python -m pgmoe.prof_summary --traffic FETCH.db WRITE.db NAME  # HBM bytes per launch
+    python -m pgmoe.prof_summary --trace-json RUN_results.db [COMMAND]  # per-kernel averages, JSON
 
 The kernel-trace mode groups dispatches by kernel name, grid and block. For each group it
 reports the number of calls, the average / min / max duration in microseconds, and the
@@ -37,6 +38,24 @@ def summarise(db: str) -> str:
         out.append(f"| `{n}` | {gx}x{gy} | {wx} | {k} | {tot / k / 1e3:.2f} | {mn / 1e3:.2f} | {mx / 1e3:.2f} | "
                    f"{'/'.join(str(v) for v in res)} |")
     return "\n".join(out)
+
+
+def trace_json(db: str, command: str = "") -> dict:
+    """{"command": ..., "kernels": {name: {"calls", "avg_us", "min_us", "max_us"}}} of a
+    kernel-trace database (dispatches grouped by kernel name and launch shape; the most
+    called shape of each name is kept)."""
+    c = sqlite3.connect(db)
+    rows = c.execute("select name, duration, grid_x, grid_y, workgroup_x from kernels").fetchall()
+    agg = collections.defaultdict(list)
+    for name, dur, gx, gy, wx in rows:
+        agg[(name.split("(")[0], gx, gy, wx)].append(dur)
+    best = {}
+    for (n, gx, gy, wx), ds in agg.items():
+        if n not in best or len(ds) > best[n]["calls"]:
+            best[n] = {"calls": len(ds), "avg_us": round(sum(ds) / len(ds) / 1e3, 3),
+                       "min_us": round(min(ds) / 1e3, 3), "max_us": round(max(ds) / 1e3, 3),
+                       "grid": [gx, gy], "block": wx}
+    return {"command": command, "kernels": best}
 
 
 def pmc_table(db: str, pattern: str = "") -> dict:
@@ -116,6 +135,9 @@ if __name__ == "__main__":
     if len(sys.argv) >= 5 and sys.argv[1] == "--traffic":
         import json
         print(json.dumps(traffic(sys.argv[2], sys.argv[3], sys.argv[4]), indent=1))
+    elif len(sys.argv) >= 3 and sys.argv[1] == "--trace-json":
+        import json
+        print(json.dumps(trace_json(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else ""), indent=1))
     elif len(sys.argv) >= 3 and sys.argv[1] == "--pmc":
         print(summarise_pmc(sys.argv[2], sys.argv[3] if len(sys.argv) > 3 else ""))
     else:
