@@ -94,12 +94,38 @@ class Hip:
         return float(f.value)
 
 
-def kernel_durations(torch, hip, mods, x, reps: int):
+# Short names of the forward's kernels (as pgmoe_moe_forward_timed reports their launches).
+_KNAMES = (("router_gemm_kernel", "router"), ("router_logits_kernel", "router"), ("topk_kernel", "topk"),
+           ("dispatch_count_kernel", "dispatch_count"), ("identity_dispatch_kernel", "sh_dispatch"),
+           ("dispatch_kernel", "dispatch"), ("gemm_split_reduce_kernel<true>", "gemm_gateup_reduce"),
+           ("gemm_split_reduce_kernel<false>", "gemm_down_reduce"), ("rowscale_kernel", "rowscale"),
+           ("combine_kernel", "combine"), ("dec_gu_kernel", "dec_gu"), ("dec_dc_kernel", "dec_dc"),
+           ("dec_down_kernel", "dec_down"))
+
+
+def short_names(raw):
+    """Short labels of the launches: the products by their template's GATEUP flag; after the
+    shared expert's identity dispatch, its products (and its gate's router) get "sh_"."""
+    out, shared = [], False
+    for r in raw:
+        if "gemm_kernel<" in r:
+            n = "gemm_gateup" if ", true," in r else "gemm_down"
+        else:
+            n = next((v for k, v in _KNAMES if k in r), r)
+        shared = shared or n == "sh_dispatch"
+        if shared and n == "router":
+            n = "gate"
+        out.append("sh_" + n if shared and not n.startswith("sh_") and n != "combine" else n)
+    return out
+
+
+def kernel_durations(torch, hip, mods, x, reps: int, with_names: bool = False):
     """Average duration (ms) of each kernel of the forward, over `reps` forwards that rotate
-    the weight copies, from the events the kernels record themselves."""
+    the weight copies, from the events the kernels record themselves (and their names)."""
     from pgmoe._lib import check, lib
     n_ev = 32
     starts, stops = hip.events(n_ev), hip.events(n_ev)
+    names = (ctypes.c_char_p * n_ev)()
     M = x.shape[0]
     sums, names_n = None, 0
     for i in range(reps + 2):
@@ -109,14 +135,17 @@ def kernel_durations(torch, hip, mods, x, reps: int):
         nl = ctypes.c_int32()
         stream = torch.cuda.current_stream(x.device).cuda_stream
         check(lib().pgmoe_moe_forward_timed(m._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                                            stream, starts, stops, n_ev, ctypes.byref(nl)), "forward_timed")
+                                            stream, starts, stops, n_ev, ctypes.byref(nl), names), "forward_timed")
         torch.cuda.synchronize()
         if i < 2:
             continue  # warm-up
-        names_n = nl.value
-        d = [hip.elapsed_ms(starts[k], stops[k]) for k in range(min(names_n, n_ev))]
+        names_n = min(nl.value, n_ev)
+        d = [hip.elapsed_ms(starts[k], stops[k]) for k in range(names_n)]
         sums = d if sums is None else [s + v for s, v in zip(sums, d)]
-    return [s / reps for s in sums]
+    avg = [s / reps for s in sums]
+    if with_names:
+        return avg, short_names([names[k].decode() for k in range(names_n)])
+    return avg
 
 
 # ----------------------------------------------------------------------------- timing
@@ -292,15 +321,6 @@ def load_traffic(kernel: str):
     return None, None
 
 
-def prefill_names(n: int, shared: bool):
-    """Kernel names of a prefill forward's launches, in launch order (pgmoe.h)."""
-    head = ["router", "topk"] + (["dispatch_count"] if n - (12 if shared else 7) == 1 else []) + ["dispatch"]
-    names = head + ["gemm_gateup", "rowscale", "gemm_down"]
-    if shared:
-        names += ["sh_dispatch", "sh_gemm_gateup", "sh_rowscale", "sh_gemm_down", "sh_gate"]
-    return names + ["combine"]
-
-
 def layer_flops(spec, M: int, pairs: int) -> float:
     f = 2.0 * pairs * 3 * spec.hidden * spec.inter
     if spec.shared_inter:
@@ -353,8 +373,7 @@ def config_section(torch, oracle, hip, dev, name: str, m_dec: int, m_pf: int, st
     xp_np = lay.draw_x(m_pf)
     xp = torch.from_numpy(xp_np).to(dev)
     msp = eager_step_ms(torch, mods, xp, pf_steps, 2)
-    kd = kernel_durations(torch, hip, mods, xp, max(3, pf_steps // 2))
-    names = prefill_names(len(kd), bool(spec.shared_inter))
+    kd, names = kernel_durations(torch, hip, mods, xp, max(3, pf_steps // 2), with_names=True)
     _, idxp, _ = ol.route(xp_np)
     n_act_p = len(np.unique(idxp))
     fl = layer_flops(spec, m_pf, m_pf * spec.top_k)
@@ -489,8 +508,7 @@ def main() -> int:
         pref = pol.forward_tokens(xp_np, pidx, pw, tokens=ptoks)
         pgot = got.cpu().numpy()[ptoks]
         ms = eager_step_ms(torch, pmods, xp, args.prefill_steps, 2)
-        kd = kernel_durations(torch, hip, pmods, xp, max(3, args.prefill_steps // 2))
-        names = prefill_names(len(kd), False)
+        kd, names = kernel_durations(torch, hip, pmods, xp, max(3, args.prefill_steps // 2), with_names=True)
         i_gu, i_dn = names.index("gemm_gateup"), names.index("gemm_down")
         P = M * pspec.top_k
         fl_gu = 2.0 * P * pspec.hidden * 2 * pspec.inter

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define PGMOE_ABI_VERSION 2
+#define PGMOE_ABI_VERSION 3
 
 #define PGMOE_OK 0
 #define PGMOE_E_INVALID (-1)     /* bad argument, shape or pointer */
@@ -221,13 +221,17 @@ int pgmoe_dequant_rows(const pgmoe_weights* W, const int32_t* rows, int32_t n, v
  * benchmarks and profilers that want each kernel's duration from the caller's own stream.
  * The i-th kernel the call launches (i < n_events) records start_events[i] when it begins
  * and stop_events[i] when it ends (hipEvent_t handles created by the caller; either array
- * may be NULL).  *n_launches (if not NULL) receives the number of kernels launched.
+ * may be NULL), and kernel_names[i] (if that array is not NULL) points to a static string
+ * naming the kernel as its launch writes it (e.g. "(gemm_kernel<QT, true, PG_GU_CT,
+ * PG_GU_WM>)").  *n_launches (if not NULL) receives the number of kernels launched.
  * Launch order: decode (M <= 8): gate/up (router and routing folded in), [shared gate/up,
- * shared down], down + combine (or down, combine); prefill: router, top-k, dispatch, gate/up, row-scale, down,
- * [shared: identity dispatch, gate/up, row-scale, down, shared gate], combine. */
+ * shared down], down + combine (or down, combine); prefill: router, top-k, dispatch
+ * (a counting pass first when it takes several workgroups), gate/up, row-scale, down,
+ * [shared: identity dispatch, gate/up, row-scale, down, shared gate], combine; a product
+ * split over K when its tiles cannot fill the chip is followed by its reduce kernel. */
 int pgmoe_moe_forward_timed(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
                             size_t ws_bytes, void* stream, void** start_events, void** stop_events,
-                            int32_t n_events, int32_t* n_launches);
+                            int32_t n_events, int32_t* n_launches, const char** kernel_names);
 
 /* ---- stages of the forward, exposed for tests and for callers that fuse around them ---- */
 

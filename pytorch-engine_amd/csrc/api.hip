@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -74,7 +75,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
     size_t rlog, status, desc, xsum, isum, s_isum;
-    size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, dcounts, inter, a16, rs, partial;
+    size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, dcounts, inter, a16, rs, partial, raw;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
 };
@@ -121,6 +122,16 @@ static Layout layout_for(const pgmoe_layer* L, int M, int rlog_experts = 0) {
     o.rs = take(c, gemm ? P * 4 : 0);
     // the fused decode down kernel combines in place; otherwise per-pair partial rows
     o.partial = take(c, (gemm || !decode_fused_down((int)P, (int)I)) ? P * H * 4 : 0);
+    if (gemm) {  // split-K scratch, shared by the products in turn (stream-ordered)
+        size_t r = gemm_split_bytes((int64_t)P, (int)E, (int)I, (int)H, true);
+        r = std::max(r, gemm_split_bytes((int64_t)P, (int)E, (int)H, (int)I, false));
+        if (L->has_shared) {
+            const int Is = L->sh_gate.n_rows;
+            r = std::max(r, gemm_split_bytes(M, 1, Is, (int)H, true));
+            r = std::max(r, gemm_split_bytes(M, 1, (int)H, Is, false));
+        }
+        o.raw = take(c, r);
+    }
     if (L->has_shared) {
         const size_t Is = L->sh_gate.n_rows;
         o.s_offsets = take(c, 2 * 4);
@@ -177,10 +188,10 @@ static int check_layer(const pgmoe_layer* L, LayerMats* lm) {
 // The same kernels with one matrix triple applied to every token with weight 1 (the
 // shared expert's launches without a router).
 struct DenseLayout {
-    size_t offsets, perm, inv, active, nact, tile_off, w, inter, isum, a16, rs, total;
+    size_t offsets, perm, inv, active, nact, tile_off, w, inter, isum, a16, rs, raw, total;
 };
 
-static DenseLayout dense_layout(int M, int I) {
+static DenseLayout dense_layout(int M, int I, int H) {
     DenseLayout o{};
     const bool gemm = M > decode_tokens_max();
     size_t c = 0;
@@ -195,6 +206,7 @@ static DenseLayout dense_layout(int M, int I) {
     o.isum = take(c, gemm ? 0 : (size_t)M * (I / 16) * 4);
     o.a16 = take(c, gemm ? (size_t)M * I * 2 : 0);
     o.rs = take(c, gemm ? (size_t)M * 4 : 0);
+    o.raw = take(c, gemm ? std::max(gemm_split_bytes(M, 1, I, H, true), gemm_split_bytes(M, 1, H, I, false)) : 0);
     o.total = c;
     return o;
 }
@@ -222,7 +234,7 @@ extern "C" {
 size_t pgmoe_dense_workspace_bytes(const pgmoe_dense* D, int32_t M) {
     Mats g, u, d;
     if (M < 0 || check_dense(D, &g, &u, &d)) return 0;
-    return dense_layout(M, g.N).total;
+    return dense_layout(M, g.N, D->hidden).total;
 }
 
 int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, float* out, void* ws, size_t ws_bytes,
@@ -234,7 +246,7 @@ int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, floa
     if (M == 0) return PGMOE_OK;
     if (!x || !out || !ws) return fail(PGMOE_E_INVALID, "dense_forward: NULL pointer");
     if ((uintptr_t)ws & 255) return fail(PGMOE_E_INVALID, "workspace must be 256-byte aligned");
-    const DenseLayout o = dense_layout(M, g.N);
+    const DenseLayout o = dense_layout(M, g.N, D->hidden);
     if (ws_bytes < o.total) return fail(PGMOE_E_WORKSPACE, "workspace %zu bytes, need %zu", ws_bytes, o.total);
     uint8_t* b = (uint8_t*)ws;
 #define WS(T, f) reinterpret_cast<T*>(b + o.f)
@@ -253,12 +265,12 @@ int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, floa
                                        st)))
         return rc;
     if ((rc = launch_gateup(g, u, x, M, 1, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
-                            WS(int32_t, nact), WS(int32_t, tile_off), 1, WS(float, inter), st)))
+                            WS(int32_t, nact), WS(int32_t, tile_off), 1, WS(float, inter), st, WS(float, raw))))
         return rc;
     // identity order: sorted pair p is token p, so the down rows are the output rows
     return launch_down(d, WS(float, inter), M, 1, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
                        WS(int32_t, nact), WS(int32_t, tile_off), WS(float, w), 1, WS(uint16_t, a16), WS(float, rs),
-                       out, st);
+                       out, st, WS(float, raw));
 #undef WS
 }
 
@@ -435,11 +447,11 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
                               WS(int32_t, dcounts))))
         return rc;
     if ((rc = launch_gateup(lm.gate, lm.up, x, M, K, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
-                            WS(int32_t, nact), WS(int32_t, tile_off), mode, WS(float, inter), st)))
+                            WS(int32_t, nact), WS(int32_t, tile_off), mode, WS(float, inter), st, WS(float, raw))))
         return rc;
     if ((rc = launch_down(lm.down, WS(float, inter), M, K, WS(int32_t, offsets), WS(int32_t, perm),
                           WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), WS(float, w), mode,
-                          WS(uint16_t, a16), WS(float, rs), WS(float, partial), st)))
+                          WS(uint16_t, a16), WS(float, rs), WS(float, partial), st, WS(float, raw))))
         return rc;
     const float* shared = nullptr;
     const float* shared_logit = nullptr;
@@ -450,11 +462,11 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
             return rc;
         if ((rc = launch_gateup(lm.sg, lm.su, x, M, 1, WS(int32_t, s_offsets), WS(int32_t, s_perm),
                                 WS(int32_t, s_active), WS(int32_t, s_nact), WS(int32_t, s_tile_off), mode,
-                                WS(float, s_inter), st)))
+                                WS(float, s_inter), st, WS(float, raw))))
             return rc;
         if ((rc = launch_down(lm.sd, WS(float, s_inter), M, 1, WS(int32_t, s_offsets), WS(int32_t, s_perm),
                               WS(int32_t, s_active), WS(int32_t, s_nact), WS(int32_t, s_tile_off), WS(float, s_w),
-                              mode, WS(uint16_t, s_a16), WS(float, s_rs), WS(float, s_partial), st)))
+                              mode, WS(uint16_t, s_a16), WS(float, s_rs), WS(float, s_partial), st, WS(float, raw))))
             return rc;
         shared = WS(float, s_partial);
         if (L->sh_inp_gate) {
@@ -592,9 +604,9 @@ int pgmoe_moe_status(const pgmoe_layer* L, void* ws, size_t ws_bytes, int32_t* s
 
 int pgmoe_moe_forward_timed(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* ws,
                             size_t ws_bytes, void* stream, void** start_events, void** stop_events, int32_t n_events,
-                            int32_t* n_launches) {
+                            int32_t* n_launches, const char** kernel_names) {
     if (n_events < 0) return fail(PGMOE_E_INVALID, "negative event count");
-    LaunchTiming t{(hipEvent_t*)start_events, (hipEvent_t*)stop_events, n_events, 0};
+    LaunchTiming t{(hipEvent_t*)start_events, (hipEvent_t*)stop_events, kernel_names, n_events, 0};
     launch_timing() = &t;
     const int rc = pgmoe_moe_forward(L, x, M, out, ws, ws_bytes, stream);
     launch_timing() = nullptr;

@@ -334,7 +334,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     int N, int K, const uint16_t* __restrict__ act, int topk, int E, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm, const int32_t* __restrict__ tile_off, int n_ntiles,
     const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out,
-    const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1) {
+    const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1, int ksplit, int kper, float* __restrict__ raw) {
     using L = GLay<QT, CT, WM>;
     constexpr int NW = L::NW, WN = L::WN, RS = L::RS, WR = 32 * RS;  // WR rows per wave
     constexpr int CH = L::CH;
@@ -346,14 +346,19 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     PG_MARK(GATEUP ? 4 : 5, 0);
     PG_SET(6, 1u + (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4));  // HW_ID (CU, SIMD, wave)
     PG_SET(7, 1u + (uint32_t)__builtin_amdgcn_s_getreg((15 << 11) | 20));  // XCC_ID
-    if (!gemm_tile_of(blockIdx.x, n_ntiles, tile_off[E], mt, nt)) return;
+    // split K (ksplit > 1): block = (tile, split ks); split ks takes super-blocks
+    // [ks kper, (ks + 1) kper) and writes raw accumulators, reduced by gemm_split_reduce_kernel
+    const int ks = ksplit > 1 ? (int)(blockIdx.x % ksplit) : 0;
+    if (!gemm_tile_of(ksplit > 1 ? blockIdx.x / ksplit : blockIdx.x, n_ntiles, tile_off[E], mt, nt)) return;
     const int e = gemm_tile_expert(tile_off, E, mt);
     const int m0 = offsets[e] + (mt - tile_off[e]) * kGM;
     const int mrows = min(kGM, offsets[e + 1] - m0);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;  // waves w and w + WN: same columns
-    const int units = K >> 6, nb = K >> 8;
+    const int nb = K >> 8;
+    const int u0 = 4 * ks * kper;                       // first unit of this block's K range
+    const int units = 4 * (min(nb, (ks + 1) * kper) - ks * kper);  // its units (>= 4)
     // A source rows: gate/up gathers token rows of x, down reads its own pair rows.  Rows
     // past the tile's pairs repeat its last pair: they only feed accumulator rows that
     // are never stored.
@@ -409,7 +414,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     const uint32_t sbase = lds_addr(smem);
     // Issue every copy of unit u into stage st (u clamped: the last steps repeat it).
     auto copy_unit = [&](auto ac, int u, int st) {  // ac: A copies (integral_constant)
-        u = min(u, units - 1);
+        u = u0 + min(u, units - 1);  // relative unit -> absolute (past the range: repeat the last)
         const uint32_t S = sbase + st * L::STAGE;
 #pragma unroll
         for (int q = 0; q < decltype(ac)::value; ++q)
@@ -471,6 +476,26 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     vm_wait<0>();  // the clamped copies past the last unit land before the block ends
     PG_MARK(GATEUP ? 4 : 5, 4);
     if (!active) return;
+    if (ksplit > 1) {  // raw sums of this K range: [ks][p][c], gate/up c < 2N (up at N + c), down c < N
+        const int NC = GATEUP ? 2 * N : N;
+        float* rb = raw + (int64_t)ks * offsets[E] * NC;
+#pragma unroll
+        for (int j = 0; j < CT; ++j) {
+            const int jj = GATEUP ? j % (CT / 2) : j;
+            const int c = GATEUP ? nt * (kGN / 2) + 16 * CT * wn + 32 * jj + (lane & 31)
+                                 : nt * kGN + 32 * CT * wn + 32 * j + (lane & 31);
+            if (c >= N) continue;
+            const int cc = GATEUP && j >= CT / 2 ? N + c : c;
+#pragma unroll
+            for (int i = 0; i < RS; ++i)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int r = WR * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                    if (r < mrows) rb[(int64_t)(m0 + r) * NC + cc] = acc[i][j][v];
+                }
+        }
+        return;
+    }
     // epilogue: register v of tile (i, j) is row 32i + 8(v/4) + 4(l/32) + v%4, column
     // 32j + l%32 of the wave tile
     if (GATEUP) {
@@ -511,7 +536,82 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     PG_FLUSH(GATEUP ? 4 : 5);
 }
 
+// The epilogue of a split-K product over every sorted pair p < P: the S raw partial sums
+// of each output added in split order, then gate/up: inter[p][c] = silu(g) * u; down:
+// partial[p][c] = rs[p] * topk_w[perm[p]] * acc (the unsplit kernel's epilogues).
+template <bool GATEUP>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __restrict__ raw, int S, int64_t P,
+                                                                int N, const float* __restrict__ rs,
+                                                                const float* __restrict__ topk_w,
+                                                                const int32_t* __restrict__ perm,
+                                                                float* __restrict__ out) {
+    const int64_t n = P * N;
+    const int NC = GATEUP ? 2 * N : N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t p = i / N;
+        const int c = (int)(i - p * N);
+        const float* r = raw + p * NC + c;
+        float a = r[0], b = GATEUP ? r[N] : 0.f;
+        for (int k = 1; k < S; ++k) {
+            a = a + r[(int64_t)k * P * NC];
+            if (GATEUP) b = b + r[(int64_t)k * P * NC + N];
+        }
+        out[i] = GATEUP ? silu_fast(a) * b : (rs[p] * topk_w[perm[p]]) * a;
+    }
+}
+
 int gemm_tile_pairs() { return kGM; }
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+// K splits of a grouped product whose tiles would not fill the chip: tiles (an estimate:
+// exact for one expert, P / 256 plus half the possible remainder tiles otherwise) times N
+// tiles below one workgroup per CU (a workgroup's LDS fills a CU) gets the smallest split
+// count that reaches it, cut at super-block boundaries (kper super-blocks per split, every
+// split non-empty).
+GemmSplit gemm_split(int64_t P, int E, int N, int K, bool gateup) {
+    GemmSplit sp{1, K >> 8};
+    if (P <= 0) return sp;
+    const int64_t tiles = div_up(P, kGM) + (E > 1 ? (P < E ? P : E) / 2 : 0);
+    const int64_t blocks = tiles * div_up(N, gateup ? kGN / 2 : kGN);
+    const int64_t want = device_cus();
+    if (blocks >= want) return sp;
+    const int nb = K >> 8;
+    int s = (int)div_up(want, blocks);
+    s = s < nb ? s : nb;
+    s = s < 32 ? s : 32;
+    if (s <= 1) return sp;
+    sp.kper = div_up(nb, s);
+    sp.ksplit = div_up(nb, sp.kper);
+    return sp;
+}
+
+size_t gemm_split_bytes(int64_t P, int E, int N, int K, bool gateup) {
+    const GemmSplit sp = gemm_split(P, E, N, K, gateup);
+    return sp.ksplit > 1 ? (size_t)sp.ksplit * P * (gateup ? 2 * N : N) * 4 : 0;
+}
+
+static int launch_split_reduce(bool gateup, const float* raw, int S, int64_t P, int N, const float* rs,
+                               const float* topk_w, const int32_t* perm, float* out, hipStream_t st) {
+    const int64_t n = P * N;
+    const int blocks = (int)(div_up(n, 256) < 16384 ? div_up(n, 256) : 16384);
+    if (gateup)
+        PG_LAUNCH(gemm_split_reduce_kernel<true>, dim3(blocks), dim3(256), 0, st, raw, S, P, N, rs, topk_w, perm, out);
+    else
+        PG_LAUNCH(gemm_split_reduce_kernel<false>, dim3(blocks), dim3(256), 0, st, raw, S, P, N, rs, topk_w, perm, out);
+    return check_launch("gemm split reduce");
+}
 
 // Wave layout of each product (build-time choices): CT column tiles per wave, WM waves
 // along M.  Measured on the Qwen3 Zipf prefill (M = 4096): gate/up (K = 2048, Q4_K) is
@@ -538,17 +638,19 @@ static int gemm_max_mtiles(int64_t P, int E) {
 }
 
 int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
-                       const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st) {
+                       const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st, float* raw) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
     if (g.qtype != PGMOE_Q8_0 && (!g.scales || !u.scales))
         return fail(PGMOE_E_INVALID, "gemm gate/up: K-quant weights need their scale plane (pgmoe_build_scale_plane)");
     const int nnt = div_up(g.N, kGN / 2);
-    const dim3 grid(gemm_max_mtiles(P, E) * nnt);
+    const GemmSplit sp = raw ? gemm_split(P, E, g.N, g.K, true) : GemmSplit{1, g.K >> 8};
+    const dim3 grid(gemm_max_mtiles(P, E) * nnt * sp.ksplit);
 #define PG_GU(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, true, PG_GU_CT, PG_GU_WM>), grid, dim3(64 * GLay<QT, PG_GU_CT, PG_GU_WM>::NW), 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
-              E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter, g.scales, u.scales)
+              E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter, g.scales, u.scales, \
+              sp.ksplit, sp.kper, raw)
     switch (g.qtype) {
     case PGMOE_Q4_K: PG_GU(PGMOE_Q4_K); break;
     case PGMOE_Q6_K: PG_GU(PGMOE_Q6_K); break;
@@ -556,22 +658,25 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
     default: return fail(PGMOE_E_UNSUPPORTED, "gemm gate/up: qtype %d", g.qtype);
     }
 #undef PG_GU
-    return check_launch("gemm_gateup");
+    int rc = check_launch("gemm_gateup");
+    if (rc || sp.ksplit == 1) return rc;
+    return launch_split_reduce(true, raw, sp.ksplit, P, g.N, nullptr, nullptr, nullptr, inter, st);
 }
 
 int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M, int topk, const int32_t* offsets,
                      const int32_t* perm, const int32_t* tile_off, const float* topk_w, float* partial,
-                     hipStream_t st) {
+                     hipStream_t st, float* raw) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
     if (d.qtype != PGMOE_Q8_0 && !d.scales)
         return fail(PGMOE_E_INVALID, "gemm down: K-quant weights need their scale plane (pgmoe_build_scale_plane)");
     const int nnt = div_up(d.N, kGN);
-    const dim3 grid(gemm_max_mtiles(P, E) * nnt);
+    const GemmSplit sp = raw ? gemm_split(P, E, d.N, d.K, false) : GemmSplit{1, d.K >> 8};
+    const dim3 grid(gemm_max_mtiles(P, E) * nnt * sp.ksplit);
 #define PG_DN(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, false, PG_DN_CT, PG_DN_WM>), grid, dim3(64 * GLay<QT, PG_DN_CT, PG_DN_WM>::NW), 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
-              topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial, d.scales, d.scales)
+              topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial, d.scales, d.scales, sp.ksplit, sp.kper, raw)
     switch (d.qtype) {
     case PGMOE_Q4_K: PG_DN(PGMOE_Q4_K); break;
     case PGMOE_Q6_K: PG_DN(PGMOE_Q6_K); break;
@@ -579,7 +684,9 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     default: return fail(PGMOE_E_UNSUPPORTED, "gemm down: qtype %d", d.qtype);
     }
 #undef PG_DN
-    return check_launch("gemm_down");
+    int rc = check_launch("gemm_down");
+    if (rc || sp.ksplit == 1) return rc;
+    return launch_split_reduce(false, raw, sp.ksplit, P, d.N, rs, topk_w, perm, partial, st);
 }
 
 }  // namespace pgmoe

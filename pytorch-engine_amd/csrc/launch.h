@@ -13,16 +13,18 @@ namespace pgmoe {
 struct LaunchTiming {
     hipEvent_t* start;
     hipEvent_t* stop;
+    const char** names;  // optional: the kernel (as written at its launch) of each launch
     int n, next;
 };
 LaunchTiming*& launch_timing();  // this thread's armed timing (nullptr when off)
 
-inline void timing_events(hipEvent_t* s, hipEvent_t* e) {
+inline void timing_events(hipEvent_t* s, hipEvent_t* e, const char* name) {
     LaunchTiming* t = launch_timing();
     if (t) {
         if (t->next < t->n) {
             *s = t->start ? t->start[t->next] : nullptr;
             *e = t->stop ? t->stop[t->next] : nullptr;
+            if (t->names) t->names[t->next] = name;
         }
         ++t->next;
     }
@@ -32,7 +34,7 @@ inline void timing_events(hipEvent_t* s, hipEvent_t* e) {
 #define PG_LAUNCH(kernel, grid, block, shmem, st, ...)                                            \
     do {                                                                                          \
         hipEvent_t pg_ev_s = nullptr, pg_ev_e = nullptr;                                          \
-        ::pgmoe::timing_events(&pg_ev_s, &pg_ev_e);                                               \
+        ::pgmoe::timing_events(&pg_ev_s, &pg_ev_e, #kernel);                                      \
         if (pg_ev_s || pg_ev_e)                                                                   \
             hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, pg_ev_s, pg_ev_e, 0, __VA_ARGS__); \
         else                                                                                      \
@@ -52,10 +54,10 @@ int launch_identity_dispatch(int M, int tile_rows, int32_t* offsets, int32_t* pe
                              int32_t* active, int32_t* n_active, int32_t* tile_off, float* w, hipStream_t st);
 int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                   const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
-                  int mode, float* inter, hipStream_t st);
+                  int mode, float* inter, hipStream_t st, float* raw = nullptr);
 int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_t* offsets, const int32_t* perm,
                 const int32_t* active, const int32_t* n_active, const int32_t* tile_off, const float* topk_w,
-                int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st);
+                int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st, float* raw = nullptr);
 // clear (optional): n_clear words the kernel sets to zero (the decode router's tagged logits).
 int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H, const float* shared,
                    const float* shared_logit, float* out, hipStream_t st, uint64_t* clear = nullptr,
@@ -116,11 +118,21 @@ int decode_rlog_words(int M, int E);
 // Whether the fused down + combine kernel can stage P inter rows of K values.
 bool decode_fused_down(int P, int K);
 // Prefill grouped GEMMs (gemm.hip); tile_off counts gemm_tile_pairs()-row tiles.
+// raw (optional): scratch of gemm_split_bytes(...) for a split-K run when the tiles would
+// not fill the chip; null runs the product unsplit.
 int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
-                       const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st);
+                       const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st,
+                       float* raw = nullptr);
 int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M, int topk, const int32_t* offsets,
                      const int32_t* perm, const int32_t* tile_off, const float* topk_w, float* partial,
-                     hipStream_t st);
+                     hipStream_t st, float* raw = nullptr);
+// K split of a grouped product: ksplit workgroups per tile, kper super-blocks each.
+struct GemmSplit {
+    int ksplit, kper;
+};
+GemmSplit gemm_split(int64_t P, int E, int N, int K, bool gateup);
+// Scratch bytes of the raw partial sums of a split product (0 when it runs unsplit).
+size_t gemm_split_bytes(int64_t P, int E, int N, int K, bool gateup);
 int gemm_tile_pairs();
 int64_t layout_bytes(int qtype, int64_t rows, int64_t cols);
 // Scale plane (relayout.hip): bytes of one matrix's plane (0 for Q8_0, -1 if unsupported)

@@ -113,7 +113,7 @@ size_t linear_ws_bytes(const Mats& w, int M, bool staged) {
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     size_t n = 4 * al(8) + 3 * al((size_t)M * 4);  // offsets, tile_off, active, nact | perm, inv, unit weights
     if (staged) n += al((size_t)M * w.N * 4);
-    return n;
+    return n + al(gemm_split_bytes(M, 1, w.N, w.K, false));  // split-K partial sums
 }
 
 int launch_linear(const Mats& w, const float* bias, const uint16_t* x, int M, void* out, int out_f16, uint8_t* ws,
@@ -137,10 +137,12 @@ int launch_linear(const Mats& w, const float* bias, const uint16_t* x, int M, vo
     int32_t* inv = (int32_t*)take((size_t)M * 4);
     float* ones = (float*)take((size_t)M * 4);
     float* prod = staged ? (float*)take((size_t)M * w.N * 4) : (float*)out;
+    const size_t rb = gemm_split_bytes(M, 1, w.N, w.K, false);
+    float* raw = rb ? (float*)take(rb) : nullptr;
     int rc = launch_identity_dispatch(M, gemm_tile_rows(), offsets, perm, inv, active, nact, tile_off, ones, st);
     if (rc) return rc;
     // the down GEMM's epilogue scales row p by rs[p] * topk_w[perm[p]]: both 1 here
-    if ((rc = launch_gemm_down(w, x, ones, M, 1, offsets, perm, tile_off, ones, prod, st))) return rc;
+    if ((rc = launch_gemm_down(w, x, ones, M, 1, offsets, perm, tile_off, ones, prod, st, raw))) return rc;
     if (!staged) return PGMOE_OK;
     const int64_t n = (int64_t)M * w.N;
     const int blocks = (int)(div_up(n, 256) < 8192 ? div_up(n, 256) : 8192);

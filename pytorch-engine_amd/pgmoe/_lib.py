@@ -12,7 +12,7 @@ from typing import Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libpgmoe.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 Q4_0, Q5_0, Q8_0, Q4_K, Q6_K = 2, 6, 8, 12, 14
 # GGUF expert formats with a HIP path; Q4_0 and Q5_0 are relaid out as Q8_0 (their values exactly)
@@ -93,7 +93,8 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_dense_workspace_bytes.argtypes = [ctypes.POINTER(Dense), _I32]
     L.pgmoe_dense_forward.argtypes = [ctypes.POINTER(Dense), _P, _I32, _P, _P, ctypes.c_size_t, _P]
     L.pgmoe_moe_forward_timed.argtypes = [ctypes.POINTER(Layer), _P, _I32, _P, _P, ctypes.c_size_t, _P,
-                                          ctypes.POINTER(_P), ctypes.POINTER(_P), _I32, ctypes.POINTER(_I32)]
+                                          ctypes.POINTER(_P), ctypes.POINTER(_P), _I32, ctypes.POINTER(_I32),
+                                          ctypes.POINTER(ctypes.c_char_p)]
     L.pgmoe_linear_workspace_bytes.restype = ctypes.c_size_t
     L.pgmoe_linear_workspace_bytes.argtypes = [ctypes.POINTER(Weights), _I32, _I32, _I32]
     L.pgmoe_linear_forward.argtypes = [ctypes.POINTER(Weights), _P, _P, _I32, _P, _I32, _P, ctypes.c_size_t, _P]

@@ -163,24 +163,33 @@ def test_all_tokens_one_expert_and_top_k_equals_e():
 
 
 def test_timed_forward_matches_forward_and_times_every_launch():
-    """pgmoe_moe_forward_timed: same bits as the forward; one event pair per kernel."""
+    """pgmoe_moe_forward_timed: same bits as the forward; one event pair and one kernel name
+    per launch, in the documented order."""
     import ctypes
     from gpu_helpers import HipEvents
     from pgmoe._lib import check, lib
     lay, ol, mod = _pair("tiny")
     starts, stops = HipEvents(16), HipEvents(16)
-    for M, n_expected in ((1, 2), (16, 7)):  # decode: gate/up (router folded in), down+combine; prefill: 7
+    # decode: gate/up (router folded in), down + combine; prefill: router, top-k, dispatch,
+    # gate/up, row-scale, down, combine, each product possibly followed by its split reduce
+    want = {1: ["dec_gu_kernel", "dec_dc_kernel"],
+            16: ["router_", "topk_kernel", "dispatch_kernel", ", true,", "rowscale_kernel", ", false,",
+                 "combine_kernel"]}
+    for M in (1, 16):
         x = torch.from_numpy(lay.draw_x(M)).to("cuda:0")
         ref = mod(x)
         out = torch.empty_like(ref)
         ws = mod._workspace(M)
         n = ctypes.c_int32()
+        names = (ctypes.c_char_p * 16)()
         stream = torch.cuda.current_stream().cuda_stream
         check(lib().pgmoe_moe_forward_timed(mod._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(),
-                                            ws.numel(), stream, starts.ev, stops.ev, 16, ctypes.byref(n)),
+                                            ws.numel(), stream, starts.ev, stops.ev, 16, ctypes.byref(n), names),
               "forward_timed")
         torch.cuda.synchronize()
-        assert n.value == n_expected
+        got = [names[i].decode() for i in range(n.value)]
+        main = [g for g in got if "split_reduce" not in g and "dispatch_count" not in g]
+        assert len(main) == len(want[M]) and all(w in g for w, g in zip(want[M], main)), got
         assert torch.equal(out, ref)
         if M <= 8:  # decode leaves the router's tagged logits (first in the workspace) at zero
             assert int(ws[:16 * M * mod.n_experts * 8].view(torch.int32).abs().sum().item()) == 0  # 16 copies
@@ -189,7 +198,7 @@ def test_timed_forward_matches_forward_and_times_every_launch():
             assert 0.0 < d < 50.0, (M, i, d)
         # fewer events than launches: the rest run untimed, same result
         check(lib().pgmoe_moe_forward_timed(mod._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(),
-                                            ws.numel(), stream, starts.ev, None, 1, None), "forward_timed")
+                                            ws.numel(), stream, starts.ev, None, 1, None, None), "forward_timed")
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
 
