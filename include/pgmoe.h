@@ -63,6 +63,13 @@ extern "C" {
 #define PGMOE_Q4_K 12
 #define PGMOE_Q6_K 14
 
+/* Gate activation of the gated FFNs: act(gate) * up (exec_fused_act_mul_rowscale,
+ * quant_kernels.py:1423-1475).  SiLU g / (1 + e^-g); GELU with the tanh approximation
+ * 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))), the reference's use_gelu for gemma
+ * architectures (model.py:868). */
+#define PGMOE_ACT_SILU 0
+#define PGMOE_ACT_GELU_TANH 1
+
 typedef struct pgmoe_weights {
     int32_t qtype;      /* PGMOE_Q4_K / PGMOE_Q6_K / PGMOE_Q8_0 */
     int32_t n_rows;     /* N: output features per matrix */
@@ -85,12 +92,14 @@ typedef struct pgmoe_layer {
     int32_t has_shared;
     pgmoe_weights sh_gate, sh_up, sh_down; /* [I_s, H], [I_s, H], [H, I_s] */
     const float* sh_inp_gate; /* [H] fp32 or NULL: sigmoid gate on the shared expert */
+    int32_t act;              /* PGMOE_ACT_*: the experts' gate activation (model.py:868) */
 } pgmoe_layer;
 
 /* A dense SwiGLU FFN: one matrix triple, no router (GGUFDenseMLP, model.py:778-846). */
 typedef struct pgmoe_dense {
     int32_t hidden;               /* H */
     pgmoe_weights gate, up, down; /* [I, H], [I, H], [H, I], n_mats = 1 */
+    int32_t act;                  /* PGMOE_ACT_* */
 } pgmoe_dense;
 
 int pgmoe_abi_version(void);

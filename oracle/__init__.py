@@ -60,7 +60,9 @@ def lib() -> ctypes.CDLL:
         L.or_act_rowscale.argtypes = [_P, _P, _I, _I, _P, _P]
         L.or_act_rowscale.restype = None
         L.or_add_rmsnorm.argtypes = [_P, _I, _P, _I, _P, _I, _I, ctypes.c_float, _P, _P, _I]
-        L.or_moe_forward_tokens.argtypes = [_I, _I, _I, _I] + [ctypes.POINTER(_Weights)] * 6 + [
+        L.or_gelu_tanh.restype = ctypes.c_double
+        L.or_gelu_tanh.argtypes = [ctypes.c_double]
+        L.or_moe_forward_tokens.argtypes = [_I, _I, _I, _I, _I] + [ctypes.POINTER(_Weights)] * 6 + [
             _P, _P, _P, _P, _P, _I, _P]
         _lib = L
     return _lib
@@ -171,6 +173,7 @@ class OracleLayer:
     sh_up: Optional[tuple] = None
     sh_down: Optional[tuple] = None
     sh_inp_gate: Optional[np.ndarray] = None
+    act: int = 0  # 0 SiLU, 1 GELU-tanh (gemma architectures, model.py:868)
 
     @classmethod
     def from_gguf(cls, gguf: Any, config: Any, layer_idx: int = 0,
@@ -184,7 +187,11 @@ class OracleLayer:
                 return np.frombuffer(raw, dtype=np.float32).reshape(info.shape).copy()
             if info.qtype == 1:
                 return np.frombuffer(raw, dtype=np.float16).reshape(info.shape).astype(np.float32)
-            raise ValueError(f"{name}: oracle reads F32/F16 only")
+            if int(info.qtype) in BLOCK:  # quantised: the ggml block values
+                shp = tuple(int(v) for v in info.shape)
+                rows = int(np.prod(shp[:-1])) if len(shp) > 1 else 1
+                return dequant(int(info.qtype), np.asarray(raw), rows, shp[-1]).reshape(shp)
+            raise ValueError(f"{name}: oracle reads F32 / F16 / GGUF-block tensors only")
 
         def q(name: str, mats: bool) -> tuple:
             info = gguf.tensors[name]
@@ -204,7 +211,7 @@ class OracleLayer:
                    top_k=max(1, int(config.n_experts_used)), norm_topk=bool(config.norm_topk_prob),
                    router_w=rw, gate=q(f"{p}.ffn_gate_exps.weight", True),
                    up=q(f"{p}.ffn_up_exps.weight", True), down=q(f"{p}.ffn_down_exps.weight", True),
-                   router_bias=router_bias, **kw)
+                   router_bias=router_bias, act=1 if str(config.arch).startswith("gemma") else 0, **kw)
 
     def route(self, x: np.ndarray):
         logits = router_logits(x, self.router_w, self.router_bias)
@@ -231,14 +238,19 @@ class OracleLayer:
         keep = [self.gate, self.up, self.down, self.sh_gate, self.sh_up, self.sh_down]
         ws = [mk(t) for t in keep]
         sig = None if self.sh_inp_gate is None else np.ascontiguousarray(self.sh_inp_gate, np.float32)
-        rc = lib().or_moe_forward_tokens(H, self.n_experts, self.top_k, conv, *ws, _ptr(sig), _ptr(x),
+        rc = lib().or_moe_forward_tokens(H, self.n_experts, self.top_k, conv, self.act, *ws, _ptr(sig), _ptr(x),
                                          _ptr(idx), _ptr(w), _ptr(toks), len(toks), _ptr(out))
         _check(rc, "moe_forward_tokens")
         return out
 
 
+def gelu_tanh(g: float) -> float:
+    """The oracle's tanh-approximation GELU (or_gelu_tanh), in double."""
+    return float(lib().or_gelu_tanh(float(g)))
+
+
 def dense_forward(x: np.ndarray, gate: tuple, up: tuple, down: tuple,
-                  tokens: Optional[Sequence[int]] = None, conv: int = 0) -> np.ndarray:
+                  tokens: Optional[Sequence[int]] = None, conv: int = 0, act: int = 0) -> np.ndarray:
     """float64 output of a dense SwiGLU FFN (GGUFDenseMLP.forward, model.py:839-846) for
     `tokens`: the expert FFN of or_moe_forward_tokens applied as its shared expert to a
     layer with no routed experts.  gate / up / down: (qtype, rows, cols, GGUF bytes)."""
@@ -250,7 +262,7 @@ def dense_forward(x: np.ndarray, gate: tuple, up: tuple, down: tuple,
     keep = [gate, up, down]
     ws = [ctypes.pointer(_Weights(t[0], t[1], t[2], t[3].ctypes.data)) for t in keep]
     none = np.zeros(1, dtype=np.int32)
-    rc = lib().or_moe_forward_tokens(H, 0, 0, conv, None, None, None, *ws, None, _ptr(x), _ptr(none),
+    rc = lib().or_moe_forward_tokens(H, 0, 0, conv, act, None, None, None, *ws, None, _ptr(x), _ptr(none),
                                      _ptr(none.view(np.float32)), _ptr(toks), len(toks), _ptr(out))
     _check(rc, "moe_forward_tokens (dense)")
     return out

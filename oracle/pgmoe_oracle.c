@@ -314,6 +314,14 @@ static int64_t row_bytes(const or_weights* w) {
 
 static double silu_d(double g) { return g / (1.0 + exp(-g)); }
 
+/* GELU, tanh approximation (F.gelu(approximate="tanh"), the reference's use_gelu branch,
+ * quant_kernels.py:1471, kernel :752-756). */
+double or_gelu_tanh(double g) {
+    return 0.5 * g * (1.0 + tanh(0.7978845608028654 * (g + 0.044715 * g * g * g)));
+}
+
+static double act_d(int act, double g) { return act ? or_gelu_tanh(g) : silu_d(g); }
+
 /* y[t][n] = sum_k W[mat][n][k] * xin[t][k] for a set of T input vectors (double). */
 static int matvecs(const or_weights* w, int mat, int conv, const double* xin, int T, double* y) {
     float* row = (float*)malloc(sizeof(float) * (size_t)w->n_cols);
@@ -333,9 +341,10 @@ static int matvecs(const or_weights* w, int mat, int conv, const double* xin, in
     return 0;
 }
 
-/* SwiGLU expert on T inputs: out[t][:] = down(silu(gate x) * (up x)), all in double
+/* Gated expert on T inputs: out[t][:] = down(act(gate x) * (up x)), act = SiLU (0) or the
+ * tanh GELU (1), all in double
  * (the "fp32-intermediate" variant of model.py:916-919 with the fp16 casts removed). */
-static int expert_ffn(const or_weights* g, const or_weights* u, const or_weights* d, int mat, int conv,
+static int expert_ffn(const or_weights* g, const or_weights* u, const or_weights* d, int mat, int conv, int act,
                       const double* xin, int T, double* out) {
     int I = g->n_rows;
     double* gv = (double*)malloc(sizeof(double) * (size_t)T * I);
@@ -344,7 +353,7 @@ static int expert_ffn(const or_weights* g, const or_weights* u, const or_weights
     if (!gv || !uv) goto done;
     if ((rc = matvecs(g, mat, conv, xin, T, gv))) goto done;
     if ((rc = matvecs(u, mat, conv, xin, T, uv))) goto done;
-    for (int64_t i = 0; i < (int64_t)T * I; ++i) gv[i] = silu_d(gv[i]) * uv[i];
+    for (int64_t i = 0; i < (int64_t)T * I; ++i) gv[i] = act_d(act, gv[i]) * uv[i];
     rc = matvecs(d, mat, conv, gv, T, out);
 done:
     free(gv);
@@ -355,8 +364,9 @@ done:
 /* Full layer for a subset of tokens, given routing (idx, w) for all M tokens.
  * out[j][h] for tokens[j]; routed experts combined in ascending expert id
  * (model.py:911-922), then the sigmoid-gated shared expert added (model.py:924-935).
+ * act: the gate activation of every expert (0 SiLU, 1 GELU-tanh for gemma, model.py:868).
  * shared_* may be NULL.  Accumulation in double. */
-int or_moe_forward_tokens(int H, int E, int K, int conv,
+int or_moe_forward_tokens(int H, int E, int K, int conv, int act,
                           const or_weights* gate, const or_weights* up, const or_weights* down,
                           const or_weights* sh_gate, const or_weights* sh_up, const or_weights* sh_down,
                           const float* sh_inp_gate,
@@ -383,7 +393,7 @@ int or_moe_forward_tokens(int H, int E, int K, int conv,
                     ++T;
                 }
         if (!T) continue;
-        if ((rc = expert_ffn(gate, up, down, e, conv, xsel, T, tmp))) goto done;
+        if ((rc = expert_ffn(gate, up, down, e, conv, act, xsel, T, tmp))) goto done;
         for (int s = 0; s < T; ++s) {
             int j = sel[s] / K, k = sel[s] % K;
             double wk = (double)w[(int64_t)tokens[j] * K + k];
@@ -407,7 +417,7 @@ int or_moe_forward_tokens(int H, int E, int K, int conv,
         }
     }
     if (sh_gate && sh_up && sh_down) {
-        if ((rc = expert_ffn(sh_gate, sh_up, sh_down, 0, conv, xt, n_tokens, tmp))) goto done;
+        if ((rc = expert_ffn(sh_gate, sh_up, sh_down, 0, conv, act, xt, n_tokens, tmp))) goto done;
         for (int j = 0; j < n_tokens; ++j) {
             double gsc = 1.0;
             if (sh_inp_gate) {

@@ -9,7 +9,7 @@ its PyTorch CPU branch:
   fp16 rounding of sub-block scale products;
 * W4 / W8 matmul as chunked fp32 dequant (4096 rows) + fp32 ``F.linear``, result cast to
   the input dtype (quant_kernels.py:1276-1291, :1408-1420);
-* SwiGLU + dynamic row-scale with fp16 ``down_in`` (quant_kernels.py:1467-1475);
+* SwiGLU (GeGLU for gemma) + dynamic row-scale with fp16 ``down_in`` (quant_kernels.py:1467-1475);
 * the per-expert loop in ascending expert id with ``index_add_`` (model.py:898-937).
 
 ``faithful=True`` keeps the reference's fp16 casts (variant A: overflows to inf at
@@ -104,8 +104,9 @@ def w8_matmul(x: torch.Tensor, qw: torch.Tensor, sc: torch.Tensor) -> torch.Tens
     return out
 
 
-def act_rowscale(g: torch.Tensor, u: torch.Tensor, faithful: bool):
-    inter = F.silu(g.float()) * u.float()
+def act_rowscale(g: torch.Tensor, u: torch.Tensor, faithful: bool, use_gelu: bool = False):
+    act = F.gelu(g.float(), approximate="tanh") if use_gelu else F.silu(g.float())
+    inter = act * u.float()
     rs = (inter.abs().amax(dim=-1, keepdim=True) / 16384.0).clamp(min=1.0)
     down_in = inter / rs
     if faithful:
@@ -164,13 +165,13 @@ class PortMoE:
             xe = x2.index_select(0, tok).to(xe_dtype)
             g = self.gate(e, xe)
             u = self.up(e, xe)
-            din, rs = act_rowscale(g, u, faithful)
+            din, rs = act_rowscale(g, u, faithful, bool(L.act))
             d = self.down(e, din.to(xe_dtype)).float() * rs
             out.index_add_(0, tok, d * tw[tok, slot].unsqueeze(-1))
         if self.shared is not None:
             sg, su, sd = self.shared
             xs = x2.to(xe_dtype)
-            din, rs = act_rowscale(sg(0, xs), su(0, xs), faithful)
+            din, rs = act_rowscale(sg(0, xs), su(0, xs), faithful, bool(L.act))
             so = sd(0, din.to(xe_dtype)).float() * rs
             if self.sh_inp is not None:
                 so = so * torch.sigmoid(F.linear(x2.float(), self.sh_inp))

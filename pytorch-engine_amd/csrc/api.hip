@@ -164,6 +164,8 @@ static int check_layer(const pgmoe_layer* L, LayerMats* lm) {
     if (L->top_k < 1 || L->top_k > L->n_experts || L->top_k > 16)
         return fail(PGMOE_E_UNSUPPORTED, "top_k %d outside [1, min(E, 16)]", L->top_k);
     if (!L->router_w) return fail(PGMOE_E_INVALID, "NULL router weight");
+    if (L->act != PGMOE_ACT_SILU && L->act != PGMOE_ACT_GELU_TANH)
+        return fail(PGMOE_E_UNSUPPORTED, "activation %d (SiLU = 0, GELU-tanh = 1)", L->act);
     int rc;
     if ((rc = check_weights(&L->gate, "gate", &lm->gate)) || (rc = check_weights(&L->up, "up", &lm->up)) ||
         (rc = check_weights(&L->down, "down", &lm->down)) || (rc = check_pair(lm->gate, lm->up, "experts")))
@@ -215,6 +217,8 @@ static int check_dense(const pgmoe_dense* D, Mats* g, Mats* u, Mats* d) {
     if (!D) return fail(PGMOE_E_INVALID, "NULL dense layer");
     if (D->hidden <= 0 || D->hidden % 256 || D->hidden > 65536)
         return fail(PGMOE_E_UNSUPPORTED, "hidden size %d must be a positive multiple of 256 (<= 65536)", D->hidden);
+    if (D->act != PGMOE_ACT_SILU && D->act != PGMOE_ACT_GELU_TANH)
+        return fail(PGMOE_E_UNSUPPORTED, "activation %d (SiLU = 0, GELU-tanh = 1)", D->act);
     int rc;
     if ((rc = check_weights(&D->gate, "dense gate", g)) || (rc = check_weights(&D->up, "dense up", u)) ||
         (rc = check_weights(&D->down, "dense down", d)) || (rc = check_pair(*g, *u, "dense")))
@@ -252,7 +256,8 @@ int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, floa
 #define WS(T, f) reinterpret_cast<T*>(b + o.f)
     const hipStream_t st = as_stream(stream);
     if (M <= decode_tokens_max()) {  // gate/up + SwiGLU, then down straight into out
-        if ((rc = launch_dec_gateup_ident(g, u, x, nullptr, M, WS(float, inter), WS(float, isum), st))) return rc;
+        if ((rc = launch_dec_gateup_ident(g, u, x, nullptr, M, WS(float, inter), WS(float, isum), st, D->act)))
+            return rc;
         // the 8-row, 16-wave down blocks when the SwiGLU rows fit in LDS, else the per-expert one
         if (decode_fused_down(M, g.N))
             return launch_dec_down_combine(d, WS(float, inter), WS(float, isum), nullptr, M, 1, 1, nullptr, nullptr,
@@ -265,7 +270,8 @@ int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, floa
                                        st)))
         return rc;
     if ((rc = launch_gateup(g, u, x, M, 1, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
-                            WS(int32_t, nact), WS(int32_t, tile_off), 1, WS(float, inter), st, WS(float, raw))))
+                            WS(int32_t, nact), WS(int32_t, tile_off), 1, WS(float, inter), st, WS(float, raw),
+                            D->act)))
         return rc;
     // identity order: sorted pair p is token p, so the down rows are the output rows
     return launch_down(d, WS(float, inter), M, 1, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
@@ -413,13 +419,13 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
                                            sgw ? WS(float, s_logit) : nullptr, WS(uint64_t, rlog),
                                            WS(int32_t, status), L->has_shared ? WS(float, xsum) : nullptr, E,
                                            L->norm_topk, WS(int32_t, desc), flat, max_active, WS(float, inter),
-                                           WS(float, isum), st)))
+                                           WS(float, isum), st, L->act)))
             return rc;
         const float* shared = nullptr;
         const float* shared_logit = nullptr;
         if (L->has_shared) {
             if ((rc = launch_dec_gateup_ident(lm.sg, lm.su, x, WS(float, xsum), M, WS(float, s_inter),
-                                              WS(float, s_isum), st)))
+                                              WS(float, s_isum), st, L->act)))
                 return rc;
             if (decode_fused_down(M, lm.sd.K))
                 rc = launch_dec_down_combine(lm.sd, WS(float, s_inter), WS(float, s_isum), nullptr, M, 1, 1, nullptr,
@@ -447,7 +453,8 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
                               WS(int32_t, dcounts))))
         return rc;
     if ((rc = launch_gateup(lm.gate, lm.up, x, M, K, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
-                            WS(int32_t, nact), WS(int32_t, tile_off), mode, WS(float, inter), st, WS(float, raw))))
+                            WS(int32_t, nact), WS(int32_t, tile_off), mode, WS(float, inter), st, WS(float, raw),
+                            L->act)))
         return rc;
     if ((rc = launch_down(lm.down, WS(float, inter), M, K, WS(int32_t, offsets), WS(int32_t, perm),
                           WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), WS(float, w), mode,
@@ -462,7 +469,7 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
             return rc;
         if ((rc = launch_gateup(lm.sg, lm.su, x, M, 1, WS(int32_t, s_offsets), WS(int32_t, s_perm),
                                 WS(int32_t, s_active), WS(int32_t, s_nact), WS(int32_t, s_tile_off), mode,
-                                WS(float, s_inter), st, WS(float, raw))))
+                                WS(float, s_inter), st, WS(float, raw), L->act)))
             return rc;
         if ((rc = launch_down(lm.sd, WS(float, s_inter), M, 1, WS(int32_t, s_offsets), WS(int32_t, s_perm),
                               WS(int32_t, s_active), WS(int32_t, s_nact), WS(int32_t, s_tile_off), WS(float, s_w),

@@ -158,6 +158,14 @@ __device__ __forceinline__ void kscale(uint32_t D, uint32_t Mb, uint32_t MD, int
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+// GELU, tanh approximation: 0.5 g (1 + tanh(z)), z = sqrt(2/pi) (g + 0.044715 g^3), with
+// tanh(z) = 1 - 2 / (1 + e^(2z)) (saturates to +-1 for large |z|).
+__device__ __forceinline__ float gelu_tanh(float g) {
+    const float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    return 0.5f * g * (2.0f - 2.0f / (1.0f + expf(2.0f * z)));
+}
+// The gate activation PGMOE_ACT_* of a gated FFN.
+__device__ __forceinline__ float gate_act(int act, float g) { return act ? gelu_tanh(g) : silu(g); }
 
 // Direct global -> LDS copy (global_load_lds_dwordx4): lane l's 16 bytes at g land at
 // lds + 16 * l, so one wave fills 1 KB of LDS and holds no registers for the data.  `lds`

@@ -13,8 +13,9 @@ namespace pgmoe {
 
 int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
-                      int max_active, float* inter, float* isum, hipStream_t st) {
-    const DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, nullptr, M, g.n_mats, 0, {}};
+                      int max_active, float* inter, float* isum, hipStream_t st, int act) {
+    DecDisp dp{kDispatch, offsets, perm, active, n_active, nullptr, nullptr, nullptr, M, g.n_mats, 0, {}};
+    dp.act = act;
 #define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, topk, M, dp, RouterIn{}, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL
@@ -23,12 +24,13 @@ int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const flo
 int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
                              const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, int32_t* status,
                              float* xsum_out, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
-                             float* inter, float* isum, hipStream_t st) {
+                             float* inter, float* isum, hipStream_t st, int act) {
     if (M < 1 || M > kDecTM) return fail(PGMOE_E_INVALID, "routed decode handles 1..%d tokens", kDecTM);
     if (topk > 16 || E > 512 || M * topk > 128)
         return fail(PGMOE_E_UNSUPPORTED, "routed decode: top_k <= 16, E <= 512, M*top_k <= 128");
-    const DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, rlog, desc, status, M, E, norm,
-                     {flat.offsets, flat.perm, flat.inv, flat.active, flat.n_active, flat.w}};
+    DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, rlog, desc, status, M, E, norm,
+               {flat.offsets, flat.perm, flat.inv, flat.active, flat.n_active, flat.w}};
+    dp.act = act;
     const RouterIn rt{rw, bias, sgw, s_logit, xsum_out};
 #define CALL(QT) dec_gateup_q<QT>(g, u, x, nullptr, topk, M, dp, rt, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
@@ -46,8 +48,9 @@ int launch_dec_linear(const Mats& w, const uint16_t* x, int M, const float* bias
 }
 
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
-                            float* isum, hipStream_t st) {
-    const DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
+                            float* isum, hipStream_t st, int act) {
+    DecDisp dp{kIdent, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, M, 1, 0, {}};
+    dp.act = act;
 #define CALL(QT) dec_gateup_q<QT>(g, u, x, xsum, 1, M, dp, RouterIn{}, 1, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)
 #undef CALL

@@ -819,6 +819,7 @@ struct DecDisp {
     FlatRoute flat;       // kRoute: optional flat arrays, published by block (0, 0)
     const float* bias;    // kLinear: [N] added to the outputs, or null
     int out_f16;          // kLinear: outputs as fp16 (round to nearest even) instead of fp32
+    int act;              // gate activation PGMOE_ACT_* of the gate/up epilogue
 };
 
 // Router work folded into the routed gate/up launch: with R = ceil(rows / blocks) (1
@@ -1041,7 +1042,7 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
                 g += red[ww][t][rr];
                 u += red[ww + 1][t][rr];
             }
-            const float v = silu(g) * u;
+            const float v = gate_act(dp.act, g) * u;
             const int orow = blockIdx.x * RB + rr;
             if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
             if (isum) {

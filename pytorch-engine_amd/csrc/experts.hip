@@ -111,14 +111,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // --------------------------------------------------------------------------- launchers
 int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                   const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
-                  int mode, float* inter, hipStream_t st, float* raw) {
+                  int mode, float* inter, hipStream_t st, float* raw, int act) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
     if (mode == 0)
         return launch_dec_gateup(g, u, x, nullptr, topk, M, offsets, perm, active, n_active, (int)(P < E ? P : E),
-                                 inter, nullptr, st);
-    return launch_gemm_gateup(g, u, x, M, topk, offsets, perm, tile_off, inter, st, raw);
+                                 inter, nullptr, st, act);
+    return launch_gemm_gateup(g, u, x, M, topk, offsets, perm, tile_off, inter, st, raw, act);
 }
 
 int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_t* offsets, const int32_t* perm,

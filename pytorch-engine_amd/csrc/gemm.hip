@@ -134,6 +134,13 @@ __device__ __forceinline__ gh8 deq8(const uint32_t (&m)[4], float a, float c) {
 __device__ __forceinline__ float silu_fast(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
 }
+// GELU (tanh approximation) with the same hardware exp2 / reciprocal:
+// 0.5 g (1 + tanh(z)) = g - g / (1 + e^(2z)), z = sqrt(2/pi) (g + 0.044715 g^3).
+__device__ __forceinline__ float gelu_fast(float g) {
+    const float z = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    return g - g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(2.8853900817779268f * z));
+}
+__device__ __forceinline__ float act_fast(int act, float g) { return act ? gelu_fast(g) : silu_fast(g); }
 
 __device__ __forceinline__ void magic8(uint32_t lo, uint32_t hi, uint32_t (&m)[4]) {
     m[0] = __builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u);
@@ -334,7 +341,8 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     int N, int K, const uint16_t* __restrict__ act, int topk, int E, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm, const int32_t* __restrict__ tile_off, int n_ntiles,
     const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out,
-    const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1, int ksplit, int kper, float* __restrict__ raw) {
+    const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1, int ksplit, int kper, float* __restrict__ raw,
+    int gate_act) {
     using L = GLay<QT, CT, WM>;
     constexpr int NW = L::NW, WN = L::WN, RS = L::RS, WR = 32 * RS;  // WR rows per wave
     constexpr int CH = L::CH;
@@ -510,7 +518,8 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int r = WR * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                        if (r < mrows) out[(int64_t)(m0 + r) * N + col] = silu_fast(acc[i][j][v]) * acc[i][j + CT / 2][v];
+                        if (r < mrows)
+                            out[(int64_t)(m0 + r) * N + col] = act_fast(gate_act, acc[i][j][v]) * acc[i][j + CT / 2][v];
                     }
             }
         }
@@ -544,7 +553,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
                                                                 int N, const float* __restrict__ rs,
                                                                 const float* __restrict__ topk_w,
                                                                 const int32_t* __restrict__ perm,
-                                                                float* __restrict__ out) {
+                                                                float* __restrict__ out, int act) {
     const int64_t n = P * N;
     const int NC = GATEUP ? 2 * N : N;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
@@ -556,7 +565,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
             a = a + r[(int64_t)k * P * NC];
             if (GATEUP) b = b + r[(int64_t)k * P * NC + N];
         }
-        out[i] = GATEUP ? silu_fast(a) * b : (rs[p] * topk_w[perm[p]]) * a;
+        out[i] = GATEUP ? act_fast(act, a) * b : (rs[p] * topk_w[perm[p]]) * a;
     }
 }
 
@@ -603,13 +612,15 @@ size_t gemm_split_bytes(int64_t P, int E, int N, int K, bool gateup) {
 }
 
 static int launch_split_reduce(bool gateup, const float* raw, int S, int64_t P, int N, const float* rs,
-                               const float* topk_w, const int32_t* perm, float* out, hipStream_t st) {
+                               const float* topk_w, const int32_t* perm, float* out, hipStream_t st, int act) {
     const int64_t n = P * N;
     const int blocks = (int)(div_up(n, 256) < 16384 ? div_up(n, 256) : 16384);
     if (gateup)
-        PG_LAUNCH(gemm_split_reduce_kernel<true>, dim3(blocks), dim3(256), 0, st, raw, S, P, N, rs, topk_w, perm, out);
+        PG_LAUNCH(gemm_split_reduce_kernel<true>, dim3(blocks), dim3(256), 0, st, raw, S, P, N, rs, topk_w, perm, out,
+                  act);
     else
-        PG_LAUNCH(gemm_split_reduce_kernel<false>, dim3(blocks), dim3(256), 0, st, raw, S, P, N, rs, topk_w, perm, out);
+        PG_LAUNCH(gemm_split_reduce_kernel<false>, dim3(blocks), dim3(256), 0, st, raw, S, P, N, rs, topk_w, perm, out,
+                  act);
     return check_launch("gemm split reduce");
 }
 
@@ -638,7 +649,8 @@ static int gemm_max_mtiles(int64_t P, int E) {
 }
 
 int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
-                       const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st, float* raw) {
+                       const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st, float* raw,
+                       int act) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
@@ -650,7 +662,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
 #define PG_GU(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, true, PG_GU_CT, PG_GU_WM>), grid, dim3(64 * GLay<QT, PG_GU_CT, PG_GU_WM>::NW), 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
               E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter, g.scales, u.scales, \
-              sp.ksplit, sp.kper, raw)
+              sp.ksplit, sp.kper, raw, act)
     switch (g.qtype) {
     case PGMOE_Q4_K: PG_GU(PGMOE_Q4_K); break;
     case PGMOE_Q6_K: PG_GU(PGMOE_Q6_K); break;
@@ -660,7 +672,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
 #undef PG_GU
     int rc = check_launch("gemm_gateup");
     if (rc || sp.ksplit == 1) return rc;
-    return launch_split_reduce(true, raw, sp.ksplit, P, g.N, nullptr, nullptr, nullptr, inter, st);
+    return launch_split_reduce(true, raw, sp.ksplit, P, g.N, nullptr, nullptr, nullptr, inter, st, act);
 }
 
 int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M, int topk, const int32_t* offsets,
@@ -676,7 +688,8 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     const dim3 grid(gemm_max_mtiles(P, E) * nnt * sp.ksplit);
 #define PG_DN(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, false, PG_DN_CT, PG_DN_WM>), grid, dim3(64 * GLay<QT, PG_DN_CT, PG_DN_WM>::NW), 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
-              topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial, d.scales, d.scales, sp.ksplit, sp.kper, raw)
+              topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial, d.scales, d.scales, sp.ksplit, sp.kper, raw, \
+              PGMOE_ACT_SILU)
     switch (d.qtype) {
     case PGMOE_Q4_K: PG_DN(PGMOE_Q4_K); break;
     case PGMOE_Q6_K: PG_DN(PGMOE_Q6_K); break;
@@ -686,7 +699,7 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
 #undef PG_DN
     int rc = check_launch("gemm_down");
     if (rc || sp.ksplit == 1) return rc;
-    return launch_split_reduce(false, raw, sp.ksplit, P, d.N, rs, topk_w, perm, partial, st);
+    return launch_split_reduce(false, raw, sp.ksplit, P, d.N, rs, topk_w, perm, partial, st, PGMOE_ACT_SILU);
 }
 
 }  // namespace pgmoe

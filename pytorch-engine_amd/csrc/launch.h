@@ -54,7 +54,7 @@ int launch_identity_dispatch(int M, int tile_rows, int32_t* offsets, int32_t* pe
                              int32_t* active, int32_t* n_active, int32_t* tile_off, float* w, hipStream_t st);
 int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                   const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
-                  int mode, float* inter, hipStream_t st, float* raw = nullptr);
+                  int mode, float* inter, hipStream_t st, float* raw = nullptr, int act = PGMOE_ACT_SILU);
 int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_t* offsets, const int32_t* perm,
                 const int32_t* active, const int32_t* n_active, const int32_t* tile_off, const float* topk_w,
                 int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st, float* raw = nullptr);
@@ -67,7 +67,7 @@ int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows,
 // Decode expert stages (M <= decode_tokens_max()).
 int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
-                      int max_active, float* inter, float* isum, hipStream_t st);
+                      int max_active, float* inter, float* isum, hipStream_t st, int act = PGMOE_ACT_SILU);
 int launch_dec_down(const Mats& d, const float* inter, const float* isum, int M, const int32_t* offsets,
                     const int32_t* perm, const int32_t* active, const int32_t* n_active, int max_active,
                     const float* topk_w, float* partial, hipStream_t st);
@@ -85,7 +85,7 @@ struct DecFlat {
 int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
                              const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, int32_t* status,
                              float* xsum_out, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
-                             float* inter, float* isum, hipStream_t st);
+                             float* inter, float* isum, hipStream_t st, int act = PGMOE_ACT_SILU);
 // Routing a forward produced, read back from its workspace in sorted pair order (decode:
 // from the descriptor at desc; prefill: from the flat arrays).  offsets [E+1]; pair_*[P].
 int launch_route_readback(int decode, const int32_t* desc, const int32_t* idx, const float* w,
@@ -105,7 +105,7 @@ int launch_linear(const Mats& w, const float* bias, const uint16_t* x, int M, vo
 // Rows rows[0..n) of w decoded to out [n, K] (fp32, or fp16 with out_f16).
 int launch_dequant_rows(const Mats& w, const int32_t* rows, int n, void* out, int out_f16, hipStream_t st);
 int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int M, float* inter,
-                            float* isum, hipStream_t st);
+                            float* isum, hipStream_t st, int act = PGMOE_ACT_SILU);
 int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st);
 // clear (may be null): n_clear words the kernel sets to zero (the decode router's tagged logits).
 // desc null: the identity (matrix 0 applied to every token with weight 1; P = M, K = 1).
@@ -122,7 +122,7 @@ bool decode_fused_down(int P, int K);
 // not fill the chip; null runs the product unsplit.
 int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                        const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st,
-                       float* raw = nullptr);
+                       float* raw = nullptr, int act = PGMOE_ACT_SILU);
 int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M, int topk, const int32_t* offsets,
                      const int32_t* perm, const int32_t* tile_off, const float* topk_w, float* partial,
                      hipStream_t st, float* raw = nullptr);

@@ -51,6 +51,7 @@ class Layer(ctypes.Structure):
         ("sh_up", Weights),
         ("sh_down", Weights),
         ("sh_inp_gate", _P),
+        ("act", _I32),
     ]
 
 
@@ -60,6 +61,7 @@ class Dense(ctypes.Structure):
         ("gate", Weights),
         ("up", Weights),
         ("down", Weights),
+        ("act", _I32),
     ]
 
 
@@ -144,3 +146,4 @@ EXPORTS = (
 )
 
 STATUS_SPIN_TIMEOUT = 1  # PGMOE_STATUS_SPIN_TIMEOUT
+ACT_SILU, ACT_GELU_TANH = 0, 1  # PGMOE_ACT_*

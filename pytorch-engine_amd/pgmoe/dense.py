@@ -9,8 +9,8 @@ with prefix ``blk.{layer_idx}`` or ``prefix_override``, and computes
 ``forward(x) -> fp32`` = down(silu(gate x) * (up x)) (model.py:839-846) with the same HIP
 kernels as the MoE experts: the weights stay in the 64-row tile layout of their GGUF
 bits, and one C-ABI call (pgmoe_dense_forward) enqueues the gate/up + SwiGLU and down
-products without a host sync.  The reference's GeGLU variant (gemma) has no kernel and
-raises NotImplementedError, as HipSparseMoEMLP does.
+products without a host sync.  gemma architectures take the reference's GeGLU (the
+tanh-approximation GELU in place of SiLU), as HipSparseMoEMLP does.
 """
 
 from __future__ import annotations
@@ -20,7 +20,7 @@ from typing import Any, Optional
 import torch
 import torch.nn as nn
 
-from ._lib import Dense, check, lib
+from ._lib import ACT_GELU_TANH, ACT_SILU, Dense, check, lib
 from .moe import _ExpertTensor, _load_lock
 from .workspace import WorkspacePool
 
@@ -38,9 +38,7 @@ class HipDenseMLP(nn.Module):
             device = torch.device("cuda", torch.cuda.current_device())
         lib()  # fail now, not at the first forward, when the HIP library is missing
         self.device = device
-        self.use_gelu = str(config.arch).startswith("gemma")
-        if self.use_gelu:
-            raise NotImplementedError("GeGLU FFNs (gemma) are not implemented by the HIP kernels")
+        self.use_gelu = str(config.arch).startswith("gemma")  # GeGLU (model.py:800)
         prefix = prefix_override or f"blk.{layer_idx}"
         with _load_lock, torch.cuda.device(device):
             self.gate_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate.weight", device, False)
@@ -67,6 +65,7 @@ class HipDenseMLP(nn.Module):
         D.gate = self.gate_proj.weights()
         D.up = self.up_proj.weights()
         D.down = self.down_proj.weights()
+        D.act = ACT_GELU_TANH if self.use_gelu else ACT_SILU
         return D
 
     def workspace_bytes(self, M: int) -> int:

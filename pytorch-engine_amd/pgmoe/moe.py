@@ -25,7 +25,7 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from ._lib import STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES, Layer, Weights, check, lib
+from ._lib import ACT_GELU_TANH, ACT_SILU, STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES, Layer, Weights, check, lib
 from .workspace import WorkspacePool
 
 _F32, _F16, _BF16 = 0, 1, 30
@@ -33,17 +33,27 @@ _load_lock = threading.Lock()
 
 
 def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.Tensor:
-    """fp32 copy of an unquantised tensor on ``device`` (quant_kernels.py:1097-1116 for
-    F32 / F16 / BF16; quantised router weights are not supported here)."""
+    """fp32 copy of a router / gate / norm tensor on ``device`` (quant_kernels.py:1095-1114):
+    F32 / F16 / BF16 converted, and quantised ones (Q4_K, Q6_K, Q8_0, Q4_0, Q5_0; the
+    reference's gguf.quants.dequantize branch) dequantised once on the device to the values
+    the ggml block definitions give.  CPU targets take the float types only."""
     info = gguf_file.tensors[name]
     raw = gguf_file.get_tensor_bytes(name)
+    shape = tuple(int(s) for s in info.shape)
     if info.qtype == _F32:
-        arr = torch.from_numpy(np.frombuffer(raw, dtype=np.float32).reshape(info.shape).copy())
+        arr = torch.from_numpy(np.frombuffer(raw, dtype=np.float32).reshape(shape).copy())
     elif info.qtype == _F16:
-        arr = torch.from_numpy(np.frombuffer(raw, dtype=np.float16).reshape(info.shape).copy()).float()
+        arr = torch.from_numpy(np.frombuffer(raw, dtype=np.float16).reshape(shape).copy()).float()
     elif info.qtype == _BF16:
-        u16 = np.frombuffer(raw, dtype=np.uint16).reshape(info.shape).copy()
+        u16 = np.frombuffer(raw, dtype=np.uint16).reshape(shape).copy()
         arr = torch.from_numpy(u16.view(np.int16)).view(torch.bfloat16).float()
+    elif int(info.qtype) in SUPPORTED_QTYPES and torch.device(device).type == "cuda":
+        cols = shape[-1]
+        rows = int(np.prod(shape[:-1])) if len(shape) > 1 else 1
+        if cols % 256:
+            raise NotImplementedError(f"{name}: quantised rows of {cols} weights (a multiple of 256 is needed)")
+        src = torch.from_numpy(np.ascontiguousarray(np.asarray(raw)).view(np.uint8)).to(device)
+        return ops.dequant_matrix(int(info.qtype), src, rows, cols).reshape(shape).contiguous()
     else:
         raise NotImplementedError(f"{name}: router/gate tensors of ggml type {info.qtype} are not supported")
     return arr.to(device=device, dtype=torch.float32).contiguous()
@@ -100,9 +110,7 @@ class HipSparseMoEMLP(nn.Module):
         self.n_experts = int(config.n_experts)
         self.top_k = max(1, int(config.n_experts_used))
         self.norm_topk_prob = bool(config.norm_topk_prob)
-        self.use_gelu = str(config.arch).startswith("gemma")
-        if self.use_gelu:
-            raise NotImplementedError("GeGLU experts (gemma) are not implemented by the HIP kernels")
+        self.use_gelu = str(config.arch).startswith("gemma")  # GeGLU experts (model.py:868)
 
         prefix = f"blk.{layer_idx}"
         with _load_lock, torch.cuda.device(device):
@@ -144,6 +152,7 @@ class HipSparseMoEMLP(nn.Module):
         L.n_experts = self.n_experts
         L.top_k = self.top_k
         L.norm_topk = int(self.norm_topk_prob)
+        L.act = ACT_GELU_TANH if self.use_gelu else ACT_SILU
         L.router_w = self.router_weight.data_ptr()
         L.router_bias = self.router_bias.data_ptr() if self.router_bias is not None else None
         L.gate = self.gate_exps.weights()

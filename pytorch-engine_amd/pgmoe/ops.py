@@ -88,6 +88,27 @@ def make_weights(qtype: int, buf: torch.Tensor, n_mats: int, rows: int, cols: in
                    plane.data_ptr() if plane is not None else None)
 
 
+def dequant_rows(w: Weights, rows: torch.Tensor, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Rows `rows` (int32 device tensor) of the one-matrix weights `w`, dequantised on the device
+    (pgmoe_dequant_rows): [len(rows), K] fp32 or fp16."""
+    dev = _need_cuda(rows)
+    code = {torch.float32: 0, torch.float16: 1}[out_dtype]
+    out = torch.empty((rows.numel(), w.n_cols), dtype=out_dtype, device=dev)
+    if rows.numel():
+        check(lib().pgmoe_dequant_rows(w, rows.data_ptr(), rows.numel(), out.data_ptr(), code, _stream(dev)),
+              "pgmoe_dequant_rows")
+    return out
+
+
+def dequant_matrix(qtype: int, raw: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """A whole GGUF matrix (raw bytes on the device) dequantised to fp32 [rows, cols] on the
+    device: relaid out, then every row decoded."""
+    buf = relayout(qtype, raw, 1, rows, cols)
+    w = make_weights(device_qtype(qtype), buf, 1, rows, cols)
+    ids = torch.arange(rows, dtype=torch.int32, device=raw.device)
+    return dequant_rows(w, ids)
+
+
 def router_topk(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], k: int, norm: bool
                 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     dev = _need_cuda(x, w, bias)

@@ -107,5 +107,4 @@ def test_dense_zero_tokens_and_contract_errors():
     with pytest.raises(ValueError):
         mod(torch.zeros((2, lay.spec.hidden + 256), dtype=torch.float16, device="cuda:0"))
     gem = SyntheticDense(DenseSpec("g", 256, 512, DENSE_CONFIGS["dense_tiny"].qtypes, arch="gemma2"))
-    with pytest.raises(NotImplementedError):
-        HipDenseMLP(gem.gguf, gem.config, 0, torch.device("cuda", 0))
+    assert HipDenseMLP(gem.gguf, gem.config, 0, torch.device("cuda", 0)).use_gelu  # GeGLU (model.py:800)

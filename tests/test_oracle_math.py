@@ -221,3 +221,22 @@ def test_layer_zero_input_and_weight_linearity():
     # a token subset gives the same rows as the full pass
     ys = L.forward_tokens(x, idx, w, tokens=[3, 1])
     np.testing.assert_allclose(ys, y1[[3, 1]], rtol=0, atol=0)
+
+
+def test_gelu_tanh_matches_torch_and_kernel_identity():
+    """or_gelu_tanh against torch's F.gelu(approximate="tanh") (the reference's CPU branch,
+    quant_kernels.py:1471) in float64, and the identity the kernels evaluate,
+    0.5 g (1 + tanh z) = g - g / (1 + e^(2z)), on the same points (large |g| included)."""
+    import torch
+    import torch.nn.functional as F
+    g = np.concatenate([np.linspace(-12, 12, 241), [-80.0, -30.0, 0.0, 1e-6, 30.0, 80.0]])
+    ours = np.array([oracle.gelu_tanh(v) for v in g])
+    ref = F.gelu(torch.from_numpy(g), approximate="tanh").numpy()
+    np.testing.assert_allclose(ours, ref, rtol=1e-12, atol=1e-15)
+    z = 0.7978845608028654 * (g + 0.044715 * g ** 3)
+    with np.errstate(over="ignore"):
+        kern = g - g / (1.0 + np.exp(2.0 * z))
+    np.testing.assert_allclose(kern, ref, rtol=1e-12, atol=1e-12)
+    # a plausible slip (the exact erf GELU) is caught by the same check
+    exact = F.gelu(torch.from_numpy(g)).numpy()
+    assert not np.allclose(exact, ref, rtol=1e-6, atol=1e-9)
