@@ -21,6 +21,11 @@
  * base + (rg * K/256 + b) * CH * 1024 holds CH 16-byte chunks per row, chunk-major:
  * chunk c of row r at + c*1024 + r*16.  Chunk contents (same bits as the GGUF block):
  *   Q4_K (type 12, CH 9):  c0 = d, dmin, 12 scale bytes;  c1..c8 = qs[16(c-1) .. +16]
+ *   Q5_K (type 13, CH 11): c0..c8 as Q4_K (the GGUF block's bytes 0-15 and 48-175);
+ *                          c9, c10 = the 256 fifth bits (qh, bytes 16-47) regrouped per
+ *                          64-weight quarter p: 8 bytes at chunk 9 + (p >> 1), byte 8(p & 1),
+ *                          as two 32-bit words t = 0, 1 whose bit 8(l & 3) + (l >> 2) is
+ *                          the fifth bit of element 64p + 32t + l (GGUF: bit 2p + t of qh[l])
  *   Q6_K (type 14, CH 13): c0..c7 = ql[16c ..];  c8..c11 = qh[16(c-8) ..];  c12 = the 16
  *                          int8 scales; the fp16 d in a plane after all tiles:
  *                          d(rg, b, r) at base + ceil(N/64)*(K/256)*13*1024
@@ -34,7 +39,7 @@
  * chunk per (64-row group rg, super-block b, 64-weight unit c = 0..3), matrices
  * pgmoe_scale_plane_bytes() apart: row r of chunk (rg, b, c) at
  * scales + ((rg*(K/256) + b)*4 + c)*1024 + r*16 holds four floats
- *   Q4_K: {a0, c0, a1, c1} of sub-blocks 2c + t: a = d*sc, c = -(dmin*m) - 1024*a
+ *   Q4_K, Q5_K: {a0, c0, a1, c1} of sub-blocks 2c + t: a = d*sc, c = -(dmin*m) - 1024*a
  *   Q6_K: {a0, a1, a2, a3}: a_g = d * scale[8*(c >> 1) + 2g + (c & 1)]
  * (the values a lane computes from the chunk bytes otherwise).  pgmoe_build_scale_plane()
  * writes it from the device layout.
@@ -61,6 +66,7 @@ extern "C" {
 #define PGMOE_Q5_0 6  /* source format only: relaid out as PGMOE_Q8_0 (exact values) */
 #define PGMOE_Q8_0 8
 #define PGMOE_Q4_K 12
+#define PGMOE_Q5_K 13
 #define PGMOE_Q6_K 14
 
 /* Gate activation of the gated FFNs: act(gate) * up (exec_fused_act_mul_rowscale,
@@ -71,7 +77,7 @@ extern "C" {
 #define PGMOE_ACT_GELU_TANH 1
 
 typedef struct pgmoe_weights {
-    int32_t qtype;      /* PGMOE_Q4_K / PGMOE_Q6_K / PGMOE_Q8_0 */
+    int32_t qtype;      /* PGMOE_Q4_K / PGMOE_Q5_K / PGMOE_Q6_K / PGMOE_Q8_0 */
     int32_t n_rows;     /* N: output features per matrix */
     int32_t n_cols;     /* K: input features (multiple of 256 for K-quants, 64 for Q8_0) */
     int32_t n_mats;     /* experts (1 for a shared expert) */

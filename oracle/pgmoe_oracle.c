@@ -9,7 +9,10 @@
  *
  * Parity pins (see tests/test_oracle_*.py):
  *   or_dequant_rows      golden vectors written by the reference's own repack
- *                        (quant_kernels.py:854-1036) + closed-form special cases
+ *                        (quant_kernels.py:854-1036) + closed-form special cases;
+ *                        Q5_K: equals Q4_K on the same header/qs with qh = 0, one
+ *                        qh bit adds exactly 16*d*sc at its element, and the numpy
+ *                        restatement of the reference's Q5_K repack (torch_port)
  *   or_router_logits     textbook dot product (checked against float64 numpy to
  *                        fp32 rounding), fixed reduction order mirrored by the
  *                        GPU router kernel bit for bit
@@ -27,6 +30,7 @@
 #define QT_Q5_0 6
 #define QT_Q8_0 8
 #define QT_Q4_K 12
+#define QT_Q5_K 13
 #define QT_Q6_K 14
 
 /* ---------------- IEEE half <-> float (exact / round-to-nearest-even) ---------- */
@@ -122,6 +126,28 @@ static void decode_q4k_block(const uint8_t* b, int conv, float* out) {
     }
 }
 
+/* Q5_K: [d f16][dmin f16][12 scale bytes][qh 32][qs 128]; element n = 32s + l of
+ * sub-block s = 2c + t: q = ((qs[32c + l] >> 4t) & 15) | (((qh[l] >> s) & 1) << 4), value
+ * (d*sc_s) q - dmin*m_s (ggml dequantize_row_q5_K; the reference's W8 repack of Q5_K,
+ * quant_kernels.py:984-1004, with conv = 1: both products rounded to fp16). */
+static void decode_q5k_block(const uint8_t* b, int conv, float* out) {
+    float d = or_half_to_float(rd16(b));
+    float dmin = or_half_to_float(rd16(b + 2));
+    const uint8_t* qh = b + 16;
+    const uint8_t* qs = b + 48;
+    for (int s = 0; s < 8; ++s) {
+        int sc, m;
+        q4k_scale_min(b + 4, s, &sc, &m);
+        float a = d * (float)sc, z = dmin * (float)m;
+        if (conv) { a = rnd16(a); z = rnd16(z); }
+        int c = s >> 1, hi = s & 1;
+        for (int l = 0; l < 32; ++l) {
+            int q = ((qs[32 * c + l] >> (4 * hi)) & 0xF) | (((qh[l] >> s) & 1) << 4);
+            out[32 * s + l] = a * (float)q - z;
+        }
+    }
+}
+
 /* Q6_K: [ql 128][qh 64][sc int8 16][d f16]; element n = 128h + 32s + l
  * (quant_kernels.py:968-982). */
 static void decode_q6k_block(const uint8_t* b, int conv, float* out) {
@@ -176,6 +202,7 @@ int or_block_geometry(int qtype, int* per_block, int* block_bytes) {
     case QT_Q4_0: *per_block = 32; *block_bytes = 18; return 0;
     case QT_Q5_0: *per_block = 32; *block_bytes = 22; return 0;
     case QT_Q4_K: *per_block = 256; *block_bytes = 144; return 0;
+    case QT_Q5_K: *per_block = 256; *block_bytes = 176; return 0;
     case QT_Q6_K: *per_block = 256; *block_bytes = 210; return 0;
     case QT_Q8_0: *per_block = 32; *block_bytes = 34; return 0;
     default: return -1;
@@ -191,6 +218,7 @@ int or_dequant_rows(int qtype, int conv, const uint8_t* blocks, int64_t rows, in
         const uint8_t* b = blocks + i * bb;
         float* o = out + i * pb;
         if (qtype == QT_Q4_K) decode_q4k_block(b, conv, o);
+        else if (qtype == QT_Q5_K) decode_q5k_block(b, conv, o);
         else if (qtype == QT_Q6_K) decode_q6k_block(b, conv, o);
         else if (qtype == QT_Q4_0) decode_q4_0_block(b, o);
         else if (qtype == QT_Q5_0) decode_q5_0_block(b, o);

@@ -5,8 +5,8 @@ It reproduces what ``GGUFSparseMoEMLP.forward`` does when every ``exec_*`` helpe
 its PyTorch CPU branch:
 
 * load-time repack of GGUF blocks into the reference's W4 / W8 structure-of-arrays
-  (quant_kernels.py:854-904 for Q4_K -> W4, :945-982 for Q8_0 / Q6_K -> W8), with the
-  fp16 rounding of sub-block scale products;
+  (quant_kernels.py:854-904 for Q4_K -> W4, :945-1004 for Q8_0 / Q6_K / Q5_K -> W8), with
+  the fp16 rounding of sub-block scale products;
 * W4 / W8 matmul as chunked fp32 dequant (4096 rows) + fp32 ``F.linear``, result cast to
   the input dtype (quant_kernels.py:1276-1291, :1408-1420);
 * SwiGLU (GeGLU for gemma) + dynamic row-scale with fp16 ``down_in`` (quant_kernels.py:1467-1475);
@@ -25,7 +25,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from . import OracleLayer, Q4_K, Q6_K, Q8_0
+from . import OracleLayer, Q4_K, Q5_K, Q6_K, Q8_0
 
 
 def _k_scales(s12: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
@@ -55,7 +55,9 @@ def repack_w4(raw: np.ndarray, qtype: int, rows: int, cols: int):
 
 
 def repack_w8(raw: np.ndarray, qtype: int, rows: int, cols: int):
-    """Q8_0 / Q6_K blocks -> (qweight i8 [rows, cols], scales f16 [rows, cols/16])."""
+    """Q8_0 / Q6_K / Q5_K blocks -> (qweight i8 [rows, cols], scales f16 [rows, cols/16],
+    zeros f16 [rows, cols/16] or None)."""
+    zeros = None
     if qtype == Q8_0:
         blk = raw.reshape(-1, 34)
         d = blk[:, 0:2].copy().view(np.float16)  # [nb, 1]
@@ -73,9 +75,22 @@ def repack_w8(raw: np.ndarray, qtype: int, rows: int, cols: int):
         sc = blk[:, 192:208].copy().view(np.int8).astype(np.float32)
         d = blk[:, 208:210].copy().view(np.float16).astype(np.float32)
         scales = (d * sc).astype(np.float16).reshape(rows, cols // 16)
+    elif qtype == Q5_K:  # quant_kernels.py:984-1004: 5-bit codes 0..31, scale and zero per 32
+        blk = raw.reshape(-1, 176)
+        nb = blk.shape[0]
+        d = blk[:, 0:4].copy().view(np.float16).astype(np.float32)  # [nb, 2] = (d, dmin)
+        sc, mn = _k_scales(blk[:, 4:16])
+        qh = blk[:, 16:48].reshape(nb, 1, 32)
+        qs = blk[:, 48:176].reshape(nb, 4, 32)
+        lo = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 8, 32)  # sub-block 2c + nibble
+        hi = (qh >> np.arange(8, dtype=np.uint8).reshape(1, 8, 1)) & 1  # sub-block s: bit s
+        q = (lo | (hi << 4)).astype(np.int8).reshape(rows, cols)
+        scales = np.repeat((d[:, 0:1] * sc).astype(np.float16), 2, axis=1).reshape(rows, cols // 16)
+        zeros = np.repeat((d[:, 1:2] * mn).astype(np.float16), 2, axis=1).reshape(rows, cols // 16)
+        zeros = torch.from_numpy(np.ascontiguousarray(zeros))
     else:
-        raise ValueError("W8 repack restated for Q8_0 / Q6_K only")
-    return torch.from_numpy(np.ascontiguousarray(q)), torch.from_numpy(np.ascontiguousarray(scales))
+        raise ValueError("W8 repack restated for Q8_0 / Q6_K / Q5_K only")
+    return torch.from_numpy(np.ascontiguousarray(q)), torch.from_numpy(np.ascontiguousarray(scales)), zeros
 
 
 def w4_matmul(x: torch.Tensor, qw: torch.Tensor, sc: torch.Tensor, zr: torch.Tensor) -> torch.Tensor:
@@ -92,7 +107,7 @@ def w4_matmul(x: torch.Tensor, qw: torch.Tensor, sc: torch.Tensor, zr: torch.Ten
     return out
 
 
-def w8_matmul(x: torch.Tensor, qw: torch.Tensor, sc: torch.Tensor) -> torch.Tensor:
+def w8_matmul(x: torch.Tensor, qw: torch.Tensor, sc: torch.Tensor, zr: Optional[torch.Tensor] = None) -> torch.Tensor:
     M, K = x.shape
     N = qw.shape[0]
     xf = x.float()
@@ -100,6 +115,8 @@ def w8_matmul(x: torch.Tensor, qw: torch.Tensor, sc: torch.Tensor) -> torch.Tens
     for r0 in range(0, N, 4096):
         r1 = min(N, r0 + 4096)
         w = qw[r0:r1].float().view(r1 - r0, K // 16, 16) * sc[r0:r1].float().unsqueeze(-1)
+        if zr is not None:
+            w = w - zr[r0:r1].float().unsqueeze(-1)
         out[:, r0:r1] = F.linear(xf, w.reshape(r1 - r0, K)).to(x.dtype)
     return out
 
@@ -125,13 +142,14 @@ class _Proj:
             qw, sc, zr = repack_w4(raw, qtype, rows, k)
             self.w = (qw.view(n_mats, n, k // 2), sc.view(n_mats, n, k // 32), zr.view(n_mats, n, k // 32))
         else:
-            qw, sc = repack_w8(raw, qtype, rows, k)
-            self.w = (qw.view(n_mats, n, k), sc.view(n_mats, n, k // 16))
+            qw, sc, zr = repack_w8(raw, qtype, rows, k)
+            self.w = (qw.view(n_mats, n, k), sc.view(n_mats, n, k // 16),
+                      None if zr is None else zr.view(n_mats, n, k // 16))
 
     def __call__(self, mat: int, x: torch.Tensor) -> torch.Tensor:
         if self.qtype == Q4_K:
             return w4_matmul(x, self.w[0][mat], self.w[1][mat], self.w[2][mat])
-        return w8_matmul(x, self.w[0][mat], self.w[1][mat])
+        return w8_matmul(x, self.w[0][mat], self.w[1][mat], None if self.w[2] is None else self.w[2][mat])
 
 
 class PortMoE:
@@ -194,5 +212,8 @@ def dense_weights(t: tuple, mat: int = 0, n_mats: Optional[int] = None) -> np.nd
         pk = qw.view(n, k // 32, 16)
         q = torch.cat([(pk & 15).float(), ((pk >> 4) & 15).float()], dim=-1)
         return (q * sc.float().unsqueeze(-1) - zr.float().unsqueeze(-1)).reshape(n, k).numpy()
-    qw, sc = (a[mat] for a in p.w)
-    return (qw.float().view(p.n, p.k // 16, 16) * sc.float().unsqueeze(-1)).reshape(p.n, p.k).numpy()
+    qw, sc = p.w[0][mat], p.w[1][mat]
+    w = qw.float().view(p.n, p.k // 16, 16) * sc.float().unsqueeze(-1)
+    if p.w[2] is not None:
+        w = w - p.w[2][mat].float().unsqueeze(-1)
+    return w.reshape(p.n, p.k).numpy()

@@ -262,6 +262,10 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
 // so the 64 lanes of a wavefront reading chunk c of 64 consecutive rows touch 1 KB of
 // contiguous memory.  Chunk contents (same bits as the GGUF block):
 //   Q4_K (CH 9):  c0 = d, dmin, 12 scale bytes;  c1..c8 = qs[16(c-1) .. +16]
+//   Q5_K (CH 11): c0..c8 as Q4_K;  c9, c10 = the fifth bits per 64-weight quarter p:
+//                 word t (t = 0, 1) at chunk 9 + (p >> 1), byte 8(p & 1) + 4t, bit
+//                 8(l & 3) + (l >> 2) = fifth bit of element 64p + 32t + l (GGUF: bit
+//                 2p + t of qh[l]); (w >> k) & 0x01010101 gives elements 4k .. 4k+3
 //   Q6_K (CH 13): c0..c7 = ql[16c ..];  c8..c11 = qh[16(c-8) ..];  c12 = sc[16];
 //                 fp16 d in a plane after all tiles: d(rg, b, r) at
 //                 base + ng*nb*13*1024 + ((rg*nb + b)*64 + r)*2
@@ -270,6 +274,7 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
 // N is padded to a multiple of 64 (padding rows are zero and never stored to outputs).
 template <int QT> struct Tile;
 template <> struct Tile<PGMOE_Q4_K> { static constexpr int CH = 9; };
+template <> struct Tile<PGMOE_Q5_K> { static constexpr int CH = 11; };
 template <> struct Tile<PGMOE_Q6_K> { static constexpr int CH = 13; };
 template <> struct Tile<PGMOE_Q8_0> { static constexpr int CH = 17; };
 
@@ -283,88 +288,18 @@ __device__ __forceinline__ const uint8_t* tile_ptr(const uint8_t* mat, int nb, i
 // ---------------------------------------------------------------- quant groups
 // The MFMA GEMM stages weights in units of 64 consecutive weights of one row (four
 // groups of 16 sharing an affine scale, w = a*q - b).  Unit u covers row elements
-//   unit_col(u, g) + [0, 16) for g = 0..3:
-//   Q4_K: block u/4, qs bytes [32c, 32c+32) with c = u%4: groups at 64c + {0,16,32,48}
+//   col(u, g) + [0, 16) for g = 0..3:
+//   Q4_K, Q5_K: block u/4, qs bytes [32c, 32c+32) with c = u%4: groups at 64c + {0,16,32,48}
 //         (low nibbles -> sub-block 2c, high nibbles -> sub-block 2c+1)
 //   Q6_K: block u/4, (h, half) = ((u%4)>>1, u&1): groups s at 128h + 16half + 32s
 //   Q8_0: block u/4, Q8_0 blocks 2(u%4), 2(u%4)+1: groups at 64(u%4) + 16g
-template <int QT> struct Fmt;
-
-template <> struct Fmt<PGMOE_Q4_K> {
+template <int QT> struct Fmt {
     __device__ static __forceinline__ int col(int u, int g) { return 64 * u + 16 * g; }
-    __device__ static __forceinline__ void group(const uint8_t* mat, int K, int N, int row, int u, int g,
-                                                 float q[16], float& a, float& b) {
-        const int nb = K >> 8;
-        const uint8_t* t = tile_ptr<PGMOE_Q4_K>(mat, nb, row >> 6, u >> 2) + (row & 63) * 16;
-        const int c = u & 3;
-        const uint4 hdr = *(const uint4*)t;
-        const uint4 qv = *(const uint4*)(t + (1 + 2 * c + (g & 1)) * 1024);
-        const int s = 2 * c + (g >> 1);
-        const uint32_t D = hdr.y, Mb = hdr.z, MD = hdr.w;  // scale bytes 0-3, 4-7, 8-11
-        int sc, mn;
-        if (s < 4) {
-            sc = (D >> (8 * s)) & 63;
-            mn = (Mb >> (8 * s)) & 63;
-        } else {
-            const int j = s - 4;
-            const uint32_t md = (MD >> (8 * j)) & 0xff;
-            sc = (md & 0x0f) | (((D >> (8 * j)) >> 2) & 0x30);
-            mn = (md >> 4) | (((Mb >> (8 * j)) >> 2) & 0x30);
-        }
-        a = lo_half(hdr.x) * (float)sc;
-        b = hi_half(hdr.x) * (float)mn;
-        const int sh = 4 * (g >> 1);
-        const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) q[i] = (float)((w[i >> 2] >> (8 * (i & 3) + sh)) & 0xf);
-    }
 };
-
 template <> struct Fmt<PGMOE_Q6_K> {
     __device__ static __forceinline__ int col(int u, int g) {
         const int un = u & 3;
         return 256 * (u >> 2) + 128 * (un >> 1) + 16 * (un & 1) + 32 * g;
-    }
-    __device__ static __forceinline__ void group(const uint8_t* mat, int K, int N, int row, int u, int g,
-                                                 float q[16], float& a, float& b) {
-        const int nb = K >> 8;
-        const int rg = row >> 6, r = row & 63, blk = u >> 2, h = (u & 3) >> 1, half = u & 1;
-        const uint8_t* t = tile_ptr<PGMOE_Q6_K>(mat, nb, rg, blk) + r * 16;
-        const uint4 lo = *(const uint4*)(t + (4 * h + 2 * (g & 1) + half) * 1024);  // ql[64h + 32(s&1) + 16half ..]
-        const uint4 hi = *(const uint4*)(t + (8 + 2 * h + half) * 1024);           // qh[32h + 16half ..]
-        const int scb = 8 * h + 2 * g + half;
-        const uint32_t scw = *(const uint32_t*)(t + 12 * 1024 + (scb & ~3));
-        const int64_t dplane = (int64_t)row_groups(N) * nb * 13 * 1024;
-        const uint16_t db = *(const uint16_t*)(mat + dplane + (((int64_t)rg * nb + blk) * 64 + r) * 2);
-        const int sc = (int)(int8_t)((scw >> (8 * (scb & 3))) & 0xff);
-        a = h2f(db) * (float)sc;
-        b = 32.0f * a;
-        const int lsh = 4 * (g >> 1), hsh = 2 * g;
-        const uint32_t lw[4] = {lo.x, lo.y, lo.z, lo.w};
-        const uint32_t hw[4] = {hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int sft = 8 * (i & 3);
-            const int v = ((lw[i >> 2] >> (sft + lsh)) & 0xf) | (((hw[i >> 2] >> (sft + hsh)) & 3) << 4);
-            q[i] = (float)v;
-        }
-    }
-};
-
-template <> struct Fmt<PGMOE_Q8_0> {
-    __device__ static __forceinline__ int col(int u, int g) { return 64 * u + 16 * g; }
-    __device__ static __forceinline__ void group(const uint8_t* mat, int K, int N, int row, int u, int g,
-                                                 float q[16], float& a, float& b) {
-        const int nb = K >> 8;
-        const uint8_t* t = tile_ptr<PGMOE_Q8_0>(mat, nb, row >> 6, u >> 2) + (row & 63) * 16;
-        const int j = u & 3;
-        const uint4 qv = *(const uint4*)(t + (4 * j + g) * 1024);
-        const uint32_t dw = *(const uint32_t*)(t + 16 * 1024 + 4 * j);  // d of Q8_0 blocks 2j, 2j+1
-        a = (g < 2) ? lo_half(dw) : hi_half(dw);
-        b = 0.0f;
-        const uint32_t w[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) q[i] = (float)(int8_t)((w[i >> 2] >> (8 * (i & 3))) & 0xff);
     }
 };
 

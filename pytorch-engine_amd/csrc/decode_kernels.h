@@ -50,6 +50,7 @@ __device__ __forceinline__ uint32_t q6_word(uint32_t qlA, uint32_t qlB, uint32_t
 // Raw 16-byte chunks of one (row, 256-weight super-block), loaded ahead of their use.
 template <int QT> struct Raw;
 template <> struct Raw<PGMOE_Q4_K> { uint4 c[9]; };
+template <> struct Raw<PGMOE_Q5_K> { uint4 c[11]; };
 template <> struct Raw<PGMOE_Q6_K> { uint4 c[13]; uint32_t d; };
 template <> struct Raw<PGMOE_Q8_0> { uint4 c[17]; };
 
@@ -71,6 +72,7 @@ __device__ __forceinline__ void load_raw(Raw<QT>& r, const uint8_t* mat, int N, 
 // super-block:
 //   Q4_K: elements 64p .. 64p+63 (sub-blocks 2p: low nibbles, 2p+1: high nibbles of
 //         qs[32p .. 32p+31]) -> chunks 0 (d, dmin, scales), 1+2p, 2+2p
+//   Q5_K: as Q4_K, plus the quarter's 8 bytes of fifth bits (chunk 9 + (p >> 1))
 //   Q6_K: (h, g) = (p >> 1, p & 1): elements 128h + 32s + 16g + [0, 16) for s = 0..3
 //         (sub-blocks 8h + 2s + g) -> ql chunks 4h+g, 4h+2+g, qh chunk 8+2h+g, scale
 //         bytes 8h .. 8h+7 and d
@@ -83,16 +85,18 @@ __device__ __forceinline__ u32x4 ldq(const uint8_t* p) { return *(const u32x4*)p
 
 template <int QT> struct Qtr;
 template <> struct Qtr<PGMOE_Q4_K> { u32x4 h, a, b; };
+template <> struct Qtr<PGMOE_Q5_K> { u32x4 h, a, b; u32x2 hb; };
 template <> struct Qtr<PGMOE_Q6_K> { u32x4 la, lb, qh; u32x2 sc; uint32_t d; };
 template <> struct Qtr<PGMOE_Q8_0> { u32x4 c0, c1, c2, c3; uint32_t d; };
 
 template <int QT>
 __device__ __forceinline__ void load_qtr(Qtr<QT>& q, const uint8_t* mat, int N, int nb, int row, int j, int p) {
     const uint8_t* t = tile_ptr<QT>(mat, nb, row >> 6, j) + (row & 63) * 16;
-    if constexpr (QT == PGMOE_Q4_K) {
+    if constexpr (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K) {
         q.h = ldq(t);
         q.a = ldq(t + (1 + 2 * p) * 1024);
         q.b = ldq(t + (2 + 2 * p) * 1024);
+        if constexpr (QT == PGMOE_Q5_K) q.hb = *(const u32x2*)(t + (9 + (p >> 1)) * 1024 + 8 * (p & 1));
     } else if constexpr (QT == PGMOE_Q6_K) {
         const int h = p >> 1, g = p & 1;
         q.la = ldq(t + (4 * h + g) * 1024);
@@ -132,20 +136,28 @@ __device__ __forceinline__ void ldx16(const uint16_t* xr, uint32_t (&v)[8]) {
 // staged fp16 token rows (row stride xrs halves), xss: their 16-element sums (row stride
 // srs).  Codes enter v_dot2_f32_f16 as fp16 (1024 + code); the offset returns through the
 // 16-element sums, as in the whole-super-block path.
-template <int TM>
-__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const uint16_t* xs, int xrs,
-                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
-    const float dd = lo_half(q.h.x), dm = hi_half(q.h.x);
+// Q4_K / Q5_K (HB: the fifth bits, word hb.x for sub-block 2p, hb.y for 2p+1; bits k,
+// 8+k, 16+k, 24+k of a word belong to elements 4k .. 4k+3): sub-block 2p from the low
+// nibbles, 2p+1 from the high nibbles.
+template <int TM, bool HB>
+__device__ __forceinline__ void gu_qtr_k(const u32x4& h, const u32x4& qa, const u32x4& qb, const u32x2& hb,
+                                         int j, int p, const uint16_t* xs, int xrs, const float* xss, int srs,
+                                         uint32_t toks, int cnt, float* acc) {
+    const float dd = lo_half(h.x), dm = hi_half(h.x);
     int s0, m0, s1, m1;
-    kscale(q.h.y, q.h.z, q.h.w, 2 * p, s0, m0);
-    kscale(q.h.y, q.h.z, q.h.w, 2 * p + 1, s1, m1);
+    kscale(h.y, h.z, h.w, 2 * p, s0, m0);
+    kscale(h.y, h.z, h.w, 2 * p + 1, s1, m1);
     const float a0 = dd * (float)s0, b0 = dm * (float)m0 + 1024.0f * a0;
     const float a1 = dd * (float)s1, b1 = dm * (float)m1 + 1024.0f * a1;
-    const uint32_t w8[8] = {q.a.x, q.a.y, q.a.z, q.a.w, q.b.x, q.b.y, q.b.z, q.b.w};
+    const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     uint32_t lo[16], hi[16];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const uint32_t l = w8[k] & 0x0f0f0f0fu, hh = (w8[k] >> 4) & 0x0f0f0f0fu;
+        uint32_t l = w8[k] & 0x0f0f0f0fu, hh = (w8[k] >> 4) & 0x0f0f0f0fu;
+        if constexpr (HB) {
+            l |= ((hb.x >> k) & 0x01010101u) << 4;
+            hh |= ((hb.y >> k) & 0x01010101u) << 4;
+        }
         lo[2 * k] = magic2(l, kSel01);
         lo[2 * k + 1] = magic2(l, kSel23);
         hi[2 * k] = magic2(hh, kSel01);
@@ -173,6 +185,17 @@ __device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, c
             acc[t] += a0 * tl - b0 * (sx[0] + sx[1]) + a1 * th - b1 * (sx[2] + sx[3]);
         }
     }
+}
+
+template <int TM>
+__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const uint16_t* xs, int xrs,
+                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
+    gu_qtr_k<TM, false>(q.h, q.a, q.b, u32x2{0u, 0u}, j, p, xs, xrs, xss, srs, toks, cnt, acc);
+}
+template <int TM>
+__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q5_K>& q, int j, int p, const uint16_t* xs, int xrs,
+                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
+    gu_qtr_k<TM, true>(q.h, q.a, q.b, q.hb, j, p, xs, xrs, xss, srs, toks, cnt, acc);
 }
 
 // fp16 value 1024 + q6 (6-bit code), weight = d * sc * (q6 - 32).
@@ -276,19 +299,24 @@ __device__ __forceinline__ float dotf(const float* qf, const float* xr) {
     return T;
 }
 
-template <int TM>
-__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const float* xs, int xrs,
-                                       const float* iss, int srs, int cnt, float* part) {
-    const float dd = lo_half(q.h.x), dm = hi_half(q.h.x);
-    const uint32_t w8[8] = {q.a.x, q.a.y, q.a.z, q.a.w, q.b.x, q.b.y, q.b.z, q.b.w};
+template <int TM, bool HB>
+__device__ __forceinline__ void dn_qtr_k(const u32x4& h, const u32x4& qa, const u32x4& qb, const u32x2& hb, int j,
+                                         int p, const float* xs, int xrs, const float* iss, int srs, int cnt,
+                                         float* part) {
+    const float dd = lo_half(h.x), dm = hi_half(h.x);
+    const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
     for (int hi = 0; hi < 2; ++hi) {
         int sc, mn;
-        kscale(q.h.y, q.h.z, q.h.w, 2 * p + hi, sc, mn);
+        kscale(h.y, h.z, h.w, 2 * p + hi, sc, mn);
         const float a = dd * (float)sc, bm = dm * (float)mn;
         float qf[32];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) bytes_f((w8[k] >> (4 * hi)) & 0x0f0f0f0fu, qf + 4 * k);
+        for (int k = 0; k < 8; ++k) {
+            uint32_t v = (w8[k] >> (4 * hi)) & 0x0f0f0f0fu;
+            if constexpr (HB) v |= (((hi ? hb.y : hb.x) >> k) & 0x01010101u) << 4;
+            bytes_f(v, qf + 4 * k);
+        }
         const int e0 = 256 * j + 64 * p + 32 * hi;
         const int xo = xpos_f(e0);
 #pragma unroll
@@ -300,6 +328,17 @@ __device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, c
             }
         }
     }
+}
+
+template <int TM>
+__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const float* xs, int xrs,
+                                       const float* iss, int srs, int cnt, float* part) {
+    dn_qtr_k<TM, false>(q.h, q.a, q.b, u32x2{0u, 0u}, j, p, xs, xrs, iss, srs, cnt, part);
+}
+template <int TM>
+__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q5_K>& q, int j, int p, const float* xs, int xrs,
+                                       const float* iss, int srs, int cnt, float* part) {
+    dn_qtr_k<TM, true>(q.h, q.a, q.b, q.hb, j, p, xs, xrs, iss, srs, cnt, part);
 }
 
 template <int TM>
@@ -398,13 +437,13 @@ __device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q6_K>& r, const float
             }
 }
 
-template <int TM>
-__device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q4_K>& r, const float* x, const float* isum, int K,
-                                           int me, float* acc) {
+template <int TM, int QT>
+__device__ __forceinline__ void dn_compute_k(const Raw<QT>& r, const float* x, const float* isum, int K, int me,
+                                             float* acc) {
     const uint4 hd = r.c[0];
     const float dd = lo_half(hd.x), dm = hi_half(hd.x);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {  // sub-block s: qs bytes 32(s/2).., nibble s&1
+    for (int s = 0; s < 8; ++s) {  // sub-block s: qs bytes 32(s/2).., nibble s&1 (Q5_K: fifth-bit word s)
         int sc, mn;
         kscale(hd.y, hd.z, hd.w, s, sc, mn);
         const float a = dd * (float)sc, bm = dm * (float)mn;
@@ -414,7 +453,12 @@ __device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q4_K>& r, const float
         float qf[32];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const uint32_t v = (w8[k] >> sh) & 0x0f0f0f0fu;
+            uint32_t v = (w8[k] >> sh) & 0x0f0f0f0fu;
+            if constexpr (QT == PGMOE_Q5_K) {  // word s at chunk 9 + (s >> 2), dword s & 3
+                const uint4 hc = r.c[9 + (s >> 2)];
+                const uint32_t hw = (s & 3) == 0 ? hc.x : (s & 3) == 1 ? hc.y : (s & 3) == 2 ? hc.z : hc.w;
+                v |= ((hw >> k) & 0x01010101u) << 4;
+            }
             qf[4 * k + 0] = (float)(v & 0xff);
             qf[4 * k + 1] = (float)((v >> 8) & 0xff);
             qf[4 * k + 2] = (float)((v >> 16) & 0xff);
@@ -432,6 +476,17 @@ __device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q4_K>& r, const float
             }
         }
     }
+}
+
+template <int TM>
+__device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q4_K>& r, const float* x, const float* isum, int K,
+                                           int me, float* acc) {
+    dn_compute_k<TM, PGMOE_Q4_K>(r, x, isum, K, me, acc);
+}
+template <int TM>
+__device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q5_K>& r, const float* x, const float* isum, int K,
+                                           int me, float* acc) {
+    dn_compute_k<TM, PGMOE_Q5_K>(r, x, isum, K, me, acc);
 }
 
 template <int TM>

@@ -46,18 +46,24 @@ typedef float gf4 __attribute__((ext_vector_type(4)));
 // CH chunks of quant bytes plus one scale chunk (whole 1 KB chunks):
 //   Q4_K: qs chunks 1 + 2c, 2 + 2c (c = u % 4); scales: chunk u of the row group's scale
 //         plane ({a, c} of sub-blocks 2c, 2c + 1 in fp32, decoded at load time)
+//   Q5_K: as Q4_K, plus the fifth-bit chunk 9 + (c >> 1) (the unit's words at bytes 8(c & 1))
 //   Q6_K: ql chunks 4h + half, 4h + 2 + half, qh chunk 8 + 2h + half ((h, half) =
 //         ((u % 4) >> 1, u & 1)); scales: chunk u of the scale plane (a of its four
 //         16-weight sub-blocks)
 //   Q8_0: chunks 4c .. 4c + 3 (the qs of Q8_0 blocks 2c, 2c + 1); scales: tile chunk 16
 // Group g of the unit (k = 16g .. 16g + 15) reads, for the 8 weights 8h .. 8h + 7 of a lane
 // half h, bytes 8h .. 8h + 7 of one staged chunk:
-//   Q4_K: chunk g & 1, nibble g >> 1;  Q6_K: ql chunk g & 1 (nibble g >> 1) and the qh
+//   Q4_K: chunk g & 1, nibble g >> 1;  Q5_K: the same, and fifth-bit word g >> 1 (bits
+//   4(g & 1) + 2h, + 1);  Q6_K: ql chunk g & 1 (nibble g >> 1) and the qh
 //   chunk (bits 2g, 2g + 1);  Q8_0: chunk g.
 template <int QT> struct GStage;
 template <> struct GStage<PGMOE_Q4_K> {
     static constexpr int CH = 2, HC = -1;  // HC: tile chunk of the scales (-1: scale plane)
     __device__ static __forceinline__ int chunk(int u, int cc) { return 1 + 2 * (u & 3) + cc; }
+};
+template <> struct GStage<PGMOE_Q5_K> {
+    static constexpr int CH = 3, HC = -1;
+    __device__ static __forceinline__ int chunk(int u, int cc) { return cc < 2 ? 1 + 2 * (u & 3) + cc : 9 + ((u & 3) >> 1); }
 };
 template <> struct GStage<PGMOE_Q6_K> {
     static constexpr int CH = 3, HC = -1;
@@ -174,6 +180,38 @@ template <> struct GCol<PGMOE_Q4_K> {
         const int sh = 4 * (g >> 1);
         uint32_t m[4];
         magic8((s.x >> sh) & 0x0f0f0f0fu, (s.y >> sh) & 0x0f0f0f0fu, m);
+        return deq8(m, a[g >> 1], c[g >> 1]);
+    }
+};
+
+template <> struct GCol<PGMOE_Q5_K> {
+    u32x2 q[2], hw;    // qs chunks (bytes 8h .. 8h+7), the unit's two fifth-bit words
+    gf4 sv;            // scale plane, as Q4_K
+    float a[2], c[2];
+    int hs;            // 2h: the lane half's first element quad within a 16-element group
+    __device__ __forceinline__ void fetch(const uint8_t* B, int bg, int rig, int h, int u) {
+        const uint8_t* base = B + bg * 4 * 1024 + rig * 16;
+        q[0] = *(const u32x2*)(base + 8 * h);
+        q[1] = *(const u32x2*)(base + 1024 + 8 * h);
+        hw = *(const u32x2*)(base + 2 * 1024 + 8 * (u & 1));
+        sv = *(const gf4*)(base + 3 * 1024);
+        hs = 2 * h;
+    }
+    __device__ __forceinline__ void prep(int u) {
+        a[0] = sv.x;
+        c[0] = sv.y;
+        a[1] = sv.z;
+        c[1] = sv.w;
+    }
+    __device__ __forceinline__ gh8 group(int g) const {
+        // elements 16(g & 1) + 8h + [0, 8) of sub-block 2(u%4) + (g >> 1): quads 4(g & 1) + 2h, + 1
+        const u32x2 s = q[g & 1];
+        const uint32_t w = (g >> 1) ? hw.y : hw.x;
+        const int sh = 4 * (g >> 1), hb = 4 * (g & 1) + hs;
+        const uint32_t c0 = ((s.x >> sh) & 0x0f0f0f0fu) | (((w >> hb) & 0x01010101u) << 4);
+        const uint32_t c1 = ((s.y >> sh) & 0x0f0f0f0fu) | (((w >> (hb + 1)) & 0x01010101u) << 4);
+        uint32_t m[4];
+        magic8(c0, c1, m);
         return deq8(m, a[g >> 1], c[g >> 1]);
     }
 };
@@ -665,6 +703,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
               sp.ksplit, sp.kper, raw, act)
     switch (g.qtype) {
     case PGMOE_Q4_K: PG_GU(PGMOE_Q4_K); break;
+    case PGMOE_Q5_K: PG_GU(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: PG_GU(PGMOE_Q6_K); break;
     case PGMOE_Q8_0: PG_GU(PGMOE_Q8_0); break;
     default: return fail(PGMOE_E_UNSUPPORTED, "gemm gate/up: qtype %d", g.qtype);
@@ -692,6 +731,7 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
               PGMOE_ACT_SILU)
     switch (d.qtype) {
     case PGMOE_Q4_K: PG_DN(PGMOE_Q4_K); break;
+    case PGMOE_Q5_K: PG_DN(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: PG_DN(PGMOE_Q6_K); break;
     case PGMOE_Q8_0: PG_DN(PGMOE_Q8_0); break;
     default: return fail(PGMOE_E_UNSUPPORTED, "gemm down: qtype %d", d.qtype);

@@ -8,6 +8,7 @@ namespace pgmoe {
 
 template <int QT> struct Gguf;
 template <> struct Gguf<PGMOE_Q4_K> { static constexpr int per = 256, bytes = 144; };
+template <> struct Gguf<PGMOE_Q5_K> { static constexpr int per = 256, bytes = 176; };
 template <> struct Gguf<PGMOE_Q6_K> { static constexpr int per = 256, bytes = 210; };
 template <> struct Gguf<PGMOE_Q8_0> { static constexpr int per = 32, bytes = 34; };
 template <> struct Gguf<PGMOE_Q4_0> { static constexpr int per = 32, bytes = 18; };
@@ -45,7 +46,30 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
     // GGUF bytes of this (row, 256-weight block)
     constexpr int sb = Gguf<QT>::bytes * (256 / Gguf<QT>::per);
     const uint8_t* s = src + mat * (int64_t)N * nb * sb + ((int64_t)row * nb + b) * sb;
-    if (QT == PGMOE_Q4_K || QT == PGMOE_Q6_K) {
+    if (QT == PGMOE_Q5_K) {  // GGUF: d, dmin, scales (0-15), qh (16-47), qs (48-175)
+        for (int c = 0; c < 9; ++c) {
+            if (real) copy16(t + c * 1024, s + (c == 0 ? 0 : 48 + 16 * (c - 1)));
+            else zero16(t + c * 1024);
+        }
+        // fifth bits regrouped: word (p, tt) bit 8(l & 3) + (l >> 2) = bit 2p + tt of qh[l]
+        uint32_t w[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = 0;
+        if (real) {
+            for (int l = 0; l < 32; ++l) {
+                const uint32_t hb = s[16 + l];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[i] |= ((hb >> i) & 1u) << (8 * (l & 3) + (l >> 2));
+            }
+        }
+        for (int i = 0; i < 8; ++i) {  // word i = (p, tt) = (i >> 1, i & 1)
+            uint8_t* d = t + (9 + (i >> 2)) * 1024 + 4 * (i & 3);
+            d[0] = (uint8_t)w[i];
+            d[1] = (uint8_t)(w[i] >> 8);
+            d[2] = (uint8_t)(w[i] >> 16);
+            d[3] = (uint8_t)(w[i] >> 24);
+        }
+    } else if (QT == PGMOE_Q4_K || QT == PGMOE_Q6_K) {
         for (int c = 0; c < CH; ++c) {
             if (real) copy16(t + c * 1024, s + 16 * c);
             else zero16(t + c * 1024);
@@ -122,8 +146,8 @@ __global__ void scale_plane_kernel(const uint8_t* __restrict__ src, int64_t n_ma
     const int64_t tb = rem >> 8;  // rg * nb + b
     const uint8_t* md = src + mat * src_stride;
     float4 v;
-    if (QT == PGMOE_Q4_K) {
-        const uint4 hd = *(const uint4*)(md + tb * (9 * 1024) + r * 16);
+    if (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K) {
+        const uint4 hd = *(const uint4*)(md + tb * (Tile<QT>::CH * 1024) + r * 16);
         const float d = lo_half(hd.x), dm = hi_half(hd.x);
         float a[2], cc[2];
 #pragma unroll
@@ -166,6 +190,10 @@ int launch_scale_plane(int qtype, const uint8_t* src, int64_t n_mats, int64_t ro
         PG_LAUNCH(scale_plane_kernel<PGMOE_Q4_K>, grid, dim3(256), 0, st, src, n_mats, (int)rows, nb, src_stride,
                   dst, dst_stride);
         break;
+    case PGMOE_Q5_K:
+        PG_LAUNCH(scale_plane_kernel<PGMOE_Q5_K>, grid, dim3(256), 0, st, src, n_mats, (int)rows, nb, src_stride,
+                  dst, dst_stride);
+        break;
     case PGMOE_Q6_K:
         PG_LAUNCH(scale_plane_kernel<PGMOE_Q6_K>, grid, dim3(256), 0, st, src, n_mats, (int)rows, nb, src_stride,
                   dst, dst_stride);
@@ -181,6 +209,7 @@ int64_t layout_bytes(int qtype, int64_t rows, int64_t cols) {
     const int64_t ng = (rows + 63) / 64, nb = cols / 256;
     switch (qtype) {
     case PGMOE_Q4_K: return ng * nb * 9 * 1024;
+    case PGMOE_Q5_K: return ng * nb * 11 * 1024;
     case PGMOE_Q6_K: return ng * nb * (13 * 1024 + 128);
     case PGMOE_Q8_0:
     case PGMOE_Q4_0:
@@ -199,6 +228,9 @@ int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows,
     switch (qtype) {
     case PGMOE_Q4_K:
         PG_LAUNCH(relayout_kernel<PGMOE_Q4_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        break;
+    case PGMOE_Q5_K:
+        PG_LAUNCH(relayout_kernel<PGMOE_Q5_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
         break;
     case PGMOE_Q6_K:
         PG_LAUNCH(relayout_kernel<PGMOE_Q6_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);

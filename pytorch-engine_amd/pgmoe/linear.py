@@ -65,8 +65,8 @@ class GGUFQuantLinear(nn.Module):
             self.weight = weight.to(dev, torch.float16).contiguous()
             return
         if gguf_qtype not in SUPPORTED_QTYPES:
-            raise NotImplementedError(f"ggml type {gguf_qtype} has no HIP kernel (supported: Q4_K, Q6_K, Q8_0, "
-                                      "and Q4_0 / Q5_0 relaid out as Q8_0)")
+            raise NotImplementedError(f"ggml type {gguf_qtype} has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, "
+                                      "Q8_0, and Q4_0 / Q5_0 relaid out as Q8_0)")
         if self.in_features % 256:
             raise NotImplementedError(f"{self.in_features} input features is not a multiple of 256")
         self.qtype = ops.device_qtype(gguf_qtype)

@@ -12,9 +12,10 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import Q4_0, Q4_K, Q5_0, Q6_K, Q8_0, Weights, check, lib
+from ._lib import Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, Weights, check, lib
 
-GGUF_BLOCK = {Q4_K: (256, 144), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18), Q5_0: (32, 22)}
+GGUF_BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18),
+              Q5_0: (32, 22)}
 
 
 def device_qtype(qtype: int) -> int:

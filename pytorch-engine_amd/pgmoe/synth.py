@@ -9,7 +9,7 @@ drawn.
 Block contents follow the reference tests' random-block pattern
 (tests/test_pygguf_engine.py:34-67): uniform random bytes with the fp16 super-block
 scale(s) overwritten, here with d = |N(0,1)| * 0.02 * scale and dmin = |N(0,1)| * 0.01 * scale
-(Q4_K / Q6_K) and Q8_0 blocks of d = |N(0,1)| * 0.01 * scale with int8 quants uniform in
+(Q4_K / Q5_K / Q6_K) and Q8_0 blocks of d = |N(0,1)| * 0.01 * scale with int8 quants uniform in
 [-127, 127].  ``scale=1`` is the benchmark scale; ``scale=0.01`` gives realistic GGUF
 magnitudes where fp16 intermediates stay finite.
 """
@@ -23,7 +23,8 @@ import numpy as np
 
 from .gguf import GGMLType, InMemoryGGUF, MoEConfig
 
-Q4_0, Q5_0, Q4_K, Q6_K, Q8_0 = GGMLType.Q4_0, GGMLType.Q5_0, GGMLType.Q4_K, GGMLType.Q6_K, GGMLType.Q8_0
+Q4_0, Q5_0, Q4_K, Q5_K, Q6_K, Q8_0 = (GGMLType.Q4_0, GGMLType.Q5_0, GGMLType.Q4_K, GGMLType.Q5_K, GGMLType.Q6_K,
+                                      GGMLType.Q8_0)
 
 __all__ = ["LayerSpec", "CONFIGS", "SyntheticLayer", "DenseSpec", "DENSE_CONFIGS", "SyntheticDense",
            "random_blocks", "zipf_bias"]
@@ -76,9 +77,9 @@ CONFIGS: Dict[str, LayerSpec] = {
 def random_blocks(rng: np.random.Generator, qtype: int, rows: int, cols: int,
                   scale: float = 1.0) -> np.ndarray:
     """Raw GGUF bytes for a [rows, cols] matrix of random blocks (uint8, flat)."""
-    if qtype == Q4_K:
+    if qtype in (Q4_K, Q5_K):
         nb = rows * (cols // 256)
-        raw = rng.integers(0, 256, size=(nb, 144), dtype=np.uint8)
+        raw = rng.integers(0, 256, size=(nb, 144 if qtype == Q4_K else 176), dtype=np.uint8)
         d = (np.abs(rng.standard_normal(nb)) * (0.02 * scale)).astype(np.float16)
         dmin = (np.abs(rng.standard_normal(nb)) * (0.01 * scale)).astype(np.float16)
         raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)

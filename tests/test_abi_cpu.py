@@ -31,7 +31,8 @@ def test_library_exports_every_header_symbol():
 def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
     L = _lib.lib()
     for qt, rows, cols, per, bb in [(12, 768, 2048, 256, 144), (14, 2048, 768, 256, 210),
-                                    (8, 2560, 3584, 32, 34), (14, 1, 256, 256, 210), (8, 100, 512, 32, 34)]:
+                                    (8, 2560, 3584, 32, 34), (14, 1, 256, 256, 210), (8, 100, 512, 32, 34),
+                                    (13, 768, 2048, 256, 176), (13, 5, 512, 256, 176)]:
         padded_rows = (rows + 63) // 64 * 64
         raw = padded_rows * (cols // per) * bb
         assert L.pgmoe_weight_bytes(qt, rows, cols) == (raw + 255) // 256 * 256
@@ -39,7 +40,6 @@ def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
             assert L.pgmoe_weight_bytes(qt, rows, cols) == rows * (cols // per) * bb
     assert L.pgmoe_weight_bytes(12, 4, 100) == -1  # not a whole K-quant block row
     assert L.pgmoe_weight_bytes(3, 4, 256) == -1   # Q4_1 has no kernel
-    assert L.pgmoe_weight_bytes(13, 4, 256) == -1  # nor Q5_K
     assert L.pgmoe_weight_bytes(6, 4, 256) == L.pgmoe_weight_bytes(8, 4, 256)  # Q5_0 is stored as Q8_0
     assert L.pgmoe_weight_bytes(8, 4, 96) == -1    # rows must be whole 256-weight tiles
     assert L.pgmoe_weight_bytes(8, 4, 320) == -1

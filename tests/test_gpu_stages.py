@@ -14,7 +14,7 @@ from pgmoe.synth import random_blocks
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-Q4_K, Q6_K, Q8_0 = 12, 14, 8
+Q4_K, Q5_K, Q6_K, Q8_0 = 12, 13, 14, 8
 
 
 @pytest.fixture(scope="module")
@@ -28,8 +28,8 @@ def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
     """The device layout of include/pgmoe.h (64-row tiles of 16-byte chunks), in numpy."""
     out = np.zeros(n_mats * stride, dtype=np.uint8)
     nb, ng = cols // 256, (rows + 63) // 64
-    bpb = {Q4_K: 144, Q6_K: 210, Q8_0: 272}[qtype]  # GGUF bytes per 256 weights
-    CH = {Q4_K: 9, Q6_K: 13, Q8_0: 17}[qtype]
+    bpb = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 272}[qtype]  # GGUF bytes per 256 weights
+    CH = {Q4_K: 9, Q5_K: 11, Q6_K: 13, Q8_0: 17}[qtype]
     sb = raw.reshape(n_mats, rows, nb, bpb)
     for m in range(n_mats):
         base = m * stride
@@ -38,7 +38,19 @@ def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
             for b in range(nb):
                 blk = sb[m, r, b]
                 t = base + (g * nb + b) * CH * 1024 + rr * 16
-                if qtype in (Q4_K, Q6_K):
+                if qtype == Q5_K:  # header + qs as Q4_K, then the fifth bits per quarter
+                    for c in range(9):
+                        src = 0 if c == 0 else 48 + 16 * (c - 1)
+                        out[t + c * 1024:t + c * 1024 + 16] = blk[src:src + 16]
+                    qh = blk[16:48].astype(np.uint64)
+                    for p in range(4):
+                        for tt in range(2):
+                            word = 0
+                            for l in range(32):
+                                word |= int((qh[l] >> np.uint64(2 * p + tt)) & np.uint64(1)) << (8 * (l & 3) + (l >> 2))
+                            o = t + (9 + (p >> 1)) * 1024 + 8 * (p & 1) + 4 * tt
+                            out[o:o + 4] = np.array([word], dtype="<u4").view(np.uint8)
+                elif qtype in (Q4_K, Q6_K):
                     for c in range(CH):
                         out[t + c * 1024:t + c * 1024 + 16] = blk[16 * c:16 * c + 16]
                     if qtype == Q6_K:
@@ -54,7 +66,7 @@ def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
 
 
 @pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q8_0, 5, 256, 2),
-                                                    (Q6_K, 130, 768, 2), (Q8_0, 64, 512, 1)])
+                                                    (Q6_K, 130, 768, 2), (Q8_0, 64, 512, 1), (Q5_K, 70, 512, 2)])
 def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
     from pgmoe import ops
     rng = np.random.default_rng(rows * cols)
@@ -65,7 +77,7 @@ def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
     ref = _np_relayout(qtype, raw, n_mats, rows, cols, stride)
     # bytes past the tiles (alignment padding between matrices) are unspecified
     ng, nb = (rows + 63) // 64, cols // 256
-    mb = ng * nb * {Q4_K: 9 * 1024, Q6_K: 13 * 1024 + 128, Q8_0: 17 * 1024}[qtype]
+    mb = ng * nb * {Q4_K: 9 * 1024, Q5_K: 11 * 1024, Q6_K: 13 * 1024 + 128, Q8_0: 17 * 1024}[qtype]
     for m in range(n_mats):
         assert np.array_equal(got[m * stride:m * stride + mb], ref[m * stride:m * stride + mb])
 
@@ -146,7 +158,7 @@ def _np_scale_plane(qtype, raw, n_mats, rows, cols):
     """The scale plane of include/pgmoe.h in numpy (fp32, the kernel's expressions and
     operation order): per (64-row group, super-block, unit c) 64 rows of four floats."""
     nb, ng = cols // 256, (rows + 63) // 64
-    bpb = {Q4_K: 144, Q6_K: 210}[qtype]
+    bpb = {Q4_K: 144, Q5_K: 176, Q6_K: 210}[qtype]
     sb = np.zeros((n_mats, ng * 64, nb, bpb), dtype=np.uint8)  # pad rows: zero bytes
     sb[:, :rows] = raw.reshape(n_mats, rows, nb, bpb)
     out = np.zeros((n_mats, ng, nb, 4, 64, 4), dtype=np.float32)
@@ -157,7 +169,7 @@ def _np_scale_plane(qtype, raw, n_mats, rows, cols):
             for b in range(nb):
                 blk = sb[m, r, b]
                 for c in range(4):
-                    if qtype == Q4_K:
+                    if qtype in (Q4_K, Q5_K):
                         d, dmin = blk[0:4].view(np.float16).astype(np.float32)
                         q = blk[4:16].astype(np.int64)
                         vals = []
@@ -178,7 +190,8 @@ def _np_scale_plane(qtype, raw, n_mats, rows, cols):
     return out.reshape(n_mats, -1)
 
 
-@pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q4_K, 130, 256, 2)])
+@pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q4_K, 130, 256, 2),
+                                                    (Q5_K, 70, 512, 2)])
 def test_scale_plane_bits(dev, qtype, rows, cols, n_mats):
     """The load-time scale plane equals its numpy restatement bit for bit (pad rows too)."""
     from pgmoe import ops
@@ -215,7 +228,9 @@ def test_mfma_products_need_the_scale_plane(dev):
     (Q6_K, Q8_0, 768, 256, 3, 1, 6, 0), (Q4_K, Q6_K, 2304, 512, 5, 2, 8, 0),
     (Q4_K, Q6_K, 512, 256, 8, 2, 40, 1), (Q4_K, Q4_K, 256, 512, 4, 2, 130, 1),
     (Q8_0, Q8_0, 256, 512, 6, 3, 70, 1), (Q6_K, Q8_0, 256, 256, 3, 1, 9, 1),
-    (Q4_K, Q6_K, 512, 256, 8, 2, 3, 1), (Q8_0, Q4_K, 512, 256, 3, 2, 17, 1)])
+    (Q4_K, Q6_K, 512, 256, 8, 2, 3, 1), (Q8_0, Q4_K, 512, 256, 3, 2, 17, 1),
+    (Q5_K, Q5_K, 512, 256, 8, 2, 1, 0), (Q5_K, Q5_K, 256, 512, 4, 2, 8, 0), (Q5_K, Q6_K, 768, 512, 5, 2, 6, 0),
+    (Q5_K, Q5_K, 512, 256, 8, 2, 40, 1), (Q5_K, Q5_K, 256, 512, 4, 2, 130, 1), (Q6_K, Q5_K, 512, 256, 3, 1, 9, 1)])
 def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
     """inter and the weighted down partials against float64 numpy over decoded weights.
     Tolerance: the decode GEMV forms exact fp16 products of (1024 + code) and x and

@@ -39,7 +39,7 @@ def test_port_repack_bitwise(golden, name):
             qw, sc, zr = torch_port.repack_w4(raw, QT[name], ROWS, COLS)
             assert np.array_equal(zr.numpy().view(np.uint16), golden[f"dq_{name}_{tag}_zeros"].view(np.uint16))
         else:
-            qw, sc = torch_port.repack_w8(raw, QT[name], ROWS, COLS)
+            qw, sc, _ = torch_port.repack_w8(raw, QT[name], ROWS, COLS)
         assert np.array_equal(qw.numpy(), golden[f"dq_{name}_{tag}_qweight"])
         assert np.array_equal(sc.numpy().view(np.uint16), golden[f"dq_{name}_{tag}_scales"].view(np.uint16))
 
