@@ -20,6 +20,10 @@
  * stored as tiles of 64 rows x one 256-weight super-block; tile (rg, b) at
  * base + (rg * K/256 + b) * CH * 1024 holds CH 16-byte chunks per row, chunk-major:
  * chunk c of row r at + c*1024 + r*16.  Chunk contents (same bits as the GGUF block):
+ *   Q4_1 (type 3, CH 10):  c0 = the fp16 d of the super-block's 8 Q4_1 blocks, c1 = their
+ *                          fp16 m; c2..c9 = their 4-bit codes in the Q4_K arrangement
+ *                          (byte 32j + l of c2..c9: code of element 64j + l in the low
+ *                          nibble, of element 64j + 32 + l in the high one); value d q + m
  *   Q4_K (type 12, CH 9):  c0 = d, dmin, 12 scale bytes;  c1..c8 = qs[16(c-1) .. +16]
  *   Q5_K (type 13, CH 11): c0..c8 as Q4_K (the GGUF block's bytes 0-15 and 48-175);
  *                          c9, c10 = the 256 fifth bits (qh, bytes 16-47) regrouped per
@@ -40,6 +44,7 @@
  * pgmoe_scale_plane_bytes() apart: row r of chunk (rg, b, c) at
  * scales + ((rg*(K/256) + b)*4 + c)*1024 + r*16 holds four floats
  *   Q4_K, Q5_K: {a0, c0, a1, c1} of sub-blocks 2c + t: a = d*sc, c = -(dmin*m) - 1024*a
+ *   Q4_1:       {a0, c0, a1, c1} of blocks 2c + t: a = d, c = m - 1024*a
  *   Q6_K: {a0, a1, a2, a3}: a_g = d * scale[8*(c >> 1) + 2g + (c & 1)]
  * (the values a lane computes from the chunk bytes otherwise).  pgmoe_build_scale_plane()
  * writes it from the device layout.
@@ -62,7 +67,8 @@ extern "C" {
 #define PGMOE_E_WORKSPACE (-3)   /* workspace too small */
 #define PGMOE_E_HIP (-4)         /* HIP runtime error (launch or query) */
 
-#define PGMOE_Q4_0 2  /* source format only: relaid out as PGMOE_Q8_0 (exact values) */
+#define PGMOE_Q4_0 2  /* source format only: relaid out as PGMOE_Q4_1 with m = -8d (exact values) */
+#define PGMOE_Q4_1 3
 #define PGMOE_Q5_0 6  /* source format only: relaid out as PGMOE_Q8_0 (exact values) */
 #define PGMOE_Q8_0 8
 #define PGMOE_Q4_K 12
@@ -77,7 +83,7 @@ extern "C" {
 #define PGMOE_ACT_GELU_TANH 1
 
 typedef struct pgmoe_weights {
-    int32_t qtype;      /* PGMOE_Q4_K / PGMOE_Q5_K / PGMOE_Q6_K / PGMOE_Q8_0 */
+    int32_t qtype;      /* PGMOE_Q4_1 / PGMOE_Q4_K / PGMOE_Q5_K / PGMOE_Q6_K / PGMOE_Q8_0 */
     int32_t n_rows;     /* N: output features per matrix */
     int32_t n_cols;     /* K: input features (multiple of 256 for K-quants, 64 for Q8_0) */
     int32_t n_mats;     /* experts (1 for a shared expert) */
@@ -111,15 +117,16 @@ typedef struct pgmoe_dense {
 int pgmoe_abi_version(void);
 const char* pgmoe_last_error(void);
 
-/* Bytes of one matrix in the device layout (== GGUF bytes; Q4_0: the Q8_0 layout it is
- * converted to); -1 if unsupported. */
+/* Bytes of one matrix in the device layout (== GGUF bytes; Q4_0: the Q4_1 layout it is
+ * converted to, Q5_0: the Q8_0 layout); -1 if unsupported. */
 int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
 
 /* GGUF blocks (device, n_mats matrices back to back) -> device layout.
  * Load-time replacement of repack_gguf_to_w4a16 / repack_gguf_to_w8a16
  * (quant_kernels.py:854-1036), keeping the GGUF bits instead of re-quantising.  A Q4_0
- * (Q5_0) source is written in the Q8_0 layout with qs = q - 8 (q - 16) and the same d
- * (every value kept exactly); pass the result as PGMOE_Q8_0 weights. */
+ * source is written in the Q4_1 layout with the same d and codes and m = -8d (exact for
+ * |d| < 8188; pass the result as PGMOE_Q4_1 weights); a Q5_0 source in the Q8_0 layout
+ * with qs = q - 16 and the same d (pass it as PGMOE_Q8_0).  Every value is kept exactly. */
 int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
                            void* dst, void* stream);
 

@@ -12,7 +12,9 @@
  *                        (quant_kernels.py:854-1036) + closed-form special cases;
  *                        Q5_K: equals Q4_K on the same header/qs with qh = 0, one
  *                        qh bit adds exactly 16*d*sc at its element, and the numpy
- *                        restatement of the reference's Q5_K repack (torch_port)
+ *                        restatement of the reference's Q5_K repack (torch_port);
+ *                        Q4_1: equals Q4_0 when m = -8d, closed form on exact
+ *                        values, and the restated W4 repack of Q4_0 / Q4_1
  *   or_router_logits     textbook dot product (checked against float64 numpy to
  *                        fp32 rounding), fixed reduction order mirrored by the
  *                        GPU router kernel bit for bit
@@ -27,6 +29,7 @@
 #include <string.h>
 
 #define QT_Q4_0 2
+#define QT_Q4_1 3
 #define QT_Q5_0 6
 #define QT_Q8_0 8
 #define QT_Q4_K 12
@@ -185,6 +188,18 @@ static void decode_q4_0_block(const uint8_t* b, float* out) {
     }
 }
 
+/* Q4_1: [d f16][m f16][16 bytes: weight l in the low nibble of byte l, weight 16 + l in
+ * the high nibble]; value d * q + m (ggml dequantize_row_q4_1; the reference's W4 repack,
+ * quant_kernels.py:870-875: scale d, zero -m). */
+static void decode_q4_1_block(const uint8_t* b, float* out) {
+    float d = or_half_to_float(rd16(b));
+    float m = or_half_to_float(rd16(b + 2));
+    for (int l = 0; l < 16; ++l) {
+        out[l] = d * (float)(b[4 + l] & 15) + m;
+        out[16 + l] = d * (float)(b[4 + l] >> 4) + m;
+    }
+}
+
 /* Q5_0: [d f16][qh u32 LE: bit l = 5th bit of weight l][16 bytes: weight l in the low
  * nibble of byte l, weight 16 + l in the high nibble]; value d * (q - 16)
  * (ggml dequantize_row_q5_0). */
@@ -200,6 +215,7 @@ static void decode_q5_0_block(const uint8_t* b, float* out) {
 int or_block_geometry(int qtype, int* per_block, int* block_bytes) {
     switch (qtype) {
     case QT_Q4_0: *per_block = 32; *block_bytes = 18; return 0;
+    case QT_Q4_1: *per_block = 32; *block_bytes = 20; return 0;
     case QT_Q5_0: *per_block = 32; *block_bytes = 22; return 0;
     case QT_Q4_K: *per_block = 256; *block_bytes = 144; return 0;
     case QT_Q5_K: *per_block = 256; *block_bytes = 176; return 0;
@@ -221,6 +237,7 @@ int or_dequant_rows(int qtype, int conv, const uint8_t* blocks, int64_t rows, in
         else if (qtype == QT_Q5_K) decode_q5k_block(b, conv, o);
         else if (qtype == QT_Q6_K) decode_q6k_block(b, conv, o);
         else if (qtype == QT_Q4_0) decode_q4_0_block(b, o);
+        else if (qtype == QT_Q4_1) decode_q4_1_block(b, o);
         else if (qtype == QT_Q5_0) decode_q5_0_block(b, o);
         else decode_q8_0_block(b, o);
     }

@@ -5,8 +5,8 @@ It reproduces what ``GGUFSparseMoEMLP.forward`` does when every ``exec_*`` helpe
 its PyTorch CPU branch:
 
 * load-time repack of GGUF blocks into the reference's W4 / W8 structure-of-arrays
-  (quant_kernels.py:854-904 for Q4_K -> W4, :945-1004 for Q8_0 / Q6_K / Q5_K -> W8), with
-  the fp16 rounding of sub-block scale products;
+  (quant_kernels.py:854-904 for Q4_0 / Q4_1 / Q4_K -> W4, :945-1004 for Q8_0 / Q6_K / Q5_K
+  -> W8), with the fp16 rounding of sub-block scale products;
 * W4 / W8 matmul as chunked fp32 dequant (4096 rows) + fp32 ``F.linear``, result cast to
   the input dtype (quant_kernels.py:1276-1291, :1408-1420);
 * SwiGLU (GeGLU for gemma) + dynamic row-scale with fp16 ``down_in`` (quant_kernels.py:1467-1475);
@@ -25,7 +25,9 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from . import OracleLayer, Q4_K, Q5_K, Q6_K, Q8_0
+from . import OracleLayer, Q4_0, Q4_1, Q4_K, Q5_K, Q6_K, Q8_0
+
+W4_TYPES = (Q4_0, Q4_1, Q4_K)  # the reference's 4-bit repack (SUB_5BIT_W4_QTYPES)
 
 
 def _k_scales(s12: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
@@ -39,9 +41,20 @@ def _k_scales(s12: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
 
 
 def repack_w4(raw: np.ndarray, qtype: int, rows: int, cols: int):
-    """Q4_K blocks -> (qweight u8 [rows, cols/2], scales f16 [rows, cols/32], zeros f16)."""
+    """Q4_0 / Q4_1 / Q4_K blocks -> (qweight u8 [rows, cols/2], scales f16 [rows, cols/32],
+    zeros f16); byte i of a 32-weight group holds weight i (low nibble) and 16 + i (high)."""
+    if qtype in (Q4_0, Q4_1):  # quant_kernels.py:864-875: scale d, zero 8d (Q4_0) / -m (Q4_1)
+        bb = 18 if qtype == Q4_0 else 20
+        blk = raw.reshape(-1, bb)
+        d = blk[:, 0:2].copy().view(np.float16).reshape(rows, cols // 32)
+        if qtype == Q4_0:
+            z = (d.astype(np.float32) * 8.0).astype(np.float16)
+        else:
+            z = (-blk[:, 2:4].copy().view(np.float16).astype(np.float32)).astype(np.float16).reshape(rows, cols // 32)
+        packed = np.ascontiguousarray(blk[:, bb - 16:bb]).reshape(rows, cols // 2)
+        return torch.from_numpy(packed), torch.from_numpy(np.ascontiguousarray(d)), torch.from_numpy(z)
     if qtype != Q4_K:
-        raise ValueError("W4 repack restated for Q4_K only")
+        raise ValueError("W4 repack restated for Q4_0 / Q4_1 / Q4_K only")
     blk = raw.reshape(-1, 144)
     nb = blk.shape[0]
     d = blk[:, 0:4].copy().view(np.float16).astype(np.float32)  # [nb, 2] = (d, dmin)
@@ -138,7 +151,7 @@ class _Proj:
         qtype, n, k, raw = t
         self.qtype, self.n, self.k = qtype, n, k
         rows = n * n_mats
-        if qtype == Q4_K:
+        if qtype in W4_TYPES:
             qw, sc, zr = repack_w4(raw, qtype, rows, k)
             self.w = (qw.view(n_mats, n, k // 2), sc.view(n_mats, n, k // 32), zr.view(n_mats, n, k // 32))
         else:
@@ -147,7 +160,7 @@ class _Proj:
                       None if zr is None else zr.view(n_mats, n, k // 16))
 
     def __call__(self, mat: int, x: torch.Tensor) -> torch.Tensor:
-        if self.qtype == Q4_K:
+        if self.qtype in W4_TYPES:
             return w4_matmul(x, self.w[0][mat], self.w[1][mat], self.w[2][mat])
         return w8_matmul(x, self.w[0][mat], self.w[1][mat], None if self.w[2] is None else self.w[2][mat])
 
@@ -206,7 +219,7 @@ class PortMoE:
 def dense_weights(t: tuple, mat: int = 0, n_mats: Optional[int] = None) -> np.ndarray:
     """fp32 dense weights of one matrix as the W4/W8 repack defines them (q*s - z)."""
     p = _Proj(t, n_mats if n_mats is not None else 1)
-    if p.qtype == Q4_K:
+    if p.qtype in W4_TYPES:
         qw, sc, zr = (a[mat] for a in p.w)
         n, k = p.n, p.k
         pk = qw.view(n, k // 32, 16)

@@ -261,6 +261,8 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
 //     tile(rg, b) = base + (rg * nb + b) * CH * 1024,   chunk c of row r at + c*1024 + r*16
 // so the 64 lanes of a wavefront reading chunk c of 64 consecutive rows touch 1 KB of
 // contiguous memory.  Chunk contents (same bits as the GGUF block):
+//   Q4_1 (CH 10): c0 = fp16 d of the 8 Q4_1 blocks, c1 = their fp16 m;  c2..c9 = the codes
+//                 in the Q4_K arrangement (c2..c9 as Q4_K's c1..c8); value d q + m
 //   Q4_K (CH 9):  c0 = d, dmin, 12 scale bytes;  c1..c8 = qs[16(c-1) .. +16]
 //   Q5_K (CH 11): c0..c8 as Q4_K;  c9, c10 = the fifth bits per 64-weight quarter p:
 //                 word t (t = 0, 1) at chunk 9 + (p >> 1), byte 8(p & 1) + 4t, bit
@@ -273,6 +275,7 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
 //                 c16 = their 8 fp16 d
 // N is padded to a multiple of 64 (padding rows are zero and never stored to outputs).
 template <int QT> struct Tile;
+template <> struct Tile<PGMOE_Q4_1> { static constexpr int CH = 10; };
 template <> struct Tile<PGMOE_Q4_K> { static constexpr int CH = 9; };
 template <> struct Tile<PGMOE_Q5_K> { static constexpr int CH = 11; };
 template <> struct Tile<PGMOE_Q6_K> { static constexpr int CH = 13; };
@@ -289,7 +292,7 @@ __device__ __forceinline__ const uint8_t* tile_ptr(const uint8_t* mat, int nb, i
 // The MFMA GEMM stages weights in units of 64 consecutive weights of one row (four
 // groups of 16 sharing an affine scale, w = a*q - b).  Unit u covers row elements
 //   col(u, g) + [0, 16) for g = 0..3:
-//   Q4_K, Q5_K: block u/4, qs bytes [32c, 32c+32) with c = u%4: groups at 64c + {0,16,32,48}
+//   Q4_1, Q4_K, Q5_K: block u/4, qs bytes [32c, 32c+32) with c = u%4: groups at 64c + {0,16,32,48}
 //         (low nibbles -> sub-block 2c, high nibbles -> sub-block 2c+1)
 //   Q6_K: block u/4, (h, half) = ((u%4)>>1, u&1): groups s at 128h + 16half + 32s
 //   Q8_0: block u/4, Q8_0 blocks 2(u%4), 2(u%4)+1: groups at 64(u%4) + 16g

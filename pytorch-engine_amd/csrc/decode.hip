@@ -5,6 +5,7 @@ namespace pgmoe {
 
 #define PG_BY_QTYPE(qt, what, call)                                  \
     switch (qt) {                                                    \
+    case PGMOE_Q4_1: return call(PGMOE_Q4_1);                        \
     case PGMOE_Q4_K: return call(PGMOE_Q4_K);                        \
     case PGMOE_Q5_K: return call(PGMOE_Q5_K);                        \
     case PGMOE_Q6_K: return call(PGMOE_Q6_K);                        \

@@ -49,6 +49,7 @@ __device__ __forceinline__ uint32_t q6_word(uint32_t qlA, uint32_t qlB, uint32_t
 // ============================================================================ tiles
 // Raw 16-byte chunks of one (row, 256-weight super-block), loaded ahead of their use.
 template <int QT> struct Raw;
+template <> struct Raw<PGMOE_Q4_1> { uint4 c[10]; };
 template <> struct Raw<PGMOE_Q4_K> { uint4 c[9]; };
 template <> struct Raw<PGMOE_Q5_K> { uint4 c[11]; };
 template <> struct Raw<PGMOE_Q6_K> { uint4 c[13]; uint32_t d; };
@@ -73,6 +74,8 @@ __device__ __forceinline__ void load_raw(Raw<QT>& r, const uint8_t* mat, int N, 
 //   Q4_K: elements 64p .. 64p+63 (sub-blocks 2p: low nibbles, 2p+1: high nibbles of
 //         qs[32p .. 32p+31]) -> chunks 0 (d, dmin, scales), 1+2p, 2+2p
 //   Q5_K: as Q4_K, plus the quarter's 8 bytes of fifth bits (chunk 9 + (p >> 1))
+//   Q4_1: as Q4_K, with the codes in chunks 2+2p, 3+2p and, in place of the header, the
+//         fp16 d and m of blocks 2p, 2p+1 (chunk 0 / chunk 1, bytes 4p .. 4p+3)
 //   Q6_K: (h, g) = (p >> 1, p & 1): elements 128h + 32s + 16g + [0, 16) for s = 0..3
 //         (sub-blocks 8h + 2s + g) -> ql chunks 4h+g, 4h+2+g, qh chunk 8+2h+g, scale
 //         bytes 8h .. 8h+7 and d
@@ -84,6 +87,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ u32x4 ldq(const uint8_t* p) { return *(const u32x4*)p; }
 
 template <int QT> struct Qtr;
+template <> struct Qtr<PGMOE_Q4_1> { uint32_t dw, mw; u32x4 a, b; };
 template <> struct Qtr<PGMOE_Q4_K> { u32x4 h, a, b; };
 template <> struct Qtr<PGMOE_Q5_K> { u32x4 h, a, b; u32x2 hb; };
 template <> struct Qtr<PGMOE_Q6_K> { u32x4 la, lb, qh; u32x2 sc; uint32_t d; };
@@ -92,7 +96,12 @@ template <> struct Qtr<PGMOE_Q8_0> { u32x4 c0, c1, c2, c3; uint32_t d; };
 template <int QT>
 __device__ __forceinline__ void load_qtr(Qtr<QT>& q, const uint8_t* mat, int N, int nb, int row, int j, int p) {
     const uint8_t* t = tile_ptr<QT>(mat, nb, row >> 6, j) + (row & 63) * 16;
-    if constexpr (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K) {
+    if constexpr (QT == PGMOE_Q4_1) {
+        q.dw = *(const uint32_t*)(t + 4 * p);
+        q.mw = *(const uint32_t*)(t + 1024 + 4 * p);
+        q.a = ldq(t + (2 + 2 * p) * 1024);
+        q.b = ldq(t + (3 + 2 * p) * 1024);
+    } else if constexpr (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K) {
         q.h = ldq(t);
         q.a = ldq(t + (1 + 2 * p) * 1024);
         q.b = ldq(t + (2 + 2 * p) * 1024);
@@ -136,19 +145,15 @@ __device__ __forceinline__ void ldx16(const uint16_t* xr, uint32_t (&v)[8]) {
 // staged fp16 token rows (row stride xrs halves), xss: their 16-element sums (row stride
 // srs).  Codes enter v_dot2_f32_f16 as fp16 (1024 + code); the offset returns through the
 // 16-element sums, as in the whole-super-block path.
-// Q4_K / Q5_K (HB: the fifth bits, word hb.x for sub-block 2p, hb.y for 2p+1; bits k,
-// 8+k, 16+k, 24+k of a word belong to elements 4k .. 4k+3): sub-block 2p from the low
-// nibbles, 2p+1 from the high nibbles.
+// Q4_K / Q5_K / Q4_1: weight a q - z with (a0, z0) for sub-block 2p (the low nibbles) and
+// (a1, z1) for 2p+1 (the high nibbles).  HB: the fifth bits (Q5_K), word hb.x for
+// sub-block 2p, hb.y for 2p+1; bits k, 8+k, 16+k, 24+k of a word belong to elements
+// 4k .. 4k+3.
 template <int TM, bool HB>
-__device__ __forceinline__ void gu_qtr_k(const u32x4& h, const u32x4& qa, const u32x4& qb, const u32x2& hb,
-                                         int j, int p, const uint16_t* xs, int xrs, const float* xss, int srs,
-                                         uint32_t toks, int cnt, float* acc) {
-    const float dd = lo_half(h.x), dm = hi_half(h.x);
-    int s0, m0, s1, m1;
-    kscale(h.y, h.z, h.w, 2 * p, s0, m0);
-    kscale(h.y, h.z, h.w, 2 * p + 1, s1, m1);
-    const float a0 = dd * (float)s0, b0 = dm * (float)m0 + 1024.0f * a0;
-    const float a1 = dd * (float)s1, b1 = dm * (float)m1 + 1024.0f * a1;
+__device__ __forceinline__ void gu_qtr_k(float a0, float z0, float a1, float z1, const u32x4& qa, const u32x4& qb,
+                                         const u32x2& hb, int j, int p, const uint16_t* xs, int xrs,
+                                         const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
+    const float b0 = z0 + 1024.0f * a0, b1 = z1 + 1024.0f * a1;
     const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
     uint32_t lo[16], hi[16];
 #pragma unroll
@@ -187,15 +192,38 @@ __device__ __forceinline__ void gu_qtr_k(const u32x4& h, const u32x4& qa, const 
     }
 }
 
+// (a, z) of K-quant sub-blocks 2p, 2p+1 from the header chunk: a = d sc, z = dmin m.
+__device__ __forceinline__ void kq_scales(const u32x4& h, int p, float& a0, float& z0, float& a1, float& z1) {
+    const float dd = lo_half(h.x), dm = hi_half(h.x);
+    int s0, m0, s1, m1;
+    kscale(h.y, h.z, h.w, 2 * p, s0, m0);
+    kscale(h.y, h.z, h.w, 2 * p + 1, s1, m1);
+    a0 = dd * (float)s0;
+    z0 = dm * (float)m0;
+    a1 = dd * (float)s1;
+    z1 = dm * (float)m1;
+}
+
 template <int TM>
 __device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const uint16_t* xs, int xrs,
                                        const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
-    gu_qtr_k<TM, false>(q.h, q.a, q.b, u32x2{0u, 0u}, j, p, xs, xrs, xss, srs, toks, cnt, acc);
+    float a0, z0, a1, z1;
+    kq_scales(q.h, p, a0, z0, a1, z1);
+    gu_qtr_k<TM, false>(a0, z0, a1, z1, q.a, q.b, u32x2{0u, 0u}, j, p, xs, xrs, xss, srs, toks, cnt, acc);
 }
 template <int TM>
 __device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q5_K>& q, int j, int p, const uint16_t* xs, int xrs,
                                        const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
-    gu_qtr_k<TM, true>(q.h, q.a, q.b, q.hb, j, p, xs, xrs, xss, srs, toks, cnt, acc);
+    float a0, z0, a1, z1;
+    kq_scales(q.h, p, a0, z0, a1, z1);
+    gu_qtr_k<TM, true>(a0, z0, a1, z1, q.a, q.b, q.hb, j, p, xs, xrs, xss, srs, toks, cnt, acc);
+}
+// Q4_1: a = d, z = -m of blocks 2p, 2p+1.
+template <int TM>
+__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q4_1>& q, int j, int p, const uint16_t* xs, int xrs,
+                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
+    gu_qtr_k<TM, false>(lo_half(q.dw), -lo_half(q.mw), hi_half(q.dw), -hi_half(q.mw), q.a, q.b, u32x2{0u, 0u}, j,
+                        p, xs, xrs, xss, srs, toks, cnt, acc);
 }
 
 // fp16 value 1024 + q6 (6-bit code), weight = d * sc * (q6 - 32).
@@ -300,16 +328,13 @@ __device__ __forceinline__ float dotf(const float* qf, const float* xr) {
 }
 
 template <int TM, bool HB>
-__device__ __forceinline__ void dn_qtr_k(const u32x4& h, const u32x4& qa, const u32x4& qb, const u32x2& hb, int j,
-                                         int p, const float* xs, int xrs, const float* iss, int srs, int cnt,
-                                         float* part) {
-    const float dd = lo_half(h.x), dm = hi_half(h.x);
+__device__ __forceinline__ void dn_qtr_k(float a0, float z0, float a1, float z1, const u32x4& qa, const u32x4& qb,
+                                         const u32x2& hb, int j, int p, const float* xs, int xrs, const float* iss,
+                                         int srs, int cnt, float* part) {
     const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
     for (int hi = 0; hi < 2; ++hi) {
-        int sc, mn;
-        kscale(h.y, h.z, h.w, 2 * p + hi, sc, mn);
-        const float a = dd * (float)sc, bm = dm * (float)mn;
+        const float a = hi ? a1 : a0, bm = hi ? z1 : z0;
         float qf[32];
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -333,12 +358,22 @@ __device__ __forceinline__ void dn_qtr_k(const u32x4& h, const u32x4& qa, const 
 template <int TM>
 __device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q4_K>& q, int j, int p, const float* xs, int xrs,
                                        const float* iss, int srs, int cnt, float* part) {
-    dn_qtr_k<TM, false>(q.h, q.a, q.b, u32x2{0u, 0u}, j, p, xs, xrs, iss, srs, cnt, part);
+    float a0, z0, a1, z1;
+    kq_scales(q.h, p, a0, z0, a1, z1);
+    dn_qtr_k<TM, false>(a0, z0, a1, z1, q.a, q.b, u32x2{0u, 0u}, j, p, xs, xrs, iss, srs, cnt, part);
 }
 template <int TM>
 __device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q5_K>& q, int j, int p, const float* xs, int xrs,
                                        const float* iss, int srs, int cnt, float* part) {
-    dn_qtr_k<TM, true>(q.h, q.a, q.b, q.hb, j, p, xs, xrs, iss, srs, cnt, part);
+    float a0, z0, a1, z1;
+    kq_scales(q.h, p, a0, z0, a1, z1);
+    dn_qtr_k<TM, true>(a0, z0, a1, z1, q.a, q.b, q.hb, j, p, xs, xrs, iss, srs, cnt, part);
+}
+template <int TM>
+__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q4_1>& q, int j, int p, const float* xs, int xrs,
+                                       const float* iss, int srs, int cnt, float* part) {
+    dn_qtr_k<TM, false>(lo_half(q.dw), -lo_half(q.mw), hi_half(q.dw), -hi_half(q.mw), q.a, q.b, u32x2{0u, 0u}, j,
+                        p, xs, xrs, iss, srs, cnt, part);
 }
 
 template <int TM>
@@ -442,13 +477,23 @@ __device__ __forceinline__ void dn_compute_k(const Raw<QT>& r, const float* x, c
                                              float* acc) {
     const uint4 hd = r.c[0];
     const float dd = lo_half(hd.x), dm = hi_half(hd.x);
+    constexpr int QC = QT == PGMOE_Q4_1 ? 2 : 1;  // first code chunk
 #pragma unroll
     for (int s = 0; s < 8; ++s) {  // sub-block s: qs bytes 32(s/2).., nibble s&1 (Q5_K: fifth-bit word s)
-        int sc, mn;
-        kscale(hd.y, hd.z, hd.w, s, sc, mn);
-        const float a = dd * (float)sc, bm = dm * (float)mn;
+        float a, bm;
+        if constexpr (QT == PGMOE_Q4_1) {  // d, m: fp16 word s of chunks 0, 1
+            const uint32_t dwd = (s >> 1) == 0 ? r.c[0].x : (s >> 1) == 1 ? r.c[0].y : (s >> 1) == 2 ? r.c[0].z : r.c[0].w;
+            const uint32_t mwd = (s >> 1) == 0 ? r.c[1].x : (s >> 1) == 1 ? r.c[1].y : (s >> 1) == 2 ? r.c[1].z : r.c[1].w;
+            a = (s & 1) ? hi_half(dwd) : lo_half(dwd);
+            bm = -((s & 1) ? hi_half(mwd) : lo_half(mwd));
+        } else {
+            int sc, mn;
+            kscale(hd.y, hd.z, hd.w, s, sc, mn);
+            a = dd * (float)sc;
+            bm = dm * (float)mn;
+        }
         const int c2 = s >> 1, sh = 4 * (s & 1);
-        const uint4 qa = r.c[1 + 2 * c2], qb = r.c[2 + 2 * c2];
+        const uint4 qa = r.c[QC + 2 * c2], qb = r.c[QC + 1 + 2 * c2];
         const uint32_t w8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
         float qf[32];
 #pragma unroll
@@ -487,6 +532,11 @@ template <int TM>
 __device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q5_K>& r, const float* x, const float* isum, int K,
                                            int me, float* acc) {
     dn_compute_k<TM, PGMOE_Q5_K>(r, x, isum, K, me, acc);
+}
+template <int TM>
+__device__ __forceinline__ void dn_compute(const Raw<PGMOE_Q4_1>& r, const float* x, const float* isum, int K,
+                                           int me, float* acc) {
+    dn_compute_k<TM, PGMOE_Q4_1>(r, x, isum, K, me, acc);
 }
 
 template <int TM>

@@ -47,6 +47,8 @@ typedef float gf4 __attribute__((ext_vector_type(4)));
 //   Q4_K: qs chunks 1 + 2c, 2 + 2c (c = u % 4); scales: chunk u of the row group's scale
 //         plane ({a, c} of sub-blocks 2c, 2c + 1 in fp32, decoded at load time)
 //   Q5_K: as Q4_K, plus the fifth-bit chunk 9 + (c >> 1) (the unit's words at bytes 8(c & 1))
+//   Q4_1: code chunks 2 + 2c, 3 + 2c; scales: chunk u of the scale plane ({a, c} of blocks
+//         2c, 2c + 1), as Q4_K
 //   Q6_K: ql chunks 4h + half, 4h + 2 + half, qh chunk 8 + 2h + half ((h, half) =
 //         ((u % 4) >> 1, u & 1)); scales: chunk u of the scale plane (a of its four
 //         16-weight sub-blocks)
@@ -60,6 +62,10 @@ template <int QT> struct GStage;
 template <> struct GStage<PGMOE_Q4_K> {
     static constexpr int CH = 2, HC = -1;  // HC: tile chunk of the scales (-1: scale plane)
     __device__ static __forceinline__ int chunk(int u, int cc) { return 1 + 2 * (u & 3) + cc; }
+};
+template <> struct GStage<PGMOE_Q4_1> {
+    static constexpr int CH = 2, HC = -1;
+    __device__ static __forceinline__ int chunk(int u, int cc) { return 2 + 2 * (u & 3) + cc; }
 };
 template <> struct GStage<PGMOE_Q5_K> {
     static constexpr int CH = 3, HC = -1;
@@ -183,6 +189,9 @@ template <> struct GCol<PGMOE_Q4_K> {
         return deq8(m, a[g >> 1], c[g >> 1]);
     }
 };
+
+// Q4_1: the staged bytes and plane of Q4_K (codes in the same arrangement, {a, c} per block).
+template <> struct GCol<PGMOE_Q4_1> : GCol<PGMOE_Q4_K> {};
 
 template <> struct GCol<PGMOE_Q5_K> {
     u32x2 q[2], hw;    // qs chunks (bytes 8h .. 8h+7), the unit's two fifth-bit words
@@ -702,6 +711,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
               E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter, g.scales, u.scales, \
               sp.ksplit, sp.kper, raw, act)
     switch (g.qtype) {
+    case PGMOE_Q4_1: PG_GU(PGMOE_Q4_1); break;
     case PGMOE_Q4_K: PG_GU(PGMOE_Q4_K); break;
     case PGMOE_Q5_K: PG_GU(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: PG_GU(PGMOE_Q6_K); break;
@@ -730,6 +740,7 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
               topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial, d.scales, d.scales, sp.ksplit, sp.kper, raw, \
               PGMOE_ACT_SILU)
     switch (d.qtype) {
+    case PGMOE_Q4_1: PG_DN(PGMOE_Q4_1); break;
     case PGMOE_Q4_K: PG_DN(PGMOE_Q4_K); break;
     case PGMOE_Q5_K: PG_DN(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: PG_DN(PGMOE_Q6_K); break;

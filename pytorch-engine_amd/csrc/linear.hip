@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void bias_cast_kernel(const float* __restrict_
 
 // Row `rows[i]` of W (N x K in the tile layout), super-block b, decoded to 256 values:
 // one thread per (i, b); an id outside [0, N) gives a row of NaN.  Values as the ggml block definitions give them, products in fp32
-// (Q4_K, Q5_K: d*sc*q - dmin*m; Q6_K: d*sc*(q - 32); Q8_0: d*q).
+// (Q4_K, Q5_K: d*sc*q - dmin*m; Q4_1: d*q - (-m); Q6_K: d*sc*(q - 32); Q8_0: d*q).
 template <int QT>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ base, int N, int K,
                                                            const int32_t* __restrict__ rows, int n,
@@ -55,16 +55,26 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
         else
             ((float*)out)[o + e] = v;
     };
-    if constexpr (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K) {  // chunk 0: d, dmin, 12 scale bytes; 1..8: qs; 9, 10: qh
+    if constexpr (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K || QT == PGMOE_Q4_1) {
+        // Q4_K / Q5_K: chunk 0 = d, dmin, 12 scale bytes; 1..8: qs; 9, 10: fifth bits
+        // Q4_1: chunk 0 = 8 fp16 d, 1 = 8 fp16 m; 2..9: qs (the Q4_K arrangement)
+        constexpr int QC = QT == PGMOE_Q4_1 ? 2 : 1;
         const uint4 h = *(const uint4*)t;
         const float d = lo_half(h.x), dmin = hi_half(h.x);
         for (int s = 0; s < 8; ++s) {
-            int sc, mn;
-            kscale(h.y, h.z, h.w, s, sc, mn);
-            const float a = d * (float)sc, z = dmin * (float)mn;
+            float a, z;
+            if constexpr (QT == PGMOE_Q4_1) {
+                a = h2f((uint16_t)(byte(0, 2 * s) | (byte(0, 2 * s + 1) << 8)));
+                z = -h2f((uint16_t)(byte(1, 2 * s) | (byte(1, 2 * s + 1) << 8)));
+            } else {
+                int sc, mn;
+                kscale(h.y, h.z, h.w, s, sc, mn);
+                a = d * (float)sc;
+                z = dmin * (float)mn;
+            }
             for (int l = 0; l < 32; ++l) {
                 const int j = 32 * (s >> 1) + l;  // qs byte
-                int q = (byte(1 + (j >> 4), j & 15) >> (4 * (s & 1))) & 15;
+                int q = (byte(QC + (j >> 4), j & 15) >> (4 * (s & 1))) & 15;
                 if constexpr (QT == PGMOE_Q5_K)  // fifth-bit word s: chunk 9 + (s >> 2), byte 4(s & 3) + (l & 3)
                     q |= ((byte(9 + (s >> 2), 4 * (s & 3) + (l & 3)) >> (l >> 2)) & 1) << 4;
                 put(32 * s + l, a * (float)q - z);
@@ -97,6 +107,7 @@ int launch_dequant_rows(const Mats& w, const int32_t* rows, int n, void* out, in
     const dim3 grid((unsigned)div_up(threads, 256));
 #define DQ(QT) PG_LAUNCH(dequant_rows_kernel<QT>, grid, dim3(256), 0, st, w.base, w.N, w.K, rows, n, out, out_f16)
     switch (w.qtype) {
+    case PGMOE_Q4_1: DQ(PGMOE_Q4_1); break;
     case PGMOE_Q4_K: DQ(PGMOE_Q4_K); break;
     case PGMOE_Q5_K: DQ(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: DQ(PGMOE_Q6_K); break;

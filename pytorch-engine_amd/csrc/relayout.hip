@@ -12,6 +12,7 @@ template <> struct Gguf<PGMOE_Q5_K> { static constexpr int per = 256, bytes = 17
 template <> struct Gguf<PGMOE_Q6_K> { static constexpr int per = 256, bytes = 210; };
 template <> struct Gguf<PGMOE_Q8_0> { static constexpr int per = 32, bytes = 34; };
 template <> struct Gguf<PGMOE_Q4_0> { static constexpr int per = 32, bytes = 18; };
+template <> struct Gguf<PGMOE_Q4_1> { static constexpr int per = 32, bytes = 20; };
 template <> struct Gguf<PGMOE_Q5_0> { static constexpr int per = 32, bytes = 22; };
 
 __device__ __forceinline__ void copy16(uint8_t* d, const uint8_t* s) {
@@ -24,9 +25,10 @@ __device__ __forceinline__ void zero16(uint8_t* d) {
     for (int i = 0; i < 16; ++i) d[i] = 0;
 }
 
-// One thread per (matrix, padded row, 256-weight block).  Q4_0 and Q5_0 sources are
-// written as Q8_0 tiles: d * (q - 8) and d * (q - 16) (5-bit q) are the Q8_0 values d * qs
-// with qs = q - 8 / q - 16 (same d, same 32-weight blocks), so every value is kept exactly.
+// One thread per (matrix, padded row, 256-weight block).  Q5_0 sources are written as Q8_0
+// tiles: d * (q - 16) (5-bit q) is the Q8_0 value d * qs with qs = q - 16 (same d, same
+// 32-weight blocks).  Q4_0 sources are written as Q4_1 tiles: d * (q - 8) = d q + m with
+// m = -8d (exact in fp16 for |d| < 8188).  Every value is kept exactly.
 template <int QT>
 __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats, int N, int nb,
                                 uint8_t* __restrict__ dst, int64_t dst_stride) {
@@ -38,7 +40,7 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
     const int64_t rem = gid % per_mat;
     const int row = (int)(rem / nb), b = (int)(rem % nb);
     const int rg = row >> 6, r = row & 63;
-    constexpr int DT = (QT == PGMOE_Q4_0 || QT == PGMOE_Q5_0) ? PGMOE_Q8_0 : QT;  // device layout
+    constexpr int DT = QT == PGMOE_Q5_0 ? PGMOE_Q8_0 : QT == PGMOE_Q4_0 ? PGMOE_Q4_1 : QT;  // device layout
     constexpr int CH = Tile<DT>::CH;
     uint8_t* md = dst + mat * dst_stride;
     uint8_t* t = md + ((int64_t)rg * nb + b) * (CH * 1024) + r * 16;
@@ -97,20 +99,35 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
             t[16 * 1024 + 2 * j] = real ? bj[0] : 0;
             t[16 * 1024 + 2 * j + 1] = real ? bj[1] : 0;
         }
-    } else if (QT == PGMOE_Q4_0) {  // eight 18-byte blocks per 256 weights -> Q8_0 tiles
+    } else if (QT == PGMOE_Q4_0 || QT == PGMOE_Q4_1) {  // eight 18 / 20-byte blocks -> Q4_1 tiles
+        constexpr int BB = Gguf<QT>::bytes, QO = QT == PGMOE_Q4_0 ? 2 : 4;  // block bytes, qs offset
+        // codes of element l of block j: low nibble of qs[l] (l < 16), high nibble of qs[l - 16]
+        auto code = [&](int j, int l) -> uint32_t {
+            const uint8_t b = s[BB * j + QO + (l & 15)];
+            return l < 16 ? (b & 15u) : (uint32_t)(b >> 4);
+        };
         for (int j = 0; j < 8; ++j) {
-            const uint8_t* bj = s + 18 * j;
-            uint8_t lo[16], hi[16];
-#pragma unroll
-            for (int l = 0; l < 16; ++l) {
-                const int q = real ? bj[2 + l] : 0x88;  // pad rows: nibbles 8 -> 0
-                lo[l] = (uint8_t)(int8_t)((q & 15) - 8);
-                hi[l] = (uint8_t)(int8_t)((q >> 4) - 8);
+            uint16_t d = 0, m = 0;  // pad rows: d = m = 0
+            if (real) {
+                d = (uint16_t)s[BB * j] | ((uint16_t)s[BB * j + 1] << 8);
+                if (QT == PGMOE_Q4_1)
+                    m = (uint16_t)s[BB * j + 2] | ((uint16_t)s[BB * j + 3] << 8);
+                else
+                    m = __builtin_bit_cast(uint16_t, (half_t)(-8.0f * h2f(d)));
             }
-            copy16(t + (2 * j) * 1024, lo);
-            copy16(t + (2 * j + 1) * 1024, hi);
-            t[16 * 1024 + 2 * j] = real ? bj[0] : 0;
-            t[16 * 1024 + 2 * j + 1] = real ? bj[1] : 0;
+            t[2 * j] = (uint8_t)d;
+            t[2 * j + 1] = (uint8_t)(d >> 8);
+            t[1024 + 2 * j] = (uint8_t)m;
+            t[1024 + 2 * j + 1] = (uint8_t)(m >> 8);
+        }
+        for (int c = 0; c < 8; ++c) {  // Q4_K arrangement: byte 32J + l = element 64J + l | element 64J + 32 + l
+            uint8_t v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int k = 16 * c + i, J = k >> 5, l = k & 31;
+                v[i] = real ? (uint8_t)(code(2 * J, l) | (code(2 * J + 1, l) << 4)) : 0;
+            }
+            copy16(t + (2 + c) * 1024, v);
         }
     } else {  // Q8_0: eight 34-byte blocks per 256 weights
         for (int j = 0; j < 8; ++j) {
@@ -146,7 +163,12 @@ __global__ void scale_plane_kernel(const uint8_t* __restrict__ src, int64_t n_ma
     const int64_t tb = rem >> 8;  // rg * nb + b
     const uint8_t* md = src + mat * src_stride;
     float4 v;
-    if (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K) {
+    if (QT == PGMOE_Q4_1) {  // fp16 d in chunk 0, m in chunk 1
+        const uint8_t* tt = md + tb * (10 * 1024) + r * 16;
+        const uint32_t dw = *(const uint32_t*)(tt + 4 * c), mw = *(const uint32_t*)(tt + 1024 + 4 * c);
+        const float a0 = lo_half(dw), a1 = hi_half(dw);
+        v = make_float4(a0, lo_half(mw) - 1024.0f * a0, a1, hi_half(mw) - 1024.0f * a1);
+    } else if (QT == PGMOE_Q4_K || QT == PGMOE_Q5_K) {
         const uint4 hd = *(const uint4*)(md + tb * (Tile<QT>::CH * 1024) + r * 16);
         const float d = lo_half(hd.x), dm = hi_half(hd.x);
         float a[2], cc[2];
@@ -173,7 +195,7 @@ __global__ void scale_plane_kernel(const uint8_t* __restrict__ src, int64_t n_ma
 
 int64_t scale_plane_bytes(int qtype, int64_t rows, int64_t cols) {
     if (qtype == PGMOE_Q4_0 || qtype == PGMOE_Q5_0 || layout_bytes(qtype, rows, cols) < 0)
-        return -1;  // Q4_0 / Q5_0: source formats
+        return -1;  // Q4_0 / Q5_0: source formats (their device layouts are Q4_1 / Q8_0)
     if (qtype == PGMOE_Q8_0) return 0;
     return (int64_t)row_groups((int)rows) * (cols / 256) * 4 * 1024;
 }
@@ -186,6 +208,10 @@ int launch_scale_plane(int qtype, const uint8_t* src, int64_t n_mats, int64_t ro
     if (n == 0) return PGMOE_OK;
     const dim3 grid((unsigned)((n + 255) / 256));
     switch (qtype) {
+    case PGMOE_Q4_1:
+        PG_LAUNCH(scale_plane_kernel<PGMOE_Q4_1>, grid, dim3(256), 0, st, src, n_mats, (int)rows, nb, src_stride,
+                  dst, dst_stride);
+        break;
     case PGMOE_Q4_K:
         PG_LAUNCH(scale_plane_kernel<PGMOE_Q4_K>, grid, dim3(256), 0, st, src, n_mats, (int)rows, nb, src_stride,
                   dst, dst_stride);
@@ -211,9 +237,10 @@ int64_t layout_bytes(int qtype, int64_t rows, int64_t cols) {
     case PGMOE_Q4_K: return ng * nb * 9 * 1024;
     case PGMOE_Q5_K: return ng * nb * 11 * 1024;
     case PGMOE_Q6_K: return ng * nb * (13 * 1024 + 128);
+    case PGMOE_Q4_0:  // stored as Q4_1
+    case PGMOE_Q4_1: return ng * nb * 10 * 1024;
     case PGMOE_Q8_0:
-    case PGMOE_Q4_0:
-    case PGMOE_Q5_0: return ng * nb * 17 * 1024;  // Q4_0 / Q5_0 are stored as Q8_0
+    case PGMOE_Q5_0: return ng * nb * 17 * 1024;  // Q5_0 is stored as Q8_0
     default: return -1;
     }
 }
@@ -240,6 +267,9 @@ int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows,
         break;
     case PGMOE_Q4_0:
         PG_LAUNCH(relayout_kernel<PGMOE_Q4_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        break;
+    case PGMOE_Q4_1:
+        PG_LAUNCH(relayout_kernel<PGMOE_Q4_1>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
         break;
     case PGMOE_Q5_0:
         PG_LAUNCH(relayout_kernel<PGMOE_Q5_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);

@@ -14,9 +14,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libpgmoe.so")
 ABI_VERSION = 3
 
-Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 6, 8, 12, 13, 14
-# GGUF expert formats with a HIP path; Q4_0 and Q5_0 are relaid out as Q8_0 (their values exactly)
-SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q5_0)
+Q4_0, Q4_1, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 3, 6, 8, 12, 13, 14
+# GGUF expert formats with a HIP path; Q4_0 is relaid out as Q4_1, Q5_0 as Q8_0 (their values exactly)
+SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0)
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

@@ -35,7 +35,7 @@ from .workspace import WorkspacePool
 
 _F32, _F16, _BF16 = 0, 1, 30
 _FLOAT_TYPES = (_F32, _F16, _BF16)
-_W4_TYPES = (2, 12)  # Q4_0, Q4_K: the reference's 4-bit "w4" mode
+_W4_TYPES = (2, 3, 12)  # Q4_0, Q4_1, Q4_K: the reference's 4-bit "w4" mode
 _OUT = {torch.float32: 0, torch.float16: 1}
 
 
@@ -66,7 +66,7 @@ class GGUFQuantLinear(nn.Module):
             return
         if gguf_qtype not in SUPPORTED_QTYPES:
             raise NotImplementedError(f"ggml type {gguf_qtype} has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, "
-                                      "Q8_0, and Q4_0 / Q5_0 relaid out as Q8_0)")
+                                      "Q8_0, Q4_1, and Q4_0 / Q5_0 relaid out as Q4_1 / Q8_0)")
         if self.in_features % 256:
             raise NotImplementedError(f"{self.in_features} input features is not a multiple of 256")
         self.qtype = ops.device_qtype(gguf_qtype)

@@ -9,8 +9,8 @@ pygguf_engine/model.py:849-937, reading the same tensors:
     blk.{i}.ffn_gate_inp_shexp.weight       optional shared-expert sigmoid gate [H]
 
 and the config fields ``n_experts``, ``n_experts_used``, ``norm_topk_prob`` and ``arch``.
-Expert weights stay in GGUF block form on the device (Q4_K as-is, Q6_K / Q8_0 moved
-into aligned planes of the same bits); the whole forward is one C-ABI call that
+Expert weights stay in GGUF block form on the device (the same bits moved into 64-row
+tiles; Q4_0 / Q5_0 stored with the same values as Q4_1 / Q8_0); the whole forward is one C-ABI call that
 enqueues router, top-k, dispatch, expert products and combine without a host sync.
 """
 
@@ -34,7 +34,7 @@ _load_lock = threading.Lock()
 
 def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.Tensor:
     """fp32 copy of a router / gate / norm tensor on ``device`` (quant_kernels.py:1095-1114):
-    F32 / F16 / BF16 converted, and quantised ones (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q5_0; the
+    F32 / F16 / BF16 converted, and quantised ones (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0; the
     reference's gguf.quants.dequantize branch) dequantised once on the device to the values
     the ggml block definitions give.  CPU targets take the float types only."""
     info = gguf_file.tensors[name]
@@ -75,7 +75,8 @@ class _ExpertTensor:
         if self.gguf_qtype not in SUPPORTED_QTYPES:
             raise NotImplementedError(
                 f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
-                "has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, Q8_0, and Q4_0 / Q5_0 relaid out as Q8_0)")
+                "has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, Q8_0, Q4_1, and Q4_0 / Q5_0 relaid out as Q4_1 / "
+                "Q8_0)")
         if self.cols % 256:
             raise ValueError(f"{name}: {self.cols} input features is not a multiple of 256")
         raw_np = gguf_file.get_tensor_bytes(name)

@@ -23,8 +23,8 @@ import numpy as np
 
 from .gguf import GGMLType, InMemoryGGUF, MoEConfig
 
-Q4_0, Q5_0, Q4_K, Q5_K, Q6_K, Q8_0 = (GGMLType.Q4_0, GGMLType.Q5_0, GGMLType.Q4_K, GGMLType.Q5_K, GGMLType.Q6_K,
-                                      GGMLType.Q8_0)
+Q4_0, Q4_1, Q5_0, Q4_K, Q5_K, Q6_K, Q8_0 = (GGMLType.Q4_0, GGMLType.Q4_1, GGMLType.Q5_0, GGMLType.Q4_K,
+                                            GGMLType.Q5_K, GGMLType.Q6_K, GGMLType.Q8_0)
 
 __all__ = ["LayerSpec", "CONFIGS", "SyntheticLayer", "DenseSpec", "DENSE_CONFIGS", "SyntheticDense",
            "random_blocks", "zipf_bias"]
@@ -94,6 +94,13 @@ def random_blocks(rng: np.random.Generator, qtype: int, rows: int, cols: int,
         raw = rng.integers(0, 256, size=(nb, 22), dtype=np.uint8)
         d = (np.abs(rng.standard_normal(nb)) * (0.02 * scale)).astype(np.float16)
         raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+    elif qtype == Q4_1:  # d = |N| * 0.02 scale, m = -N(0, 1) * 0.1 scale (centres the codes)
+        nb = rows * (cols // 32)
+        raw = rng.integers(0, 256, size=(nb, 20), dtype=np.uint8)
+        d = (np.abs(rng.standard_normal(nb)) * (0.02 * scale)).astype(np.float16)
+        m = (-np.abs(rng.standard_normal(nb)) * (0.1 * scale)).astype(np.float16)
+        raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        raw[:, 2:4] = m.view(np.uint8).reshape(nb, 2)
     elif qtype == Q4_0:
         nb = rows * (cols // 32)
         raw = rng.integers(0, 256, size=(nb, 18), dtype=np.uint8)

@@ -39,7 +39,9 @@ def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
         if rows % 64 == 0:  # no padding: exactly the GGUF bytes
             assert L.pgmoe_weight_bytes(qt, rows, cols) == rows * (cols // per) * bb
     assert L.pgmoe_weight_bytes(12, 4, 100) == -1  # not a whole K-quant block row
-    assert L.pgmoe_weight_bytes(3, 4, 256) == -1   # Q4_1 has no kernel
+    assert L.pgmoe_weight_bytes(7, 4, 256) == -1   # Q5_1 has no kernel
+    assert L.pgmoe_weight_bytes(10, 4, 256) == -1  # nor Q2_K
+    assert L.pgmoe_weight_bytes(3, 64, 256) == 64 * 8 * 20  # Q4_1: the GGUF bytes
     assert L.pgmoe_weight_bytes(6, 4, 256) == L.pgmoe_weight_bytes(8, 4, 256)  # Q5_0 is stored as Q8_0
     assert L.pgmoe_weight_bytes(8, 4, 96) == -1    # rows must be whole 256-weight tiles
     assert L.pgmoe_weight_bytes(8, 4, 320) == -1

@@ -20,7 +20,7 @@ from pgmoe.synth import random_blocks
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q4_K, Q6_K, Q8_0 = 2, 12, 14, 8
+Q4_0, Q4_1, Q4_K, Q6_K, Q8_0 = 2, 3, 12, 14, 8
 QT = {"q4_k": Q4_K, "q6_k": Q6_K, "q8_0": Q8_0}
 
 
@@ -36,7 +36,7 @@ def _lin(qt, N, K, seed, dev, bias=False, scale=0.01):
     rng = np.random.default_rng(seed)
     raw = random_blocks(rng, qt, N, K, scale)
     b = torch.from_numpy(rng.standard_normal(N).astype(np.float16)).float() if bias else None
-    mode = "w4" if qt in (Q4_0, Q4_K) else "w8"
+    mode = "w4" if qt in (Q4_0, Q4_1, Q4_K) else "w8"
     return GGUFQuantLinear(mode, K, N, qt, raw=raw, bias=b, device=dev), raw, b
 
 
@@ -78,7 +78,8 @@ def test_reference_matmul_golden(dev, golden, name):
 
 @pytest.mark.parametrize("qt,N,K,bias", [(Q4_K, 4096, 2048, False), (Q6_K, 512, 2048, True),
                                          (Q8_0, 3584, 3584, True), (Q4_K, 1000, 4096, False),
-                                         (Q6_K, 32000, 4096, False), (Q4_0, 2048, 2048, False)])
+                                         (Q6_K, 32000, 4096, False), (Q4_0, 2048, 2048, False),
+                                         (Q4_1, 1536, 2048, True)])
 @pytest.mark.parametrize("M", [1, 8, 512])
 def test_linear_shapes(dev, qt, N, K, bias, M):
     log(f"linear qt={qt} N={N} K={K} bias={bias} M={M}")
@@ -124,7 +125,7 @@ def test_fused_pack_equals_separate(dev):
 
 
 def test_embed_lookup(dev):
-    for qt, N, K in ((Q4_K, 300, 512), (Q6_K, 77, 768), (Q8_0, 129, 256)):
+    for qt, N, K in ((Q4_K, 300, 512), (Q6_K, 77, 768), (Q8_0, 129, 256), (Q4_1, 70, 512), (Q4_0, 65, 256)):
         lin, raw, _ = _lin(qt, N, K, qt, dev, scale=1.0)
         ids = torch.tensor([[0, N - 1, 5], [64, 63, 5]], dtype=torch.int64)
         got = lin.embed_lookup(ids, dtype=torch.float32)
@@ -144,4 +145,4 @@ def test_unsupported_widths_and_formats(dev):
     with pytest.raises(NotImplementedError):
         GGUFQuantLinear("w8", 96, 4, Q8_0, raw=np.zeros(4 * 3 * 34, np.uint8), device=dev)
     with pytest.raises(NotImplementedError):
-        GGUFQuantLinear("w4", 256, 4, 3, raw=np.zeros(4 * 8 * 20, np.uint8), device=dev)  # Q4_1
+        GGUFQuantLinear("w8", 256, 4, 7, raw=np.zeros(4 * 8 * 24, np.uint8), device=dev)  # Q5_1

@@ -14,7 +14,7 @@ from pgmoe.synth import random_blocks
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-Q4_K, Q5_K, Q6_K, Q8_0 = 12, 13, 14, 8
+Q4_1, Q4_K, Q5_K, Q6_K, Q8_0 = 3, 12, 13, 14, 8
 
 
 @pytest.fixture(scope="module")
@@ -28,8 +28,8 @@ def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
     """The device layout of include/pgmoe.h (64-row tiles of 16-byte chunks), in numpy."""
     out = np.zeros(n_mats * stride, dtype=np.uint8)
     nb, ng = cols // 256, (rows + 63) // 64
-    bpb = {Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 272}[qtype]  # GGUF bytes per 256 weights
-    CH = {Q4_K: 9, Q5_K: 11, Q6_K: 13, Q8_0: 17}[qtype]
+    bpb = {Q4_1: 160, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 272}[qtype]  # GGUF bytes per 256 weights
+    CH = {Q4_1: 10, Q4_K: 9, Q5_K: 11, Q6_K: 13, Q8_0: 17}[qtype]
     sb = raw.reshape(n_mats, rows, nb, bpb)
     for m in range(n_mats):
         base = m * stride
@@ -38,7 +38,18 @@ def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
             for b in range(nb):
                 blk = sb[m, r, b]
                 t = base + (g * nb + b) * CH * 1024 + rr * 16
-                if qtype == Q5_K:  # header + qs as Q4_K, then the fifth bits per quarter
+                if qtype == Q4_1:  # d's, m's, then the codes in the Q4_K arrangement
+                    for j in range(8):
+                        bj = blk[20 * j:20 * j + 20]
+                        out[t + 2 * j:t + 2 * j + 2] = bj[0:2]
+                        out[t + 1024 + 2 * j:t + 1024 + 2 * j + 2] = bj[2:4]
+                    code = np.concatenate([np.concatenate([blk[20 * j + 4:20 * j + 20] & 15, blk[20 * j + 4:20 * j + 20] >> 4])
+                                           for j in range(8)])  # element 32j + l
+                    qs = np.array([code[64 * (k >> 5) + (k & 31)] | (code[64 * (k >> 5) + 32 + (k & 31)] << 4)
+                                   for k in range(128)], dtype=np.uint8)
+                    for c in range(8):
+                        out[t + (2 + c) * 1024:t + (2 + c) * 1024 + 16] = qs[16 * c:16 * c + 16]
+                elif qtype == Q5_K:  # header + qs as Q4_K, then the fifth bits per quarter
                     for c in range(9):
                         src = 0 if c == 0 else 48 + 16 * (c - 1)
                         out[t + c * 1024:t + c * 1024 + 16] = blk[src:src + 16]
@@ -66,7 +77,8 @@ def _np_relayout(qtype, raw, n_mats, rows, cols, stride):
 
 
 @pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q8_0, 5, 256, 2),
-                                                    (Q6_K, 130, 768, 2), (Q8_0, 64, 512, 1), (Q5_K, 70, 512, 2)])
+                                                    (Q6_K, 130, 768, 2), (Q8_0, 64, 512, 1), (Q5_K, 70, 512, 2),
+                                                    (Q4_1, 70, 512, 2)])
 def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
     from pgmoe import ops
     rng = np.random.default_rng(rows * cols)
@@ -77,7 +89,7 @@ def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
     ref = _np_relayout(qtype, raw, n_mats, rows, cols, stride)
     # bytes past the tiles (alignment padding between matrices) are unspecified
     ng, nb = (rows + 63) // 64, cols // 256
-    mb = ng * nb * {Q4_K: 9 * 1024, Q5_K: 11 * 1024, Q6_K: 13 * 1024 + 128, Q8_0: 17 * 1024}[qtype]
+    mb = ng * nb * {Q4_1: 10 * 1024, Q4_K: 9 * 1024, Q5_K: 11 * 1024, Q6_K: 13 * 1024 + 128, Q8_0: 17 * 1024}[qtype]
     for m in range(n_mats):
         assert np.array_equal(got[m * stride:m * stride + mb], ref[m * stride:m * stride + mb])
 
@@ -158,7 +170,7 @@ def _np_scale_plane(qtype, raw, n_mats, rows, cols):
     """The scale plane of include/pgmoe.h in numpy (fp32, the kernel's expressions and
     operation order): per (64-row group, super-block, unit c) 64 rows of four floats."""
     nb, ng = cols // 256, (rows + 63) // 64
-    bpb = {Q4_K: 144, Q5_K: 176, Q6_K: 210}[qtype]
+    bpb = {Q4_1: 160, Q4_K: 144, Q5_K: 176, Q6_K: 210}[qtype]
     sb = np.zeros((n_mats, ng * 64, nb, bpb), dtype=np.uint8)  # pad rows: zero bytes
     sb[:, :rows] = raw.reshape(n_mats, rows, nb, bpb)
     out = np.zeros((n_mats, ng, nb, 4, 64, 4), dtype=np.float32)
@@ -169,7 +181,12 @@ def _np_scale_plane(qtype, raw, n_mats, rows, cols):
             for b in range(nb):
                 blk = sb[m, r, b]
                 for c in range(4):
-                    if qtype in (Q4_K, Q5_K):
+                    if qtype == Q4_1:  # a = d, c = m - 1024 a of blocks 2c, 2c + 1
+                        vals = []
+                        for s in (2 * c, 2 * c + 1):
+                            dq, mq = blk[20 * s:20 * s + 4].view(np.float16).astype(np.float32)
+                            vals += [f32(dq), f32(mq) - f32(1024.0) * f32(dq)]
+                    elif qtype in (Q4_K, Q5_K):
                         d, dmin = blk[0:4].view(np.float16).astype(np.float32)
                         q = blk[4:16].astype(np.int64)
                         vals = []
@@ -191,7 +208,7 @@ def _np_scale_plane(qtype, raw, n_mats, rows, cols):
 
 
 @pytest.mark.parametrize("qtype,rows,cols,n_mats", [(Q4_K, 8, 512, 3), (Q6_K, 7, 768, 3), (Q4_K, 130, 256, 2),
-                                                    (Q5_K, 70, 512, 2)])
+                                                    (Q5_K, 70, 512, 2), (Q4_1, 70, 512, 2)])
 def test_scale_plane_bits(dev, qtype, rows, cols, n_mats):
     """The load-time scale plane equals its numpy restatement bit for bit (pad rows too)."""
     from pgmoe import ops
@@ -230,7 +247,9 @@ def test_mfma_products_need_the_scale_plane(dev):
     (Q8_0, Q8_0, 256, 512, 6, 3, 70, 1), (Q6_K, Q8_0, 256, 256, 3, 1, 9, 1),
     (Q4_K, Q6_K, 512, 256, 8, 2, 3, 1), (Q8_0, Q4_K, 512, 256, 3, 2, 17, 1),
     (Q5_K, Q5_K, 512, 256, 8, 2, 1, 0), (Q5_K, Q5_K, 256, 512, 4, 2, 8, 0), (Q5_K, Q6_K, 768, 512, 5, 2, 6, 0),
-    (Q5_K, Q5_K, 512, 256, 8, 2, 40, 1), (Q5_K, Q5_K, 256, 512, 4, 2, 130, 1), (Q6_K, Q5_K, 512, 256, 3, 1, 9, 1)])
+    (Q5_K, Q5_K, 512, 256, 8, 2, 40, 1), (Q5_K, Q5_K, 256, 512, 4, 2, 130, 1), (Q6_K, Q5_K, 512, 256, 3, 1, 9, 1),
+    (Q4_1, Q4_1, 512, 256, 8, 2, 1, 0), (Q4_1, Q4_1, 256, 512, 4, 2, 8, 0), (Q4_1, Q6_K, 512, 256, 8, 2, 40, 1),
+    (Q4_1, Q4_1, 256, 512, 4, 2, 130, 1)])
 def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
     """inter and the weighted down partials against float64 numpy over decoded weights.
     Tolerance: the decode GEMV forms exact fp16 products of (1024 + code) and x and

@@ -1,13 +1,15 @@
 """Q4_0 experts (the format of the reference's synthetic qwen35moe test model,
-tests/test_pygguf_engine.py:424-440): the oracle's Q4_0 decoder pinned by reduction to
-the golden-pinned Q8_0 decoder, and the C-ABI sizes (Q4_0 is stored as Q8_0)."""
+tests/test_pygguf_engine.py:424-440) and Q4_1 / Q5_0: the oracle's decoders pinned by
+reduction to the golden-pinned Q8_0 decoder (Q4_0, Q5_0) and to Q4_0 (Q4_1 with m = -8d),
+closed forms on exact values, the restated W4 repack of the reference, and the C-ABI sizes
+(Q4_0 is stored as Q4_1, Q5_0 as Q8_0)."""
 
 import numpy as np
 
 import oracle
 from pgmoe.synth import random_blocks
 
-Q4_0, Q8_0 = 2, 8
+Q4_0, Q4_1, Q8_0 = 2, 3, 8
 
 
 def q4_0_as_q8_0(raw: np.ndarray) -> np.ndarray:
@@ -37,11 +39,47 @@ def test_q4_0_decoder_equals_q8_0_of_the_same_values():
     np.testing.assert_array_equal(v[0, 16:], np.full(16, 0.5 * 7))
 
 
-def test_q4_0_sizes_are_q8_0_sizes():
+def q4_0_as_q4_1(raw: np.ndarray) -> np.ndarray:
+    """Q4_0 blocks -> the Q4_1 blocks of the same values: same d and codes, m = -8d."""
+    b = raw.reshape(-1, 18)
+    out = np.empty((b.shape[0], 20), dtype=np.uint8)
+    out[:, 0:2] = b[:, 0:2]
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32)
+    out[:, 2:4] = (-8.0 * d).astype(np.float16).view(np.uint8)
+    out[:, 4:20] = b[:, 2:18]
+    return out.reshape(-1)
+
+
+def test_q4_1_decoder():
+    rng = np.random.default_rng(8)
+    raw = random_blocks(rng, Q4_0, 5, 512)
+    np.testing.assert_array_equal(oracle.dequant(Q4_1, q4_0_as_q4_1(raw), 5, 512), oracle.dequant(Q4_0, raw, 5, 512))
+    # closed form: d q + m, weight l from the low nibble of byte l, 16 + l from the high one
+    blk = np.zeros(20, dtype=np.uint8)
+    blk[0:2] = np.array([0.5], dtype=np.float16).view(np.uint8)
+    blk[2:4] = np.array([-1.25], dtype=np.float16).view(np.uint8)
+    blk[4:20] = np.arange(16, dtype=np.uint8) | (np.uint8(3) << 4)
+    v = oracle.dequant(Q4_1, blk, 1, 32)[0]
+    np.testing.assert_array_equal(v[:16], 0.5 * np.arange(16) - 1.25)
+    np.testing.assert_array_equal(v[16:], np.full(16, 0.5 * 3 - 1.25))
+
+
+def test_q4_1_and_q4_0_match_the_reference_w4_repack_restated():
+    from oracle import torch_port
+    rng = np.random.default_rng(9)
+    for qt in (Q4_0, Q4_1):
+        raw = random_blocks(rng, qt, 6, 512)
+        np.testing.assert_array_equal(torch_port.dense_weights((qt, 6, 512, raw)), oracle.dequant(qt, raw, 6, 512))
+
+
+def test_q4_0_sizes_are_q4_1_sizes():
     from pgmoe._lib import lib
     L = lib()
     for rows, cols in ((64, 256), (100, 2048), (768, 2048)):
-        assert L.pgmoe_weight_bytes(Q4_0, rows, cols) == L.pgmoe_weight_bytes(Q8_0, rows, cols) > 0
+        ng, nb = (rows + 63) // 64, cols // 256
+        assert L.pgmoe_weight_bytes(Q4_0, rows, cols) == L.pgmoe_weight_bytes(Q4_1, rows, cols) == ng * nb * 10 * 1024
+        assert L.pgmoe_scale_plane_bytes(Q4_1, rows, cols) == ng * nb * 4 * 1024
+        assert L.pgmoe_scale_plane_bytes(Q4_0, rows, cols) == -1  # a source format only
         assert L.pgmoe_scale_plane_bytes(Q8_0, rows, cols) == 0
 
 
