@@ -1021,7 +1021,7 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     //    With TM >= 4 tokens, TM / 2 waves share a row, two tokens each (the logits are per
     //    (token, row), so the split changes no value; a wave then keeps all of its chunk
     //    loads in flight at once).
-    constexpr int TS = TM >= 4 ? TM / 2 : 1, TH = TM / TS;  // router waves per row, tokens per wave
+    constexpr int TS = TM < 4 ? TM : 4, TH = TM / TS;  // router waves per row, tokens per wave
     for (int gi = w; fused && gi < rpb * TS; gi += nw) {  // (row, token group) gi; a block with
         const int e = bid * rpb + gi / TS, t0 = (gi % TS) * TH;  // fewer waves takes several
         if (e < rows && t0 < M) {
@@ -1451,7 +1451,7 @@ inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const flo
     const int W = gu_waves(dp.mode == kLinear ? ((g.K >> 8) + 1) / 2 : g.K >> 8), gx = div_up(g.N, 16);
     const int gy = gu_slot_blocks(max_active);
     // every router row needs a wave (TM / 2 with 4+ tokens)
-    const int gmin = dp.mode == kRoute ? div_up((dp.E + (rt.extra_w ? 1 : 0)) * (TM >= 4 ? TM / 2 : 1), gx * W) : 1;
+    const int gmin = dp.mode == kRoute ? div_up((dp.E + (rt.extra_w ? 1 : 0)) * (TM < 4 ? TM : 4), gx * W) : 1;
     const size_t sh = gu_lds_bytes(dp.M, g.K);
     // slot rows: as many as fit in one round of resident blocks (blocks loop over the rest)
 #define PG_GU(MODE, RE)                                                                                         \
