@@ -1003,7 +1003,14 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ RouteShared R;
     __shared__ float red[16][TM][RB];  // per-wave row partials
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nth = blockDim.x, nw = nth >> 6;
+    // With 4+ tokens (blocks then take several slots) the first pass of the next slot is
+    // loaded before this slot's epilogue, so its weights stream during the reduction and
+    // the inter stores; with fewer the registers this takes cost more than it saves (and
+    // Q5_K's fifth-bit words leave no room for it within 128 registers).  With 4+ tokens
+    // the wave index is made scalar, which frees registers.
+    constexpr bool pf = TM >= 4 && QT != PGMOE_Q5_K && (MODE == kRoute || MODE == kDispatch);
+    const int tid = threadIdx.x, lane = tid & 63, nth = blockDim.x, nw = nth >> 6;
+    const int w = TM >= 4 ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int M = dp.M;
     const int nb = K >> 8, xrs = (K >> 6) * kXuH, srs = K >> 4;
     const bool pub = MODE == kRoute && blockIdx.x == 0 && blockIdx.y == 0;
@@ -1096,31 +1103,57 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     const int row = blockIdx.x * RB + r;  // < row_groups(N) * 64: padded tile rows are readable
     constexpr bool lin = MODE == kLinear;  // one matrix: item = super-block, every wave on it
     const int nit = lin ? nb : 2 * nb;
-    for (int a = blockIdx.y;; a += gridDim.y) {
-        SlotInfo si;
+    auto slot_at = [&](int a) -> SlotInfo {
         if constexpr (MODE == kRoute && TM == 1)
-            si = pub ? slot_info<1>(R, M, a, lane, w == 0 && a == 0) : slot_info1(R, a, topk);
+            return pub ? slot_info<1>(R, M, a, lane, w == 0 && a == 0) : slot_info1(R, a, topk);
         else if constexpr (MODE == kRoute)
-            si = slot_info<TM>(R, M, a, lane, w == 0 && pub && a == 0);
+            return slot_info<TM>(R, M, a, lane, w == 0 && pub && a == 0);
         else
-            si = slot_plain<MODE>(dp, a, topk);
-        if (si.e < 0) break;  // uniform over the block
+            return slot_plain<MODE>(dp, a, topk);
+    };
+    auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
+        return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
+    };
+    // items, two per wave at a time (both quarters' loads in flight together): pass `it`
+    // holds items it and it + nw (the second clamped to a readable item past the end);
+    // q0, q1: the prefetched pass
+    Qtr<QT> q0, q1;
+    auto load_pass = [&](const uint8_t* mat, int it) {
+        const int it1 = min(it + nw, nit - 1);
+        load_qtr<QT>(q0, mat, N, nb, row, lin ? it : it >> 1, p);
+        load_qtr<QT>(q1, mat, N, nb, row, lin ? it1 : it1 >> 1, p);
+    };
+    int a = blockIdx.y;
+    SlotInfo si = slot_at(a);
+    if constexpr (pf)
+        if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
+    while (si.e >= 0) {  // uniform over the block
         PG_MARK(1, 2);
-        // items, two per wave at a time (both quarters' loads in flight together)
-        const uint8_t* mat = (!lin && (w & 1)) ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
+        const uint8_t* mat = mat_of(si.e);
         float acc[TM];
 #pragma unroll
         for (int t = 0; t < TM; ++t) acc[t] = 0.f;
         for (int it = w; it < nit; it += 2 * nw) {
             const int it1 = it + nw;
-            Qtr<QT> q0, q1;
             const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
-            load_qtr<QT>(q0, mat, N, nb, row, j0, p);
-            load_qtr<QT>(q1, mat, N, nb, row, j1, p);
-            gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-            if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+            if constexpr (pf) {
+                if (it != w) load_pass(mat, it);
+                gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+            } else {
+                Qtr<QT> l0, l1;
+                load_qtr<QT>(l0, mat, N, nb, row, j0, p);
+                load_qtr<QT>(l1, mat, N, nb, row, j1, p);
+                gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+            }
         }
         PG_MARK(1, 4);
+        SlotInfo sn;
+        if constexpr (pf) {
+            sn = slot_at(a + gridDim.y);
+            if (sn.e >= 0 && w < nit) load_pass(mat_of(sn.e), w);
+        }
         // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
 #pragma unroll
         for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
@@ -1162,6 +1195,11 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         }
         if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
         __syncthreads();                           // red is rewritten by the next slot
+        a += gridDim.y;
+        if constexpr (pf)
+            si = sn;
+        else
+            si = slot_at(a);
     }
     // block (0, 0) publishes the routing last: its stores then stay off the block's own
     // critical path (a barrier would wait for them)
