@@ -83,7 +83,7 @@ int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum
 #undef CALL
 }
 
-bool decode_fused_down(int P, int K) { return P <= 128 && dc_lds_bytes(P, K) <= dec_lds_limit(); }
+bool decode_fused_down(int P, int K) { return P <= 128 && dc_chunk(P, K) >= 1; }
 
 // The device's LDS per block less 16 KB for the decode kernels' static arrays, cached per
 // device (hipDeviceAttributeMaxSharedMemoryPerBlock).

@@ -1244,6 +1244,36 @@ __device__ __forceinline__ void dc_item(const Qtr<QT>& q, bool valid, int it, in
     }
 }
 
+// Lanes -> rows (lanes r + 8k), waves -> tokens' outputs: out[t, row] = the block's sum
+// (+ shared[t, row] * sigmoid(shared_logit[t])).  red: [16][TM][8] LDS.
+template <int TM>
+__device__ __forceinline__ void dc_finish(float* acc, float (*red)[TM][8], int M, int N,
+                                          const float* __restrict__ shared, const float* __restrict__ shared_logit,
+                                          float* __restrict__ out) {
+    constexpr int RB = 8;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nth = blockDim.x, nw = nth >> 6;
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+    if (lane < RB) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) red[w][t][lane] = acc[t];
+    }
+    __syncthreads();
+    for (int i = tid; i < M * RB; i += nth) {
+        const int t = i / RB, rr = i % RB;
+        float v = 0.f;
+        for (int ww = 0; ww < nw; ++ww) v += red[ww][t][rr];
+        const int orow = blockIdx.x * RB + rr;
+        if (orow < N) {
+            if (shared) {
+                const float g = shared_logit ? 1.0f / (1.0f + expf(-shared_logit[t])) : 1.0f;
+                v += shared[(int64_t)t * N + orow] * g;
+            }
+            out[(int64_t)t * N + orow] = v;
+        }
+    }
+}
+
 template <int QT, int TM>
 __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict__ dbase, int64_t dstride, int N,
                                                       int K, const float* __restrict__ inter,
@@ -1307,30 +1337,98 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
         load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, row, it1 % nb, p);
     }
     PG_MARK(3, 2);
-    // 3. lanes -> rows (lanes r + 8k), waves -> tokens' outputs
-#pragma unroll
-    for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
-    if (lane < RB) {
-#pragma unroll
-        for (int t = 0; t < TM; ++t) red[w][t][r] = acc[t];
-    }
-    __syncthreads();
-    PG_MARK(3, 3);
-    for (int i = tid; i < M * RB; i += nth) {
-        const int t = i / RB, rr = i % RB;
-        float v = 0.f;
-        for (int ww = 0; ww < nw; ++ww) v += red[ww][t][rr];
-        const int orow = blockIdx.x * RB + rr;
-        if (orow < N) {
-            if (shared) {
-                const float g = shared_logit ? 1.0f / (1.0f + expf(-shared_logit[t])) : 1.0f;
-                v += shared[(int64_t)t * N + orow] * g;
-            }
-            out[(int64_t)t * N + orow] = v;
-        }
-    }
+    dc_finish<TM>(acc, red, M, N, shared, shared_logit, out);
     PG_MARK(3, 4);
     PG_FLUSH(3);
+}
+
+// Fused down + combine when the inter / isum rows do not fit in LDS at once: the same
+// block, lanes and sums as dec_dc_kernel, with the rows staged one chunk of JC super-block
+// columns at a time (the host picks the most that fit).  In a chunk of JCc columns
+// starting at super-block j0, the items (active slot a, super-block j0 + jj),
+// it = a * JCc + jj, go two per wave per pass as in dec_dc_kernel; the first pass of the
+// next chunk is loaded before that chunk is staged.  Each lane's item order depends only
+// on the routing and JC, so results are reproducible run to run.
+// Dynamic LDS: xs [P][JC*4][68] f32 | iss [P][JC*16] f32.
+template <int QT, int TM>
+__global__ __launch_bounds__(1024) void dec_dc_chunk_kernel(const uint8_t* __restrict__ dbase, int64_t dstride,
+                                                            int N, int K, int JC, const float* __restrict__ inter,
+                                                            const float* __restrict__ isum,
+                                                            const int32_t* __restrict__ desc, int M, int P,
+                                                            const float* __restrict__ shared,
+                                                            const float* __restrict__ shared_logit,
+                                                            float* __restrict__ out, uint64_t* __restrict__ clear,
+                                                            int n_clear) {
+    constexpr int RB = 8;
+    clear_words(clear, n_clear);  // the gate/up launch is done with them
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int d_pb[128], d_cnt[128], d_tok[128];
+    __shared__ float d_w[128];
+    __shared__ float red[16][TM][RB];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nth = blockDim.x, nw = nth >> 6;
+    const int nb = K >> 8, xrs = JC * 4 * kXuF, srs = JC * 16;
+    float* xs = (float*)smem;
+    float* iss = xs + P * xrs;
+    const int r = lane & 7, p = (lane >> 3) & 3, u = lane >> 5;
+    const int row = blockIdx.x * RB + r;
+    // 1. the experts of this lane's first two items, their weights, then the pair table
+    const bool ident = desc == nullptr;
+    const int A = ident ? 1 : desc[0];  // active slots
+    int j0 = 0, JCc = JC < nb ? JC : nb;
+    Qtr<QT> q0, q1;
+    auto load_pass = [&](int it0, int it1) {  // items it0, it1 of the current chunk (any)
+        const int a0 = it0 / JCc, a1 = it1 / JCc;
+        const int e0 = ident ? 0 : desc[kDescSlot + 4 * min(a0, 127)];  // both slots first
+        const int e1 = ident ? 0 : desc[kDescSlot + 4 * min(a1, 127)];
+        load_qtr<QT>(q0, dbase + (int64_t)(a0 < A ? e0 : 0) * dstride, N, nb, row, j0 + it0 % JCc, p);
+        load_qtr<QT>(q1, dbase + (int64_t)(a1 < A ? e1 : 0) * dstride, N, nb, row, j0 + it1 % JCc, p);
+    };
+    int it0 = 2 * w + u, it1 = it0 + 2 * nw;
+    load_pass(it0, it1);
+    for (int i = tid; i < P; i += nth) {
+        d_pb[i] = ident ? 0 : desc[kDescSlot + 4 * i + 1];
+        d_cnt[i] = ident ? P : desc[kDescSlot + 4 * i + 2];
+        d_tok[i] = ident ? i : desc[kDescPair + 2 * i];
+        d_w[i] = ident ? 1.0f : __builtin_bit_cast(float, desc[kDescPair + 2 * i + 1]);
+    }
+    float acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+    for (;;) {
+        {  // stage the chunk: columns [256 j0, 256 (j0 + JCc)) of every pair's rows and sums
+            const int kq = JCc * 64, sq = JCc * 4;  // 16-byte words of a row's chunk, of its sums
+            const float* src = inter + 256 * j0;
+            copy_idx<4, u32x4>(
+                P * kq, tid, nth, [=](int i) { return (const u32x4*)(src + (int64_t)(i / kq) * K + 4 * (i % kq)); },
+                [=](int i) { return (u32x4*)(xs + (i / kq) * xrs + xpos_f(4 * (i % kq))); });
+            const float* ssrc = isum + 16 * j0;
+            copy_idx<2, u32x4>(
+                P * sq, tid, nth,
+                [=](int i) { return (const u32x4*)(ssrc + (int64_t)(i / sq) * (K >> 4) + 4 * (i % sq)); },
+                [=](int i) { return (u32x4*)(iss + (i / sq) * srs + 4 * (i % sq)); });
+        }
+        __syncthreads();
+        // 2. the chunk's items, two per lane per pass
+        const int S = A * JCc;
+        for (;;) {
+            dc_item<QT, TM>(q0, it0 < S, it0, JCc, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
+            dc_item<QT, TM>(q1, it1 < S, it1, JCc, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
+            it0 += 4 * nw;
+            it1 += 4 * nw;
+            if (it0 - u >= S) break;  // wave-uniform (it0 - u is the pass's first item): no item left
+            load_pass(it0, it1);      // (rare) more items than lanes: next pass
+        }
+        if (j0 + JCc >= nb) break;
+        // the next chunk's first pass, then (once every wave is done with this chunk) its rows
+        j0 += JCc;
+        JCc = JC < nb - j0 ? JC : nb - j0;
+        it0 = 2 * w + u;
+        it1 = it0 + 2 * nw;
+        load_pass(it0, it1);
+        __syncthreads();
+    }
+    // 3. lanes and waves -> the tokens' outputs
+    dc_finish<TM>(acc, red, M, N, shared, shared_logit, out);
 }
 
 // Per-expert down GEMV: partial[p, row] = w[perm[p]] * (inter_p . d_row) for the pairs of
@@ -1473,10 +1571,21 @@ inline int dc_waves(int items) {
     const int w = (items + 1) / 2;
     return w < 1 ? 1 : w > 16 ? 16 : w;
 }
-inline size_t dc_lds_bytes(int P, int K) { return (size_t)P * (K / 64) * kXuF * 4 + (size_t)P * (K / 16) * 4; }
+// Its staging: JC super-block columns of P inter rows (padded units) and their sums.
+inline size_t dc_lds_bytes(int P, int JC) { return (size_t)P * JC * (4 * kXuF * 4 + 16 * 4); }
+size_t dec_lds_limit();
+// Columns per staging chunk of the fused down + combine: all K / 256 when the rows fit
+// (dec_dc_kernel); else, for rows of at most 32 super-blocks, the most that fit
+// (dec_dc_chunk_kernel); 0: neither (the per-expert down and combine kernels instead,
+// measured faster for longer rows: with K = 14336 and few experts they stream each
+// expert's rows with more blocks).
+inline int dc_chunk(int P, int K) {
+    const int nb = K >> 8;
+    const int jc = (int)(dec_lds_limit() / dc_lds_bytes(P, 1));
+    return jc >= nb ? nb : nb <= 32 ? jc : 0;
+}
 
 // Dynamic LDS a block of the current device may take beside the kernels' static arrays.
-size_t dec_lds_limit();
 // Of gy slot rows of gx blocks each, how many fit in one round of resident blocks of
 // `kernel` on the current device (at least 1): a grid past that waits a whole block
 // duration for its last round.
@@ -1526,9 +1635,14 @@ template <int QT, int TM>
 inline void dc_launch(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
                       int max_active, const float* shared, const float* shared_logit, float* out, uint64_t* clear,
                       int n_clear, hipStream_t st) {
-    const int W = dc_waves(max_active * (d.K >> 8));
-    PG_LAUNCH((dec_dc_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, d.K), st, d.base,
-              d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out, clear, n_clear);
+    const int nb = d.K >> 8, JC = dc_chunk(P, d.K);
+    const int W = dc_waves(max_active * JC);  // items of a chunk
+    if (JC >= nb)
+        PG_LAUNCH((dec_dc_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, nb), st, d.base,
+                  d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out, clear, n_clear);
+    else
+        PG_LAUNCH((dec_dc_chunk_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, JC), st,
+                  d.base, d.stride, d.N, d.K, JC, inter, isum, desc, M, P, shared, shared_logit, out, clear, n_clear);
 }
 
 #define PG_TM(F, QT, RB, W, ...)                   \
@@ -1597,7 +1711,7 @@ int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, con
     int dec_down_combine_q<QT>(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M,   \
                                int P, int max_active, const float* shared, const float* shared_logit, float* out,   \
                                uint64_t* clear, int n_clear, hipStream_t st) {                                      \
-        if (P > 128 || dc_lds_bytes(P, d.K) > dec_lds_limit())                                                      \
+        if (P > 128 || dc_chunk(P, d.K) < 1)                                                                        \
             return fail(PGMOE_E_UNSUPPORTED, "decode down + combine: %d pairs of %d inputs exceed LDS", P, d.K);    \
         PG_TM2(dc_launch, QT, d, inter, isum, desc, M, P, max_active, shared, shared_logit, out, clear, n_clear, \
                st);                                                                                                 \

@@ -115,7 +115,8 @@ int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum
 int decode_desc_words();
 // 64-bit words of the decode router's ready-tagged logits (all copies) for M tokens.
 int decode_rlog_words(int M, int E);
-// Whether the fused down + combine kernel can stage P inter rows of K values.
+// Whether the fused down + combine kernels take P inter rows of K values (staged in LDS
+// whole, or a chunk of super-block columns at a time for rows of up to 32 super-blocks).
 bool decode_fused_down(int P, int K);
 // Prefill grouped GEMMs (gemm.hip); tile_off counts gemm_tile_pairs()-row tiles.
 // raw (optional): scratch of gemm_split_bytes(...) for a split-K run when the tiles would
