@@ -100,7 +100,7 @@ _KNAMES = (("router_gemm_kernel", "router"), ("router_logits_kernel", "router"),
            ("dispatch_kernel", "dispatch"), ("gemm_split_reduce_kernel<true>", "gemm_gateup_reduce"),
            ("gemm_split_reduce_kernel<false>", "gemm_down_reduce"), ("rowscale_kernel", "rowscale"),
            ("combine_kernel", "combine"), ("dec_gu_kernel", "dec_gu"), ("dec_dc_kernel", "dec_dc"),
-           ("dec_down_kernel", "dec_down"))
+           ("dec_dc_chunk_kernel", "dec_dc"), ("dec_down_kernel", "dec_down"))
 
 
 def short_names(raw):
