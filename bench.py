@@ -316,7 +316,10 @@ def load_traffic(kernel: str):
                 rec = json.load(f)
         except (OSError, ValueError):
             continue
-        if rec.get("kernel", "").split("pgmoe::")[-1].startswith(kernel):
+        name = rec.get("kernel_pattern") or rec.get("kernel", "")
+        if name.split("pgmoe::")[-1].startswith(kernel):
+            rec.setdefault("source", f"{os.path.relpath(path, REPO)}: FETCH_SIZE + WRITE_SIZE of "
+                                     f"{name} per dispatch, copy-calibrated")
             return rec.get("bytes_per_launch"), rec
     return None, None
 

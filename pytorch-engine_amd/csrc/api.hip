@@ -107,7 +107,7 @@ static Layout layout_for(const pgmoe_layer* L, int M, int rlog_experts = 0) {
     o.status = take(c, 4);
     o.desc = take(c, gemm ? 0 : (size_t)decode_desc_words() * 4);
     o.xsum = take(c, gemm ? 0 : (size_t)M * (H / 16) * 4);
-    o.isum = take(c, gemm ? 0 : P * (I / 16) * 4);
+    o.isum = take(c, gemm ? 0 : P * (I / 8) * 4);  // 16-row sums, or 8-row sums at one token
     o.s_isum = take(c, (gemm || !L->has_shared) ? 0 : (size_t)M * (L->sh_gate.n_rows / 16) * 4);
     o.logits = take(c, gemm ? (size_t)M * E * 4 : 0);
     o.idx = take(c, P * 4);
@@ -262,7 +262,7 @@ int pgmoe_dense_forward(const pgmoe_dense* D, const uint16_t* x, int32_t M, floa
             return rc;
         // the 8-row, 16-wave down blocks when the SwiGLU rows fit in LDS, else the per-expert one
         if (decode_fused_down(M, g.N))
-            return launch_dec_down_combine(d, WS(float, inter), WS(float, isum), nullptr, M, 1, 1, nullptr, nullptr,
+            return launch_dec_down_combine(d, WS(float, inter), WS(float, isum), 0, nullptr, M, 1, 1, nullptr, nullptr,
                                            out, nullptr, 0, st);
         return launch_dec_down_ident(d, WS(float, inter), WS(float, isum), M, out, st);
     }
@@ -430,7 +430,7 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
                                               WS(float, s_isum), st, L->act)))
                 return rc;
             if (decode_fused_down(M, lm.sd.K))
-                rc = launch_dec_down_combine(lm.sd, WS(float, s_inter), WS(float, s_isum), nullptr, M, 1, 1, nullptr,
+                rc = launch_dec_down_combine(lm.sd, WS(float, s_inter), WS(float, s_isum), 0, nullptr, M, 1, 1, nullptr,
                                              nullptr, WS(float, s_partial), nullptr, 0, st);
             else
                 rc = launch_dec_down_ident(lm.sd, WS(float, s_inter), WS(float, s_isum), M, WS(float, s_partial), st);
@@ -439,9 +439,11 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
             if (sgw) shared_logit = WS(float, s_logit);
         }
         if (fused)
-            return launch_dec_down_combine(lm.down, WS(float, inter), WS(float, isum), WS(int32_t, desc), M, K,
+            return launch_dec_down_combine(lm.down, WS(float, inter), WS(float, isum),
+                                           decode_isum_rows8(lm.gate.qtype, M), WS(int32_t, desc), M, K,
                                            max_active, shared, shared_logit, out, WS(uint64_t, rlog), decode_rlog_words(M, E), st);
-        if ((rc = launch_dec_down(lm.down, WS(float, inter), WS(float, isum), M, WS(int32_t, offsets),
+        // (one token: the down kernel forms its 16-row sums itself from the staged rows)
+        if ((rc = launch_dec_down(lm.down, WS(float, inter), M == 1 ? nullptr : WS(float, isum), M, WS(int32_t, offsets),
                                   WS(int32_t, perm), WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, w),
                                   WS(float, partial), st)))
             return rc;

@@ -13,6 +13,18 @@ namespace pgmoe {
     }                                                                \
     return fail(PGMOE_E_UNSUPPORTED, what ": qtype %d", qt);
 
+bool decode_isum_rows8(int qtype, int M) {
+    if (M != 1) return false;
+    switch (qtype) {
+    case PGMOE_Q4_1: return gu_rows8<PGMOE_Q4_1>();
+    case PGMOE_Q4_K: return gu_rows8<PGMOE_Q4_K>();
+    case PGMOE_Q5_K: return gu_rows8<PGMOE_Q5_K>();
+    case PGMOE_Q6_K: return gu_rows8<PGMOE_Q6_K>();
+    case PGMOE_Q8_0: return gu_rows8<PGMOE_Q8_0>();
+    }
+    return false;
+}
+
 int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,
                       int max_active, float* inter, float* isum, hipStream_t st, int act) {
@@ -74,11 +86,11 @@ int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, 
 #undef CALL
 }
 
-int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int K,
-                            int max_active, const float* shared, const float* shared_logit, float* out,
+int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, int isum8, const int32_t* desc,
+                            int M, int K, int max_active, const float* shared, const float* shared_logit, float* out,
                             uint64_t* clear, int n_clear, hipStream_t st) {
     if (M < 1 || M > kDecTM || M * K > 128) return fail(PGMOE_E_INVALID, "down + combine: 1..%d tokens", kDecTM);
-#define CALL(QT) dec_down_combine_q<QT>(d, inter, isum, desc, M, M * K, max_active, shared, shared_logit, out, clear, n_clear, st)
+#define CALL(QT) dec_down_combine_q<QT>(d, inter, isum, isum8, desc, M, M * K, max_active, shared, shared_logit, out, clear, n_clear, st)
     PG_BY_QTYPE(d.qtype, "decode down + combine", CALL)
 #undef CALL
 }

@@ -965,7 +965,8 @@ __device__ __forceinline__ SlotInfo slot_plain(const DecDisp& dp, int a, int top
     return si;
 }
 
-// Gate/up + SwiGLU.  Block = 16 rows of the experts of active slots blockIdx.y,
+// Gate/up + SwiGLU.  Block = 16 rows (8 for one routed token in the gu_rows8 formats, set
+// out in the kernel) of the experts of active slots blockIdx.y,
 // + gridDim.y, ...; W (even) waves: wave w owns the items it = w, w + W, ... of the
 // 2 * (K/256) (matrix = it & 1, super-block j = it >> 1), lane = (row r = lane & 15,
 // quarter p = lane >> 4).  Every token row is staged in LDS (fp16, padded units) while the
@@ -974,7 +975,8 @@ __device__ __forceinline__ SlotInfo slot_plain(const DecDisp& dp, int a, int top
 // by sorted pair p_begin + t.
 // Dynamic LDS: xs [M][K/64][72] fp16 | xss [M][K/16] f32.
 // xsum (optional): 16-element sums of the x rows [M][K/16] (else computed from xs);
-// isum (optional output): 16-element sums of the inter rows [P][N/16].
+// isum (optional output): 16-element sums of the inter rows [P][N/16] (8-row blocks: 8-element
+// sums [P][N/8]).
 template <int RE>
 __device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteShared& R, bool pub, int lane, int w,
                                             int nw, [[maybe_unused]] unsigned long long& t_ready) {
@@ -990,6 +992,10 @@ __device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteSh
     }
 }
 
+// The one-token routed gate/up runs 8-row blocks (and leaves 8-row sums) for the formats
+// of at most 11 chunks a tile (Q4_1, Q4_K, Q5_K); Q6_K and Q8_0 keep 16-row blocks, which
+// measured faster for their larger rows.
+template <int QT> constexpr bool gu_rows8() { return Tile<QT>::CH <= 11; }
 // MODE: DecMode (fixed per instantiation, so each kernel holds only its own path); RE:
 // logit words per lane of the routing waves (kRoute: E <= 64 * RE).
 template <int QT, int TM, int MODE, int RE>
@@ -1111,95 +1117,146 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         else
             return slot_plain<MODE>(dp, a, topk);
     };
-    auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
-        return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
-    };
-    // items, two per wave at a time (both quarters' loads in flight together): pass `it`
-    // holds items it and it + nw (the second clamped to a readable item past the end);
-    // q0, q1: the prefetched pass
-    Qtr<QT> q0, q1;
-    auto load_pass = [&](const uint8_t* mat, int it) {
-        const int it1 = min(it + nw, nit - 1);
-        load_qtr<QT>(q0, mat, N, nb, row, lin ? it : it >> 1, p);
-        load_qtr<QT>(q1, mat, N, nb, row, lin ? it1 : it1 >> 1, p);
-    };
-    int a = blockIdx.y;
-    SlotInfo si = slot_at(a);
-    if constexpr (pf)
-        if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
-    while (si.e >= 0) {  // uniform over the block
-        PG_MARK(1, 2);
-        const uint8_t* mat = mat_of(si.e);
-        float acc[TM];
-#pragma unroll
-        for (int t = 0; t < TM; ++t) acc[t] = 0.f;
-        for (int it = w; it < nit; it += 2 * nw) {
-            const int it1 = it + nw;
-            const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
-            if constexpr (pf) {
-                if (it != w) load_pass(mat, it);
-                gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-            } else {
+    // One token (h8): 8-row blocks, three a CU (384 16-row blocks left half the CUs with
+    // two, which end last).  Lane = (row r of 8, quarter p, matrix u = lane >> 5 (0 gate,
+    // 1 up)); wave w takes super-blocks w, w + W, ... of both matrices, two at a time.  The
+    // inter rows' sums go out as 8-row sums (isum [P][N/8]).
+    constexpr bool h8 = MODE == kRoute && TM == 1 && gu_rows8<QT>();
+    if constexpr (h8) {
+        const int r8 = lane & 7, p8 = (lane >> 3) & 3, u8 = lane >> 5;
+        const int row8 = blockIdx.x * 8 + r8;
+        float* red8 = &red[0][0][0];  // [W][2][8]
+        for (int a = blockIdx.y;; a += gridDim.y) {
+            const SlotInfo si = slot_at(a);
+            if (si.e < 0) break;  // uniform over the block
+            PG_MARK(1, 2);
+            const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
+            float acc[1] = {0.f};
+            for (int j = w; j < nb; j += 2 * nw) {
+                const int j1 = j + nw;
                 Qtr<QT> l0, l1;
-                load_qtr<QT>(l0, mat, N, nb, row, j0, p);
-                load_qtr<QT>(l1, mat, N, nb, row, j1, p);
-                gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
+                load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
+                gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
             }
-        }
-        PG_MARK(1, 4);
-        SlotInfo sn;
-        if constexpr (pf) {
-            sn = slot_at(a + gridDim.y);
-            if (sn.e >= 0 && w < nit) load_pass(mat_of(sn.e), w);
-        }
-        // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
-#pragma unroll
-        for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
-        if (p == 0) {
-#pragma unroll
-            for (int t = 0; t < TM; ++t)
-                if (t < si.count) red[w][t][r] = acc[t];
-        }
-        __syncthreads();
-        // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
-        // of a token is a shuffle reduction inside its group
-        const int cnt = si.count, p0 = si.p_begin;
-        if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
-            const int t = tid >> 4, rr = tid & 15;
-            const int orow = blockIdx.x * RB + rr;
-            float v = red[0][t][rr];
-            for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
-            if (orow < N) {
-                if (dp.bias) v = v + dp.bias[orow];
-                if (dp.out_f16)
-                    ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
-                else
-                    inter[(int64_t)(p0 + t) * N + orow] = v;
+            PG_MARK(1, 4);
+            // quarters -> rows (lanes r, r+8, r+16, r+24 of each half); waves in LDS
+            float v8 = acc[0];
+            v8 += xor_lane<8>(v8);
+            v8 += xor_lane<16>(v8);
+            if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
+            __syncthreads();
+            if (tid < 8) {  // row rr of the token's SwiGLU row
+                const int rr = tid;
+                float gs = 0.f, us = 0.f;
+                for (int ww = 0; ww < nw; ++ww) {
+                    gs += red8[(ww * 2) * 8 + rr];
+                    us += red8[(ww * 2 + 1) * 8 + rr];
+                }
+                const float v = gate_act(dp.act, gs) * us;
+                const int orow = blockIdx.x * 8 + rr;
+                if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
+                if (isum) {
+                    const float sm = group_sum<8>(v);
+                    if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
+                }
             }
-        } else if (tid < cnt * RB) {
-            const int t = tid >> 4, rr = tid & 15;
-            float g = 0.f, u = 0.f;
-            for (int ww = 0; ww < nw; ww += 2) {
-                g += red[ww][t][rr];
-                u += red[ww + 1][t][rr];
-            }
-            const float v = gate_act(dp.act, g) * u;
-            const int orow = blockIdx.x * RB + rr;
-            if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
-            if (isum) {
-                const float sm = group_sum<16>(v);
-                if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
-            }
+            if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
+            __syncthreads();                           // red is rewritten by the next slot
         }
-        if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
-        __syncthreads();                           // red is rewritten by the next slot
-        a += gridDim.y;
+    }
+    if constexpr (!h8) {
+        auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
+            return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
+        };
+        // items, two per wave at a time (both quarters' loads in flight together): pass `it`
+        // holds items it and it + nw (the second clamped to a readable item past the end);
+        // q0, q1: the prefetched pass
+        Qtr<QT> q0, q1;
+        auto load_pass = [&](const uint8_t* mat, int it) {
+            const int it1 = min(it + nw, nit - 1);
+            load_qtr<QT>(q0, mat, N, nb, row, lin ? it : it >> 1, p);
+            load_qtr<QT>(q1, mat, N, nb, row, lin ? it1 : it1 >> 1, p);
+        };
+        int a = blockIdx.y;
+        SlotInfo si = slot_at(a);
         if constexpr (pf)
-            si = sn;
-        else
-            si = slot_at(a);
+            if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
+        while (si.e >= 0) {  // uniform over the block
+            PG_MARK(1, 2);
+            const uint8_t* mat = mat_of(si.e);
+            float acc[TM];
+    #pragma unroll
+            for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+            for (int it = w; it < nit; it += 2 * nw) {
+                const int it1 = it + nw;
+                const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
+                if constexpr (pf) {
+                    if (it != w) load_pass(mat, it);
+                    gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                } else {
+                    Qtr<QT> l0, l1;
+                    load_qtr<QT>(l0, mat, N, nb, row, j0, p);
+                    load_qtr<QT>(l1, mat, N, nb, row, j1, p);
+                    gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                }
+            }
+            PG_MARK(1, 4);
+            SlotInfo sn;
+            if constexpr (pf) {
+                sn = slot_at(a + gridDim.y);
+                if (sn.e >= 0 && w < nit) load_pass(mat_of(sn.e), w);
+            }
+            // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
+    #pragma unroll
+            for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+            if (p == 0) {
+    #pragma unroll
+                for (int t = 0; t < TM; ++t)
+                    if (t < si.count) red[w][t][r] = acc[t];
+            }
+            __syncthreads();
+            // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
+            // of a token is a shuffle reduction inside its group
+            const int cnt = si.count, p0 = si.p_begin;
+            if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
+                const int t = tid >> 4, rr = tid & 15;
+                const int orow = blockIdx.x * RB + rr;
+                float v = red[0][t][rr];
+                for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
+                if (orow < N) {
+                    if (dp.bias) v = v + dp.bias[orow];
+                    if (dp.out_f16)
+                        ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
+                    else
+                        inter[(int64_t)(p0 + t) * N + orow] = v;
+                }
+            } else if (tid < cnt * RB) {
+                const int t = tid >> 4, rr = tid & 15;
+                float g = 0.f, u = 0.f;
+                for (int ww = 0; ww < nw; ww += 2) {
+                    g += red[ww][t][rr];
+                    u += red[ww + 1][t][rr];
+                }
+                const float v = gate_act(dp.act, g) * u;
+                const int orow = blockIdx.x * RB + rr;
+                if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
+                if (isum) {
+                    const float sm = group_sum<16>(v);
+                    if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
+                }
+            }
+            if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
+            __syncthreads();                           // red is rewritten by the next slot
+            a += gridDim.y;
+            if constexpr (pf)
+                si = sn;
+            else
+                si = slot_at(a);
+        }
     }
     // block (0, 0) publishes the routing last: its stores then stay off the block's own
     // critical path (a barrier would wait for them)
@@ -1277,7 +1334,8 @@ __device__ __forceinline__ void dc_finish(float* acc, float (*red)[TM][8], int M
 template <int QT, int TM>
 __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict__ dbase, int64_t dstride, int N,
                                                       int K, const float* __restrict__ inter,
-                                                      const float* __restrict__ isum, const int32_t* __restrict__ desc,
+                                                      const float* __restrict__ isum, int isum8,
+                                                      const int32_t* __restrict__ desc,
                                                       int M, int P, const float* __restrict__ shared,
                                                       const float* __restrict__ shared_logit,
                                                       float* __restrict__ out, uint64_t* __restrict__ clear,
@@ -1317,7 +1375,10 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
     copy_idx<4, u32x4>(
         P * kq, tid, nth, [=](int i) { return (const u32x4*)(inter + 4 * (int64_t)i); },
         [=](int i) { return (u32x4*)(xs + (i / kq) * xrs + xpos_f(4 * (i % kq))); });
-    copy_words<2>((u32x4*)iss, (const u32x4*)isum, P * (K >> 6), tid, nth);
+    if (isum8)  // 8-row sums (the one-token gate/up): pairs of them
+        for (int i = tid; i < P * (K >> 4); i += nth) iss[i] = isum[2 * i] + isum[2 * i + 1];
+    else
+        copy_words<2>((u32x4*)iss, (const u32x4*)isum, P * (K >> 6), tid, nth);
     __syncthreads();
     PG_MARK(3, 1);
     // 2. items, two per lane per pass
@@ -1353,7 +1414,7 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
 template <int QT, int TM>
 __global__ __launch_bounds__(1024) void dec_dc_chunk_kernel(const uint8_t* __restrict__ dbase, int64_t dstride,
                                                             int N, int K, int JC, const float* __restrict__ inter,
-                                                            const float* __restrict__ isum,
+                                                            const float* __restrict__ isum, int isum8,
                                                             const int32_t* __restrict__ desc, int M, int P,
                                                             const float* __restrict__ shared,
                                                             const float* __restrict__ shared_logit,
@@ -1401,11 +1462,20 @@ __global__ __launch_bounds__(1024) void dec_dc_chunk_kernel(const uint8_t* __res
             copy_idx<4, u32x4>(
                 P * kq, tid, nth, [=](int i) { return (const u32x4*)(src + (int64_t)(i / kq) * K + 4 * (i % kq)); },
                 [=](int i) { return (u32x4*)(xs + (i / kq) * xrs + xpos_f(4 * (i % kq))); });
-            const float* ssrc = isum + 16 * j0;
-            copy_idx<2, u32x4>(
-                P * sq, tid, nth,
-                [=](int i) { return (const u32x4*)(ssrc + (int64_t)(i / sq) * (K >> 4) + 4 * (i % sq)); },
-                [=](int i) { return (u32x4*)(iss + (i / sq) * srs + 4 * (i % sq)); });
+            if (isum8) {  // 8-row sums (the one-token gate/up): pairs of them
+                const int sc = JCc * 16;
+                for (int i = tid; i < P * sc; i += nth) {
+                    const int pr = i / sc, c = i - pr * sc;
+                    const float* s8 = isum + (int64_t)pr * (K >> 3) + 32 * j0 + 2 * c;
+                    iss[pr * srs + c] = s8[0] + s8[1];
+                }
+            } else {
+                const float* ssrc = isum + 16 * j0;
+                copy_idx<2, u32x4>(
+                    P * sq, tid, nth,
+                    [=](int i) { return (const u32x4*)(ssrc + (int64_t)(i / sq) * (K >> 4) + 4 * (i % sq)); },
+                    [=](int i) { return (u32x4*)(iss + (i / sq) * srs + 4 * (i % sq)); });
+            }
         }
         __syncthreads();
         // 2. the chunk's items, two per lane per pass
@@ -1595,7 +1665,11 @@ template <int QT, int TM>
 inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, const DecDisp& dp,
                       const RouterIn& rt, int max_active, float* inter, float* isum, hipStream_t st) {
     // a linear has half the items of a gate/up pair: two per wave as well
-    const int W = gu_waves(dp.mode == kLinear ? ((g.K >> 8) + 1) / 2 : g.K >> 8), gx = div_up(g.N, 16);
+    // the one-token routed launch: 8-row blocks, ceil(K/512) waves (both matrices a wave)
+    const bool h8 = dp.mode == kRoute && TM == 1 && gu_rows8<QT>();
+    const int nbk = g.K >> 8, W8 = (nbk + 1) / 2;
+    const int W = h8 ? (W8 > 16 ? 16 : W8) : gu_waves(dp.mode == kLinear ? (nbk + 1) / 2 : nbk);
+    const int gx = div_up(g.N, h8 ? 8 : 16);
     const int gy = gu_slot_blocks(max_active);
     // every router row needs a wave (TM / 2 with 4+ tokens)
     const int gmin = dp.mode == kRoute ? div_up((dp.E + (rt.extra_w ? 1 : 0)) * (TM < 4 ? TM : 4), gx * W) : 1;
@@ -1632,17 +1706,18 @@ inline void dn_launch(const Mats& d, const float* inter, const float* isum, cons
 }
 
 template <int QT, int TM>
-inline void dc_launch(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
-                      int max_active, const float* shared, const float* shared_logit, float* out, uint64_t* clear,
-                      int n_clear, hipStream_t st) {
+inline void dc_launch(const Mats& d, const float* inter, const float* isum, int isum8, const int32_t* desc, int M,
+                      int P, int max_active, const float* shared, const float* shared_logit, float* out,
+                      uint64_t* clear, int n_clear, hipStream_t st) {
     const int nb = d.K >> 8, JC = dc_chunk(P, d.K);
     const int W = dc_waves(max_active * JC);  // items of a chunk
     if (JC >= nb)
         PG_LAUNCH((dec_dc_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, nb), st, d.base,
-                  d.stride, d.N, d.K, inter, isum, desc, M, P, shared, shared_logit, out, clear, n_clear);
+                  d.stride, d.N, d.K, inter, isum, isum8, desc, M, P, shared, shared_logit, out, clear, n_clear);
     else
         PG_LAUNCH((dec_dc_chunk_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, JC), st,
-                  d.base, d.stride, d.N, d.K, JC, inter, isum, desc, M, P, shared, shared_logit, out, clear, n_clear);
+                  d.base, d.stride, d.N, d.K, JC, inter, isum, isum8, desc, M, P, shared, shared_logit, out, clear,
+                  n_clear);
 }
 
 #define PG_TM(F, QT, RB, W, ...)                   \
@@ -1680,9 +1755,9 @@ template <int QT>
 int dec_down_q(const Mats& d, const float* inter, const float* isum, int M, int mode, const DecDisp& dp,
                int max_active, const float* topk_w, float* partial, hipStream_t st);
 template <int QT>
-int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int P,
-                       int max_active, const float* shared, const float* shared_logit, float* out, uint64_t* clear,
-                       int n_clear, hipStream_t st);
+int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, int isum8, const int32_t* desc, int M,
+                       int P, int max_active, const float* shared, const float* shared_logit, float* out,
+                       uint64_t* clear, int n_clear, hipStream_t st);
 
 #define PG_DEFINE_DECODE_GATEUP(QT)                                                                                  \
     template <>                                                                                                     \
@@ -1708,13 +1783,14 @@ int dec_down_combine_q(const Mats& d, const float* inter, const float* isum, con
 
 #define PG_DEFINE_DECODE_DOWN_COMBINE(QT)                                                                            \
     template <>                                                                                                     \
-    int dec_down_combine_q<QT>(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M,   \
-                               int P, int max_active, const float* shared, const float* shared_logit, float* out,   \
-                               uint64_t* clear, int n_clear, hipStream_t st) {                                      \
+    int dec_down_combine_q<QT>(const Mats& d, const float* inter, const float* isum, int isum8,                    \
+                               const int32_t* desc, int M, int P, int max_active, const float* shared,              \
+                               const float* shared_logit, float* out, uint64_t* clear, int n_clear,                 \
+                               hipStream_t st) {                                                                    \
         if (P > 128 || dc_chunk(P, d.K) < 1)                                                                        \
             return fail(PGMOE_E_UNSUPPORTED, "decode down + combine: %d pairs of %d inputs exceed LDS", P, d.K);    \
-        PG_TM2(dc_launch, QT, d, inter, isum, desc, M, P, max_active, shared, shared_logit, out, clear, n_clear, \
-               st);                                                                                                 \
+        PG_TM2(dc_launch, QT, d, inter, isum, isum8, desc, M, P, max_active, shared, shared_logit, out, clear,   \
+               n_clear, st);                                                                                        \
         return check_launch("dec_down_combine");                                                                    \
     }
 

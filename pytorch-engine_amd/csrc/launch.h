@@ -81,7 +81,9 @@ struct DecFlat {
 // the forward's last kernel clears them), and, when xsum_out is set, the 16-element sums
 // of x for the shared expert's launches.
 // status: the workspace status word a wave whose bounded wait for the logits gave up
-// marks (kStatusSpinTimeout), or null.
+// marks (kStatusSpinTimeout), or null.  isum gets 16-row sums [P][N/16], or 8-row sums
+// [P][N/8] where decode_isum_rows8(g.qtype, M).
+bool decode_isum_rows8(int qtype, int M);
 int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
                              const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, int32_t* status,
                              float* xsum_out, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
@@ -109,8 +111,10 @@ int launch_dec_gateup_ident(const Mats& g, const Mats& u, const uint16_t* x, con
 int launch_dec_down_ident(const Mats& d, const float* inter, const float* isum, int M, float* out, hipStream_t st);
 // clear (may be null): n_clear words the kernel sets to zero (the decode router's tagged logits).
 // desc null: the identity (matrix 0 applied to every token with weight 1; P = M, K = 1).
-int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, const int32_t* desc, int M, int K,
-                            int max_active, const float* shared, const float* shared_logit, float* out,
+// isum8: isum holds 8-row sums [P][K/8] (the routed gate/up's where decode_isum_rows8),
+// else 16-row sums.
+int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum, int isum8, const int32_t* desc,
+                            int M, int K, int max_active, const float* shared, const float* shared_logit, float* out,
                             uint64_t* clear, int n_clear, hipStream_t st);
 int decode_desc_words();
 // 64-bit words of the decode router's ready-tagged logits (all copies) for M tokens.

@@ -5,6 +5,11 @@ against the oracle, and the same bits run to run.
 
 With top_k = 8 and I = 1280 (5 super-blocks a row): M = 3 stages all 24 rows at once;
 M = 4 (32 rows) takes chunks of 4 + 1 columns; M = 8 (64 rows) chunks of 2 + 2 + 1.
+
+One token in Q4_1 / Q4_K / Q5_K gate/up runs 8-row blocks that leave 8-row sums of the
+SwiGLU rows, which the down kernels pair into the 16-row sums their formats use; Q6_K and
+Q8_0 gate/up keep 16-row sums.  Both are covered with the rows staged whole (top_k 8,
+I = 1280) and in chunks (top_k 16, I = 2560: 16 rows of 10 super-blocks, chunks 8 + 2).
 """
 
 import numpy as np
@@ -41,4 +46,21 @@ def test_chunked_down_combine(down):
         check_layer_output(got, ol.forward_tokens(x, idx, w))
         again = mod(xt).cpu().numpy()
         assert np.array_equal(got, again), "not reproducible run to run"
+    mod.check_status()
+
+
+@pytest.mark.parametrize("qts", [(Q4_1, Q4_1), (Q4_K, Q6_K), (Q5_K, Q4_K), (Q8_0, Q8_0), (Q6_K, Q5_K)])
+@pytest.mark.parametrize("topk,inter", [(8, 1280), (16, 2560)])
+def test_one_token_sums(qts, topk, inter):
+    gu, down = qts
+    spec = LayerSpec(f"one_{gu}_{down}_{topk}", 512, 32, topk, inter, (gu, gu, down))
+    lay, ol, mod = build_pair(spec, seed=5)
+    xs = lay.draw_x(3)
+    for rep in range(3):
+        log(f"one token gate/up {gu} down {down} top_k {topk} I {inter} row {rep}")
+        x = np.ascontiguousarray(xs[rep:rep + 1])
+        got = mod(torch.from_numpy(x).to("cuda:0")).cpu().numpy()
+        _, idx, w = ol.route(x)
+        check_forward_routing(mod, 1, idx, w)
+        check_layer_output(got, ol.forward_tokens(x, idx, w))
     mod.check_status()
