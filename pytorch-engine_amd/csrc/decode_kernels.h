@@ -992,6 +992,23 @@ __device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteSh
     }
 }
 
+// Issue priority from the slots a block has left after the current one.  Blocks of up to 8
+// waves share a CU two at a time (the 128-register bound allows 16 waves); the older
+// one's waves win the issue arbitration and it runs ahead, and the kernel then ends on
+// the other.  Lowering a block's priority as it nears its end lets the other catch up.
+// Measured with 2+ tokens: C2 (8 waves) M = 4 / 8 37.0 / 63.0 -> 35.5 / 60.3 us; blocks
+// of 14-16 waves, alone on their CU, were 1-2 % slower with it, so they keep priority 0.
+__device__ __forceinline__ void slot_prio(int left) {
+    if (left >= 3)
+        __builtin_amdgcn_s_setprio(3);
+    else if (left == 2)
+        __builtin_amdgcn_s_setprio(2);
+    else if (left == 1)
+        __builtin_amdgcn_s_setprio(1);
+    else
+        __builtin_amdgcn_s_setprio(0);
+}
+
 // The one-token routed gate/up runs 8-row blocks (and leaves 8-row sums) for the formats
 // of at most 11 chunks a tile (Q4_1, Q4_K, Q5_K); Q6_K and Q8_0 keep 16-row blocks, which
 // measured faster for their larger rows.
@@ -1185,6 +1202,8 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
             if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
         while (si.e >= 0) {  // uniform over the block
             PG_MARK(1, 2);
+            if constexpr (MODE == kRoute && TM >= 2)
+                if (nw <= 8) slot_prio((si.n_act - 1 - a) / (int)gridDim.y);  // two blocks a CU
             const uint8_t* mat = mat_of(si.e);
             float acc[TM];
     #pragma unroll
