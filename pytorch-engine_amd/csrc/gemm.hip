@@ -1,10 +1,10 @@
 // Prefill (M > 8) grouped expert products on the MFMA cores.
 //
-// A tile is 256 sorted pairs of one expert x 256 output columns.  The block is 4 waves
-// (one per SIMD; each owns all 256 rows x 64 columns, 256 fp32 accumulators per lane in
-// AGPRs, so every B column is decoded once) or 8 waves (two per SIMD; 128 rows x 64
-// columns each, every B column decoded by two waves), as 8 x 2 or 4 x 2
-// v_mfma_f32_32x32x16_f16 tiles per wave.  The K loop steps one 64-weight unit at a time
+// A tile is 256 sorted pairs of one expert x 256 output columns.  The gate/up block is 4
+// waves (one per SIMD; each owns all 256 rows x 64 columns, 256 fp32 accumulators per
+// lane in AGPRs), the down block 8 waves (two per SIMD; each all 256 rows x 32 columns),
+// so every B column is decoded once, as 8 x 2 or 8 x 1 v_mfma_f32_32x32x16_f16 tiles per
+// wave (other layouts are build-time choices: CT column tiles, WM waves along M).  The K loop steps one 64-weight unit at a time
 // through a ring of three LDS stages filled by direct HBM -> LDS copies three units
 // ahead: the fp16 activation rows (16-byte slots XOR-swizzled by row) and the raw GGUF
 // bytes of the 256 weight rows (whole 1 KB chunks of the 64-row tile layout, with their
@@ -392,6 +392,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     int gate_act) {
     using L = GLay<QT, CT, WM>;
     constexpr int NW = L::NW, WN = L::WN, RS = L::RS, WR = 32 * RS;  // WR rows per wave
+    static_assert(!GATEUP || CT >= 2, "gate/up: each wave holds gate and matching up columns");
     constexpr int CH = L::CH;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * L::STAGE];
     __shared__ int rowsrc[kGM];
@@ -469,6 +470,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     const uint32_t sbase = lds_addr(smem);
     // Issue every copy of unit u into stage st (u clamped: the last steps repeat it).
     auto copy_unit = [&](auto ac, int u, int st) {  // ac: A copies (integral_constant)
+        static_assert(decltype(ac)::value <= L::AQ, "more A copies than the wave's row octets");
         u = u0 + min(u, units - 1);  // relative unit -> absolute (past the range: repeat the last)
         const uint32_t S = sbase + st * L::STAGE;
 #pragma unroll
@@ -512,10 +514,12 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     // is done with it (see gemm_loop).  The loop is instantiated per NI (a whole copy each)
     // so the register allocation of one copy never has to merge the others'.
     PG_MARK(GATEUP ? 4 : 5, 1);
-    // With one wave along M (NW = 4) wave w copies row octet w of every 32-row slice q, so
-    // the slices without pairs (q >= ni) are not copied at all; with two, every slice is.
+    // With one wave along M and 4 waves, wave w copies row octet w of every 32-row slice q,
+    // so the slices without pairs (q >= ni) are not copied at all; otherwise (8 waves: each
+    // copies octets w, w + 8, ...) every slice is.
 #define PG_GLOOP(NI_) \
-    gemm_loop<QT, NI_, CT, RS, WM == 1 ? NI_ : L::AQ, L::BQ, L::STAGE>(smem, units, bgj, rigj, wm, lane, acc, copy_unit);
+    gemm_loop<QT, NI_, CT, RS, (WM == 1 && L::NW == 4) ? NI_ : L::AQ, L::BQ, L::STAGE>(smem, units, bgj, rigj, wm, \
+                                                                                     lane, acc, copy_unit);
     switch (ni) {
     case 8: if constexpr (RS == 8) { PG_GLOOP(8) } break;
     case 7: if constexpr (RS == 8) { PG_GLOOP(7) } break;
@@ -674,18 +678,20 @@ static int launch_split_reduce(bool gateup, const float* raw, int S, int64_t P, 
 // Wave layout of each product (build-time choices): CT column tiles per wave, WM waves
 // along M.  Measured on the Qwen3 Zipf prefill (M = 4096): gate/up (K = 2048, Q4_K) is
 // fastest with 4 waves (WM = 1: half the B decode per SIMD, no copies of empty slices),
-// down (K = 768, Q6_K) with 8 (WM = 2: 231 us against 278 us with 4).
+// down with 8 waves of 256 rows x 32 columns (CT = 1, WM = 1: each B column decoded once,
+// two waves a SIMD): Q6_K 229 -> 225 us, Mixtral's Q4_K 770 -> 712 us against 8 waves of
+// 128 x 64 (CT = 2, WM = 2, every B column decoded by two waves).
 #ifndef PG_GU_CT
 #define PG_GU_CT 2
 #endif
 #ifndef PG_DN_CT
-#define PG_DN_CT 2
+#define PG_DN_CT 1
 #endif
 #ifndef PG_GU_WM
 #define PG_GU_WM 1
 #endif
 #ifndef PG_DN_WM
-#define PG_DN_WM 2
+#define PG_DN_WM 1
 #endif
 
 // Upper bound of 256-row tiles for P pairs over at most E experts, rounded up to whole
