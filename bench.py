@@ -459,8 +459,8 @@ def main() -> int:
     m_list = sorted({1} | {int(v) for v in args.m_list.split(",") if v})
     for M in m_list:
         x = torch.from_numpy(lay.draw_x(M)).to(dev)
-        steps = args.steps if M == 1 else max(50, args.steps // 4)
-        warm = args.warmup if M == 1 else max(10, args.warmup // 4)
+        # every M is timed like the headline: --warmup untimed, then --steps timed forwards
+        steps, warm = args.steps, args.warmup
         ms = graph_step_ms(torch, mods, x, steps, warm)
         ms_eager = eager_step_ms(torch, mods, x, max(50, steps // 4), 10)
         _, idx, _ = ol.route(lay.draw_x(M))
