@@ -112,6 +112,10 @@ size_t dec_lds_limit() {
     return cached[dev];
 }
 
+int resident_blocks(const void* kernel, int threads, size_t lds) {
+    return resident_rows(kernel, threads, lds, 1, 1 << 30);
+}
+
 int resident_rows(const void* kernel, int threads, size_t lds, int gx, int gy) {
     static int cus[64] = {};
     int dev = 0;

@@ -1014,8 +1014,10 @@ __device__ __forceinline__ void slot_prio(int left) {
 // measured faster for their larger rows.
 template <int QT> constexpr bool gu_rows8() { return Tile<QT>::CH <= 11; }
 // MODE: DecMode (fixed per instantiation, so each kernel holds only its own path); RE:
-// logit words per lane of the routing waves (kRoute: E <= 64 * RE).
-template <int QT, int TM, int MODE, int RE>
+// logit words per lane of the routing waves (kRoute: E <= 64 * RE); RL: the grid is one
+// round of resident blocks and each block loops over row blocks blockIdx.x, + gridDim.x,
+// ... (launched so when the row blocks outnumber the resident blocks).
+template <int QT, int TM, int MODE, int RE, bool RL>
 __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict__ gbase,
                                                       const uint8_t* __restrict__ ubase, int64_t gstride,
                                                       int64_t ustride, int N, int K, const uint16_t* __restrict__ x,
@@ -1139,142 +1141,299 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     // 1 up)); wave w takes super-blocks w, w + W, ... of both matrices, two at a time.  The
     // inter rows' sums go out as 8-row sums (isum [P][N/8]).
     constexpr bool h8 = MODE == kRoute && TM == 1 && gu_rows8<QT>();
-    if constexpr (h8) {
-        const int r8 = lane & 7, p8 = (lane >> 3) & 3, u8 = lane >> 5;
-        const int row8 = blockIdx.x * 8 + r8;
-        float* red8 = &red[0][0][0];  // [W][2][8]
-        for (int a = blockIdx.y;; a += gridDim.y) {
-            const SlotInfo si = slot_at(a);
-            if (si.e < 0) break;  // uniform over the block
-            PG_MARK(1, 2);
-            const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
-            float acc[1] = {0.f};
-            for (int j = w; j < nb; j += 2 * nw) {
-                const int j1 = j + nw;
-                Qtr<QT> l0, l1;
-                load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
-                load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
-                gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
-                if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
-            }
-            PG_MARK(1, 4);
-            // quarters -> rows (lanes r, r+8, r+16, r+24 of each half); waves in LDS
-            float v8 = acc[0];
-            v8 += xor_lane<8>(v8);
-            v8 += xor_lane<16>(v8);
-            if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
-            __syncthreads();
-            if (tid < 8) {  // row rr of the token's SwiGLU row
-                const int rr = tid;
-                float gs = 0.f, us = 0.f;
-                for (int ww = 0; ww < nw; ++ww) {
-                    gs += red8[(ww * 2) * 8 + rr];
-                    us += red8[(ww * 2 + 1) * 8 + rr];
-                }
-                const float v = gate_act(dp.act, gs) * us;
-                const int orow = blockIdx.x * 8 + rr;
-                if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
-                if (isum) {
-                    const float sm = group_sum<8>(v);
-                    if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
-                }
-            }
-            if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
-            __syncthreads();                           // red is rewritten by the next slot
-        }
-    }
-    if constexpr (!h8) {
-        auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
-            return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
-        };
-        // items, two per wave at a time (both quarters' loads in flight together): pass `it`
-        // holds items it and it + nw (the second clamped to a readable item past the end);
-        // q0, q1: the prefetched pass
-        Qtr<QT> q0, q1;
-        auto load_pass = [&](const uint8_t* mat, int it) {
-            const int it1 = min(it + nw, nit - 1);
-            load_qtr<QT>(q0, mat, N, nb, row, lin ? it : it >> 1, p);
-            load_qtr<QT>(q1, mat, N, nb, row, lin ? it1 : it1 >> 1, p);
-        };
-        int a = blockIdx.y;
-        SlotInfo si = slot_at(a);
-        if constexpr (pf)
-            if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
-        while (si.e >= 0) {  // uniform over the block
-            PG_MARK(1, 2);
-            if constexpr (MODE == kRoute && TM >= 2)
-                if (nw <= 8) slot_prio((si.n_act - 1 - a) / (int)gridDim.y);  // two blocks a CU
-            const uint8_t* mat = mat_of(si.e);
-            float acc[TM];
-    #pragma unroll
-            for (int t = 0; t < TM; ++t) acc[t] = 0.f;
-            for (int it = w; it < nit; it += 2 * nw) {
-                const int it1 = it + nw;
-                const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
-                if constexpr (pf) {
-                    if (it != w) load_pass(mat, it);
-                    gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                    if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                } else {
+    // One row block per block (the grid covers the rows), or (RL) row blocks blockIdx.x,
+    // + gridDim.x, ... per block: the two forms are kept apart so the first compiles as
+    // it does without the second.
+    if constexpr (!RL) {
+        if constexpr (h8) {
+            const int r8 = lane & 7, p8 = (lane >> 3) & 3, u8 = lane >> 5;
+            const int row8 = blockIdx.x * 8 + r8;
+            float* red8 = &red[0][0][0];  // [W][2][8]
+            for (int a = blockIdx.y;; a += gridDim.y) {
+                const SlotInfo si = slot_at(a);
+                if (si.e < 0) break;  // uniform over the block
+                PG_MARK(1, 2);
+                const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
+                float acc[1] = {0.f};
+                for (int j = w; j < nb; j += 2 * nw) {
+                    const int j1 = j + nw;
                     Qtr<QT> l0, l1;
-                    load_qtr<QT>(l0, mat, N, nb, row, j0, p);
-                    load_qtr<QT>(l1, mat, N, nb, row, j1, p);
-                    gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                    if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
+                    load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
+                    gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
                 }
-            }
-            PG_MARK(1, 4);
-            SlotInfo sn;
-            if constexpr (pf) {
-                sn = slot_at(a + gridDim.y);
-                if (sn.e >= 0 && w < nit) load_pass(mat_of(sn.e), w);
-            }
-            // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
-    #pragma unroll
-            for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
-            if (p == 0) {
-    #pragma unroll
-                for (int t = 0; t < TM; ++t)
-                    if (t < si.count) red[w][t][r] = acc[t];
-            }
-            __syncthreads();
-            // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
-            // of a token is a shuffle reduction inside its group
-            const int cnt = si.count, p0 = si.p_begin;
-            if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
-                const int t = tid >> 4, rr = tid & 15;
-                const int orow = blockIdx.x * RB + rr;
-                float v = red[0][t][rr];
-                for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
-                if (orow < N) {
-                    if (dp.bias) v = v + dp.bias[orow];
-                    if (dp.out_f16)
-                        ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
-                    else
-                        inter[(int64_t)(p0 + t) * N + orow] = v;
+                PG_MARK(1, 4);
+                // quarters -> rows (lanes r, r+8, r+16, r+24 of each half); waves in LDS
+                float v8 = acc[0];
+                v8 += xor_lane<8>(v8);
+                v8 += xor_lane<16>(v8);
+                if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
+                __syncthreads();
+                if (tid < 8) {  // row rr of the token's SwiGLU row
+                    const int rr = tid;
+                    float gs = 0.f, us = 0.f;
+                    for (int ww = 0; ww < nw; ++ww) {
+                        gs += red8[(ww * 2) * 8 + rr];
+                        us += red8[(ww * 2 + 1) * 8 + rr];
+                    }
+                    const float v = gate_act(dp.act, gs) * us;
+                    const int orow = blockIdx.x * 8 + rr;
+                    if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
+                    if (isum) {
+                        const float sm = group_sum<8>(v);
+                        if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
+                    }
                 }
-            } else if (tid < cnt * RB) {
-                const int t = tid >> 4, rr = tid & 15;
-                float g = 0.f, u = 0.f;
-                for (int ww = 0; ww < nw; ww += 2) {
-                    g += red[ww][t][rr];
-                    u += red[ww + 1][t][rr];
-                }
-                const float v = gate_act(dp.act, g) * u;
-                const int orow = blockIdx.x * RB + rr;
-                if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
-                if (isum) {
-                    const float sm = group_sum<16>(v);
-                    if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
-                }
+                if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
+                __syncthreads();                           // red is rewritten by the next slot
             }
-            if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
-            __syncthreads();                           // red is rewritten by the next slot
-            a += gridDim.y;
+        }
+        if constexpr (!h8) {
+            auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
+                return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
+            };
+            // items, two per wave at a time (both quarters' loads in flight together): pass `it`
+            // holds items it and it + nw (the second clamped to a readable item past the end);
+            // q0, q1: the prefetched pass
+            Qtr<QT> q0, q1;
+            auto load_pass = [&](const uint8_t* mat, int it) {
+                const int it1 = min(it + nw, nit - 1);
+                load_qtr<QT>(q0, mat, N, nb, row, lin ? it : it >> 1, p);
+                load_qtr<QT>(q1, mat, N, nb, row, lin ? it1 : it1 >> 1, p);
+            };
+            int a = blockIdx.y;
+            SlotInfo si = slot_at(a);
             if constexpr (pf)
-                si = sn;
-            else
-                si = slot_at(a);
+                if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
+            while (si.e >= 0) {  // uniform over the block
+                PG_MARK(1, 2);
+                if constexpr (MODE == kRoute && TM >= 2)
+                    if (nw <= 8) slot_prio((si.n_act - 1 - a) / (int)gridDim.y);  // two blocks a CU
+                const uint8_t* mat = mat_of(si.e);
+                float acc[TM];
+        #pragma unroll
+                for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+                for (int it = w; it < nit; it += 2 * nw) {
+                    const int it1 = it + nw;
+                    const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
+                    if constexpr (pf) {
+                        if (it != w) load_pass(mat, it);
+                        gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                        if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    } else {
+                        Qtr<QT> l0, l1;
+                        load_qtr<QT>(l0, mat, N, nb, row, j0, p);
+                        load_qtr<QT>(l1, mat, N, nb, row, j1, p);
+                        gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                        if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    }
+                }
+                PG_MARK(1, 4);
+                SlotInfo sn;
+                if constexpr (pf) {
+                    sn = slot_at(a + gridDim.y);
+                    if (sn.e >= 0 && w < nit) load_pass(mat_of(sn.e), w);
+                }
+                // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
+        #pragma unroll
+                for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+                if (p == 0) {
+        #pragma unroll
+                    for (int t = 0; t < TM; ++t)
+                        if (t < si.count) red[w][t][r] = acc[t];
+                }
+                __syncthreads();
+                // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
+                // of a token is a shuffle reduction inside its group
+                const int cnt = si.count, p0 = si.p_begin;
+                if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
+                    const int t = tid >> 4, rr = tid & 15;
+                    const int orow = blockIdx.x * RB + rr;
+                    float v = red[0][t][rr];
+                    for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
+                    if (orow < N) {
+                        if (dp.bias) v = v + dp.bias[orow];
+                        if (dp.out_f16)
+                            ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
+                        else
+                            inter[(int64_t)(p0 + t) * N + orow] = v;
+                    }
+                } else if (tid < cnt * RB) {
+                    const int t = tid >> 4, rr = tid & 15;
+                    float g = 0.f, u = 0.f;
+                    for (int ww = 0; ww < nw; ww += 2) {
+                        g += red[ww][t][rr];
+                        u += red[ww + 1][t][rr];
+                    }
+                    const float v = gate_act(dp.act, g) * u;
+                    const int orow = blockIdx.x * RB + rr;
+                    if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
+                    if (isum) {
+                        const float sm = group_sum<16>(v);
+                        if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
+                    }
+                }
+                if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
+                __syncthreads();                           // red is rewritten by the next slot
+                a += gridDim.y;
+                if constexpr (pf)
+                    si = sn;
+                else
+                    si = slot_at(a);
+            }
+        }
+    } else {
+        if constexpr (h8) {
+            const int r8 = lane & 7, p8 = (lane >> 3) & 3, u8 = lane >> 5;
+            float* red8 = &red[0][0][0];  // [W][2][8]
+            // row blocks bx = blockIdx.x, + gridDim.x, ..., each with every slot of the column
+            const int nrb = (N + 7) >> 3;
+            for (int bx = blockIdx.x;; bx += gridDim.x) {
+                const int row8 = bx * 8 + r8;
+                for (int a = blockIdx.y;; a += gridDim.y) {
+                    const SlotInfo si = slot_at(a);
+                    if (si.e < 0) break;  // uniform over the block
+                    PG_MARK(1, 2);
+                    const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
+                    float acc[1] = {0.f};
+                    for (int j = w; j < nb; j += 2 * nw) {
+                        const int j1 = j + nw;
+                        Qtr<QT> l0, l1;
+                        load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
+                        load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
+                        gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                        if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    }
+                    PG_MARK(1, 4);
+                    // quarters -> rows (lanes r, r+8, r+16, r+24 of each half); waves in LDS
+                    float v8 = acc[0];
+                    v8 += xor_lane<8>(v8);
+                    v8 += xor_lane<16>(v8);
+                    if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
+                    __syncthreads();
+                    if (tid < 8) {  // row rr of the token's SwiGLU row
+                        const int rr = tid;
+                        float gs = 0.f, us = 0.f;
+                        for (int ww = 0; ww < nw; ++ww) {
+                            gs += red8[(ww * 2) * 8 + rr];
+                            us += red8[(ww * 2 + 1) * 8 + rr];
+                        }
+                        const float v = gate_act(dp.act, gs) * us;
+                        const int orow = bx * 8 + rr;
+                        if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
+                        if (isum) {
+                            const float sm = group_sum<8>(v);
+                            if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
+                        }
+                    }
+                    if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
+                    __syncthreads();                           // red is rewritten by the next slot
+                }
+                if (bx + (int)gridDim.x >= nrb) break;
+                __syncthreads();  // red is rewritten by the next row block
+            }
+        }
+        if constexpr (!h8) {
+            // row blocks bx = blockIdx.x, + gridDim.x, ..., each with every slot of the column
+            const int nrb = (N + RB - 1) / RB;
+            for (int bx = blockIdx.x;; bx += gridDim.x) {
+                const int row = bx * RB + r;
+                auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
+                    return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
+                };
+                // items, two per wave at a time (both quarters' loads in flight together): pass `it`
+                // holds items it and it + nw (the second clamped to a readable item past the end);
+                // q0, q1: the prefetched pass
+                Qtr<QT> q0, q1;
+                auto load_pass = [&](const uint8_t* mat, int it) {
+                    const int it1 = min(it + nw, nit - 1);
+                    load_qtr<QT>(q0, mat, N, nb, row, lin ? it : it >> 1, p);
+                    load_qtr<QT>(q1, mat, N, nb, row, lin ? it1 : it1 >> 1, p);
+                };
+                int a = blockIdx.y;
+                SlotInfo si = slot_at(a);
+                if constexpr (pf)
+                    if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
+                while (si.e >= 0) {  // uniform over the block
+                    PG_MARK(1, 2);
+                    if constexpr (MODE == kRoute && TM >= 2)
+                        if (nw <= 8) slot_prio((si.n_act - 1 - a) / (int)gridDim.y);  // two blocks a CU
+                    const uint8_t* mat = mat_of(si.e);
+                    float acc[TM];
+            #pragma unroll
+                    for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+                    for (int it = w; it < nit; it += 2 * nw) {
+                        const int it1 = it + nw;
+                        const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
+                        if constexpr (pf) {
+                            if (it != w) load_pass(mat, it);
+                            gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                            if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                        } else {
+                            Qtr<QT> l0, l1;
+                            load_qtr<QT>(l0, mat, N, nb, row, j0, p);
+                            load_qtr<QT>(l1, mat, N, nb, row, j1, p);
+                            gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                            if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                        }
+                    }
+                    PG_MARK(1, 4);
+                    SlotInfo sn;
+                    if constexpr (pf) {
+                        sn = slot_at(a + gridDim.y);
+                        if (sn.e >= 0 && w < nit) load_pass(mat_of(sn.e), w);
+                    }
+                    // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
+            #pragma unroll
+                    for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+                    if (p == 0) {
+            #pragma unroll
+                        for (int t = 0; t < TM; ++t)
+                            if (t < si.count) red[w][t][r] = acc[t];
+                    }
+                    __syncthreads();
+                    // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
+                    // of a token is a shuffle reduction inside its group
+                    const int cnt = si.count, p0 = si.p_begin;
+                    if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
+                        const int t = tid >> 4, rr = tid & 15;
+                        const int orow = bx * RB + rr;
+                        float v = red[0][t][rr];
+                        for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
+                        if (orow < N) {
+                            if (dp.bias) v = v + dp.bias[orow];
+                            if (dp.out_f16)
+                                ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
+                            else
+                                inter[(int64_t)(p0 + t) * N + orow] = v;
+                        }
+                    } else if (tid < cnt * RB) {
+                        const int t = tid >> 4, rr = tid & 15;
+                        float g = 0.f, u = 0.f;
+                        for (int ww = 0; ww < nw; ww += 2) {
+                            g += red[ww][t][rr];
+                            u += red[ww + 1][t][rr];
+                        }
+                        const float v = gate_act(dp.act, g) * u;
+                        const int orow = bx * RB + rr;
+                        if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
+                        if (isum) {
+                            const float sm = group_sum<16>(v);
+                            if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
+                        }
+                    }
+                    if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
+                    __syncthreads();                           // red is rewritten by the next slot
+                    a += gridDim.y;
+                    if constexpr (pf)
+                        si = sn;
+                    else
+                        si = slot_at(a);
+                }
+                if (bx + (int)gridDim.x >= nrb) break;
+                __syncthreads();  // red is rewritten by the next row block
+            }
         }
     }
     // block (0, 0) publishes the routing last: its stores then stay off the block's own
@@ -1325,7 +1484,7 @@ __device__ __forceinline__ void dc_item(const Qtr<QT>& q, bool valid, int it, in
 template <int TM>
 __device__ __forceinline__ void dc_finish(float* acc, float (*red)[TM][8], int M, int N,
                                           const float* __restrict__ shared, const float* __restrict__ shared_logit,
-                                          float* __restrict__ out) {
+                                          float* __restrict__ out, int bx) {
     constexpr int RB = 8;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nth = blockDim.x, nw = nth >> 6;
 #pragma unroll
@@ -1339,7 +1498,7 @@ __device__ __forceinline__ void dc_finish(float* acc, float (*red)[TM][8], int M
         const int t = i / RB, rr = i % RB;
         float v = 0.f;
         for (int ww = 0; ww < nw; ++ww) v += red[ww][t][rr];
-        const int orow = blockIdx.x * RB + rr;
+        const int orow = bx * RB + rr;
         if (orow < N) {
             if (shared) {
                 const float g = shared_logit ? 1.0f / (1.0f + expf(-shared_logit[t])) : 1.0f;
@@ -1350,7 +1509,7 @@ __device__ __forceinline__ void dc_finish(float* acc, float (*red)[TM][8], int M
     }
 }
 
-template <int QT, int TM>
+template <int QT, int TM, bool RL>
 __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict__ dbase, int64_t dstride, int N,
                                                       int K, const float* __restrict__ inter,
                                                       const float* __restrict__ isum, int isum8,
@@ -1370,7 +1529,9 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
     float* xs = (float*)smem;
     float* iss = xs + P * xrs;
     const int r = lane & 7, p = (lane >> 3) & 3, u = lane >> 5;
-    const int row = blockIdx.x * RB + r;
+    // RL: row blocks bx = blockIdx.x, + gridDim.x, ..., all on the rows staged once
+    const int nrb = (N + RB - 1) / RB;
+    int bx = blockIdx.x, row = bx * RB + r;
     PG_DECL;
     PG_MARK(3, 0);
     // 1. the experts of this lane's first two items straight from the descriptor, then
@@ -1400,24 +1561,41 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
         copy_words<2>((u32x4*)iss, (const u32x4*)isum, P * (K >> 6), tid, nth);
     __syncthreads();
     PG_MARK(3, 1);
-    // 2. items, two per lane per pass
-    float acc[TM];
-#pragma unroll
-    for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+    // 2. items, two per lane per pass (row block after row block)
     for (;;) {
-        dc_item<QT, TM>(q0, it0 < S, it0, nb, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
-        dc_item<QT, TM>(q1, it1 < S, it1, nb, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
-        it0 += 4 * nw;
-        it1 += 4 * nw;
-        if (it0 - u >= S) break;  // wave-uniform (it0 - u is the pass's first item): no item left
-        // (rare) more items than lanes: next pass
-        e0 = ident ? 0 : desc[kDescSlot + 4 * min(it0 / nb, 127)];
-        e1 = ident ? 0 : desc[kDescSlot + 4 * min(it1 / nb, 127)];
-        load_qtr<QT>(q0, dbase + (int64_t)(it0 < S ? e0 : 0) * dstride, N, nb, row, it0 % nb, p);
-        load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, row, it1 % nb, p);
+        float acc[TM];
+#pragma unroll
+        for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+        for (;;) {
+            dc_item<QT, TM>(q0, it0 < S, it0, nb, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
+            dc_item<QT, TM>(q1, it1 < S, it1, nb, p, xs, xrs, iss, srs, d_pb, d_cnt, d_tok, d_w, acc);
+            it0 += 4 * nw;
+            it1 += 4 * nw;
+            if (it0 - u >= S) break;  // wave-uniform (it0 - u is the pass's first item): no item left
+            // (rare) more items than lanes: next pass
+            e0 = ident ? 0 : desc[kDescSlot + 4 * min(it0 / nb, 127)];
+            e1 = ident ? 0 : desc[kDescSlot + 4 * min(it1 / nb, 127)];
+            load_qtr<QT>(q0, dbase + (int64_t)(it0 < S ? e0 : 0) * dstride, N, nb, row, it0 % nb, p);
+            load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, row, it1 % nb, p);
+        }
+        PG_MARK(3, 2);
+        // the next row block's first pass goes out before this one's sums are formed
+        const int bn = bx + (int)gridDim.x;
+        if (RL && bn < nrb) {
+            it0 = 2 * w + u;
+            it1 = it0 + 2 * nw;
+            e0 = ident ? 0 : desc[kDescSlot + 4 * min(it0 / nb, 127)];
+            e1 = ident ? 0 : desc[kDescSlot + 4 * min(it1 / nb, 127)];
+            const int rown = bn * RB + r;
+            load_qtr<QT>(q0, dbase + (int64_t)(it0 < S ? e0 : 0) * dstride, N, nb, rown, it0 % nb, p);
+            load_qtr<QT>(q1, dbase + (int64_t)(it1 < S ? e1 : 0) * dstride, N, nb, rown, it1 % nb, p);
+        }
+        dc_finish<TM>(acc, red, M, N, shared, shared_logit, out, bx);
+        if (!RL || bn >= nrb) break;
+        bx = bn;
+        row = bx * RB + r;
+        __syncthreads();  // red is rewritten by the next row block
     }
-    PG_MARK(3, 2);
-    dc_finish<TM>(acc, red, M, N, shared, shared_logit, out);
     PG_MARK(3, 4);
     PG_FLUSH(3);
 }
@@ -1517,7 +1695,7 @@ __global__ __launch_bounds__(1024) void dec_dc_chunk_kernel(const uint8_t* __res
         __syncthreads();
     }
     // 3. lanes and waves -> the tokens' outputs
-    dc_finish<TM>(acc, red, M, N, shared, shared_logit, out);
+    dc_finish<TM>(acc, red, M, N, shared, shared_logit, out, blockIdx.x);
 }
 
 // Per-expert down GEMV: partial[p, row] = w[perm[p]] * (inter_p . d_row) for the pairs of
@@ -1679,6 +1857,8 @@ inline int dc_chunk(int P, int K) {
 // `kernel` on the current device (at least 1): a grid past that waits a whole block
 // duration for its last round.
 int resident_rows(const void* kernel, int threads, size_t lds, int gx, int gy);
+// Blocks of `kernel` resident on the current device at once (at least 1).
+int resident_blocks(const void* kernel, int threads, size_t lds);
 
 template <int QT, int TM>
 inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, const DecDisp& dp,
@@ -1688,18 +1868,27 @@ inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const flo
     const bool h8 = dp.mode == kRoute && TM == 1 && gu_rows8<QT>();
     const int nbk = g.K >> 8, W8 = (nbk + 1) / 2;
     const int W = h8 ? (W8 > 16 ? 16 : W8) : gu_waves(dp.mode == kLinear ? (nbk + 1) / 2 : nbk);
-    const int gx = div_up(g.N, h8 ? 8 : 16);
+    int gx = div_up(g.N, h8 ? 8 : 16);
     const int gy = gu_slot_blocks(max_active);
     // every router row needs a wave (TM / 2 with 4+ tokens)
-    const int gmin = dp.mode == kRoute ? div_up((dp.E + (rt.extra_w ? 1 : 0)) * (TM < 4 ? TM : 4), gx * W) : 1;
+    const int rrows = dp.mode == kRoute ? (dp.E + (rt.extra_w ? 1 : 0)) * (TM < 4 ? TM : 4) : 0;
     const size_t sh = gu_lds_bytes(dp.M, g.K);
     // slot rows: as many as fit in one round of resident blocks (blocks loop over the rest)
 #define PG_GU(MODE, RE)                                                                                         \
     do {                                                                                                        \
-        int gyr = resident_rows((const void*)dec_gu_kernel<QT, TM, MODE, RE>, 64 * W, sh, gx, gy);              \
+        int gyr = resident_rows((const void*)dec_gu_kernel<QT, TM, MODE, RE, false>, 64 * W, sh, gx, gy);       \
+        const int res = resident_blocks((const void*)dec_gu_kernel<QT, TM, MODE, RE, true>, 64 * W, sh);        \
+        /* more row blocks than resident blocks: one round, each block looping over rows */                    \
+        const bool rl = gyr == 1 && gx > res;                                                                   \
+        if (rl) gx = res;                                                                                       \
+        const int gmin = rrows ? div_up(rrows, gx * W) : 1;                                                     \
         gyr = gyr > gmin ? gyr : gmin;                                                                          \
-        PG_LAUNCH((dec_gu_kernel<QT, TM, MODE, RE>), dim3(gx, gyr), dim3(64 * W), sh, st, g.base, u.base,       \
-                  g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt, inter, isum);                            \
+        if (rl)                                                                                                 \
+            PG_LAUNCH((dec_gu_kernel<QT, TM, MODE, RE, true>), dim3(gx, gyr), dim3(64 * W), sh, st, g.base,     \
+                      u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt, inter, isum);                \
+        else                                                                                                    \
+            PG_LAUNCH((dec_gu_kernel<QT, TM, MODE, RE, false>), dim3(gx, gyr), dim3(64 * W), sh, st, g.base,    \
+                      u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt, inter, isum);                \
     } while (0)
     if (dp.mode == kRoute) {
         if (dp.E <= 128)
@@ -1730,9 +1919,18 @@ inline void dc_launch(const Mats& d, const float* inter, const float* isum, int 
                       uint64_t* clear, int n_clear, hipStream_t st) {
     const int nb = d.K >> 8, JC = dc_chunk(P, d.K);
     const int W = dc_waves(max_active * JC);  // items of a chunk
-    if (JC >= nb)
-        PG_LAUNCH((dec_dc_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, nb), st, d.base,
-                  d.stride, d.N, d.K, inter, isum, isum8, desc, M, P, shared, shared_logit, out, clear, n_clear);
+    if (JC >= nb) {
+        // two or more row blocks per resident block: one round, each block looping over rows
+        // on the rows it staged once (fewer: the loop's registers cost more than it saves)
+        const int rb = div_up(d.N, 8);
+        const int res = resident_blocks((const void*)dec_dc_kernel<QT, TM, true>, 64 * W, dc_lds_bytes(P, nb));
+        if (rb >= 2 * res)
+            PG_LAUNCH((dec_dc_kernel<QT, TM, true>), dim3(res), dim3(64 * W), dc_lds_bytes(P, nb), st, d.base,
+                      d.stride, d.N, d.K, inter, isum, isum8, desc, M, P, shared, shared_logit, out, clear, n_clear);
+        else
+            PG_LAUNCH((dec_dc_kernel<QT, TM, false>), dim3(rb), dim3(64 * W), dc_lds_bytes(P, nb), st, d.base,
+                      d.stride, d.N, d.K, inter, isum, isum8, desc, M, P, shared, shared_logit, out, clear, n_clear);
+    }
     else
         PG_LAUNCH((dec_dc_chunk_kernel<QT, TM>), dim3(div_up(d.N, 8)), dim3(64 * W), dc_lds_bytes(P, JC), st,
                   d.base, d.stride, d.N, d.K, JC, inter, isum, isum8, desc, M, P, shared, shared_logit, out, clear,

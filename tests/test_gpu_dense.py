@@ -72,7 +72,8 @@ def test_dense_q8(M):
     _run("dense_q8", M, 8)
 
 
-@pytest.mark.parametrize("M", [1, 4096])
+# M = 1, 4, 8: the decode gate/up and down loop over row blocks (N = 12288 and 4096)
+@pytest.mark.parametrize("M", [1, 4, 8, 4096])
 def test_dense_8b(M):
     _run("dense_8b", M, 4)
 

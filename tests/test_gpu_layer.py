@@ -112,12 +112,14 @@ def test_qwen3_prefill_zipf():
     assert (counts == 0).sum() > 0 and counts.max() > 500
 
 
-@pytest.mark.parametrize("M", [1, 8, 2048])
+# M = 1..8: N = 14336 gives more gate/up row blocks (and H = 4096 down row blocks) than
+# resident blocks, so the decode launches loop over row blocks
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 2048])
 def test_mixtral(M):
     _run("mixtral_8x7b", M, 6)
 
 
-@pytest.mark.parametrize("M", [1, 8, 512])
+@pytest.mark.parametrize("M", [1, 2, 8, 512])
 def test_qwen2_shared_expert(M):
     _run("qwen2_57b_a14b", M, 6)
 
