@@ -486,7 +486,7 @@ def main() -> int:
     dom_bytes = d1["active_experts"] * gu_mat
     dom_us = ku[0]
     dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
-    trace_us = load_trace_avg("dec_gu_kernel<12, 1, 1, 2>")
+    trace_us = load_trace_avg("dec_gu_kernel<12, 1, 1, 2, false>")
     layer_gbs = d1["active_weight_bytes"] / (d1["us_per_step"] * 1e-6) / 1e9
     traffic, traffic_rec = load_traffic(dom_kernel)
 

@@ -24,5 +24,5 @@ def test_traffic_record_resolves():
 
 
 def test_trace_average_resolves():
-    us = bench.load_trace_avg("dec_gu_kernel<12, 1, 1, 2>")
+    us = bench.load_trace_avg("dec_gu_kernel<12, 1, 1, 2, false>")
     assert us is not None and 1.0 < us < 100.0
