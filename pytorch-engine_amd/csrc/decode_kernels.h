@@ -1284,155 +1284,146 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
             }
         }
     } else {
+        // Items (slot a, row block bx), slot-major, i = a * nrb + bx: block b takes items b,
+        // b + G, b + 2G, ... (G = gridDim.x; the host launches one round of resident blocks,
+        // gridDim.y = 1), so every block gets the same number of items to within one.
+        const int nrb = (N + (h8 ? 7 : RB - 1)) / (h8 ? 8 : RB);
+        const int n_items = nrb * slot_at(0).n_act;
         if constexpr (h8) {
             const int r8 = lane & 7, p8 = (lane >> 3) & 3, u8 = lane >> 5;
             float* red8 = &red[0][0][0];  // [W][2][8]
-            // row blocks bx = blockIdx.x, + gridDim.x, ..., each with every slot of the column
-            const int nrb = (N + 7) >> 3;
-            for (int bx = blockIdx.x;; bx += gridDim.x) {
+            for (int i = blockIdx.x; i < n_items; i += gridDim.x) {
+                const int a = i / nrb, bx = i - a * nrb;
                 const int row8 = bx * 8 + r8;
-                for (int a = blockIdx.y;; a += gridDim.y) {
-                    const SlotInfo si = slot_at(a);
-                    if (si.e < 0) break;  // uniform over the block
-                    PG_MARK(1, 2);
-                    const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
-                    float acc[1] = {0.f};
-                    for (int j = w; j < nb; j += 2 * nw) {
-                        const int j1 = j + nw;
-                        Qtr<QT> l0, l1;
-                        load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
-                        load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
-                        gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
-                        if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
-                    }
-                    PG_MARK(1, 4);
-                    // quarters -> rows (lanes r, r+8, r+16, r+24 of each half); waves in LDS
-                    float v8 = acc[0];
-                    v8 += xor_lane<8>(v8);
-                    v8 += xor_lane<16>(v8);
-                    if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
-                    __syncthreads();
-                    if (tid < 8) {  // row rr of the token's SwiGLU row
-                        const int rr = tid;
-                        float gs = 0.f, us = 0.f;
-                        for (int ww = 0; ww < nw; ++ww) {
-                            gs += red8[(ww * 2) * 8 + rr];
-                            us += red8[(ww * 2 + 1) * 8 + rr];
-                        }
-                        const float v = gate_act(dp.act, gs) * us;
-                        const int orow = bx * 8 + rr;
-                        if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
-                        if (isum) {
-                            const float sm = group_sum<8>(v);
-                            if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
-                        }
-                    }
-                    if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
-                    __syncthreads();                           // red is rewritten by the next slot
+                const SlotInfo si = slot_at(a);
+                PG_MARK(1, 2);
+                const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
+                float acc[1] = {0.f};
+                for (int j = w; j < nb; j += 2 * nw) {
+                    const int j1 = j + nw;
+                    Qtr<QT> l0, l1;
+                    load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
+                    load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
+                    gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
                 }
-                if (bx + (int)gridDim.x >= nrb) break;
-                __syncthreads();  // red is rewritten by the next row block
+                PG_MARK(1, 4);
+                float v8 = acc[0];
+                v8 += xor_lane<8>(v8);
+                v8 += xor_lane<16>(v8);
+                if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
+                __syncthreads();
+                if (tid < 8) {  // row rr of the token's SwiGLU row
+                    const int rr = tid;
+                    float gs = 0.f, us = 0.f;
+                    for (int ww = 0; ww < nw; ++ww) {
+                        gs += red8[(ww * 2) * 8 + rr];
+                        us += red8[(ww * 2 + 1) * 8 + rr];
+                    }
+                    const float v = gate_act(dp.act, gs) * us;
+                    const int orow = bx * 8 + rr;
+                    if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
+                    if (isum) {
+                        const float sm = group_sum<8>(v);
+                        if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
+                    }
+                }
+                if (i + (int)gridDim.x < n_items) __syncthreads();  // red is rewritten by the next item
             }
         }
         if constexpr (!h8) {
-            // row blocks bx = blockIdx.x, + gridDim.x, ..., each with every slot of the column
-            const int nrb = (N + RB - 1) / RB;
-            for (int bx = blockIdx.x;; bx += gridDim.x) {
-                const int row = bx * RB + r;
-                auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
-                    return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
-                };
-                // items, two per wave at a time (both quarters' loads in flight together): pass `it`
-                // holds items it and it + nw (the second clamped to a readable item past the end);
-                // q0, q1: the prefetched pass
-                Qtr<QT> q0, q1;
-                auto load_pass = [&](const uint8_t* mat, int it) {
-                    const int it1 = min(it + nw, nit - 1);
-                    load_qtr<QT>(q0, mat, N, nb, row, lin ? it : it >> 1, p);
-                    load_qtr<QT>(q1, mat, N, nb, row, lin ? it1 : it1 >> 1, p);
-                };
-                int a = blockIdx.y;
-                SlotInfo si = slot_at(a);
+            auto mat_of = [&](int e) {  // wave w's matrix of expert e (odd waves: up)
+                return (!lin && (w & 1)) ? ubase + (int64_t)e * ustride : gbase + (int64_t)e * gstride;
+            };
+            // passes of two items (matrix / super-block) a wave, as in the one-round form;
+            // q0, q1: the prefetched pass of row rw
+            Qtr<QT> q0, q1;
+            auto load_pass = [&](const uint8_t* mat, int rw, int it) {
+                const int it1 = min(it + nw, nit - 1);
+                load_qtr<QT>(q0, mat, N, nb, rw, lin ? it : it >> 1, p);
+                load_qtr<QT>(q1, mat, N, nb, rw, lin ? it1 : it1 >> 1, p);
+            };
+            int i = blockIdx.x;
+            SlotInfo si;
+            if (i < n_items) {
+                si = slot_at(i / nrb);
                 if constexpr (pf)
-                    if (si.e >= 0 && w < nit) load_pass(mat_of(si.e), w);
-                while (si.e >= 0) {  // uniform over the block
-                    PG_MARK(1, 2);
-                    if constexpr (MODE == kRoute && TM >= 2)
-                        if (nw <= 8) slot_prio((si.n_act - 1 - a) / (int)gridDim.y);  // two blocks a CU
-                    const uint8_t* mat = mat_of(si.e);
-                    float acc[TM];
-            #pragma unroll
-                    for (int t = 0; t < TM; ++t) acc[t] = 0.f;
-                    for (int it = w; it < nit; it += 2 * nw) {
-                        const int it1 = it + nw;
-                        const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
-                        if constexpr (pf) {
-                            if (it != w) load_pass(mat, it);
-                            gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                            if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                        } else {
-                            Qtr<QT> l0, l1;
-                            load_qtr<QT>(l0, mat, N, nb, row, j0, p);
-                            load_qtr<QT>(l1, mat, N, nb, row, j1, p);
-                            gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                            if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
-                        }
-                    }
-                    PG_MARK(1, 4);
-                    SlotInfo sn;
+                    if (w < nit) load_pass(mat_of(si.e), (i % nrb) * RB + r, w);
+            }
+            constexpr bool one = MODE == kIdent || MODE == kLinear;  // one slot: item = row block
+            while (i < n_items) {  // uniform over the block
+                const int a = one ? 0 : i / nrb, bx = i - a * nrb;
+                const int row = bx * RB + r;
+                PG_MARK(1, 2);
+                const uint8_t* mat = mat_of(si.e);
+                float acc[TM];
+#pragma unroll
+                for (int t = 0; t < TM; ++t) acc[t] = 0.f;
+                for (int it = w; it < nit; it += 2 * nw) {
+                    const int it1 = it + nw;
+                    const int j0 = lin ? it : it >> 1, j1 = lin ? min(it1, nit - 1) : min(it1, nit - 1) >> 1;
                     if constexpr (pf) {
-                        sn = slot_at(a + gridDim.y);
-                        if (sn.e >= 0 && w < nit) load_pass(mat_of(sn.e), w);
+                        if (it != w) load_pass(mat, row, it);
+                        gu_qtr<TM>(q0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                        if (it1 < nit) gu_qtr<TM>(q1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    } else {
+                        Qtr<QT> l0, l1;
+                        load_qtr<QT>(l0, mat, N, nb, row, j0, p);
+                        load_qtr<QT>(l1, mat, N, nb, row, j1, p);
+                        gu_qtr<TM>(l0, j0, p, xs, xrs, xss, srs, si.toks, si.count, acc);
+                        if (it1 < nit) gu_qtr<TM>(l1, j1, p, xs, xrs, xss, srs, si.toks, si.count, acc);
                     }
-                    // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
-            #pragma unroll
-                    for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
-                    if (p == 0) {
-            #pragma unroll
-                        for (int t = 0; t < TM; ++t)
-                            if (t < si.count) red[w][t][r] = acc[t];
-                    }
-                    __syncthreads();
-                    // thread (t, rr) = (tid / 16, tid % 16): whole 16-lane groups, so the 16-row sum
-                    // of a token is a shuffle reduction inside its group
-                    const int cnt = si.count, p0 = si.p_begin;
-                    if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
-                        const int t = tid >> 4, rr = tid & 15;
-                        const int orow = bx * RB + rr;
-                        float v = red[0][t][rr];
-                        for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
-                        if (orow < N) {
-                            if (dp.bias) v = v + dp.bias[orow];
-                            if (dp.out_f16)
-                                ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
-                            else
-                                inter[(int64_t)(p0 + t) * N + orow] = v;
-                        }
-                    } else if (tid < cnt * RB) {
-                        const int t = tid >> 4, rr = tid & 15;
-                        float g = 0.f, u = 0.f;
-                        for (int ww = 0; ww < nw; ww += 2) {
-                            g += red[ww][t][rr];
-                            u += red[ww + 1][t][rr];
-                        }
-                        const float v = gate_act(dp.act, g) * u;
-                        const int orow = bx * RB + rr;
-                        if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
-                        if (isum) {
-                            const float sm = group_sum<16>(v);
-                            if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
-                        }
-                    }
-                    if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
-                    __syncthreads();                           // red is rewritten by the next slot
-                    a += gridDim.y;
-                    if constexpr (pf)
-                        si = sn;
-                    else
-                        si = slot_at(a);
                 }
-                if (bx + (int)gridDim.x >= nrb) break;
-                __syncthreads();  // red is rewritten by the next row block
+                PG_MARK(1, 4);
+                // the next item's slot, and (pf) its first pass before this item's epilogue
+                const int in = i + (int)gridDim.x;
+                SlotInfo sn;
+                if (in < n_items) {
+                    sn = one ? si : slot_at(in / nrb);
+                    if constexpr (pf)
+                        if (w < nit) load_pass(mat_of(sn.e), (in % nrb) * RB + r, w);
+                }
+                // quarters -> rows (lanes r, r+16, r+32, r+48); waves -> gate (even) / up (odd)
+#pragma unroll
+                for (int t = 0; t < TM; ++t) acc[t] = kslot_sum<RB>(acc[t]);
+                if (p == 0) {
+#pragma unroll
+                    for (int t = 0; t < TM; ++t)
+                        if (t < si.count) red[w][t][r] = acc[t];
+                }
+                __syncthreads();
+                const int cnt = si.count, p0 = si.p_begin;
+                if (lin && tid < cnt * RB) {  // every wave's partial of the one matrix, in wave order
+                    const int t = tid >> 4, rr = tid & 15;
+                    const int orow = bx * RB + rr;
+                    float v = red[0][t][rr];
+                    for (int ww = 1; ww < nw; ++ww) v = v + red[ww][t][rr];
+                    if (orow < N) {
+                        if (dp.bias) v = v + dp.bias[orow];
+                        if (dp.out_f16)
+                            ((half_t*)inter)[(int64_t)(p0 + t) * N + orow] = (half_t)v;
+                        else
+                            inter[(int64_t)(p0 + t) * N + orow] = v;
+                    }
+                } else if (tid < cnt * RB) {
+                    const int t = tid >> 4, rr = tid & 15;
+                    float g = 0.f, u = 0.f;
+                    for (int ww = 0; ww < nw; ww += 2) {
+                        g += red[ww][t][rr];
+                        u += red[ww + 1][t][rr];
+                    }
+                    const float v = gate_act(dp.act, g) * u;
+                    const int orow = bx * RB + rr;
+                    if (orow < N) inter[(int64_t)(p0 + t) * N + orow] = v;
+                    if (isum) {
+                        const float sm = group_sum<16>(v);
+                        if (rr == 0 && orow < N) isum[(int64_t)(p0 + t) * (N >> 4) + (orow >> 4)] = sm;
+                    }
+                }
+                if (in >= n_items) break;
+                __syncthreads();  // red is rewritten by the next item
+                i = in;
+                si = sn;
             }
         }
     }
@@ -1878,11 +1869,12 @@ inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const flo
     do {                                                                                                        \
         int gyr = resident_rows((const void*)dec_gu_kernel<QT, TM, MODE, RE, false>, 64 * W, sh, gx, gy);       \
         const int res = resident_blocks((const void*)dec_gu_kernel<QT, TM, MODE, RE, true>, 64 * W, sh);        \
-        /* more row blocks than resident blocks: one round, each block looping over rows */                    \
-        const bool rl = gyr == 1 && gx > res;                                                                   \
-        if (rl) gx = res;                                                                                       \
+        /* not two slot rows in one round: one round of blocks taking (slot, row block) items */               \
+        const int gxr = gx * gy < res ? gx * gy : res;                                                          \
+        const bool rl = gyr == 1 && (gy > 1 || gx > res) && gxr * W >= rrows; /* a wave per router row */      \
+        if (rl) gx = gxr;                                                                                       \
         const int gmin = rrows ? div_up(rrows, gx * W) : 1;                                                     \
-        gyr = gyr > gmin ? gyr : gmin;                                                                          \
+        gyr = rl ? 1 : gyr > gmin ? gyr : gmin;                                                                 \
         if (rl)                                                                                                 \
             PG_LAUNCH((dec_gu_kernel<QT, TM, MODE, RE, true>), dim3(gx, gyr), dim3(64 * W), sh, st, g.base,     \
                       u.base, g.stride, u.stride, g.N, g.K, x, xsum, topk, dp, rt, inter, isum);                \
