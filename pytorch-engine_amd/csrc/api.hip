@@ -442,8 +442,10 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
             return launch_dec_down_combine(lm.down, WS(float, inter), WS(float, isum),
                                            decode_isum_rows8(lm.gate.qtype, M), WS(int32_t, desc), M, K,
                                            max_active, shared, shared_logit, out, WS(uint64_t, rlog), decode_rlog_words(M, E), st);
-        // (one token: the down kernel forms its 16-row sums itself from the staged rows)
-        if ((rc = launch_dec_down(lm.down, WS(float, inter), M == 1 ? nullptr : WS(float, isum), M, WS(int32_t, offsets),
+        // (one token, or 8-row sums from the gate/up: the down kernel forms its 16-row sums
+        // itself from the staged rows)
+        const bool own_sums = M == 1 || decode_isum_rows8(lm.gate.qtype, M);
+        if ((rc = launch_dec_down(lm.down, WS(float, inter), own_sums ? nullptr : WS(float, isum), M, WS(int32_t, offsets),
                                   WS(int32_t, perm), WS(int32_t, active), WS(int32_t, nact), max_active, WS(float, w),
                                   WS(float, partial), st)))
             return rc;

@@ -14,7 +14,7 @@ namespace pgmoe {
     return fail(PGMOE_E_UNSUPPORTED, what ": qtype %d", qt);
 
 bool decode_isum_rows8(int qtype, int M) {
-    if (M != 1) return false;
+    if (M < 1 || M > 2) return false;
     switch (qtype) {
     case PGMOE_Q4_1: return gu_rows8<PGMOE_Q4_1>();
     case PGMOE_Q4_K: return gu_rows8<PGMOE_Q4_K>();

@@ -1136,11 +1136,12 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         else
             return slot_plain<MODE>(dp, a, topk);
     };
-    // One token (h8): 8-row blocks, three a CU (384 16-row blocks left half the CUs with
-    // two, which end last).  Lane = (row r of 8, quarter p, matrix u = lane >> 5 (0 gate,
-    // 1 up)); wave w takes super-blocks w, w + W, ... of both matrices, two at a time.  The
-    // inter rows' sums go out as 8-row sums (isum [P][N/8]).
-    constexpr bool h8 = MODE == kRoute && TM == 1 && gu_rows8<QT>();
+    // One or two tokens (h8): 8-row blocks of half the waves (for C2 with one token, 768
+    // blocks three a CU, where 384 16-row blocks left half the CUs with two, which ended
+    // last).  Lane = (row r of 8, quarter p, matrix u = lane >> 5 (0 gate, 1 up)); wave w
+    // takes super-blocks w, w + W, ... of both matrices, two at a time.  The inter rows'
+    // sums go out as 8-row sums (isum [P][N/8]).
+    constexpr bool h8 = MODE == kRoute && TM <= 2 && gu_rows8<QT>();
     // One row block per block (the grid covers the rows), or (RL) row blocks blockIdx.x,
     // + gridDim.x, ... per block: the two forms are kept apart so the first compiles as
     // it does without the second.
@@ -1148,41 +1149,48 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         if constexpr (h8) {
             const int r8 = lane & 7, p8 = (lane >> 3) & 3, u8 = lane >> 5;
             const int row8 = blockIdx.x * 8 + r8;
-            float* red8 = &red[0][0][0];  // [W][2][8]
+            float* red8 = &red[0][0][0];  // [W][2][TM][8]
             for (int a = blockIdx.y;; a += gridDim.y) {
                 const SlotInfo si = slot_at(a);
                 if (si.e < 0) break;  // uniform over the block
                 PG_MARK(1, 2);
                 const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
-                float acc[1] = {0.f};
+                float acc[TM];
+#pragma unroll
+                for (int t = 0; t < TM; ++t) acc[t] = 0.f;
                 for (int j = w; j < nb; j += 2 * nw) {
                     const int j1 = j + nw;
                     Qtr<QT> l0, l1;
                     load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
                     load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
-                    gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
-                    if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    gu_qtr<TM>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    if (j1 < nb) gu_qtr<TM>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
                 }
                 PG_MARK(1, 4);
                 // quarters -> rows (lanes r, r+8, r+16, r+24 of each half); waves in LDS
-                float v8 = acc[0];
-                v8 += xor_lane<8>(v8);
-                v8 += xor_lane<16>(v8);
-                if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
+#pragma unroll
+                for (int t = 0; t < TM; ++t) {
+                    float v8 = acc[t];
+                    v8 += xor_lane<8>(v8);
+                    v8 += xor_lane<16>(v8);
+                    if (p8 == 0) red8[((w * 2 + u8) * TM + t) * 8 + r8] = v8;
+                }
                 __syncthreads();
-                if (tid < 8) {  // row rr of the token's SwiGLU row
-                    const int rr = tid;
+                // (one token: tid < 8, t = 0, the count is 1)
+                if (TM == 1 ? tid < 8 : tid < TM * 8 && (tid >> 3) < si.count) {  // row rr of token t
+                    const int t = TM == 1 ? 0 : tid >> 3, rr = TM == 1 ? tid : tid & 7;
                     float gs = 0.f, us = 0.f;
                     for (int ww = 0; ww < nw; ++ww) {
-                        gs += red8[(ww * 2) * 8 + rr];
-                        us += red8[(ww * 2 + 1) * 8 + rr];
+                        gs += red8[((ww * 2) * TM + t) * 8 + rr];
+                        us += red8[((ww * 2 + 1) * TM + t) * 8 + rr];
                     }
                     const float v = gate_act(dp.act, gs) * us;
                     const int orow = blockIdx.x * 8 + rr;
-                    if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
+                    const int64_t pr = si.p_begin + t;
+                    if (orow < N) inter[pr * N + orow] = v;
                     if (isum) {
                         const float sm = group_sum<8>(v);
-                        if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
+                        if (rr == 0 && orow < N) isum[pr * (N >> 3) + (orow >> 3)] = sm;
                     }
                 }
                 if (a + (int)gridDim.y >= si.n_act) break;  // the block's last slot
@@ -1291,41 +1299,48 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
         const int n_items = nrb * slot_at(0).n_act;
         if constexpr (h8) {
             const int r8 = lane & 7, p8 = (lane >> 3) & 3, u8 = lane >> 5;
-            float* red8 = &red[0][0][0];  // [W][2][8]
+            float* red8 = &red[0][0][0];  // [W][2][TM][8]
             for (int i = blockIdx.x; i < n_items; i += gridDim.x) {
                 const int a = i / nrb, bx = i - a * nrb;
                 const int row8 = bx * 8 + r8;
                 const SlotInfo si = slot_at(a);
                 PG_MARK(1, 2);
                 const uint8_t* mat = u8 ? ubase + (int64_t)si.e * ustride : gbase + (int64_t)si.e * gstride;
-                float acc[1] = {0.f};
+                float acc[TM];
+#pragma unroll
+                for (int t = 0; t < TM; ++t) acc[t] = 0.f;
                 for (int j = w; j < nb; j += 2 * nw) {
                     const int j1 = j + nw;
                     Qtr<QT> l0, l1;
                     load_qtr<QT>(l0, mat, N, nb, row8, j, p8);
                     load_qtr<QT>(l1, mat, N, nb, row8, min(j1, nb - 1), p8);
-                    gu_qtr<1>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
-                    if (j1 < nb) gu_qtr<1>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    gu_qtr<TM>(l0, j, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
+                    if (j1 < nb) gu_qtr<TM>(l1, j1, p8, xs, xrs, xss, srs, si.toks, si.count, acc);
                 }
                 PG_MARK(1, 4);
-                float v8 = acc[0];
-                v8 += xor_lane<8>(v8);
-                v8 += xor_lane<16>(v8);
-                if (p8 == 0) red8[(w * 2 + u8) * 8 + r8] = v8;
+#pragma unroll
+                for (int t = 0; t < TM; ++t) {
+                    float v8 = acc[t];
+                    v8 += xor_lane<8>(v8);
+                    v8 += xor_lane<16>(v8);
+                    if (p8 == 0) red8[((w * 2 + u8) * TM + t) * 8 + r8] = v8;
+                }
                 __syncthreads();
-                if (tid < 8) {  // row rr of the token's SwiGLU row
-                    const int rr = tid;
+                // (one token: tid < 8, t = 0, the count is 1)
+                if (TM == 1 ? tid < 8 : tid < TM * 8 && (tid >> 3) < si.count) {  // row rr of token t
+                    const int t = TM == 1 ? 0 : tid >> 3, rr = TM == 1 ? tid : tid & 7;
                     float gs = 0.f, us = 0.f;
                     for (int ww = 0; ww < nw; ++ww) {
-                        gs += red8[(ww * 2) * 8 + rr];
-                        us += red8[(ww * 2 + 1) * 8 + rr];
+                        gs += red8[((ww * 2) * TM + t) * 8 + rr];
+                        us += red8[((ww * 2 + 1) * TM + t) * 8 + rr];
                     }
                     const float v = gate_act(dp.act, gs) * us;
                     const int orow = bx * 8 + rr;
-                    if (orow < N) inter[(int64_t)si.p_begin * N + orow] = v;
+                    const int64_t pr = si.p_begin + t;
+                    if (orow < N) inter[pr * N + orow] = v;
                     if (isum) {
                         const float sm = group_sum<8>(v);
-                        if (rr == 0 && orow < N) isum[(int64_t)si.p_begin * (N >> 3) + (orow >> 3)] = sm;
+                        if (rr == 0 && orow < N) isum[pr * (N >> 3) + (orow >> 3)] = sm;
                     }
                 }
                 if (i + (int)gridDim.x < n_items) __syncthreads();  // red is rewritten by the next item
@@ -1856,7 +1871,7 @@ inline void gu_launch(const Mats& g, const Mats& u, const uint16_t* x, const flo
                       const RouterIn& rt, int max_active, float* inter, float* isum, hipStream_t st) {
     // a linear has half the items of a gate/up pair: two per wave as well
     // the one-token routed launch: 8-row blocks, ceil(K/512) waves (both matrices a wave)
-    const bool h8 = dp.mode == kRoute && TM == 1 && gu_rows8<QT>();
+    const bool h8 = dp.mode == kRoute && TM <= 2 && gu_rows8<QT>();
     const int nbk = g.K >> 8, W8 = (nbk + 1) / 2;
     const int W = h8 ? (W8 > 16 ? 16 : W8) : gu_waves(dp.mode == kLinear ? (nbk + 1) / 2 : nbk);
     int gx = div_up(g.N, h8 ? 8 : 16);
