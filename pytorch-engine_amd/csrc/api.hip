@@ -77,7 +77,7 @@ static int check_pair(const Mats& g, const Mats& u, const char* what) {
 // ---------------------------------------------------------------- workspace layout
 struct Layout {
     size_t rlog, status, desc, xsum, isum, s_isum;
-    size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, dcounts, inter, a16, rs, partial, raw;
+    size_t logits, idx, w, offsets, perm, inv, active, nact, tile_off, tile_map, dcounts, inter, a16, rs, partial, raw;
     size_t s_offsets, s_perm, s_inv, s_active, s_nact, s_tile_off, s_w, s_logit, s_inter, s_a16, s_rs, s_partial;
     size_t total;
 };
@@ -118,6 +118,7 @@ static Layout layout_for(const pgmoe_layer* L, int M, int rlog_experts = 0) {
     o.active = take(c, E * 4);
     o.nact = take(c, 4);
     o.tile_off = take(c, (E + 1) * 4);
+    o.tile_map = take(c, gemm ? dispatch_tile_map_words((int64_t)P, (int)E, gemm_tile_rows()) * 4 : 0);
     o.dcounts = take(c, gemm ? dispatch_ws_bytes((int64_t)P, (int)E) : 0);  // multi-block dispatch scratch
     o.inter = take(c, P * I * 4);
     o.a16 = take(c, gemm ? P * I * 2 : 0);
@@ -456,15 +457,16 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
     if ((rc = launch_topk(WS(float, logits), M, E, K, L->norm_topk, WS(int32_t, idx), WS(float, w), st))) return rc;
     if ((rc = launch_dispatch(WS(int32_t, idx), M, K, E, BM, WS(int32_t, offsets), WS(int32_t, perm),
                               WS(int32_t, inv), WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), st,
-                              WS(int32_t, dcounts))))
+                              WS(int32_t, dcounts), WS(int32_t, tile_map))))
         return rc;
     if ((rc = launch_gateup(lm.gate, lm.up, x, M, K, WS(int32_t, offsets), WS(int32_t, perm), WS(int32_t, active),
                             WS(int32_t, nact), WS(int32_t, tile_off), mode, WS(float, inter), st, WS(float, raw),
-                            L->act)))
+                            L->act, WS(int32_t, tile_map))))
         return rc;
     if ((rc = launch_down(lm.down, WS(float, inter), M, K, WS(int32_t, offsets), WS(int32_t, perm),
                           WS(int32_t, active), WS(int32_t, nact), WS(int32_t, tile_off), WS(float, w), mode,
-                          WS(uint16_t, a16), WS(float, rs), WS(float, partial), st, WS(float, raw))))
+                          WS(uint16_t, a16), WS(float, rs), WS(float, partial), st, WS(float, raw),
+                          WS(int32_t, tile_map))))
         return rc;
     const float* shared = nullptr;
     const float* shared_logit = nullptr;

@@ -95,6 +95,33 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_count_kernel(const int3
     }
 }
 
+// The grouped GEMMs' tile order (thread e < E holds expert e's pair count): every full tile
+// in expert order, then the partial last tiles by rows, most first (ties: lower expert
+// first).  Entry = expert | (tile of the expert << kTileMapShift).  rem: kMaxExperts + 4 ints.
+__device__ void write_tile_map(int total, int E, int tile_rows, int32_t* __restrict__ tile_map, int* scan_buf,
+                               int* rem) {
+    const int e = threadIdx.x;
+    const int full = e < E ? total / tile_rows : 0;
+    const int part = e < E ? total - full * tile_rows : 0;
+    const int fi = block_inclusive_scan(full, scan_buf);
+    if (e < kMaxExperts) rem[e] = part;  // 0 past E
+    if (e == E - 1) rem[kMaxExperts] = fi;  // full tiles in all
+    __syncthreads();
+    for (int j = 0; j < full; ++j) tile_map[fi - full + j] = e | (j << kTileMapShift);
+    if (part > 0) {  // rank among the partial tiles, four remainders a read
+        int rank = rem[kMaxExperts];
+        const int4* r4 = reinterpret_cast<const int4*>(rem);
+#pragma unroll 8
+        for (int o4 = 0; o4 < (E + 3) >> 2; ++o4) {
+            const int4 r = r4[o4];
+            const int o = 4 * o4;
+            rank += (r.x > part || (r.x == part && o < e)) + (r.y > part || (r.y == part && o + 1 < e)) +
+                    (r.z > part || (r.z == part && o + 2 < e)) + (r.w > part || (r.w == part && o + 3 < e));
+        }
+        tile_map[rank] = e | (full << kTileMapShift);
+    }
+}
+
 // Block g of G: the stable scatter of its chunk.  Every block derives the expert offsets
 // from the counts (G = 1: from its own); block 0 also writes offsets, the active list
 // and the GEMM tile offsets.  Within a wave, 64 ascending ids at a time are ranked among
@@ -107,10 +134,22 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
                                                                 int32_t* __restrict__ inv,
                                                                 int32_t* __restrict__ active,
                                                                 int32_t* __restrict__ n_active,
-                                                                int32_t* __restrict__ tile_off) {
+                                                                int32_t* __restrict__ tile_off,
+                                                                int32_t* __restrict__ tile_map) {
+    static_assert(kMaxExperts <= (1 << kTileMapShift), "tile map expert field");
     __shared__ int cnt[kDispWaves][kMaxExperts];
     __shared__ int scan_buf[kDispWaves];
+    __shared__ __attribute__((aligned(16))) int rem_s[kMaxExperts + 4];
+    // with counts and a tile map, the last block only writes the map (beside the scatter)
+    const int G = (int)gridDim.x - (counts && tile_map ? 1 : 0);
     const int g = blockIdx.x;
+    if (g == G) {
+        int total = 0;
+        if (threadIdx.x < E)
+            for (int gg = 0; gg < G; ++gg) total += counts[(int64_t)gg * E + threadIdx.x];
+        write_tile_map(total, E, tile_rows, tile_map, scan_buf, rem_s);
+        return;
+    }
     const int b0 = g * C, b1 = min(P, (g + 1) * C);
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     int nbits = 0;  // bits of the largest id E - 1
@@ -122,7 +161,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
     int total = 0, before = 0;
     if (e < E) {
         if (counts) {
-            for (int gg = 0; gg < (int)gridDim.x; ++gg) {
+            for (int gg = 0; gg < G; ++gg) {
                 const int c = counts[(int64_t)gg * E + e];
                 total += c;
                 before += gg < g ? c : 0;
@@ -157,6 +196,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int32_t* _
             tile_off[e] = ti - nt;
             if (e == E - 1) tile_off[E] = ti;
         }
+        if (tile_map && !counts) write_tile_map(total, E, tile_rows, tile_map, scan_buf, rem_s);  // uniform
     }
     __syncthreads();  // the bases
 
@@ -196,6 +236,12 @@ static int dispatch_blocks(int64_t P) {
 
 size_t dispatch_ws_bytes(int64_t P, int E) { return (size_t)dispatch_blocks(P) * E * 4; }
 
+// Tiles of tile_rows pairs over at most E experts: at most P / tile_rows full ones and one
+// partial tile per expert.
+size_t dispatch_tile_map_words(int64_t P, int E, int tile_rows) {
+    return (size_t)(P / tile_rows + (P < E ? P : E) + 1);
+}
+
 // Identity dispatch of M tokens to one matrix (shared expert): offsets {0, M},
 // perm = inv = 0..M-1, active {0}, n_active 1, tile_off {0, ceil(M / tile_rows)}, w = 1.
 __global__ void identity_dispatch_kernel(int M, int tile_rows, int32_t* offsets, int32_t* perm, int32_t* inv,
@@ -218,7 +264,7 @@ __global__ void identity_dispatch_kernel(int M, int tile_rows, int32_t* offsets,
 
 int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int32_t* offsets, int32_t* perm,
                     int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st,
-                    int32_t* counts) {
+                    int32_t* counts, int32_t* tile_map) {
     if (E > kMaxExperts) return fail(PGMOE_E_UNSUPPORTED, "dispatch supports at most %d experts", kMaxExperts);
     if (tile_rows <= 0) return fail(PGMOE_E_INVALID, "tile_rows must be positive");
     const int64_t P = (int64_t)M * K;
@@ -231,8 +277,9 @@ int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int3
         int rc = check_launch("dispatch_count");
         if (rc) return rc;
     }
-    PG_LAUNCH(dispatch_kernel, dim3(G), dim3(kDispThreads), 0, st, idx, (int)P, E, C,
-              (const int32_t*)(G > 1 ? counts : nullptr), tile_rows, offsets, perm, inv, active, n_active, tile_off);
+    PG_LAUNCH(dispatch_kernel, dim3(G > 1 && tile_map ? G + 1 : G), dim3(kDispThreads), 0, st, idx, (int)P, E, C,
+              (const int32_t*)(G > 1 ? counts : nullptr), tile_rows, offsets, perm, inv, active, n_active, tile_off,
+              tile_map);
     return check_launch("dispatch");
 }
 

@@ -111,19 +111,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 // --------------------------------------------------------------------------- launchers
 int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                   const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
-                  int mode, float* inter, hipStream_t st, float* raw, int act) {
+                  int mode, float* inter, hipStream_t st, float* raw, int act, const int32_t* tile_map) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
     if (mode == 0)
         return launch_dec_gateup(g, u, x, nullptr, topk, M, offsets, perm, active, n_active, (int)(P < E ? P : E),
                                  inter, nullptr, st, act);
-    return launch_gemm_gateup(g, u, x, M, topk, offsets, perm, tile_off, inter, st, raw, act);
+    return launch_gemm_gateup(g, u, x, M, topk, offsets, perm, tile_off, inter, st, raw, act, tile_map);
 }
 
 int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_t* offsets, const int32_t* perm,
                 const int32_t* active, const int32_t* n_active, const int32_t* tile_off, const float* topk_w,
-                int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st, float* raw) {
+                int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st, float* raw,
+                const int32_t* tile_map) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
@@ -141,7 +142,7 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
         PG_LAUNCH(rowscale_kernel<0>, rgrid, dim3(256), 0, st, inter, (int)P, I, a16, rs);
     int rc = check_launch("rowscale");
     if (rc) return rc;
-    return launch_gemm_down(d, a16, rs, M, topk, offsets, perm, tile_off, topk_w, partial, st, raw);
+    return launch_gemm_down(d, a16, rs, M, topk, offsets, perm, tile_off, topk_w, partial, st, raw, tile_map);
 }
 
 int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H, const float* shared,

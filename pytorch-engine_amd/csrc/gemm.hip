@@ -18,7 +18,9 @@
 //            epilogue = partial[p][h] = w_p * rs_p * acc.
 // Tiles: the dispatch's tile_off counts 256-row tiles per expert; the last tile of an
 // expert holds the remainder (1..256 rows; 32-row slices past it skip their MFMAs and,
-// with 4 waves, their activation copies).  Block ids are ordered so the N tiles of one M
+// with 4 waves, their activation copies).  With the dispatch's tile map the M tiles run
+// every full tile first, then the partial ones by rows, most first: the long tiles do not
+// land at the end of the launch (a Zipf routing scatters the large experts over the ids).  Block ids are ordered so the N tiles of one M
 // tile run back to back on one XCD (blocks go to the 8 XCDs round-robin), so its
 // gathered A rows are shared through that XCD's L2.
 // Reference: GGUFQuantMoEExperts.forward_expert (quant_kernels.py:1990-2011) ->
@@ -386,8 +388,8 @@ template <int QT, bool GATEUP, int CT, int WM>
 __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     const uint8_t* __restrict__ w0, const uint8_t* __restrict__ w1, int64_t wstride0, int64_t wstride1,
     int N, int K, const uint16_t* __restrict__ act, int topk, int E, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ perm, const int32_t* __restrict__ tile_off, int n_ntiles,
-    const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out,
+    const int32_t* __restrict__ perm, const int32_t* __restrict__ tile_off, const int32_t* __restrict__ tile_map,
+    int n_ntiles, const float* __restrict__ rs, const float* __restrict__ topk_w, float* __restrict__ out,
     const uint8_t* __restrict__ s0, const uint8_t* __restrict__ s1, int ksplit, int kper, float* __restrict__ raw,
     int gate_act) {
     using L = GLay<QT, CT, WM>;
@@ -406,8 +408,15 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     // [ks kper, (ks + 1) kper) and writes raw accumulators, reduced by gemm_split_reduce_kernel
     const int ks = ksplit > 1 ? (int)(blockIdx.x % ksplit) : 0;
     if (!gemm_tile_of(ksplit > 1 ? blockIdx.x / ksplit : blockIdx.x, n_ntiles, tile_off[E], mt, nt)) return;
-    const int e = gemm_tile_expert(tile_off, E, mt);
-    const int m0 = offsets[e] + (mt - tile_off[e]) * kGM;
+    int e, m0;
+    if (tile_map) {  // the dispatch's tile order: full tiles first, then the partial ones
+        const int tm = tile_map[mt];
+        e = tm & ((1 << kTileMapShift) - 1);
+        m0 = offsets[e] + (tm >> kTileMapShift) * kGM;
+    } else {
+        e = gemm_tile_expert(tile_off, E, mt);
+        m0 = offsets[e] + (mt - tile_off[e]) * kGM;
+    }
     const int mrows = min(kGM, offsets[e + 1] - m0);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -703,7 +712,7 @@ static int gemm_max_mtiles(int64_t P, int E) {
 
 int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                        const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st, float* raw,
-                       int act) {
+                       int act, const int32_t* tile_map) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
@@ -714,7 +723,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
     const dim3 grid(gemm_max_mtiles(P, E) * nnt * sp.ksplit);
 #define PG_GU(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, true, PG_GU_CT, PG_GU_WM>), grid, dim3(64 * GLay<QT, PG_GU_CT, PG_GU_WM>::NW), 0, st, g.base, u.base, g.stride, u.stride, g.N, g.K, x, topk, \
-              E, offsets, perm, tile_off, nnt, (const float*)nullptr, (const float*)nullptr, inter, g.scales, u.scales, \
+              E, offsets, perm, tile_off, tile_map, nnt, (const float*)nullptr, (const float*)nullptr, inter, g.scales, u.scales, \
               sp.ksplit, sp.kper, raw, act)
     switch (g.qtype) {
     case PGMOE_Q4_1: PG_GU(PGMOE_Q4_1); break;
@@ -732,7 +741,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
 
 int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M, int topk, const int32_t* offsets,
                      const int32_t* perm, const int32_t* tile_off, const float* topk_w, float* partial,
-                     hipStream_t st, float* raw) {
+                     hipStream_t st, float* raw, const int32_t* tile_map) {
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
@@ -743,7 +752,7 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     const dim3 grid(gemm_max_mtiles(P, E) * nnt * sp.ksplit);
 #define PG_DN(QT)                                                                                               \
     PG_LAUNCH((gemm_kernel<QT, false, PG_DN_CT, PG_DN_WM>), grid, dim3(64 * GLay<QT, PG_DN_CT, PG_DN_WM>::NW), 0, st, d.base, d.base, d.stride, d.stride, d.N, d.K, a16,   \
-              topk, E, offsets, perm, tile_off, nnt, rs, topk_w, partial, d.scales, d.scales, sp.ksplit, sp.kper, raw, \
+              topk, E, offsets, perm, tile_off, tile_map, nnt, rs, topk_w, partial, d.scales, d.scales, sp.ksplit, sp.kper, raw, \
               PGMOE_ACT_SILU)
     switch (d.qtype) {
     case PGMOE_Q4_1: PG_DN(PGMOE_Q4_1); break;

@@ -46,18 +46,25 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
                          float* xsum = nullptr);
 int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w, hipStream_t st);
 // counts (optional scratch of dispatch_ws_bytes): several blocks instead of one.
+// tile_map (optional, dispatch_tile_map_words ints): the grouped GEMMs' tile order, entry
+// i = expert | (tile of the expert << kTileMapShift): every full tile in expert order, then
+// each expert's partial last tile, the ones with most rows first.
+constexpr int kTileMapShift = 9;  // expert ids < 512
 int launch_dispatch(const int32_t* idx, int M, int K, int E, int tile_rows, int32_t* offsets, int32_t* perm,
                     int32_t* inv, int32_t* active, int32_t* n_active, int32_t* tile_off, hipStream_t st,
-                    int32_t* counts = nullptr);
+                    int32_t* counts = nullptr, int32_t* tile_map = nullptr);
+size_t dispatch_tile_map_words(int64_t P, int E, int tile_rows);
 size_t dispatch_ws_bytes(int64_t P, int E);
 int launch_identity_dispatch(int M, int tile_rows, int32_t* offsets, int32_t* perm, int32_t* inv,
                              int32_t* active, int32_t* n_active, int32_t* tile_off, float* w, hipStream_t st);
 int launch_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                   const int32_t* perm, const int32_t* active, const int32_t* n_active, const int32_t* tile_off,
-                  int mode, float* inter, hipStream_t st, float* raw = nullptr, int act = PGMOE_ACT_SILU);
+                  int mode, float* inter, hipStream_t st, float* raw = nullptr, int act = PGMOE_ACT_SILU,
+                  const int32_t* tile_map = nullptr);
 int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_t* offsets, const int32_t* perm,
                 const int32_t* active, const int32_t* n_active, const int32_t* tile_off, const float* topk_w,
-                int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st, float* raw = nullptr);
+                int mode, uint16_t* a16, float* rs, float* partial, hipStream_t st, float* raw = nullptr,
+                const int32_t* tile_map = nullptr);
 // clear (optional): n_clear words the kernel sets to zero (the decode router's tagged logits).
 int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H, const float* shared,
                    const float* shared_logit, float* out, hipStream_t st, uint64_t* clear = nullptr,
@@ -124,13 +131,14 @@ int decode_rlog_words(int M, int E);
 bool decode_fused_down(int P, int K);
 // Prefill grouped GEMMs (gemm.hip); tile_off counts gemm_tile_pairs()-row tiles.
 // raw (optional): scratch of gemm_split_bytes(...) for a split-K run when the tiles would
-// not fill the chip; null runs the product unsplit.
+// not fill the chip; null runs the product unsplit.  tile_map (optional): the dispatch's
+// tile order (launch_dispatch); null takes the tiles in expert order.
 int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, int topk, const int32_t* offsets,
                        const int32_t* perm, const int32_t* tile_off, float* inter, hipStream_t st,
-                       float* raw = nullptr, int act = PGMOE_ACT_SILU);
+                       float* raw = nullptr, int act = PGMOE_ACT_SILU, const int32_t* tile_map = nullptr);
 int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M, int topk, const int32_t* offsets,
                      const int32_t* perm, const int32_t* tile_off, const float* topk_w, float* partial,
-                     hipStream_t st, float* raw = nullptr);
+                     hipStream_t st, float* raw = nullptr, const int32_t* tile_map = nullptr);
 // K split of a grouped product: ksplit workgroups per tile, kper super-blocks each.
 struct GemmSplit {
     int ksplit, kper;
