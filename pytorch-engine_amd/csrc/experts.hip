@@ -68,7 +68,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
                                                       float* __restrict__ out, uint64_t* __restrict__ clear,
                                                       int n_clear) {
     if (blockIdx.y == 0) clear_words(clear, n_clear);  // decode router logits (grid x = tokens)
-    const int t = blockIdx.x;
+    // the last token first: with the grouped GEMMs' tile order the rows of each expert's
+    // last tiles were written last, and those hold its highest tokens
+    const int t = gridDim.x - 1 - blockIdx.x;
     const int c = blockIdx.y * 256 + threadIdx.x;  // float4 column
     if (4 * c >= H) return;
     int pos[16];
