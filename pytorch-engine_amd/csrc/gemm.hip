@@ -279,12 +279,22 @@ template <> struct GCol<PGMOE_Q8_0> {
 
 // ---------------------------------------------------------------- tile mapping
 // Block id -> (M tile, N tile): XCD x = id % 8 takes M tiles x, x+8, ... and runs all N
-// tiles of one M tile consecutively.  Returns false for ids past the last M tile.
+// tiles of one M tile consecutively.  With fewer than 8 M tiles, each M tile's N tiles are
+// cut into 8 / n_mtiles runs, one XCD each, so that no XCD is left without tiles.  Returns
+// false for ids past the last tile.  (The grid holds a multiple of 8 M tiles' blocks.)
 __device__ __forceinline__ bool gemm_tile_of(int id, int n_ntiles, int n_mtiles, int& mt, int& nt) {
     const int x = id % kXcd, local = id / kXcd;
-    nt = local % n_ntiles;
-    mt = (local / n_ntiles) * kXcd + x;
-    return mt < n_mtiles;
+    if (n_mtiles >= kXcd) {
+        nt = local % n_ntiles;
+        mt = (local / n_ntiles) * kXcd + x;
+        return mt < n_mtiles;
+    }
+    if (n_mtiles <= 0) return false;
+    const int runs = kXcd / n_mtiles;            // runs of N tiles per M tile
+    const int per = (n_ntiles + runs - 1) / runs;  // N tiles per run
+    mt = x % n_mtiles;
+    nt = (x / n_mtiles) * per + local;
+    return x < runs * n_mtiles && local < per && nt < n_ntiles;
 }
 
 __device__ __forceinline__ int gemm_tile_expert(const int32_t* tile_off, int E, int tile) {
