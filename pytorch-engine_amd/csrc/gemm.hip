@@ -278,23 +278,29 @@ template <> struct GCol<PGMOE_Q8_0> {
 };
 
 // ---------------------------------------------------------------- tile mapping
-// Block id -> (M tile, N tile): XCD x = id % 8 takes M tiles x, x+8, ... and runs all N
-// tiles of one M tile consecutively.  With fewer than 8 M tiles, each M tile's N tiles are
-// cut into 8 / n_mtiles runs, one XCD each, so that no XCD is left without tiles.  Returns
-// false for ids past the last tile.  (The grid holds a multiple of 8 M tiles' blocks.)
+// Block id -> (M tile, N tile).  Each M tile's N tiles form `runs` runs of consecutive N
+// tiles; run u = (M tile u / runs, run u % runs) goes to XCD u % 8 (blocks go to the 8 XCDs
+// round-robin), which runs its N tiles back to back, sharing the tile's gathered A rows
+// through its L2.  runs = 1 from 32 M tiles on (M tile x on XCD x % 8); below 8 M tiles
+// 8 / n_mtiles, so that no XCD is left without tiles; from 8 to 31, 8 / gcd(n_mtiles, 8)
+// when that divides the N tiles, so that every XCD gets as many runs.  Returns false for
+// ids past the last tile.  (The grid holds a multiple of 8 M tiles' blocks.)
 __device__ __forceinline__ bool gemm_tile_of(int id, int n_ntiles, int n_mtiles, int& mt, int& nt) {
-    const int x = id % kXcd, local = id / kXcd;
-    if (n_mtiles >= kXcd) {
-        nt = local % n_ntiles;
-        mt = (local / n_ntiles) * kXcd + x;
-        return mt < n_mtiles;
-    }
     if (n_mtiles <= 0) return false;
-    const int runs = kXcd / n_mtiles;            // runs of N tiles per M tile
+    const int x = id % kXcd, local = id / kXcd;
+    int runs = 1;
+    if (n_mtiles < kXcd) {
+        runs = kXcd / n_mtiles;
+    } else if (n_mtiles < 4 * kXcd) {
+        const int r = kXcd / min(n_mtiles & -n_mtiles, kXcd);  // 8 / gcd(n_mtiles, 8)
+        if (n_ntiles % r == 0) runs = r;
+    }
     const int per = (n_ntiles + runs - 1) / runs;  // N tiles per run
-    mt = x % n_mtiles;
-    nt = (x / n_mtiles) * per + local;
-    return x < runs * n_mtiles && local < per && nt < n_ntiles;
+    const int k = local / per, t = local - k * per;
+    const int u = x + kXcd * k;
+    mt = u / runs;
+    nt = (u - mt * runs) * per + t;
+    return mt < n_mtiles && nt < n_ntiles;
 }
 
 __device__ __forceinline__ int gemm_tile_expert(const int32_t* tile_off, int E, int tile) {
