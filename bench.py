@@ -10,13 +10,18 @@ The same JSON line carries M = 2 / 4 / 8 decode, the M = 4096 Zipf-skewed prefil
 3), the roofline of the dominant kernel, and the CPU baseline.  The CPU baseline is the
 torch-CPU restatement of the reference path, timed on this host.
 
-Weights are rotated over `--copies` device copies (default 8; 3.1 GB for this layer), so
-decode reads come from HBM rather than the 256 MB Infinity Cache.  Only the GGUF bytes of
-the distinct active experts count as algorithmic traffic.
+Weights are rotated over `--copies` device copies (default 32, each with its own token
+rows, so each copy routes to its own experts): one rotation reads about 780 MB of distinct
+expert bytes at M = 1, three times the 256 MB Infinity Cache, so decode reads come from
+HBM.  The line states those bytes (`distinct_weight_bytes_per_rotation`).  Only the GGUF
+bytes of the distinct active experts count as algorithmic traffic.
 
 Kernel durations come from pgmoe_moe_forward_timed.  Every kernel of the forward records
 HIP events at its own begin and end on the stream it runs on, which is the interval a
-kernel trace (rocprofv3 --kernel-trace) reports.
+kernel trace (rocprofv3 --kernel-trace) reports; the forwards run back to back over the
+rotated copies, as in the timed graph replays.  `roofline.frac` takes the dominant
+kernel's average from the committed kernel trace of this command
+(profiles/trace_bench.json) and reports the live event figure beside it.
 """
 
 from __future__ import annotations
@@ -49,7 +54,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--copies", type=int, default=8, help="rotated weight copies (MALL defeat)")
+    ap.add_argument("--copies", type=int, default=32, help="rotated weight copies (MALL defeat)")
     ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-dense", action="store_true", help="skip the dense FFN measurement")
@@ -119,29 +124,39 @@ def short_names(raw):
     return out
 
 
-def kernel_durations(torch, hip, mods, x, reps: int, with_names: bool = False):
+def kernel_durations(torch, hip, mods, xs, reps: int, with_names: bool = False):
     """Average duration (ms) of each kernel of the forward, over `reps` forwards that rotate
-    the weight copies, from the events the kernels record themselves (and their names)."""
+    the weight copies (copy i on its own token rows xs[i]) back to back on one stream, as
+    the timed graph replays run them, from the events the kernels record themselves (and
+    their names).  Two untimed forwards run first."""
     from pgmoe._lib import check, lib
     n_ev = 32
-    starts, stops = hip.events(n_ev), hip.events(n_ev)
+    xs = xs if isinstance(xs, (list, tuple)) else [xs] * len(mods)
+    M = xs[0].shape[0]
+    stream = torch.cuda.current_stream(xs[0].device).cuda_stream
+    starts = [hip.events(n_ev) for _ in range(reps)]
+    stops = [hip.events(n_ev) for _ in range(reps)]
     names = (ctypes.c_char_p * n_ev)()
-    M = x.shape[0]
-    sums, names_n = None, 0
-    for i in range(reps + 2):
-        m = mods[i % len(mods)]
-        out = torch.empty((M, m.hidden), dtype=torch.float32, device=x.device)
-        ws = m._workspace(M)
-        nl = ctypes.c_int32()
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        check(lib().pgmoe_moe_forward_timed(m._layer, x.data_ptr(), M, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                                            stream, starts, stops, n_ev, ctypes.byref(nl), names), "forward_timed")
-        torch.cuda.synchronize()
-        if i < 2:
-            continue  # warm-up
-        names_n = min(nl.value, n_ev)
-        d = [hip.elapsed_ms(starts[k], stops[k]) for k in range(names_n)]
-        sums = d if sums is None else [s + v for s, v in zip(sums, d)]
+    nl = ctypes.c_int32()
+    outs = [torch.empty((M, m.hidden), dtype=torch.float32, device=xs[0].device) for m in mods]
+    wss = [m._workspace(M) for m in mods]
+    for i in range(2):
+        mods[i % len(mods)](xs[i % len(mods)])
+    for r in range(reps):
+        k = r % len(mods)
+        m = mods[k]
+        check(lib().pgmoe_moe_forward_timed(m._layer, xs[k].data_ptr(), M, outs[k].data_ptr(), wss[k].data_ptr(),
+                                            wss[k].numel(), stream, starts[r], stops[r], n_ev, ctypes.byref(nl),
+                                            names), "forward_timed")
+    torch.cuda.synchronize()
+    names_n = min(nl.value, n_ev)
+    sums = [0.0] * names_n
+    for r in range(reps):
+        for k in range(names_n):
+            sums[k] += hip.elapsed_ms(starts[r][k], stops[r][k])
+    for evs in starts + stops:
+        for k in range(n_ev):
+            hip.L.hipEventDestroy(evs[k])
     avg = [s / reps for s in sums]
     if with_names:
         return avg, short_names([names[k].decode() for k in range(names_n)])
@@ -149,12 +164,14 @@ def kernel_durations(torch, hip, mods, x, reps: int, with_names: bool = False):
 
 
 # ----------------------------------------------------------------------------- timing
-def graph_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
+def graph_step_ms(torch, mods, xs, steps: int, warmup: int) -> float:
     """Per-step time of exactly `steps` forwards replayed from HIP graphs: one graph holds
-    one forward of every weight copy in turn (so a replay is `len(mods)` steps), and a
-    second graph of the first `steps % len(mods)` copies completes the count.  The timed
-    region is bracketed by synchronizations and holds no host work besides the replays."""
+    one forward of every weight copy in turn, copy i on its own token rows xs[i] (so a
+    replay is `len(mods)` steps), and a second graph of the first `steps % len(mods)`
+    copies completes the count.  The timed region is bracketed by synchronizations and
+    holds no host work besides the replays."""
     n = len(mods)
+    xs = xs if isinstance(xs, (list, tuple)) else [xs] * n
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     outs = []
@@ -162,12 +179,12 @@ def graph_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
     def capture(ms):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
-            o = [m(x) for m in ms]
+            o = [m(xs[i]) for i, m in enumerate(ms)]
         return g, o
 
     with torch.cuda.stream(s):
-        for m in mods:
-            m(x)  # allocate the workspaces outside capture
+        for i, m in enumerate(mods):
+            m(xs[i])  # allocate the workspaces outside capture
         torch.cuda.synchronize()
         full, outs = capture(mods)
         rem = steps % n
@@ -188,8 +205,8 @@ def graph_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
     ms = a.elapsed_time(b) / steps
     full.replay()
     torch.cuda.synchronize()
-    for m, o in zip(mods, outs):  # the replays compute what eager forwards compute
-        if not torch.equal(o, m(x)):
+    for i, (m, o) in enumerate(zip(mods, outs)):  # the replays compute what eager forwards compute
+        if not torch.equal(o, m(xs[i])):
             raise RuntimeError("graph replay differs from the eager forward")
     del full, part
     return ms
@@ -198,7 +215,7 @@ def graph_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
 def dense_section(torch, oracle, dev, steps: int, warmup: int, prefill_steps: int) -> dict:
     """The dense SwiGLU FFN (HipDenseMLP, the GGUFDenseMLP drop-in) on an 8B-class layer:
     parity against the oracle (M = 1, and a token sample of M = 4096), decode M = 1 from
-    graph replays over 4 weight copies (380 MB, past the 256 MB MALL), prefill M = 4096."""
+    graph replays over 6 weight copies (587 MB, past the 256 MB MALL), prefill M = 4096."""
     import numpy as np
     from pgmoe import HipDenseMLP
     from pgmoe.synth import DENSE_CONFIGS, SyntheticDense
@@ -217,12 +234,13 @@ def dense_section(torch, oracle, dev, steps: int, warmup: int, prefill_steps: in
         parity[str(M)] = {"rel_l2": float(f"{oracle.rel_l2(got, ref):.3e}"),
                           "max_rel": float(f"{oracle.max_rel(got, ref):.3e}")}
     ok = all(v["rel_l2"] <= 1e-3 and v["max_rel"] <= 2e-2 for v in parity.values())
-    mods = [base] + [base.replica() for _ in range(3)]
-    x1 = torch.from_numpy(lay.draw_x(1)).to(dev)
+    mods = [base] + [base.replica() for _ in range(5)]
+    x1, _ = rotation_inputs(torch, lay, None, len(mods), 1, dev)
     ms1 = graph_step_ms(torch, mods, x1, steps, warmup)
     xp = torch.from_numpy(lay.draw_x(4096)).to(dev)
     msp = eager_step_ms(torch, mods[:2], xp, prefill_steps, 2)
     wb = base.weight_bytes()
+    n_copies = len(mods)
     gbs = wb / (ms1 * 1e-3) / 1e9
     fl = 2.0 * 4096 * 3 * sp.hidden * sp.inter
     tf = fl / (msp * 1e-3) / 1e12
@@ -231,25 +249,40 @@ def dense_section(torch, oracle, dev, steps: int, warmup: int, prefill_steps: in
     return {"workload": f"dense SwiGLU FFN H={sp.hidden} I={sp.inter}, gate/up Q4_K, down Q6_K",
             "decode_m1": {"us_per_step": round(ms1 * 1e3, 3), "tok_per_s": round(1 / (ms1 * 1e-3), 1),
                           "weight_bytes": wb, "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                          "timing": "one forward per HIP graph replay, 4 weight copies"},
+                          "distinct_weight_bytes_per_rotation": wb * n_copies,
+                          "timing": f"one forward per HIP graph replay, {n_copies} weight copies"},
             "prefill": {"M": 4096, "us_per_step": round(msp * 1e3, 2), "tok_per_s": round(4096 / (msp * 1e-3), 1),
                         "tflops": round(tf, 1), "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4)},
             "parity": parity, **({} if ok else {"parity_failed": True})}
 
 
-def eager_step_ms(torch, mods, x, steps: int, warmup: int) -> float:
+def eager_step_ms(torch, mods, xs, steps: int, warmup: int) -> float:
     n = len(mods)
+    xs = xs if isinstance(xs, (list, tuple)) else [xs] * n
     for i in range(warmup):
-        mods[i % n](x)
+        mods[i % n](xs[i % n])
     torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()
     for i in range(steps):
-        mods[i % n](x)
+        mods[i % n](xs[i % n])
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) / steps
+
+
+def rotation_inputs(torch, lay, ol, n: int, M: int, dev):
+    """Token rows for n rotated weight copies: copy i gets its own M rows (rows i*M.. of one
+    seeded draw of n*M), so each copy routes to its own experts.  Returns the device tensors
+    and, per copy, its distinct active experts (from the oracle's routing; None without a
+    router)."""
+    import numpy as np
+    pool = lay.draw_x(M * n)
+    xs_np = [np.ascontiguousarray(pool[i * M:(i + 1) * M]) for i in range(n)]
+    xs = [torch.from_numpy(a).to(dev) for a in xs_np]
+    acts = [len(np.unique(ol.route(a)[1])) for a in xs_np] if ol is not None else None
+    return xs, acts
 
 
 def copy_probe(torch) -> None:
@@ -263,10 +296,24 @@ def copy_probe(torch) -> None:
     log(f"[bench] copy probe: 4 x {n} byte device copies")
 
 
-def cpu_baseline(lay, M: int, seconds: float, threads: int = 0, max_forwards: int = 400):
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(lay, M: int, seconds: float, threads: int = 0, max_forwards: int = 400, min_forwards: int = 3):
     """The torch-CPU restatement of the reference path (oracle/torch_port.py, fp16 casts
-    kept) timed on this host for a bounded sample: forwards of M tokens until `seconds`
-    have passed (after one warm-up forward), at most max_forwards."""
+    kept) timed on this host for a bounded sample: forwards of M tokens (after one warm-up
+    forward) until `seconds` have passed and at least min_forwards ran, at most
+    max_forwards; the rate is M over the median forward time."""
+    import statistics
     import torch
     import oracle
     from oracle import torch_port
@@ -275,26 +322,31 @@ def cpu_baseline(lay, M: int, seconds: float, threads: int = 0, max_forwards: in
     nthr = threads or cores
     prev = torch.get_num_threads()
     torch.set_num_threads(nthr)
+    times = []
     try:
         ol = oracle.OracleLayer.from_gguf(lay.gguf, lay.config, router_bias=lay.router_bias)
         port = torch_port.PortMoE(ol)
         pool = max(M, 64)
         x = torch.from_numpy(lay.draw_x(pool))
         port.forward(x[0:M], faithful=True)  # warm-up
-        n, t0 = 0, time.perf_counter()
+        t_start = time.perf_counter()
         while True:
-            o = (n * M) % (pool - M + 1)
+            o = (len(times) * M) % (pool - M + 1)
+            t0 = time.perf_counter()
             port.forward(x[o:o + M], faithful=True)
-            n += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or n >= max_forwards:
+            times.append(time.perf_counter() - t0)
+            el = time.perf_counter() - t_start
+            if len(times) >= max_forwards or (len(times) >= min_forwards and el >= seconds):
                 break
     finally:
         torch.set_num_threads(prev)
-    return {"value": round(n * M / el, 3), "unit": "tok/s", "cores": nthr, "kind": "port",
-            "sample": f"{n} forward(s) of M={M} token(s) of the {lay.spec.name} layer: oracle/torch_port.py, the "
-                      f"torch-CPU restatement of the reference CPU path (repacked W4/W8, chunked fp32 dequant + "
-                      f"F.linear, fp16 casts kept), {el:.1f} s on {nthr} of {cores} host threads"}
+    med = statistics.median(times)
+    return {"value": round(M / med, 3), "unit": "tok/s", "cores": nthr, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"{len(times)} forward(s) of M={M} token(s) of the {lay.spec.name} layer, median "
+                      f"{med * 1e3:.2f} ms per forward: oracle/torch_port.py, the torch-CPU restatement of the "
+                      f"reference CPU path (repacked W4/W8, chunked fp32 dequant + F.linear, fp16 casts kept), "
+                      f"{el:.1f} s on {nthr} of {cores} host threads"}
 
 
 def routing_bit_exact(mod, M: int, idx, oracle) -> bool:
@@ -332,7 +384,7 @@ def layer_flops(spec, M: int, pairs: int) -> float:
 
 
 def config_section(torch, oracle, hip, dev, name: str, m_dec: int, m_pf: int, steps: int, warmup: int,
-                   pf_steps: int, cpu_seconds: float, copies: int = 2) -> dict:
+                   pf_steps: int, cpu_seconds: float, copies: int = 3) -> dict:
     """One BASELINE config: parity gate, decode M = m_dec from graph replays over `copies`
     weight copies (HBM fraction of the active GGUF bytes), prefill M = m_pf eager (MFMA
     fraction of the grouped GEMMs and of the layer; for a shared expert also the HBM
@@ -360,23 +412,24 @@ def config_section(torch, oracle, hip, dev, name: str, m_dec: int, m_pf: int, st
                           "routing_bit_exact": routing_bit_exact(base, M, idx, oracle), "rows_checked": len(tk)}
     out["parity"] = parity
     ok = all(v["rel_l2"] <= 1e-3 and v["max_rel"] <= 2e-2 and v["routing_bit_exact"] for v in parity.values())
-    # decode
-    x = torch.from_numpy(lay.draw_x(m_dec)).to(dev)
-    ms = graph_step_ms(torch, mods, x, steps, warmup)
-    _, idx, _ = ol.route(lay.draw_x(m_dec))
-    n_act = len(np.unique(idx))
-    wb = base.active_weight_bytes(n_act) + base.shared_weight_bytes()
-    kd = kernel_durations(torch, hip, mods, x, 20)
+    # decode: every copy on its own token rows
+    xs, acts = rotation_inputs(torch, lay, ol, len(mods), m_dec, dev)
+    ms = graph_step_ms(torch, mods, xs, steps, warmup)
+    per_exp = base.active_weight_bytes(1)
+    wb = round(sum(acts) / len(acts) * per_exp) + base.shared_weight_bytes()
+    kd = kernel_durations(torch, hip, mods, xs, 20)
     gbs = wb / (ms * 1e-3) / 1e9
     out["decode"] = {"M": m_dec, "us_per_step": round(ms * 1e3, 3), "tok_per_s": round(m_dec / (ms * 1e-3), 1),
-                     "active_experts": n_act, "weight_bytes": wb, "hbm_gbs": round(gbs, 1),
-                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "kernel_us": [round(v * 1e3, 3) for v in kd],
+                     "active_experts": round(sum(acts) / len(acts), 2), "weight_bytes": wb,
+                     "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "kernel_us": [round(v * 1e3, 3) for v in kd],
+                     "distinct_weight_bytes_per_rotation": sum(acts) * per_exp + len(mods) * base.shared_weight_bytes(),
                      "timing": f"one forward per HIP graph replay, {copies} weight copies"}
     # prefill
     xp_np = lay.draw_x(m_pf)
     xp = torch.from_numpy(xp_np).to(dev)
     msp = eager_step_ms(torch, mods, xp, pf_steps, 2)
-    kd, names = kernel_durations(torch, hip, mods, xp, max(3, pf_steps // 2), with_names=True)
+    kd, names = kernel_durations(torch, hip, mods, [xp] * len(mods), max(3, pf_steps // 2), with_names=True)
     _, idxp, _ = ol.route(xp_np)
     n_act_p = len(np.unique(idxp))
     fl = layer_flops(spec, m_pf, m_pf * spec.top_k)
@@ -458,19 +511,21 @@ def main() -> int:
     decode = {}
     m_list = sorted({1} | {int(v) for v in args.m_list.split(",") if v})
     for M in m_list:
-        x = torch.from_numpy(lay.draw_x(M)).to(dev)
+        # every copy on its own token rows, so each routes to its own experts
+        xs, acts = rotation_inputs(torch, lay, ol, len(mods), M, dev)
         # every M is timed like the headline: --warmup untimed, then --steps timed forwards
         steps, warm = args.steps, args.warmup
-        ms = graph_step_ms(torch, mods, x, steps, warm)
-        ms_eager = eager_step_ms(torch, mods, x, max(50, steps // 4), 10)
-        _, idx, _ = ol.route(lay.draw_x(M))
-        n_act = len(np.unique(idx))
-        kd = kernel_durations(torch, hip, mods, x, 50)
-        ab = base.active_weight_bytes(n_act)
+        ms = graph_step_ms(torch, mods, xs, steps, warm)
+        ms_eager = eager_step_ms(torch, mods, xs, max(50, steps // 4), 10)
+        kd = kernel_durations(torch, hip, mods, xs, 64)
+        per_exp = base.active_weight_bytes(1)
+        n_act = sum(acts) / len(acts)
+        ab = round(n_act * per_exp)
         decode[M] = {"us_per_step": round(ms * 1e3, 3), "tok_per_s": round(M / (ms * 1e-3), 1),
                      "steps": steps, "eager_us_per_step": round(ms_eager * 1e3, 3),
-                     "active_experts": n_act, "kernel_us": [round(v * 1e3, 3) for v in kd],
+                     "active_experts": round(n_act, 3), "kernel_us": [round(v * 1e3, 3) for v in kd],
                      "active_weight_bytes": ab,
+                     "distinct_weight_bytes_per_rotation": sum(acts) * per_exp,
                      "layer_hbm_frac": round(ab / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         log(f"[bench] decode M={M}: {decode[M]}")
 
@@ -483,10 +538,13 @@ def main() -> int:
     gu_mat = base.gate_exps.gguf_bytes_per_mat + base.up_exps.gguf_bytes_per_mat
     dom_kernel, dom_names = "dec_gu_kernel", ["dec_gu", "dec_dc"]
     dom_desc = "dec_gu_kernel (router + routing + gate/up + SwiGLU), M=1"
-    dom_bytes = d1["active_experts"] * gu_mat
-    dom_us = ku[0]
-    dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
+    dom_bytes = spec.top_k * gu_mat  # one token: top_k distinct experts every step
+    ev_us = ku[0]
     trace_us = load_trace_avg("dec_gu_kernel<12, 1, 1, 2, false>")
+    # frac from the committed kernel trace of this command when it holds the kernel, the
+    # live event average beside it
+    dom_us = trace_us if trace_us else ev_us
+    dom_gbs = dom_bytes / (dom_us * 1e-6) / 1e9
     layer_gbs = d1["active_weight_bytes"] / (d1["us_per_step"] * 1e-6) / 1e9
     traffic, traffic_rec = load_traffic(dom_kernel)
 
@@ -563,7 +621,7 @@ def main() -> int:
         log(f"[bench] cpu baseline: {cpu}")
         cpu_more["qwen3_m1_1thread"] = cpu_baseline(lay, 1, args.cpu_seconds / 2, threads=1)
         if not args.no_prefill:
-            cpu_more["qwen3_zipf_prefill_m4096"] = cpu_baseline(play, 4096, 1.0, max_forwards=1)
+            cpu_more["qwen3_zipf_prefill_m4096"] = cpu_baseline(play, 4096, 1.0, max_forwards=5, min_forwards=3)
         log(f"[bench] cpu baselines: {cpu_more}")
 
     rec = {
@@ -581,18 +639,24 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "qwen3_30b_a3b MoE layer decode, M=1 token per step (H=2048, E=128, top-8, "
                                "I=768, gate/up Q4_K, down Q6_K, fp16 activations, fp32 accumulate)",
-                   "weight_copies": args.copies, "timing": "one forward per HIP graph replay"},
+                   "weight_copies": args.copies,
+                   "distinct_weight_bytes_per_rotation": d1["distinct_weight_bytes_per_rotation"],
+                   "timing": "one forward per HIP graph replay, each weight copy on its own token rows"},
         "roofline": {"bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": dom_desc, "algorithmic_bytes": dom_bytes,
-                     "algorithmic_bytes_note": f"{d1['active_experts']} active experts x ({gu_mat:,} gate + up GGUF "
+                     "algorithmic_bytes_note": f"{spec.top_k} active experts x ({gu_mat:,} gate + up GGUF "
                                                "bytes); the launch also reads the fp32 router weights "
                                                f"({router_bytes:,} B), not counted",
-                     "kernel_us": dom_us, "kernel_us_source": "HIP events the kernel records at its own begin / "
-                                                             "end, average over 50 forwards",
-                     "trace_avg_us": trace_us,
-                     "frac_from_trace": (round(dom_bytes / (trace_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
-                                         if trace_us else None),
+                     "kernel_us": round(dom_us, 3),
+                     "kernel_us_source": ("average of the kernel in the rocprofv3 kernel trace of this command, "
+                                          "profiles/trace_bench.json" if trace_us else
+                                          "HIP events the kernel records at its own begin / end (no committed "
+                                          "trace holds this kernel)"),
+                     "event_us": ev_us,
+                     "event_us_source": "HIP events the kernel records at its own begin / end, average over 64 "
+                                        "back-to-back forwards rotating the weight copies",
+                     "frac_from_events": round(dom_bytes / (ev_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "router_inclusive_gbs": round((dom_bytes + router_bytes) / (dom_us * 1e-6) / 1e9, 1),
                      "traffic_source": traffic_rec.get("source") if traffic_rec else None},
         "cpu_baseline": cpu,

@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define PGMOE_ABI_VERSION 3
+#define PGMOE_ABI_VERSION 4
 
 #define PGMOE_OK 0
 #define PGMOE_E_INVALID (-1)     /* bad argument, shape or pointer */
@@ -105,6 +105,12 @@ typedef struct pgmoe_layer {
     pgmoe_weights sh_gate, sh_up, sh_down; /* [I_s, H], [I_s, H], [H, I_s] */
     const float* sh_inp_gate; /* [H] fp32 or NULL: sigmoid gate on the shared expert */
     int32_t act;              /* PGMOE_ACT_*: the experts' gate activation (model.py:868) */
+    int32_t* status_host;     /* optional host-mapped word (hipHostMalloc'd / pinned host memory
+                                 that the device can write), or NULL: a kernel that sets a
+                                 PGMOE_STATUS_* bit in the workspace status word also ORs it in
+                                 here, so the caller can poll it with a plain host read, without
+                                 synchronising the stream; the no-alloc entry point reports
+                                 through it too.  The caller clears it. */
 } pgmoe_layer;
 
 /* A dense SwiGLU FFN: one matrix triple, no router (GGUFDenseMLP, model.py:778-846). */
@@ -167,7 +173,8 @@ int pgmoe_moe_forward(const pgmoe_layer* L, const uint16_t* x, int32_t M, float*
  *   - the first call on a device, and the first after a failed call, clears the array's
  *     state words with a kernel and so must not run under graph capture
  *     (PGMOE_E_INVALID otherwise);
- *   - pgmoe_moe_status and pgmoe_moe_routing cannot reach this workspace. */
+ *   - pgmoe_moe_status and pgmoe_moe_routing cannot reach this workspace: a kernel's
+ *     status bits reach the caller through pgmoe_layer.status_host when it is set. */
 int pgmoe_moe_forward_noalloc(const pgmoe_layer* L, const uint16_t* x, int32_t M, float* out, void* stream);
 
 /* The routing the last pgmoe_moe_forward of M tokens on this workspace produced, read back

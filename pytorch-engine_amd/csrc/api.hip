@@ -125,13 +125,14 @@ static Layout layout_for(const pgmoe_layer* L, int M, int rlog_experts = 0) {
     o.rs = take(c, gemm ? P * 4 : 0);
     // the fused decode down kernel combines in place; otherwise per-pair partial rows
     o.partial = take(c, (gemm || !decode_fused_down((int)P, (int)I)) ? P * H * 4 : 0);
-    if (gemm) {  // split-K scratch, shared by the products in turn (stream-ordered)
-        size_t r = gemm_split_bytes((int64_t)P, (int)E, (int)I, (int)H, true);
-        r = std::max(r, gemm_split_bytes((int64_t)P, (int)E, (int)H, (int)I, false));
+    if (gemm) {  // split-K scratch, shared by the products in turn (stream-ordered); sized for
+                 // the largest any smaller batch takes, so that the total never falls as M grows
+        size_t r = gemm_split_bytes_upto((int64_t)P, (int)E, (int)I, (int)H, true);
+        r = std::max(r, gemm_split_bytes_upto((int64_t)P, (int)E, (int)H, (int)I, false));
         if (L->has_shared) {
             const int Is = L->sh_gate.n_rows;
-            r = std::max(r, gemm_split_bytes(M, 1, Is, (int)H, true));
-            r = std::max(r, gemm_split_bytes(M, 1, (int)H, Is, false));
+            r = std::max(r, gemm_split_bytes_upto(M, 1, Is, (int)H, true));
+            r = std::max(r, gemm_split_bytes_upto(M, 1, (int)H, Is, false));
         }
         o.raw = take(c, r);
     }
@@ -211,7 +212,8 @@ static DenseLayout dense_layout(int M, int I, int H) {
     o.isum = take(c, gemm ? 0 : (size_t)M * (I / 16) * 4);
     o.a16 = take(c, gemm ? (size_t)M * I * 2 : 0);
     o.rs = take(c, gemm ? (size_t)M * 4 : 0);
-    o.raw = take(c, gemm ? std::max(gemm_split_bytes(M, 1, I, H, true), gemm_split_bytes(M, 1, H, I, false)) : 0);
+    o.raw = take(c, gemm ? std::max(gemm_split_bytes_upto(M, 1, I, H, true), gemm_split_bytes_upto(M, 1, H, I, false))
+                         : 0);
     o.total = c;
     return o;
 }
@@ -422,7 +424,7 @@ static int moe_forward_impl(const pgmoe_layer* L, const LayerMats& lm, const Lay
                                            sgw ? WS(float, s_logit) : nullptr, WS(uint64_t, rlog),
                                            WS(int32_t, status), L->has_shared ? WS(float, xsum) : nullptr, E,
                                            L->norm_topk, WS(int32_t, desc), flat, max_active, WS(float, inter),
-                                           WS(float, isum), st, L->act)))
+                                           WS(float, isum), st, L->act, L->status_host)))
             return rc;
         const float* shared = nullptr;
         const float* shared_logit = nullptr;

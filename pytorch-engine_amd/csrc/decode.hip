@@ -38,13 +38,14 @@ int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const flo
 int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
                              const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, int32_t* status,
                              float* xsum_out, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
-                             float* inter, float* isum, hipStream_t st, int act) {
+                             float* inter, float* isum, hipStream_t st, int act, int32_t* status_host) {
     if (M < 1 || M > kDecTM) return fail(PGMOE_E_INVALID, "routed decode handles 1..%d tokens", kDecTM);
     if (topk > 16 || E > 512 || M * topk > 128)
         return fail(PGMOE_E_UNSUPPORTED, "routed decode: top_k <= 16, E <= 512, M*top_k <= 128");
     DecDisp dp{kRoute, nullptr, nullptr, nullptr, nullptr, rlog, desc, status, M, E, norm,
                {flat.offsets, flat.perm, flat.inv, flat.active, flat.n_active, flat.w}};
     dp.act = act;
+    dp.status_host = status_host;
     const RouterIn rt{rw, bias, sgw, s_logit, xsum_out};
 #define CALL(QT) dec_gateup_q<QT>(g, u, x, nullptr, topk, M, dp, rt, max_active, inter, isum, st)
     PG_BY_QTYPE(g.qtype, "decode gate/up", CALL)

@@ -675,10 +675,12 @@ constexpr int32_t kStatusSpinTimeout = PGMOE_STATUS_SPIN_TIMEOUT;
 
 // Logits of token m for lane l (experts l + 64r; -inf past E): polls the tagged words
 // (a bounded spin with short sleeps) until every one of the wave's is written.  A wave that
-// gives up after kSpinMax polls sets kStatusSpinTimeout in *status (vector atomic OR).
+// gives up after kSpinMax polls sets kStatusSpinTimeout in *status (vector atomic OR) and,
+// when the caller gave one, in its host-mapped word *status_host (system scope, so the
+// host sees it without synchronising the stream).
 template <int RE>
 __device__ __forceinline__ void load_logits(const uint64_t* rlog, int m, int E, int lane, float (&v)[RE],
-                                            int32_t* status) {
+                                            int32_t* status, int32_t* status_host) {
     uint64_t q[RE];
     int n = 0;
     for (;;) {
@@ -694,6 +696,8 @@ __device__ __forceinline__ void load_logits(const uint64_t* rlog, int m, int E, 
         if (++n >= kSpinMax) {
             if (lane == 0 && status) __hip_atomic_fetch_or(status, kStatusSpinTimeout, __ATOMIC_RELAXED,
                                                            __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0 && status_host)
+                __hip_atomic_fetch_or(status_host, kStatusSpinTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -925,6 +929,7 @@ struct DecDisp {
     const float* bias;    // kLinear: [N] added to the outputs, or null
     int out_f16;          // kLinear: outputs as fp16 (round to nearest even) instead of fp32
     int act;              // gate activation PGMOE_ACT_* of the gate/up epilogue
+    int32_t* status_host; // kRoute: the caller's host-mapped status word (pgmoe_layer.status_host), or null
 };
 
 // Router work folded into the routed gate/up launch: with R = ceil(rows / blocks) (1
@@ -984,7 +989,7 @@ __device__ __forceinline__ void route_waves(const DecDisp& dp, int topk, RouteSh
     const int copy = (blockIdx.y * gridDim.x + blockIdx.x) % kRlogCopies;
     const uint64_t* rlog = dp.rlog + (int64_t)copy * dp.M * dp.E;
     for (int m = w; m < dp.M; m += nw) {
-        load_logits<RE>(rlog, m, dp.E, lane, v, dp.status);
+        load_logits<RE>(rlog, m, dp.E, lane, v, dp.status, dp.status_host);
 #ifdef PG_TRACE
         if (m == 0) t_ready = wall_clock64();
 #endif

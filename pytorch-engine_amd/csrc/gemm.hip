@@ -25,6 +25,7 @@
 // gathered A rows are shared through that XCD's L2.
 // Reference: GGUFQuantMoEExperts.forward_expert (quant_kernels.py:1990-2011) ->
 // exec_w4a16_matmul / exec_w8a16_matmul (:1165-1420) and model.py:916-919.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -685,6 +686,31 @@ GemmSplit gemm_split(int64_t P, int E, int N, int K, bool gateup) {
 size_t gemm_split_bytes(int64_t P, int E, int N, int K, bool gateup) {
     const GemmSplit sp = gemm_split(P, E, N, K, gateup);
     return sp.ksplit > 1 ? (size_t)sp.ksplit * P * (gateup ? 2 * N : N) * 4 : 0;
+}
+
+// The most split scratch any P' <= P pairs take.  gemm_split_bytes is not monotone in P
+// (one more M tile can lower the split count), so a workspace sized for P must hold the
+// largest of them to serve every smaller batch.  The split count never grows with P' (the
+// tile estimate never shrinks), so for each count s > 1 the largest P' still splitting at
+// least s ways is found by bisection, and the maximum lies at one of those P'.
+size_t gemm_split_bytes_upto(int64_t P, int E, int N, int K, bool gateup) {
+    size_t best = gemm_split_bytes(P, E, N, K, gateup);
+    if (P <= 0) return best;
+    const int s1 = gemm_split(1, E, N, K, gateup).ksplit;
+    for (int s = 2; s <= s1; ++s) {
+        int64_t lo = 1, hi = P;  // largest P' in [1, P] with ksplit(P') >= s (ksplit(1) >= s)
+        if (gemm_split(hi, E, N, K, gateup).ksplit >= s) {
+            lo = hi;
+        } else {
+            while (hi - lo > 1) {
+                const int64_t mid = lo + (hi - lo) / 2;
+                if (gemm_split(mid, E, N, K, gateup).ksplit >= s) lo = mid;
+                else hi = mid;
+            }
+        }
+        best = std::max(best, gemm_split_bytes(lo, E, N, K, gateup));
+    }
+    return best;
 }
 
 static int launch_split_reduce(bool gateup, const float* raw, int S, int64_t P, int N, const float* rs,

@@ -88,13 +88,15 @@ struct DecFlat {
 // the forward's last kernel clears them), and, when xsum_out is set, the 16-element sums
 // of x for the shared expert's launches.
 // status: the workspace status word a wave whose bounded wait for the logits gave up
-// marks (kStatusSpinTimeout), or null.  isum gets 16-row sums [P][N/16], or 8-row sums
+// marks (kStatusSpinTimeout), or null; status_host: the caller's host-mapped word it also
+// marks, or null.  isum gets 16-row sums [P][N/16], or 8-row sums
 // [P][N/8] where decode_isum_rows8(g.qtype, M).
 bool decode_isum_rows8(int qtype, int M);
 int launch_dec_gateup_routed(const Mats& g, const Mats& u, const uint16_t* x, int topk, int M, const float* rw,
                              const float* bias, const float* sgw, float* s_logit, uint64_t* rlog, int32_t* status,
                              float* xsum_out, int E, int norm, int32_t* desc, const DecFlat& flat, int max_active,
-                             float* inter, float* isum, hipStream_t st, int act = PGMOE_ACT_SILU);
+                             float* inter, float* isum, hipStream_t st, int act = PGMOE_ACT_SILU,
+                             int32_t* status_host = nullptr);
 // Routing a forward produced, read back from its workspace in sorted pair order (decode:
 // from the descriptor at desc; prefill: from the flat arrays).  offsets [E+1]; pair_*[P].
 int launch_route_readback(int decode, const int32_t* desc, const int32_t* idx, const float* w,
@@ -146,6 +148,9 @@ struct GemmSplit {
 GemmSplit gemm_split(int64_t P, int E, int N, int K, bool gateup);
 // Scratch bytes of the raw partial sums of a split product (0 when it runs unsplit).
 size_t gemm_split_bytes(int64_t P, int E, int N, int K, bool gateup);
+// The largest gemm_split_bytes over every P' <= P (what a workspace that serves any batch up
+// to P pairs must hold).
+size_t gemm_split_bytes_upto(int64_t P, int E, int N, int K, bool gateup);
 int gemm_tile_pairs();
 int64_t layout_bytes(int qtype, int64_t rows, int64_t cols);
 // Scale plane (relayout.hip): bytes of one matrix's plane (0 for Q8_0, -1 if unsupported)

@@ -127,7 +127,7 @@ size_t linear_ws_bytes(const Mats& w, int M, bool staged) {
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
     size_t n = 4 * al(8) + 3 * al((size_t)M * 4);  // offsets, tile_off, active, nact | perm, inv, unit weights
     if (staged) n += al((size_t)M * w.N * 4);
-    return n + al(gemm_split_bytes(M, 1, w.N, w.K, false));  // split-K partial sums
+    return n + al(gemm_split_bytes_upto(M, 1, w.N, w.K, false));  // split-K partial sums (any batch up to M)
 }
 
 int launch_linear(const Mats& w, const float* bias, const uint16_t* x, int M, void* out, int out_f16, uint8_t* ws,

@@ -12,7 +12,7 @@ from typing import Optional
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libpgmoe.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 Q4_0, Q4_1, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 3, 6, 8, 12, 13, 14
 # GGUF expert formats with a HIP path; Q4_0 is relaid out as Q4_1, Q5_0 as Q8_0 (their values exactly)
@@ -52,6 +52,7 @@ class Layer(ctypes.Structure):
         ("sh_down", Weights),
         ("sh_inp_gate", _P),
         ("act", _I32),
+        ("status_host", _P),
     ]
 
 

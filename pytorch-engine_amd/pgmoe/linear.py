@@ -151,7 +151,17 @@ class GGUFQuantLinear(nn.Module):
 
     def embed_lookup(self, token_ids: torch.Tensor, dtype: torch.dtype = torch.float16) -> torch.Tensor:
         """The rows of the given ids, dequantised (quant_kernels.py:1839): the embedding
-        table lookup that lets one quantised buffer serve token_embd and a tied lm_head."""
+        table lookup that lets one quantised buffer serve token_embd and a tied lm_head.
+
+        Ids given on the host are range-checked there (IndexError, as the reference's
+        index_select raises).  Ids already on the device are not read back: that would
+        synchronise the stream every decode step and cannot run under graph capture (the
+        reference captures this lookup in its decode graphs, model.py:1803, :2039); an id
+        outside [0, N) gives a row of NaN instead."""
+        if token_ids.device.type == "cpu" and token_ids.numel():
+            ids_host = token_ids.reshape(-1)
+            if bool(((ids_host < 0) | (ids_host >= self.out_features)).any()):
+                raise IndexError(f"token id out of range [0, {self.out_features})")
         flat = token_ids.reshape(-1).to(self.device)
         K = self.in_features
         if self.mode == "fp16":
@@ -161,9 +171,6 @@ class GGUFQuantLinear(nn.Module):
         odt = dtype if dtype in _OUT else torch.float32
         out = torch.empty((ids.numel(), K), dtype=odt, device=self.device)
         if ids.numel():
-            bad = (ids < 0) | (ids >= self.out_features)
-            if bool(bad.any()):  # (the reference's index_select raises on these too)
-                raise IndexError(f"token id out of range [0, {self.out_features})")
             check(lib().pgmoe_dequant_rows(self._w, ids.data_ptr(), ids.numel(), out.data_ptr(), _OUT[odt],
                                            torch.cuda.current_stream(self.device).cuda_stream),
                   "pgmoe_dequant_rows")

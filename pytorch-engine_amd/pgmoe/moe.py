@@ -26,10 +26,18 @@ import torch.nn as nn
 
 from . import ops
 from ._lib import ACT_GELU_TANH, ACT_SILU, STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES, Layer, Weights, check, lib
-from .workspace import WorkspacePool
+from .workspace import StatusWord, WorkspacePool
 
 _F32, _F16, _BF16 = 0, 1, 30
 _load_lock = threading.Lock()
+
+
+def raise_for_status(bits: int) -> None:
+    """RuntimeError for the PGMOE_STATUS_* bits a kernel set (0: nothing to report)."""
+    if bits & STATUS_SPIN_TIMEOUT:
+        raise RuntimeError("an earlier forward's wait for the router logits timed out: its output was wrong")
+    if bits:
+        raise RuntimeError(f"pgmoe status {bits:#x} from an earlier forward")
 
 
 def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.Tensor:
@@ -135,6 +143,8 @@ class HipSparseMoEMLP(nn.Module):
         if self.router_weight.shape[0] != self.n_experts:
             raise ValueError(f"router has {self.router_weight.shape[0]} rows, config says {self.n_experts} experts")
         self._ws = WorkspacePool(device, zeroed=True)
+        # host-mapped status word: the kernels' failure bits, readable without a stream sync
+        self._status = StatusWord(pinned=True)
         self._layer = self._build_layer()
 
     # ------------------------------------------------------------------ plumbing
@@ -155,6 +165,7 @@ class HipSparseMoEMLP(nn.Module):
         L.norm_topk = int(self.norm_topk_prob)
         L.act = ACT_GELU_TANH if self.use_gelu else ACT_SILU
         L.router_w = self.router_weight.data_ptr()
+        L.status_host = self._status.ptr()
         L.router_bias = self.router_bias.data_ptr() if self.router_bias is not None else None
         L.gate = self.gate_exps.weights()
         L.up = self.up_exps.weights()
@@ -186,21 +197,23 @@ class HipSparseMoEMLP(nn.Module):
         """Free the workspaces (only when no captured graph replays this layer any more)."""
         self._ws.release()
 
-    def check_status(self, clear: bool = True) -> None:
-        """Raise RuntimeError if a kernel of an earlier forward on the current stream flagged
-        its output as wrong (a decode wave's bounded wait for the router logits gave up).
-        Synchronises the stream; meant for health checks, not for every step."""
-        bufs = self._ws.buffers()
-        ws = bufs.get(self._stream())
-        if ws is None:
-            return
-        st = ctypes.c_int32()
-        check(lib().pgmoe_moe_status(self._layer, ws.data_ptr(), ws.numel(), ctypes.byref(st), int(clear),
-                                     self._stream()), "pgmoe_moe_status")
-        if st.value & STATUS_SPIN_TIMEOUT:
-            raise RuntimeError("a decode forward's wait for the router logits timed out: its output was wrong")
-        if st.value:
-            raise RuntimeError(f"pgmoe workspace status {st.value:#x}")
+    def check_status(self, sync: bool = False) -> None:
+        """Raise RuntimeError if a kernel of an earlier forward flagged its output as wrong (a
+        decode wave's bounded wait for the router logits gave up), and clear the flags.
+
+        Without ``sync`` this reads only the host-mapped status word the kernels also write:
+        no stream synchronisation, so it suits every step of a loop that replays captured
+        graphs (``forward`` itself checks it on entry).  With ``sync`` it also synchronises
+        and reads the status word of every workspace this layer holds, including retired
+        ones that captured graphs may still replay into."""
+        bits = self._status.take()
+        if sync:
+            st = ctypes.c_int32()
+            for ws in self._ws.all_buffers():
+                check(lib().pgmoe_moe_status(self._layer, ws.data_ptr(), ws.numel(), ctypes.byref(st), 1,
+                                             self._stream()), "pgmoe_moe_status")
+                bits |= st.value
+        raise_for_status(bits)
 
     def routing(self, M: int):
         """The routing the last forward of M tokens on the current stream produced, in sorted
@@ -230,6 +243,8 @@ class HipSparseMoEMLP(nn.Module):
             x_2d = x_2d.to(torch.float16)
         x_2d = x_2d.contiguous()
         M = x_2d.shape[0]
+        # an earlier forward's kernels may have flagged their output (a plain host read)
+        raise_for_status(self._status.take())
         out = torch.empty((M, self.hidden), dtype=torch.float32, device=self.device)
         if M:
             ws = self._workspace(M)
@@ -259,6 +274,7 @@ class HipSparseMoEMLP(nn.Module):
                 c.plane = t.plane.clone() if t.plane is not None else None
                 object.__setattr__(r, name, c)
         r._ws = self._ws.clone_empty()
+        r._status = StatusWord(pinned=True)
         r._layer = r._build_layer()
         return r
 

@@ -58,6 +58,11 @@ class WorkspacePool:
     def buffers(self) -> Dict[int, torch.Tensor]:
         return dict(self._cur)
 
+    def all_buffers(self) -> List[torch.Tensor]:
+        """Every buffer still held: the streams' current ones and the retired ones that a
+        captured graph may still replay into."""
+        return list(self._cur.values()) + list(self._retired)
+
     def release(self) -> None:
         """Free every buffer.  Only safe when no captured graph still uses one."""
         self._cur.clear()
@@ -65,3 +70,24 @@ class WorkspacePool:
 
     def clone_empty(self) -> "WorkspacePool":
         return WorkspacePool(self.device, self.zeroed)
+
+
+class StatusWord:
+    """A host word the kernels can write (pinned, device-mapped memory on a GPU host): the
+    MoE forward passes its address as ``pgmoe_layer.status_host``, and a kernel that sets a
+    status bit in its workspace ORs the bit in here too.  Reading it is a plain host load,
+    so a forward can check the word of the forwards before it without synchronising the
+    stream (a bit set by a forward still running shows up at a later check)."""
+
+    def __init__(self, pinned: bool = True) -> None:
+        self._t = torch.zeros(1, dtype=torch.int32, pin_memory=pinned)
+
+    def ptr(self) -> int:
+        return self._t.data_ptr()
+
+    def take(self) -> int:
+        """The bits set so far, cleared."""
+        v = int(self._t[0])
+        if v:
+            self._t[0] = 0
+        return v

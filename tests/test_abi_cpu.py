@@ -75,22 +75,54 @@ def test_scale_plane_bytes_and_argument_checks():
     assert L.pgmoe_build_scale_plane(12, 0x1000, 2, 64, 256, stride - 16, 0x2000, None) == -1
 
 
-def _fake_layer(E=8, K=2, H=1024, I=512, qt=12, shared=False):
+def _fake_layer(E=8, K=2, H=1024, I=512, qt=12, shared=False, shared_inter=None, down_qt=None):
     """A layer struct with aligned fake device pointers (validation never dereferences)."""
     W = _lib.Weights
+    down_qt = qt if down_qt is None else down_qt
     stride = _lib.lib().pgmoe_weight_bytes(qt, I, H)
     L = _lib.Layer()
     L.hidden, L.n_experts, L.top_k, L.norm_topk = H, E, K, 1
     L.router_w = 0x10000
     L.gate = W(qt, I, H, E, 0x100000, stride)
     L.up = W(qt, I, H, E, 0x200000, stride)
-    L.down = W(qt, H, I, E, 0x300000, _lib.lib().pgmoe_weight_bytes(qt, H, I))
+    L.down = W(down_qt, H, I, E, 0x300000, _lib.lib().pgmoe_weight_bytes(down_qt, H, I))
     if shared:
+        Is = shared_inter or 2 * I
         L.has_shared = 1
-        L.sh_gate = W(qt, 2 * I, H, 1, 0x400000, 0)
-        L.sh_up = W(qt, 2 * I, H, 1, 0x500000, 0)
-        L.sh_down = W(qt, H, 2 * I, 1, 0x600000, 0)
+        L.sh_gate = W(qt, Is, H, 1, 0x400000, 0)
+        L.sh_up = W(qt, Is, H, 1, 0x500000, 0)
+        L.sh_down = W(qt, H, Is, 1, 0x600000, 0)
     return L
+
+
+def test_workspace_bytes_never_fall_as_m_grows():
+    """A workspace sized for M serves every smaller M: pgmoe_workspace_bytes (and the dense
+    and linear sizes) never decrease from M to M + 1, though the split-K scratch of one
+    batch can exceed that of a larger one (one more M tile can lower the split count).
+    Shapes: Qwen3-30B-A3B, Mixtral-8x7B, Qwen2-57B-A14B with its shared expert."""
+    L = _lib.lib()
+    layers = {"qwen3": _fake_layer(E=128, K=8, H=2048, I=768, qt=12, down_qt=14),
+              "mixtral": _fake_layer(E=8, K=2, H=4096, I=14336, qt=12),
+              "qwen2": _fake_layer(E=64, K=8, H=3584, I=2560, qt=8, shared=True, shared_inter=20480)}
+    for name, lay in layers.items():
+        prev = 0
+        for M in range(1, 4097):
+            n = L.pgmoe_workspace_bytes(lay, M)
+            assert n >= prev, f"{name}: {M} tokens need {n} bytes, {M - 1} needed {prev}"
+            prev = n
+    W = _lib.Weights
+    dense = _lib.Dense()
+    dense.hidden = 3584
+    dense.gate = W(8, 20480, 3584, 1, 0x100000, 0)
+    dense.up = W(8, 20480, 3584, 1, 0x200000, 0)
+    dense.down = W(8, 3584, 20480, 1, 0x300000, 0)
+    lin = W(8, 20480, 3584, 1, 0x100000, 0)
+    prev_d = prev_l = 0
+    for M in range(1, 4097):
+        nd = L.pgmoe_dense_workspace_bytes(dense, M)
+        nl = L.pgmoe_linear_workspace_bytes(lin, M, 1, 0)
+        assert nd >= prev_d and nl >= prev_l, M
+        prev_d, prev_l = nd, nl
 
 
 def test_workspace_bytes_and_zero_tokens():

@@ -46,7 +46,7 @@ def test_chunked_down_combine(down):
         check_layer_output(got, ol.forward_tokens(x, idx, w))
         again = mod(xt).cpu().numpy()
         assert np.array_equal(got, again), "not reproducible run to run"
-    mod.check_status()
+    mod.check_status(sync=True)
 
 
 @pytest.mark.parametrize("qts", [(Q4_1, Q4_1), (Q4_K, Q6_K), (Q5_K, Q4_K), (Q8_0, Q8_0), (Q6_K, Q5_K)])
@@ -63,4 +63,4 @@ def test_one_token_sums(qts, topk, inter):
         _, idx, w = ol.route(x)
         check_forward_routing(mod, 1, idx, w)
         check_layer_output(got, ol.forward_tokens(x, idx, w))
-    mod.check_status()
+    mod.check_status(sync=True)

@@ -136,8 +136,42 @@ def test_embed_lookup(dev):
         g16 = lin.embed_lookup(ids)
         assert g16.dtype == torch.float16
         assert np.array_equal(g16.cpu().numpy().view(np.uint16), ref.astype(np.float16).view(np.uint16))
-        with pytest.raises(IndexError):
+        with pytest.raises(IndexError):  # ids on the host are range-checked there
             lin.embed_lookup(torch.tensor([N]))
+        # ids on the device are not read back (no host sync): an id out of range is a NaN row
+        bad = lin.embed_lookup(torch.tensor([N, 1], device=dev), dtype=torch.float32).cpu().numpy()
+        assert np.all(np.isnan(bad[0])) and np.array_equal(bad[1].view(np.uint32), dense[1].view(np.uint32))
+
+
+def test_embed_lookup_and_linear_replay_from_a_captured_graph(dev):
+    """The reference captures embed_lookup and the quantized projections in its decode
+    graphs (model.py:1803, :1827, :2039): both drop-ins record without a host sync, and
+    every replay (eager work and synchronisations between them) equals the eager result."""
+    lin, _, _ = _lin(Q4_K, 300, 512, 11, dev, scale=1.0)
+    proj, _, _ = _lin(Q4_K, 256, 512, 12, dev)
+    ids = torch.tensor([3, 299, 64], device=dev)
+    x = torch.from_numpy(np.random.default_rng(5).standard_normal((1, 512)).astype(np.float16)).to(dev)
+    e_ref = lin.embed_lookup(ids).clone()
+    y_ref = proj(x).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        lin.embed_lookup(ids)
+        proj(x)  # the stream's workspace exists before capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            e_g = lin.embed_lookup(ids)
+            y_g = proj(x)
+    torch.cuda.synchronize()
+    for i in range(3):
+        e_g.zero_()
+        y_g.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(e_g, e_ref) and torch.equal(y_g, y_ref), f"replay {i}"
+        lin.embed_lookup(torch.tensor([i], device=dev))  # eager work between replays
+        torch.cuda.synchronize()
 
 
 def test_unsupported_widths_and_formats(dev):

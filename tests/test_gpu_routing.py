@@ -52,7 +52,7 @@ def test_forward_routing_bitexact(name, Ms):
         log(f"  min top-k margin {oracle.min_topk_margin(logits, mod.top_k):.2e}")
         if M <= 8:  # the output of the same forward, every row
             check_layer_output(out.cpu().numpy(), ol.forward_tokens(x, idx, w))
-    mod.check_status()
+    mod.check_status(sync=True)
 
 
 def _tie_layer(seed=5):
@@ -92,7 +92,7 @@ def test_forward_routing_ties_lower_id_wins(M):
     out = mod(torch.from_numpy(x).to("cuda:0"))
     check_forward_routing(mod, M, idx, w)
     check_layer_output(out.cpu().numpy(), ol.forward_tokens(x, idx, w), abs_tol=2e-2 if M <= 8 else None)
-    mod.check_status()
+    mod.check_status(sync=True)
 
 
 def test_graph_replay_matches_oracle_qwen3_decode():
@@ -129,4 +129,4 @@ def test_graph_replay_matches_oracle_qwen3_decode():
             toks = np.array([0, other_M - 1], np.int32)
             check_layer_output(other.cpu().numpy()[toks], ol.forward_tokens(xo_np, oi, ow, tokens=toks))
         del g
-    mod.check_status()
+    mod.check_status(sync=True)

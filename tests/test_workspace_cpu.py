@@ -48,3 +48,31 @@ def test_unzeroed_pool_for_stateless_workspaces():
     pool = WorkspacePool(torch.device("cpu"), zeroed=False)
     w = pool.get(300, stream=0)
     assert w.numel() >= 300 and w.data_ptr() % 256 == 0
+
+
+def test_status_word_reaches_the_next_forward_without_a_sync():
+    """The failure path: a kernel whose bounded wait gives up ORs PGMOE_STATUS_SPIN_TIMEOUT
+    into the layer's host-mapped status word (pgmoe_layer.status_host); the next forward
+    (or check_status) reads it with a plain host load, raises, and clears it.  Here the
+    kernel's store is played by a host write to an unpinned CPU word."""
+    import pytest
+
+    from pgmoe import _lib
+    from pgmoe.moe import raise_for_status
+    from pgmoe.workspace import StatusWord
+
+    w = StatusWord(pinned=False)
+    assert w.ptr() != 0 and w.take() == 0
+    raise_for_status(w.take())  # nothing set: no error
+    w._t[0] = _lib.STATUS_SPIN_TIMEOUT
+    with pytest.raises(RuntimeError, match="timed out"):
+        raise_for_status(w.take())
+    assert w.take() == 0  # cleared once reported
+    w._t[0] = 0x40
+    with pytest.raises(RuntimeError, match="0x40"):
+        raise_for_status(w.take())
+    # the layer struct carries the word's address to the C entry points
+    L = _lib.Layer()
+    L.status_host = w.ptr()
+    assert L.status_host == w.ptr()
+    assert _lib.Layer.status_host.offset > _lib.Layer.act.offset
