@@ -9,6 +9,19 @@
 
 namespace pgmoe {
 
+// The prefill's streamed rows (SwiGLU rows, fp16 down input, per-pair partials, output)
+// are each written once and read once by the next kernel, and do not fit the L2: they move
+// with nontemporal loads and stores, so they do not evict the GEMMs' reused activation and
+// weight lines.  Measured on the Qwen3 Zipf prefill (M = 4096): combine 63 -> 52 us, down
+// GEMM 221 -> 214 us, gate/up 323 -> 317 us, step 712 -> 694 us; Mixtral's row-scale
+// (M = 2048) 103 -> 92 us.
+typedef float nf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t nu2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 ld_nt4(const float* p) {
+    const nf4 v = __builtin_nontemporal_load((const nf4*)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // exec_fused_act_mul_rowscale's second half on an fp32 inter row: rs = max(max|v|/16384, 1),
 // a16 = fp16(v / rs)  (quant_kernels.py:1467-1475).  One wave per row; rows of up to
 // 64 * 4 * NV values are read once into registers, longer rows are read twice.
@@ -26,7 +39,7 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const float* __restrict__
 #pragma unroll
         for (int q = 0; q < NV; ++q) {
             const int i = lane + 64 * q;
-            v[q] = i < n4 ? *(const float4*)(row + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[q] = i < n4 ? ld_nt4(row + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
             mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)), fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
         }
     } else {
@@ -44,7 +57,7 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const float* __restrict__
                             ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.y / sc)) << 16);
         const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.z / sc)) |
                             ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.w / sc)) << 16);
-        *(uint2*)(orow + 4 * i) = make_uint2(lo, hi);
+        __builtin_nontemporal_store(nu2{lo, hi}, (nu2*)(orow + 4 * i));
     };
     if (NV > 0) {
 #pragma unroll
@@ -89,7 +102,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     float4 rows[16];
 #pragma unroll
     for (int s = 0; s < 16; ++s)
-        if (s < K) rows[s] = *(const float4*)(partial + (int64_t)srt[s] * H + 4 * c);
+        if (s < K) rows[s] = ld_nt4(partial + (int64_t)srt[s] * H + 4 * c);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int s = 0; s < 16; ++s)
@@ -107,7 +120,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
         acc.z += sv.z * gate;
         acc.w += sv.w * gate;
     }
-    *(float4*)(out + (int64_t)t * H + 4 * c) = acc;
+    __builtin_nontemporal_store(nf4{acc.x, acc.y, acc.z, acc.w}, (nf4*)(out + (int64_t)t * H + 4 * c));
 }
 
 // --------------------------------------------------------------------------- launchers

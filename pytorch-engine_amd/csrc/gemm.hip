@@ -582,7 +582,8 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
         return;
     }
     // epilogue: register v of tile (i, j) is row 32i + 8(v/4) + 4(l/32) + v%4, column
-    // 32j + l%32 of the wave tile
+    // 32j + l%32 of the wave tile.  Nontemporal stores: the rows are read once, by the next
+    // kernel, and must not evict the tiles' reused lines from the L2.
     if (GATEUP) {
         // wave columns: tiles j < CT/2 gate indices nt*128 + 16 CT wn + 32j + l%32, tile
         // j + CT/2 the matching up
@@ -596,7 +597,8 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
                     for (int v = 0; v < 16; ++v) {
                         const int r = WR * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                         if (r < mrows)
-                            out[(int64_t)(m0 + r) * N + col] = act_fast(gate_act, acc[i][j][v]) * acc[i][j + CT / 2][v];
+                            __builtin_nontemporal_store(act_fast(gate_act, acc[i][j][v]) * acc[i][j + CT / 2][v],
+                                                        &out[(int64_t)(m0 + r) * N + col]);
                     }
             }
         }
@@ -614,7 +616,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
 #pragma unroll
                 for (int j = 0; j < CT; ++j) {
                     const int col = c0 + 32 * j;
-                    if (col < N) orow[col] = acc[i][j][v] * sc;
+                    if (col < N) __builtin_nontemporal_store(acc[i][j][v] * sc, &orow[col]);
                 }
             }
     }
