@@ -1,10 +1,10 @@
 // Prefill (M > 8) grouped expert products on the MFMA cores.
 //
-// A tile is 256 sorted pairs of one expert x 256 output columns.  The gate/up block is 4
-// waves (one per SIMD; each owns all 256 rows x 64 columns, 256 fp32 accumulators per
-// lane in AGPRs), the down block 8 waves (two per SIMD; each all 256 rows x 32 columns),
-// so every B column is decoded once, as 8 x 2 or 8 x 1 v_mfma_f32_32x32x16_f16 tiles per
-// wave (other layouts are build-time choices: CT column tiles, WM waves along M).  The K loop steps one 64-weight unit at a time
+// A tile is 256 sorted pairs of one expert x 256 output columns.  The gate/up block is 8
+// waves (two per SIMD; each owns 128 rows x 64 columns, so each B column is decoded by the
+// two waves of its column), the down block 8 waves (two per SIMD; each all 256 rows x 32
+// columns, every B column decoded once), as 4 x 2 or 8 x 1 v_mfma_f32_32x32x16_f16 tiles
+// per wave (other layouts are build-time choices: CT column tiles, WM waves along M).  The K loop steps one 64-weight unit at a time
 // through a ring of three LDS stages filled by direct HBM -> LDS copies three units
 // ahead: the fp16 activation rows (16-byte slots XOR-swizzled by row) and the raw GGUF
 // bytes of the 256 weight rows (whole 1 KB chunks of the 64-row tile layout, with their
@@ -412,6 +412,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     using L = GLay<QT, CT, WM>;
     constexpr int NW = L::NW, WN = L::WN, RS = L::RS, WR = 32 * RS;  // WR rows per wave
     static_assert(!GATEUP || CT >= 2, "gate/up: each wave holds gate and matching up columns");
+    static_assert(L::AQ * WN * WM == 32, "the waves' A copies cover the 32 row octets once");
     constexpr int CH = L::CH;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * L::STAGE];
     __shared__ int rowsrc[kGM];
@@ -451,13 +452,16 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     }
     __syncthreads();
 
-    // ---- copy plan.  A: wave w copies rows 8i .. 8i+7 for i = w + NW q (q < AQ); lane
-    // l takes row 8i + l/8, slot l%8 = k chunk (l%8) ^ (l/8) ^ (i & 1), and i & 1 = w & 1
-    // for every copy of the wave (NW is even).
-    const int akc = (lane & 7) ^ (lane >> 3) ^ (wave & 1);
+    // ---- copy plan.  A: wave (wm, wn) copies rows 8i .. 8i+7 for the row octets
+    // i = (32 / WM) wm + wn + WN q (q < AQ), all within its own 256 / WM rows; lane l takes
+    // row 8i + l/8, slot l%8 = k chunk (l%8) ^ (l/8) ^ (i & 1), and i & 1 = wn & 1 for every
+    // copy of the wave (WN and 32 / WM are even).  With WN = 4 copy q is octet wn of the
+    // wave's slice q, so a wave copies only its slices with pairs.
+    const int aoct = (32 / WM) * wm + wn;
+    const int akc = (lane & 7) ^ (lane >> 3) ^ (wn & 1);
     const uint16_t* arow[L::AQ];
 #pragma unroll
-    for (int q = 0; q < L::AQ; ++q) arow[q] = act + (int64_t)rowsrc[8 * (wave + NW * q) + (lane >> 3)] * K;
+    for (int q = 0; q < L::AQ; ++q) arow[q] = act + (int64_t)rowsrc[8 * (aoct + WN * q) + (lane >> 3)] * K;
     // B row groups bg: gate/up: 0, 1 = gate rows nt*128 + 64bg, 2, 3 = the same up rows;
     // down: rows nt*256 + 64bg.  Groups past N repeat the last one (their columns are
     // never stored).
@@ -501,7 +505,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
         const uint32_t S = sbase + st * L::STAGE;
 #pragma unroll
         for (int q = 0; q < decltype(ac)::value; ++q)
-            g2l(arow[q] + Fmt<QT>::col(u, akc >> 1) + 8 * (akc & 1), S + (wave + NW * q) * 1024);
+            g2l(arow[q] + Fmt<QT>::col(u, akc >> 1) + 8 * (akc & 1), S + (aoct + WN * q) * 1024);
 #pragma unroll
         for (int q = 0; q < L::BQ; ++q) {
             const uint8_t* src;
@@ -540,11 +544,11 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     // is done with it (see gemm_loop).  The loop is instantiated per NI (a whole copy each)
     // so the register allocation of one copy never has to merge the others'.
     PG_MARK(GATEUP ? 4 : 5, 1);
-    // With one wave along M and 4 waves, wave w copies row octet w of every 32-row slice q,
-    // so the slices without pairs (q >= ni) are not copied at all; otherwise (8 waves: each
-    // copies octets w, w + 8, ...) every slice is.
+    // With 4 waves along N (CT = 2), wave (wm, wn) copies row octet wn of each of its 32-row
+    // slices q, so the slices without pairs (q >= ni) are not copied at all; otherwise (8
+    // waves along N: each copies octets wn, wn + 8, ...) every slice is.
 #define PG_GLOOP(NI_) \
-    gemm_loop<QT, NI_, CT, RS, (WM == 1 && L::NW == 4) ? NI_ : L::AQ, L::BQ, L::STAGE>(smem, units, bgj, rigj, wm, \
+    gemm_loop<QT, NI_, CT, RS, (WN == 4) ? NI_ : L::AQ, L::BQ, L::STAGE>(smem, units, bgj, rigj, wm, \
                                                                                      lane, acc, copy_unit);
     switch (ni) {
     case 8: if constexpr (RS == 8) { PG_GLOOP(8) } break;
@@ -729,11 +733,16 @@ static int launch_split_reduce(bool gateup, const float* raw, int S, int64_t P, 
 }
 
 // Wave layout of each product (build-time choices): CT column tiles per wave, WM waves
-// along M.  Measured on the Qwen3 Zipf prefill (M = 4096): gate/up (K = 2048, Q4_K) is
-// fastest with 4 waves (WM = 1: half the B decode per SIMD, no copies of empty slices),
-// down with 8 waves of 256 rows x 32 columns (CT = 1, WM = 1: each B column decoded once,
-// two waves a SIMD): Q6_K 229 -> 225 us, Mixtral's Q4_K 770 -> 712 us against 8 waves of
-// 128 x 64 (CT = 2, WM = 2, every B column decoded by two waves).
+// along M.  gate/up: 8 waves of 128 rows x 64 columns (CT = 2, WM = 2; two waves a SIMD,
+// each B column decoded by the two waves of its column).  With one wave a SIMD (WM = 1,
+// 256 rows x 64 columns, every B column decoded once) the matrix cores co-execute with
+// VALU for only a fifth of their busy cycles (SQ_VALU_MFMA_COEXEC_CYCLES / _BUSY_CYCLES,
+// Mixtral's all-full-tile gate/up): the second wave's decode fills part of that.  Measured
+// (same box, two A/B pairs): Qwen3 Zipf M = 4096 gate/up 311 / 309 -> 299 / 298 us, Qwen2
+// shared gate/up 232 -> 212-218 us, Mixtral M = 2048 unchanged (1055 us).  Down: 8 waves
+// of 256 rows x 32 columns (CT = 1, WM = 1: each B column decoded once, two waves a SIMD):
+// Q6_K 229 -> 225 us, Mixtral's Q4_K 770 -> 712 us against 8 waves of 128 x 64 (CT = 2,
+// WM = 2, every B column decoded by two waves).
 #ifndef PG_GU_CT
 #define PG_GU_CT 2
 #endif
@@ -741,7 +750,7 @@ static int launch_split_reduce(bool gateup, const float* raw, int S, int64_t P, 
 #define PG_DN_CT 1
 #endif
 #ifndef PG_GU_WM
-#define PG_GU_WM 1
+#define PG_GU_WM 2
 #endif
 #ifndef PG_DN_WM
 #define PG_DN_WM 1
