@@ -1545,9 +1545,32 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
     int bx = blockIdx.x, row = bx * RB + r;
     PG_DECL;
     PG_MARK(3, 0);
+    // 0. the first IR pieces per thread of the inter rows, and of their sums, into
+    //    registers before anything else: their addresses (sorted pairs 0 .. P-1) do not
+    //    depend on the descriptor, so these loads overlap its round trip instead of
+    //    following it (one token: every piece).  Measured on Qwen3 (same box, two A/B
+    //    pairs): down + combine M = 1 7.3-7.4 -> 6.9 us, M = 2 10.2-10.3 -> 9.9-10.0 us,
+    //    M = 4 16.2-16.6 -> 15.9 us.
+    constexpr int IR = 2;
+    const int kq = K >> 2;
+    const int n_in = P * kq;                                  // 16-byte pieces of the inter rows
+    const int n_is = isum8 ? P * (K >> 4) : P * (K >> 6);    // 8-byte / 16-byte pieces of the sums
+    u32x4 ir[IR];
+#pragma unroll
+    for (int k = 0; k < IR; ++k)
+        if (tid + k * nth < n_in) ir[k] = *(const u32x4*)(inter + 4 * (int64_t)(tid + k * nth));
+    float s0 = 0.f, s1 = 0.f;       // isum8: the two 8-row sums of 16-row group tid
+    u32x4 sr = {0u, 0u, 0u, 0u};   // else: 16-byte piece tid of the 16-row sums
+    if (tid < n_is) {
+        if (isum8) {
+            s0 = isum[2 * tid];
+            s1 = isum[2 * tid + 1];
+        } else {
+            sr = *(const u32x4*)(isum + 4 * tid);
+        }
+    }
     // 1. the experts of this lane's first two items straight from the descriptor, then
-    //    their weights, then the inter rows and the pair table behind them: the weights'
-    //    latency covers the staging
+    //    their weights, then the pair table and the staging of the inter rows
     const bool ident = desc == nullptr;
     const int S = (ident ? 1 : desc[0]) * nb;  // items (active slot a, super-block j), it = a * nb + j
     int it0 = 2 * w + u, it1 = it0 + 2 * nw;
@@ -1562,14 +1585,26 @@ __global__ __launch_bounds__(1024) void dec_dc_kernel(const uint8_t* __restrict_
         d_tok[i] = ident ? i : desc[kDescPair + 2 * i];
         d_w[i] = ident ? 1.0f : __builtin_bit_cast(float, desc[kDescPair + 2 * i + 1]);
     }
-    const int kq = K >> 2;
-    copy_idx<4, u32x4>(
-        P * kq, tid, nth, [=](int i) { return (const u32x4*)(inter + 4 * (int64_t)i); },
-        [=](int i) { return (u32x4*)(xs + (i / kq) * xrs + xpos_f(4 * (i % kq))); });
-    if (isum8)  // 8-row sums (the one-token gate/up): pairs of them
-        for (int i = tid; i < P * (K >> 4); i += nth) iss[i] = isum[2 * i] + isum[2 * i + 1];
-    else
-        copy_words<2>((u32x4*)iss, (const u32x4*)isum, P * (K >> 6), tid, nth);
+#pragma unroll
+    for (int k = 0; k < IR; ++k) {
+        const int i = tid + k * nth;
+        if (i < n_in) *(u32x4*)(xs + (i / kq) * xrs + xpos_f(4 * (i % kq))) = ir[k];
+    }
+    if (n_in > IR * nth)
+        copy_idx<4, u32x4>(
+            n_in - IR * nth, tid, nth, [=](int i) { return (const u32x4*)(inter + 4 * (int64_t)(i + IR * nth)); },
+            [=](int i) {
+                const int j = i + IR * nth;
+                return (u32x4*)(xs + (j / kq) * xrs + xpos_f(4 * (j % kq)));
+            });
+    if (isum8) {  // 8-row sums (the one-token gate/up): pairs of them
+        if (tid < n_is) iss[tid] = s0 + s1;
+        for (int i = tid + nth; i < n_is; i += nth) iss[i] = isum[2 * i] + isum[2 * i + 1];
+    } else {
+        if (tid < n_is) ((u32x4*)iss)[tid] = sr;
+        if (n_is > nth)
+            copy_words<2>((u32x4*)iss + nth, (const u32x4*)isum + nth, n_is - nth, tid, nth);
+    }
     __syncthreads();
     PG_MARK(3, 1);
     // 2. items, two per lane per pass (row block after row block)
@@ -1641,6 +1676,8 @@ __global__ __launch_bounds__(1024) void dec_dc_chunk_kernel(const uint8_t* __res
     const int r = lane & 7, p = (lane >> 3) & 3, u = lane >> 5;
     const int row = blockIdx.x * RB + r;
     // 1. the experts of this lane's first two items, their weights, then the pair table
+    //    (prefetching the first chunk's rows ahead of the descriptor, as dec_dc_kernel does,
+    //    spilled here: this kernel's registers are at the 128 bound)
     const bool ident = desc == nullptr;
     const int A = ident ? 1 : desc[0];  // active slots
     int j0 = 0, JCc = JC < nb ? JC : nb;

@@ -436,6 +436,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
         m0 = offsets[e] + (mt - tile_off[e]) * kGM;
     }
     const int mrows = min(kGM, offsets[e + 1] - m0);
+    PG_SET(2, 1u + (uint32_t)mrows);  // profiling builds: the tile's rows
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;  // waves w and w + WN: same columns
