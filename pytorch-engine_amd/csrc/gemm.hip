@@ -546,10 +546,14 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     // so the register allocation of one copy never has to merge the others'.
     PG_MARK(GATEUP ? 4 : 5, 1);
     // With 4 waves along N (CT = 2), wave (wm, wn) copies row octet wn of each of its 32-row
-    // slices q, so the slices without pairs (q >= ni) are not copied at all; otherwise (8
-    // waves along N: each copies octets wn, wn + 8, ...) every slice is.
+    // slices q, so the slices without pairs (q >= ni) are not copied at all.  With 8 waves
+    // along N and one along M (the down product), copy q of wave w is octet w % 4 of slice
+    // 2q + w / 4, so ceil(ni / 2) copies a wave cover the slices with pairs (for odd ni the
+    // waves w >= 4 also copy slice ni, whose rows repeat the tile's last pair: unused, and
+    // in bounds).  Other layouts copy every slice.
 #define PG_GLOOP(NI_) \
-    gemm_loop<QT, NI_, CT, RS, (WN == 4) ? NI_ : L::AQ, L::BQ, L::STAGE>(smem, units, bgj, rigj, wm, \
+    gemm_loop<QT, NI_, CT, RS, (WN == 4) ? NI_ : (WN == 8 && WM == 1) ? (NI_ + 1) / 2 : L::AQ, L::BQ, L::STAGE>( \
+        smem, units, bgj, rigj, wm, \
                                                                                      lane, acc, copy_unit);
     switch (ni) {
     case 8: if constexpr (RS == 8) { PG_GLOOP(8) } break;
