@@ -136,6 +136,18 @@ int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
 int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
                            void* dst, void* stream);
 
+/* pgmoe_relayout_weights into zero-padded matrices: GGUF blocks of n_mats [rows, cols]
+ * matrices -> device matrices [rows_out, cols_out] (rows_out >= rows, cols_out >= cols a
+ * multiple of 256, dst matrices pgmoe_weight_bytes(qtype, rows_out, cols_out) bytes apart)
+ * whose extra rows and columns hold exact zeros.  The 32-weight formats (Q8_0, Q5_0, Q4_0,
+ * Q4_1) take any cols that is a multiple of 32; the K-quants keep cols == cols_out.  For an
+ * expert intermediate size I that is not a multiple of 256 (e.g. 1408): gate / up padded to
+ * I_out rows and down to I_out columns compute what the unpadded layer does, since the zero
+ * rows give SwiGLU values of exactly 0, which meet zero weights.  Load time only; the
+ * reference accepts these widths in its W8 / W4 repack (quant_kernels.py:958, :1966-1967). */
+int pgmoe_relayout_weights_padded(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
+                                  int64_t rows_out, int64_t cols_out, void* dst, void* stream);
+
 /* Bytes of one matrix's scale plane (0 for Q8_0, which has none; -1 if unsupported).  No
  * counterpart in the reference: it sizes the buffer of pgmoe_build_scale_plane. */
 int64_t pgmoe_scale_plane_bytes(int32_t qtype, int64_t rows, int64_t cols);

@@ -300,8 +300,25 @@ int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64
         return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld columns", qtype, (long long)cols);
     if (!src || !dst || n_mats < 1 || rows < 1) return fail(PGMOE_E_INVALID, "relayout: bad arguments");
     if ((uintptr_t)dst & 255) return fail(PGMOE_E_INVALID, "relayout: dst must be 256-byte aligned");
-    return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, (uint8_t*)dst,
+    return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, rows, cols, (uint8_t*)dst,
                            pgmoe_weight_bytes(qtype, rows, cols), as_stream(stream));
+}
+
+int pgmoe_relayout_weights_padded(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
+                                  int64_t rows_out, int64_t cols_out, void* dst, void* stream) {
+    if (layout_bytes(qtype, rows_out, cols_out) < 0)
+        return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld output columns (a multiple of 256)", qtype,
+                    (long long)cols_out);
+    const bool w32 = qtype == PGMOE_Q8_0 || qtype == PGMOE_Q4_0 || qtype == PGMOE_Q4_1 || qtype == PGMOE_Q5_0;
+    if (!src || !dst || n_mats < 1 || rows < 1 || rows > rows_out || cols < 1 || cols > cols_out)
+        return fail(PGMOE_E_INVALID, "relayout: bad arguments (rows %lld of %lld, cols %lld of %lld)", (long long)rows,
+                    (long long)rows_out, (long long)cols, (long long)cols_out);
+    if (w32 ? cols % 32 : cols != cols_out)
+        return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld source columns padded to %lld", qtype,
+                    (long long)cols, (long long)cols_out);
+    if ((uintptr_t)dst & 255) return fail(PGMOE_E_INVALID, "relayout: dst must be 256-byte aligned");
+    return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, rows_out, cols_out, (uint8_t*)dst,
+                           pgmoe_weight_bytes(qtype, rows_out, cols_out), as_stream(stream));
 }
 
 int64_t pgmoe_scale_plane_bytes(int32_t qtype, int64_t rows, int64_t cols) {

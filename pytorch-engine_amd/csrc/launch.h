@@ -69,8 +69,10 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
 int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H, const float* shared,
                    const float* shared_logit, float* out, hipStream_t st, uint64_t* clear = nullptr,
                    int n_clear = 0);
-int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, uint8_t* dst,
-                    int64_t dst_stride, hipStream_t st);
+// GGUF [n_mats, rows, cols] -> device matrices [rows_out, cols_out] (zero padding past
+// rows / cols; cols_out a multiple of 256, cols == cols_out for K-quants).
+int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, int64_t rows_out,
+                    int64_t cols_out, uint8_t* dst, int64_t dst_stride, hipStream_t st);
 // Decode expert stages (M <= decode_tokens_max()).
 int launch_dec_gateup(const Mats& g, const Mats& u, const uint16_t* x, const float* xsum, int topk, int M,
                       const int32_t* offsets, const int32_t* perm, const int32_t* active, const int32_t* n_active,

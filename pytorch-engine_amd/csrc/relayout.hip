@@ -25,12 +25,16 @@ __device__ __forceinline__ void zero16(uint8_t* d) {
     for (int i = 0; i < 16; ++i) d[i] = 0;
 }
 
-// One thread per (matrix, padded row, 256-weight block).  Q5_0 sources are written as Q8_0
-// tiles: d * (q - 16) (5-bit q) is the Q8_0 value d * qs with qs = q - 16 (same d, same
-// 32-weight blocks).  Q4_0 sources are written as Q4_1 tiles: d * (q - 8) = d q + m with
-// m = -8d (exact in fp16 for |d| < 8188).  Every value is kept exactly.
+// One thread per (matrix, padded row, 256-weight block) of the device matrix [N, 256 nb]
+// (rows padded to 64).  The source matrix is [Ns, kbs blocks of the format] (Ns <= N;
+// K-quants: kbs = nb; 32-weight formats: kbs <= 8 nb, any count): rows past Ns and 32-weight
+// blocks past kbs are written as zeros, whose value is exactly 0 in every format.  Q5_0
+// sources are written as Q8_0 tiles: d * (q - 16) (5-bit q) is the Q8_0 value d * qs with
+// qs = q - 16 (same d, same 32-weight blocks).  Q4_0 sources are written as Q4_1 tiles:
+// d * (q - 8) = d q + m with m = -8d (exact in fp16 for |d| < 8188).  Every value is kept
+// exactly.
 template <int QT>
-__global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats, int N, int nb,
+__global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats, int Ns, int kbs, int N, int nb,
                                 uint8_t* __restrict__ dst, int64_t dst_stride) {
     const int ng = row_groups(N);
     const int64_t per_mat = (int64_t)ng * 64 * nb;
@@ -44,10 +48,14 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
     constexpr int CH = Tile<DT>::CH;
     uint8_t* md = dst + mat * dst_stride;
     uint8_t* t = md + ((int64_t)rg * nb + b) * (CH * 1024) + r * 16;
-    const bool real = row < N;
-    // GGUF bytes of this (row, 256-weight block)
-    constexpr int sb = Gguf<QT>::bytes * (256 / Gguf<QT>::per);
-    const uint8_t* s = src + mat * (int64_t)N * nb * sb + ((int64_t)row * nb + b) * sb;
+    const bool real = row < Ns;
+    // GGUF bytes of this (row, 256-weight block): 32-weight blocks j of it are real while
+    // 8b + j < kbs (K-quants: one block, b < kbs = nb)
+    constexpr int BYT = Gguf<QT>::bytes, PER = Gguf<QT>::per;
+    constexpr int sb = BYT * (256 / PER);
+    const int64_t srow = (int64_t)kbs * BYT;  // source bytes per row
+    const uint8_t* s = src + (mat * Ns + (real ? row : 0)) * srow + (int64_t)b * sb;
+    auto realj = [&](int j) { return real && (PER == 256 || 8 * b + j < kbs); };
     if (QT == PGMOE_Q5_K) {  // GGUF: d, dmin, scales (0-15), qh (16-47), qs (48-175)
         for (int c = 0; c < 9; ++c) {
             if (real) copy16(t + c * 1024, s + (c == 0 ? 0 : 48 + 16 * (c - 1)));
@@ -83,32 +91,34 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
         }
     } else if (QT == PGMOE_Q5_0) {  // eight 22-byte blocks per 256 weights -> Q8_0 tiles
         for (int j = 0; j < 8; ++j) {
+            const bool rj = realj(j);
             const uint8_t* bj = s + 22 * j;
-            const uint32_t qh = real ? (uint32_t)bj[2] | ((uint32_t)bj[3] << 8) | ((uint32_t)bj[4] << 16) |
-                                           ((uint32_t)bj[5] << 24)
-                                     : 0xffffffffu;  // pad rows: q = 16 -> 0
+            const uint32_t qh = rj ? (uint32_t)bj[2] | ((uint32_t)bj[3] << 8) | ((uint32_t)bj[4] << 16) |
+                                         ((uint32_t)bj[5] << 24)
+                                   : 0xffffffffu;  // padding: q = 16 -> 0
             uint8_t lo[16], hi[16];
 #pragma unroll
             for (int l = 0; l < 16; ++l) {
-                const int q = real ? bj[6 + l] : 0;
+                const int q = rj ? bj[6 + l] : 0;
                 lo[l] = (uint8_t)(int8_t)(((q & 15) | (int)(((qh >> l) & 1) << 4)) - 16);
                 hi[l] = (uint8_t)(int8_t)(((q >> 4) | (int)(((qh >> (16 + l)) & 1) << 4)) - 16);
             }
             copy16(t + (2 * j) * 1024, lo);
             copy16(t + (2 * j + 1) * 1024, hi);
-            t[16 * 1024 + 2 * j] = real ? bj[0] : 0;
-            t[16 * 1024 + 2 * j + 1] = real ? bj[1] : 0;
+            t[16 * 1024 + 2 * j] = rj ? bj[0] : 0;
+            t[16 * 1024 + 2 * j + 1] = rj ? bj[1] : 0;
         }
     } else if (QT == PGMOE_Q4_0 || QT == PGMOE_Q4_1) {  // eight 18 / 20-byte blocks -> Q4_1 tiles
         constexpr int BB = Gguf<QT>::bytes, QO = QT == PGMOE_Q4_0 ? 2 : 4;  // block bytes, qs offset
         // codes of element l of block j: low nibble of qs[l] (l < 16), high nibble of qs[l - 16]
         auto code = [&](int j, int l) -> uint32_t {
-            const uint8_t b = s[BB * j + QO + (l & 15)];
-            return l < 16 ? (b & 15u) : (uint32_t)(b >> 4);
+            if (!realj(j)) return 0u;
+            const uint8_t bt = s[BB * j + QO + (l & 15)];
+            return l < 16 ? (bt & 15u) : (uint32_t)(bt >> 4);
         };
         for (int j = 0; j < 8; ++j) {
-            uint16_t d = 0, m = 0;  // pad rows: d = m = 0
-            if (real) {
+            uint16_t d = 0, m = 0;  // padding: d = m = 0
+            if (realj(j)) {
                 d = (uint16_t)s[BB * j] | ((uint16_t)s[BB * j + 1] << 8);
                 if (QT == PGMOE_Q4_1)
                     m = (uint16_t)s[BB * j + 2] | ((uint16_t)s[BB * j + 3] << 8);
@@ -125,14 +135,14 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int k = 16 * c + i, J = k >> 5, l = k & 31;
-                v[i] = real ? (uint8_t)(code(2 * J, l) | (code(2 * J + 1, l) << 4)) : 0;
+                v[i] = (uint8_t)(code(2 * J, l) | (code(2 * J + 1, l) << 4));
             }
             copy16(t + (2 + c) * 1024, v);
         }
     } else {  // Q8_0: eight 34-byte blocks per 256 weights
         for (int j = 0; j < 8; ++j) {
             const uint8_t* bj = s + 34 * j;
-            if (real) {
+            if (realj(j)) {
                 copy16(t + (2 * j) * 1024, bj + 2);
                 copy16(t + (2 * j + 1) * 1024, bj + 18);
                 t[16 * 1024 + 2 * j] = bj[0];
@@ -245,34 +255,38 @@ int64_t layout_bytes(int qtype, int64_t rows, int64_t cols) {
     }
 }
 
-int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, uint8_t* dst,
-                    int64_t dst_stride, hipStream_t st) {
-    const int nb = (int)(cols / 256);
-    const int64_t n = n_mats * (int64_t)row_groups((int)rows) * 64 * nb;
+int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, int64_t rows_out,
+                    int64_t cols_out, uint8_t* dst, int64_t dst_stride, hipStream_t st) {
+    const int nb = (int)(cols_out / 256);
+    int per = 256;  // weights per GGUF block
+    if (qtype == PGMOE_Q8_0 || qtype == PGMOE_Q4_0 || qtype == PGMOE_Q4_1 || qtype == PGMOE_Q5_0) per = 32;
+    const int kbs = (int)(cols / per);
+    const int64_t n = n_mats * (int64_t)row_groups((int)rows_out) * 64 * nb;
     if (n == 0) return PGMOE_OK;
     const int threads = 256;
     const dim3 grid((unsigned)((n + threads - 1) / threads));
+    const int Ns = (int)rows, N = (int)rows_out;
     switch (qtype) {
     case PGMOE_Q4_K:
-        PG_LAUNCH(relayout_kernel<PGMOE_Q4_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q4_K>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     case PGMOE_Q5_K:
-        PG_LAUNCH(relayout_kernel<PGMOE_Q5_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q5_K>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     case PGMOE_Q6_K:
-        PG_LAUNCH(relayout_kernel<PGMOE_Q6_K>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q6_K>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     case PGMOE_Q8_0:
-        PG_LAUNCH(relayout_kernel<PGMOE_Q8_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q8_0>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     case PGMOE_Q4_0:
-        PG_LAUNCH(relayout_kernel<PGMOE_Q4_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q4_0>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     case PGMOE_Q4_1:
-        PG_LAUNCH(relayout_kernel<PGMOE_Q4_1>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q4_1>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     case PGMOE_Q5_0:
-        PG_LAUNCH(relayout_kernel<PGMOE_Q5_0>, grid, dim3(threads), 0, st, src, n_mats, (int)rows, nb, dst, dst_stride);
+        PG_LAUNCH(relayout_kernel<PGMOE_Q5_0>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     default:
         return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d", qtype);

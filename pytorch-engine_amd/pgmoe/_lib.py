@@ -86,6 +86,7 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_weight_bytes.restype = _I64
     L.pgmoe_weight_bytes.argtypes = [_I32, _I64, _I64]
     L.pgmoe_relayout_weights.argtypes = [_I32, _P, _I64, _I64, _I64, _P, _P]
+    L.pgmoe_relayout_weights_padded.argtypes = [_I32, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]
     L.pgmoe_scale_plane_bytes.restype = _I64
     L.pgmoe_scale_plane_bytes.argtypes = [_I32, _I64, _I64]
     L.pgmoe_build_scale_plane.argtypes = [_I32, _P, _I64, _I64, _I64, _I64, _P, _P]
@@ -118,7 +119,8 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_combine.argtypes = [_P, _P, _I32, _I32, _I32, _P, _P, _P, _P]
     for fn in ("pgmoe_moe_forward", "pgmoe_moe_forward_timed", "pgmoe_router_topk", "pgmoe_dispatch",
                "pgmoe_dispatch_ws", "pgmoe_expert_gateup",
-               "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_build_scale_plane",
+               "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_relayout_weights_padded",
+               "pgmoe_build_scale_plane",
                "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status", "pgmoe_moe_forward_noalloc",
                "pgmoe_add_rmsnorm", "pgmoe_linear_forward", "pgmoe_dequant_rows"):
         getattr(L, fn).restype = ctypes.c_int
@@ -143,7 +145,7 @@ EXPORTS = (
     "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane", "pgmoe_dispatch_ws_bytes", "pgmoe_dispatch_ws",
     "pgmoe_dense_workspace_bytes", "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status",
     "pgmoe_moe_forward_noalloc", "pgmoe_add_rmsnorm", "pgmoe_linear_workspace_bytes", "pgmoe_linear_forward",
-    "pgmoe_dequant_rows",
+    "pgmoe_dequant_rows", "pgmoe_relayout_weights_padded",
 )
 
 STATUS_SPIN_TIMEOUT = 1  # PGMOE_STATUS_SPIN_TIMEOUT

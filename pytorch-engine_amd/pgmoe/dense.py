@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 
 from ._lib import ACT_GELU_TANH, ACT_SILU, Dense, check, lib
-from .moe import _ExpertTensor, _load_lock
+from .moe import _ExpertTensor, _load_lock, padded_inter
 from .workspace import WorkspacePool
 
 
@@ -41,15 +41,18 @@ class HipDenseMLP(nn.Module):
         self.use_gelu = str(config.arch).startswith("gemma")  # GeGLU (model.py:800)
         prefix = prefix_override or f"blk.{layer_idx}"
         with _load_lock, torch.cuda.device(device):
-            self.gate_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate.weight", device, False)
-            self.up_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_up.weight", device, False)
-            self.down_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_down.weight", device, False)
+            inter, i_out = padded_inter(gguf_file, f"{prefix}.ffn_down.weight")  # zero padding of I
+            self.gate_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate.weight", device, False, rows_out=i_out)
+            self.up_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_up.weight", device, False, rows_out=i_out)
+            self.down_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_down.weight", device, False, cols_out=i_out)
             torch.cuda.current_stream(device).synchronize()  # uploads done before host buffers go away
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
+        if g.cols != g.gguf_cols:
+            raise ValueError(f"{prefix}: hidden size {g.gguf_cols} is not a multiple of 256")
         if (u.rows, u.cols) != (g.rows, g.cols) or (d.rows, d.cols) != (g.cols, g.rows):
             raise ValueError(f"{prefix}: gate {g.rows}x{g.cols}, up {u.rows}x{u.cols} and down "
                              f"{d.rows}x{d.cols} do not form an [I, H] / [H, I] FFN")
-        self.hidden, self.inter = g.cols, g.rows
+        self.hidden, self.inter, self.inter_padded = g.cols, inter, g.rows
         self._ws = WorkspacePool(device, zeroed=False)  # the dense workspace keeps no state
         self._dense = self._build()
 

@@ -61,22 +61,27 @@ class GGUFQuantLinear(nn.Module):
                              persistent=False)
         self.register_buffer("weight", None, persistent=False)
         self.buf = self.plane = None
+        self.cols = self.in_features
         if mode == "fp16":
             self.weight = weight.to(dev, torch.float16).contiguous()
             return
         if gguf_qtype not in SUPPORTED_QTYPES:
             raise NotImplementedError(f"ggml type {gguf_qtype} has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, "
                                       "Q8_0, Q4_1, and Q4_0 / Q5_0 relaid out as Q4_1 / Q8_0)")
-        if self.in_features % 256:
-            raise NotImplementedError(f"{self.in_features} input features is not a multiple of 256")
+        # the device width: in_features, or for the 32-weight formats the next multiple of 256
+        # (zero blocks appended to every row; forward appends as many zero inputs)
+        self.cols = ops.padded_width(gguf_qtype, self.in_features)
+        if self.cols < 0:
+            raise NotImplementedError(f"{self.in_features} input features: the K-quant formats need a multiple "
+                                      "of 256, the 32-weight formats a multiple of 32")
         self.qtype = ops.device_qtype(gguf_qtype)
         lib()
         with torch.cuda.device(dev):
             src = torch.from_numpy(np.ascontiguousarray(raw)).to(dev)
-            self.buf = ops.relayout(gguf_qtype, src, 1, self.out_features, self.in_features)
-            self.plane = ops.scale_plane(self.qtype, self.buf, 1, self.out_features, self.in_features)
+            self.buf = ops.relayout(gguf_qtype, src, 1, self.out_features, self.in_features, cols_out=self.cols)
+            self.plane = ops.scale_plane(self.qtype, self.buf, 1, self.out_features, self.cols)
             torch.cuda.current_stream(dev).synchronize()  # the upload is done before `raw` may go away
-        self._w = ops.make_weights(self.qtype, self.buf, 1, self.out_features, self.in_features, self.plane)
+        self._w = ops.make_weights(self.qtype, self.buf, 1, self.out_features, self.cols, self.plane)
         self._ws = WorkspacePool(dev, zeroed=False)
 
     # ------------------------------------------------------------------ construction
@@ -135,6 +140,8 @@ class GGUFQuantLinear(nn.Module):
             return out.reshape(*orig_shape[:-1], self.out_features)
         xh = x_2d if x_2d.dtype == torch.float16 else x_2d.to(torch.float16)
         xh = xh.contiguous()
+        if self.cols != self.in_features:  # zero inputs for the zero weight blocks
+            xh = F.pad(xh, (0, self.cols - self.in_features))
         M = xh.shape[0]
         odt = x.dtype if x.dtype in _OUT else torch.float16
         out = torch.empty((M, self.out_features), dtype=odt, device=self.device)
@@ -169,11 +176,13 @@ class GGUFQuantLinear(nn.Module):
             return rows.reshape(*token_ids.shape, K)
         ids = flat.to(torch.int32).contiguous()
         odt = dtype if dtype in _OUT else torch.float32
-        out = torch.empty((ids.numel(), K), dtype=odt, device=self.device)
+        out = torch.empty((ids.numel(), self.cols), dtype=odt, device=self.device)
         if ids.numel():
             check(lib().pgmoe_dequant_rows(self._w, ids.data_ptr(), ids.numel(), out.data_ptr(), _OUT[odt],
                                            torch.cuda.current_stream(self.device).cuda_stream),
                   "pgmoe_dequant_rows")
+        if self.cols != K:
+            out = out[:, :K]
         return out.to(dtype).reshape(*token_ids.shape, K)
 
 

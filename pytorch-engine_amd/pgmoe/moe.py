@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from typing import Any, Optional
+from typing import Any, Optional, Tuple
 
 import numpy as np
 import torch
@@ -67,17 +67,34 @@ def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.
     return arr.to(device=device, dtype=torch.float32).contiguous()
 
 
-class _ExpertTensor:
-    """One quantised weight tensor ([E, N, K] or [N, K]) held in the device layout."""
+def padded_inter(gguf_file: Any, down_name: str) -> Tuple[int, int]:
+    """(I, I_out) of an FFN whose down tensor is `down_name` ([E, H, I] or [H, I]): I_out = I
+    when I is a multiple of 256; for a 32-weight down format (Q8_0, Q5_0, Q4_0, Q4_1) with I
+    a multiple of 32 (e.g. 1408), I rounded up to one of 256: gate / up then get zero rows and
+    down zero columns up to I_out, and the kernels compute the unpadded layer's values (zero
+    rows give SwiGLU values of exactly 0, which meet zero weights)."""
+    info = gguf_file.tensors[down_name]
+    inter = int(info.shape[-1])
+    io = ops.padded_width(int(info.qtype), inter)
+    if io < 0:
+        raise ValueError(f"{down_name}: {inter} input features (a multiple of 256, or of 32 for the 32-weight "
+                         "formats Q8_0, Q5_0, Q4_0, Q4_1)")
+    return inter, io
 
-    def __init__(self, gguf_file: Any, name: str, device: torch.device, three_d: bool):
+
+class _ExpertTensor:
+    """One quantised weight tensor ([E, N, K] or [N, K]) held in the device layout, as
+    [rows_out, cols_out] matrices when given (zero padding; see padded_inter)."""
+
+    def __init__(self, gguf_file: Any, name: str, device: torch.device, three_d: bool,
+                 rows_out: Optional[int] = None, cols_out: Optional[int] = None):
         info = gguf_file.tensors[name]
         shape = tuple(int(s) for s in info.shape)
         if three_d and len(shape) != 3:
             raise ValueError(f"Expected 3D MoE tensor for {name}, got shape={shape}")
         if not three_d and len(shape) != 2:
             raise ValueError(f"Expected 2D tensor for {name}, got shape={shape}")
-        self.n_mats, self.rows, self.cols = (shape if three_d else (1,) + shape)
+        self.n_mats, self.gguf_rows, self.gguf_cols = (shape if three_d else (1,) + shape)
         self.gguf_qtype = int(info.qtype)
         self.qtype = ops.device_qtype(self.gguf_qtype)  # format of the device layout
         if self.gguf_qtype not in SUPPORTED_QTYPES:
@@ -85,11 +102,16 @@ class _ExpertTensor:
                 f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
                 "has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, Q8_0, Q4_1, and Q4_0 / Q5_0 relaid out as Q4_1 / "
                 "Q8_0)")
-        if self.cols % 256:
-            raise ValueError(f"{name}: {self.cols} input features is not a multiple of 256")
+        width = ops.padded_width(self.gguf_qtype, self.gguf_cols)
+        if width < 0 or (cols_out is not None and cols_out < width):
+            raise ValueError(f"{name}: {self.gguf_cols} input features is not a multiple of 256"
+                             + (" (nor of 32 for a 32-weight format)" if width < 0 else ""))
+        self.rows = self.gguf_rows if rows_out is None else int(rows_out)
+        self.cols = width if cols_out is None else int(cols_out)
         raw_np = gguf_file.get_tensor_bytes(name)
         raw = torch.from_numpy(np.asarray(raw_np)).to(device)  # H2D copy of the GGUF bytes
-        self.buf = ops.relayout(self.gguf_qtype, raw, self.n_mats, self.rows, self.cols)
+        self.buf = ops.relayout(self.gguf_qtype, raw, self.n_mats, self.gguf_rows, self.gguf_cols, self.rows,
+                                self.cols)
         del raw
         # K-quants: the sub-block scales decoded once for the prefill MFMA products
         self.plane = ops.scale_plane(self.qtype, self.buf, self.n_mats, self.rows, self.cols)
@@ -100,7 +122,7 @@ class _ExpertTensor:
     @property
     def gguf_bytes_per_mat(self) -> int:
         per, bb = ops.GGUF_BLOCK[self.gguf_qtype]
-        return self.rows * (self.cols // per) * bb
+        return self.gguf_rows * (self.gguf_cols // per) * bb
 
 
 class HipSparseMoEMLP(nn.Module):
@@ -126,20 +148,30 @@ class HipSparseMoEMLP(nn.Module):
             router = load_float_tensor(gguf_file, f"{prefix}.ffn_gate_inp.weight", device)
             self.register_buffer("router_weight", router, persistent=False)
             self.router_bias: Optional[torch.Tensor] = None
-            self.gate_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate_exps.weight", device, True)
-            self.up_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_up_exps.weight", device, True)
-            self.down_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_exps.weight", device, True)
+            # an intermediate size that is not a multiple of 256 is zero-padded (padded_inter)
+            self.inter, self.inter_padded = padded_inter(gguf_file, f"{prefix}.ffn_down_exps.weight")
+            i_out = self.inter_padded
+            self.gate_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate_exps.weight", device, True, rows_out=i_out)
+            self.up_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_up_exps.weight", device, True, rows_out=i_out)
+            self.down_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_exps.weight", device, True,
+                                           cols_out=i_out)
             self.shared_gate = self.shared_up = self.shared_down = None
             self.shared_inp_gate: Optional[torch.Tensor] = None
             if f"{prefix}.ffn_gate_shexp.weight" in gguf_file.tensors:
-                self.shared_gate = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate_shexp.weight", device, False)
-                self.shared_up = _ExpertTensor(gguf_file, f"{prefix}.ffn_up_shexp.weight", device, False)
-                self.shared_down = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_shexp.weight", device, False)
+                _, s_out = padded_inter(gguf_file, f"{prefix}.ffn_down_shexp.weight")
+                self.shared_gate = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate_shexp.weight", device, False,
+                                                 rows_out=s_out)
+                self.shared_up = _ExpertTensor(gguf_file, f"{prefix}.ffn_up_shexp.weight", device, False,
+                                               rows_out=s_out)
+                self.shared_down = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_shexp.weight", device, False,
+                                                 cols_out=s_out)
                 gname = f"{prefix}.ffn_gate_inp_shexp.weight"
                 if gname in gguf_file.tensors:
                     self.shared_inp_gate = load_float_tensor(gguf_file, gname, device).reshape(-1).contiguous()
             torch.cuda.current_stream(device).synchronize()  # uploads done before host buffers go away
         self.hidden = int(self.router_weight.shape[1])
+        if self.gate_exps.cols != self.gate_exps.gguf_cols:
+            raise ValueError(f"{prefix}: hidden size {self.gate_exps.gguf_cols} is not a multiple of 256")
         if self.router_weight.shape[0] != self.n_experts:
             raise ValueError(f"router has {self.router_weight.shape[0]} rows, config says {self.n_experts} experts")
         self._ws = WorkspacePool(device, zeroed=True)

@@ -54,18 +54,38 @@ def weight_stride(qtype: int, rows: int, cols: int) -> int:
     return int(n)
 
 
-def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int) -> torch.Tensor:
+def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int,
+             rows_out: Optional[int] = None, cols_out: Optional[int] = None) -> torch.Tensor:
     """GGUF bytes on the device -> pgmoe device layout (uint8 [n_mats * stride]) of format
-    device_qtype(qtype)."""
+    device_qtype(qtype), of [rows_out, cols_out] matrices (default [rows, cols]) whose extra
+    rows and columns are exact zeros (pgmoe_relayout_weights_padded)."""
     dev = _need_cuda(raw)
-    stride = weight_stride(qtype, rows, cols)
+    ro = rows if rows_out is None else rows_out
+    co = cols if cols_out is None else cols_out
+    stride = weight_stride(qtype, ro, co)
     per, bb = GGUF_BLOCK[qtype]
     if raw.numel() != n_mats * rows * (cols // per) * bb:
         raise ValueError("raw byte count does not match the tensor shape")
     dst = torch.empty(n_mats * stride, dtype=torch.uint8, device=dev)
-    check(lib().pgmoe_relayout_weights(qtype, raw.data_ptr(), n_mats, rows, cols, dst.data_ptr(), _stream(dev)),
-          "pgmoe_relayout_weights")
+    if (ro, co) == (rows, cols):
+        check(lib().pgmoe_relayout_weights(qtype, raw.data_ptr(), n_mats, rows, cols, dst.data_ptr(),
+                                           _stream(dev)), "pgmoe_relayout_weights")
+    else:
+        check(lib().pgmoe_relayout_weights_padded(qtype, raw.data_ptr(), n_mats, rows, cols, ro, co, dst.data_ptr(),
+                                                  _stream(dev)), "pgmoe_relayout_weights_padded")
     return dst
+
+
+def padded_width(qtype: int, cols: int) -> int:
+    """The device width of a GGUF matrix with `cols` input features: cols itself when it is a
+    multiple of 256; for the 32-weight formats (Q8_0, Q5_0, Q4_0, Q4_1) any multiple of 32 is
+    padded up to one of 256 with zero blocks; -1 when the kernels cannot take it."""
+    if cols % 256 == 0:
+        return cols
+    per, _ = GGUF_BLOCK.get(qtype, (256, 0))
+    if per == 32 and cols % 32 == 0:
+        return (cols + 255) // 256 * 256
+    return -1
 
 
 def scale_plane(qtype: int, buf: torch.Tensor, n_mats: int, rows: int, cols: int) -> Optional[torch.Tensor]:

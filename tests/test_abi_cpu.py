@@ -176,6 +176,15 @@ def test_stage_validation_errors():
     q6 = _lib.Weights(14, 100, 256, 1, 0x2000, 0)
     assert L.pgmoe_expert_gateup(good, q6, 0x1000, 1, 1, 1, 1, 1, 1, 1, 0, 0x2000, None) == -2
     assert L.pgmoe_relayout_weights(12, 0x1000, 1, 4, 256, 0x2010, None) == -1
+    # zero-padded relayout: [rows, cols] GGUF matrices into [rows_out, cols_out] device ones
+    pad = L.pgmoe_relayout_weights_padded
+    assert pad(12, 0x1000, 1, 4, 1408, 4, 1536, 0x2000, None) == -2  # K-quant columns are not padded
+    assert pad(8, 0x1000, 1, 4, 1400, 4, 1536, 0x2000, None) == -2  # not whole 32-weight blocks
+    assert pad(8, 0x1000, 1, 4, 1408, 4, 1408, 0x2000, None) == -2  # device width not a multiple of 256
+    assert pad(8, 0x1000, 1, 5, 1408, 4, 1536, 0x2000, None) == -1  # rows > rows_out
+    assert pad(8, 0x1000, 1, 4, 1792, 4, 1536, 0x2000, None) == -1  # cols > cols_out
+    assert pad(8, 0x1000, 1, 4, 1408, 4, 1536, 0x2010, None) == -1  # misaligned dst
+    assert pad(8, None, 1, 4, 1408, 4, 1536, 0x2000, None) == -1
     assert L.pgmoe_combine(0x1000, 0x2000, 3, 0, 16, None, None, 0x3000, None) == -1
 
 
@@ -278,3 +287,14 @@ def test_noalloc_and_routing_argument_checks():
     assert L.pgmoe_moe_routing(lay, 4, 0x1008, n, 0x2000, 0x3000, 0x4000, 0x5000, None) == -1
     st = ctypes.c_int32()
     assert L.pgmoe_moe_status(lay, 0x1000, 16, ctypes.byref(st), 0, None) == -3
+
+
+def test_padded_widths():
+    """The device width of a GGUF matrix: its own when a multiple of 256; the 32-weight
+    formats (Q8_0, Q5_0, Q4_0, Q4_1) pad whole 32-weight blocks up to one; -1 otherwise."""
+    from pgmoe import ops
+    for qt in (8, 6, 2, 3):
+        assert ops.padded_width(qt, 1408) == 1536 and ops.padded_width(qt, 96) == 256
+        assert ops.padded_width(qt, 2048) == 2048 and ops.padded_width(qt, 1400) == -1
+    for qt in (12, 13, 14):
+        assert ops.padded_width(qt, 1408) == -1 and ops.padded_width(qt, 2048) == 2048

@@ -176,7 +176,9 @@ def test_embed_lookup_and_linear_replay_from_a_captured_graph(dev):
 
 def test_unsupported_widths_and_formats(dev):
     from pgmoe import GGUFQuantLinear
-    with pytest.raises(NotImplementedError):
-        GGUFQuantLinear("w8", 96, 4, Q8_0, raw=np.zeros(4 * 3 * 34, np.uint8), device=dev)
+    with pytest.raises(NotImplementedError):  # K-quants: a multiple of 256 (32-weight formats are padded)
+        GGUFQuantLinear("w4", 320, 4, Q4_K, raw=np.zeros(4 * 144, np.uint8), device=dev)
+    with pytest.raises(NotImplementedError):  # 32-weight formats: whole blocks
+        GGUFQuantLinear("w8", 80, 4, Q8_0, raw=np.zeros(4 * 3 * 34, np.uint8), device=dev)
     with pytest.raises(NotImplementedError):
         GGUFQuantLinear("w8", 256, 4, 7, raw=np.zeros(4 * 8 * 24, np.uint8), device=dev)  # Q5_1
