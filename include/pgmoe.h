@@ -67,6 +67,8 @@ extern "C" {
 #define PGMOE_E_WORKSPACE (-3)   /* workspace too small */
 #define PGMOE_E_HIP (-4)         /* HIP runtime error (launch or query) */
 
+#define PGMOE_F16 1   /* fp16 weights (GGUF F16; BF16 / F32 tensors rounded to fp16 on the host, as the
+                         reference's fp16 expert mode loads them, quant_kernels.py:1962-1964) */
 #define PGMOE_Q4_0 2  /* source format only: relaid out as PGMOE_Q4_1 with m = -8d (exact values) */
 #define PGMOE_Q4_1 3
 #define PGMOE_Q5_0 6  /* source format only: relaid out as PGMOE_Q8_0 (exact values) */
@@ -83,9 +85,10 @@ extern "C" {
 #define PGMOE_ACT_GELU_TANH 1
 
 typedef struct pgmoe_weights {
-    int32_t qtype;      /* PGMOE_Q4_1 / PGMOE_Q4_K / PGMOE_Q5_K / PGMOE_Q6_K / PGMOE_Q8_0 */
+    int32_t qtype;      /* PGMOE_Q4_1 / PGMOE_Q4_K / PGMOE_Q5_K / PGMOE_Q6_K / PGMOE_Q8_0 / PGMOE_F16 */
     int32_t n_rows;     /* N: output features per matrix */
-    int32_t n_cols;     /* K: input features (multiple of 256 for K-quants, 64 for Q8_0) */
+    int32_t n_cols;     /* K: input features, a multiple of 256 (pgmoe_relayout_weights_padded pads the
+                           32-weight formats' rows to one) */
     int32_t n_mats;     /* experts (1 for a shared expert) */
     const void* base;   /* device layout described above, 16-B aligned */
     int64_t mat_stride; /* bytes between consecutive matrices */

@@ -28,8 +28,27 @@ _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib: Optional[ctypes.CDLL] = None
 
 Q4_0, Q4_1, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 3, 6, 8, 12, 13, 14
+F32, F16, BF16 = 0, 1, 30
 BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18),
-         Q4_1: (32, 20), Q5_0: (32, 22)}
+         Q4_1: (32, 20), Q5_0: (32, 22), F16: (1, 2)}
+
+
+def fp16_expert_bytes(qtype: int, raw: np.ndarray) -> np.ndarray:
+    """The fp16 bytes of an F32 / F16 / BF16 expert tensor as the reference's fp16 expert
+    mode holds it (load_float_tensor(..., dtype=torch.float16), quant_kernels.py:1962-1964
+    and :1097-1110): F16 as stored, F32 and BF16 (widened exactly to fp32) rounded to fp16
+    to nearest even."""
+    raw = np.ascontiguousarray(raw).view(np.uint8)
+    if qtype == F16:
+        return raw.copy()
+    if qtype == F32:
+        f = raw.view(np.float32)
+    elif qtype == BF16:
+        f = (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        raise ValueError(f"qtype {qtype} is not a float type")
+    with np.errstate(over="ignore"):  # beyond fp16's range: inf, as torch's conversion gives
+        return f.astype(np.float16).view(np.uint8)
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -198,7 +217,10 @@ class OracleLayer:
             info = gguf.tensors[name]
             shp = info.shape
             n, k = (shp[1], shp[2]) if mats else (shp[0], shp[1])
-            return (int(info.qtype), int(n), int(k), np.ascontiguousarray(gguf.get_tensor_bytes(name)))
+            raw = np.ascontiguousarray(gguf.get_tensor_bytes(name))
+            if int(info.qtype) in (F32, F16, BF16):  # fp16 expert mode
+                return (F16, int(n), int(k), fp16_expert_bytes(int(info.qtype), raw))
+            return (int(info.qtype), int(n), int(k), raw)
 
         kw = {}
         if f"{p}.ffn_gate_shexp.weight" in gguf.tensors:

@@ -14,7 +14,9 @@
  *                        qh bit adds exactly 16*d*sc at its element, and the numpy
  *                        restatement of the reference's Q5_K repack (torch_port);
  *                        Q4_1: equals Q4_0 when m = -8d, closed form on exact
- *                        values, and the restated W4 repack of Q4_0 / Q4_1
+ *                        values, and the restated W4 repack of Q4_0 / Q4_1;
+ *                        F16 (the fp16 expert mode): numpy's IEEE binary16
+ *                        conversion of every bit pattern
  *   or_router_logits     textbook dot product (checked against float64 numpy to
  *                        fp32 rounding), fixed reduction order mirrored by the
  *                        GPU router kernel bit for bit
@@ -28,6 +30,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#define QT_F16 1  /* fp16 weights: the reference's fp16 expert mode (quant_kernels.py:1962-1964) */
 #define QT_Q4_0 2
 #define QT_Q4_1 3
 #define QT_Q5_0 6
@@ -221,6 +224,7 @@ int or_block_geometry(int qtype, int* per_block, int* block_bytes) {
     case QT_Q5_K: *per_block = 256; *block_bytes = 176; return 0;
     case QT_Q6_K: *per_block = 256; *block_bytes = 210; return 0;
     case QT_Q8_0: *per_block = 32; *block_bytes = 34; return 0;
+    case QT_F16: *per_block = 1; *block_bytes = 2; return 0;
     default: return -1;
     }
 }
@@ -239,6 +243,7 @@ int or_dequant_rows(int qtype, int conv, const uint8_t* blocks, int64_t rows, in
         else if (qtype == QT_Q4_0) decode_q4_0_block(b, o);
         else if (qtype == QT_Q4_1) decode_q4_1_block(b, o);
         else if (qtype == QT_Q5_0) decode_q5_0_block(b, o);
+        else if (qtype == QT_F16) o[0] = or_half_to_float(rd16(b));
         else decode_q8_0_block(b, o);
     }
     return 0;

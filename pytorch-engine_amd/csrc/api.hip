@@ -41,10 +41,10 @@ int check_launch(const char* what) {
 int check_weights(const pgmoe_weights* w, const char* what, Mats* out) {
     if (!w) return fail(PGMOE_E_INVALID, "%s: NULL weights", what);
     if (w->qtype != PGMOE_Q4_1 && w->qtype != PGMOE_Q4_K && w->qtype != PGMOE_Q5_K && w->qtype != PGMOE_Q6_K &&
-        w->qtype != PGMOE_Q8_0)
+        w->qtype != PGMOE_Q8_0 && w->qtype != PGMOE_F16)
         return fail(PGMOE_E_UNSUPPORTED,
-                    "%s: qtype %d not supported (Q4_1=3, Q4_K=12, Q5_K=13, Q6_K=14, Q8_0=8; Q4_0 weights are relaid "
-                    "out as Q4_1, Q5_0 as Q8_0)", what,
+                    "%s: qtype %d not supported (F16=1, Q4_1=3, Q4_K=12, Q5_K=13, Q6_K=14, Q8_0=8; Q4_0 weights are "
+                    "relaid out as Q4_1, Q5_0 as Q8_0)", what,
                     w->qtype);
     if (w->n_rows <= 0 || w->n_cols <= 0 || w->n_mats <= 0)
         return fail(PGMOE_E_INVALID, "%s: bad shape [%d, %d, %d]", what, w->n_mats, w->n_rows, w->n_cols);

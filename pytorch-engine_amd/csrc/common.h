@@ -273,6 +273,7 @@ __device__ __forceinline__ void router_tile(const uint16_t* __restrict__ x, cons
 //                 base + ng*nb*13*1024 + ((rg*nb + b)*64 + r)*2
 //   Q8_0 (CH 17): c0..c15 = qs of the 8 Q8_0 blocks in order (16 weights per chunk);
 //                 c16 = their 8 fp16 d
+//   F16  (CH 32): c = weights 8c .. 8c+7 of the super-block (fp16)
 // N is padded to a multiple of 64 (padding rows are zero and never stored to outputs).
 template <int QT> struct Tile;
 template <> struct Tile<PGMOE_Q4_1> { static constexpr int CH = 10; };
@@ -280,6 +281,7 @@ template <> struct Tile<PGMOE_Q4_K> { static constexpr int CH = 9; };
 template <> struct Tile<PGMOE_Q5_K> { static constexpr int CH = 11; };
 template <> struct Tile<PGMOE_Q6_K> { static constexpr int CH = 13; };
 template <> struct Tile<PGMOE_Q8_0> { static constexpr int CH = 17; };
+template <> struct Tile<PGMOE_F16> { static constexpr int CH = 32; };
 
 __host__ __device__ inline int row_groups(int N) { return (N + 63) >> 6; }
 

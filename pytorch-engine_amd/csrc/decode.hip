@@ -10,6 +10,7 @@ namespace pgmoe {
     case PGMOE_Q5_K: return call(PGMOE_Q5_K);                        \
     case PGMOE_Q6_K: return call(PGMOE_Q6_K);                        \
     case PGMOE_Q8_0: return call(PGMOE_Q8_0);                        \
+    case PGMOE_F16: return call(PGMOE_F16);                          \
     }                                                                \
     return fail(PGMOE_E_UNSUPPORTED, what ": qtype %d", qt);
 
@@ -21,6 +22,7 @@ bool decode_isum_rows8(int qtype, int M) {
     case PGMOE_Q5_K: return gu_rows8<PGMOE_Q5_K>();
     case PGMOE_Q6_K: return gu_rows8<PGMOE_Q6_K>();
     case PGMOE_Q8_0: return gu_rows8<PGMOE_Q8_0>();
+    case PGMOE_F16: return gu_rows8<PGMOE_F16>();
     }
     return false;
 }

@@ -54,6 +54,7 @@ template <> struct Raw<PGMOE_Q4_K> { uint4 c[9]; };
 template <> struct Raw<PGMOE_Q5_K> { uint4 c[11]; };
 template <> struct Raw<PGMOE_Q6_K> { uint4 c[13]; uint32_t d; };
 template <> struct Raw<PGMOE_Q8_0> { uint4 c[17]; };
+template <> struct Raw<PGMOE_F16> { uint4 c[32]; };
 
 template <int QT>
 __device__ __forceinline__ void load_raw(Raw<QT>& r, const uint8_t* mat, int N, int nb, int row, int b) {
@@ -81,6 +82,7 @@ __device__ __forceinline__ void load_raw(Raw<QT>& r, const uint8_t* mat, int N, 
 //         bytes 8h .. 8h+7 and d
 //   Q8_0: Q8_0 blocks 2p, 2p+1 = elements 64p .. 64p+63 -> chunks 4p .. 4p+3 and the two
 //         fp16 scales at chunk 16 bytes 4p .. 4p+3
+//   F16:  elements 64p .. 64p+63 -> chunks 8p .. 8p+7 (the weights themselves)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -92,6 +94,7 @@ template <> struct Qtr<PGMOE_Q4_K> { u32x4 h, a, b; };
 template <> struct Qtr<PGMOE_Q5_K> { u32x4 h, a, b; u32x2 hb; };
 template <> struct Qtr<PGMOE_Q6_K> { u32x4 la, lb, qh; u32x2 sc; uint32_t d; };
 template <> struct Qtr<PGMOE_Q8_0> { u32x4 c0, c1, c2, c3; uint32_t d; };
+template <> struct Qtr<PGMOE_F16> { u32x4 c[8]; };
 
 template <int QT>
 __device__ __forceinline__ void load_qtr(Qtr<QT>& q, const uint8_t* mat, int N, int nb, int row, int j, int p) {
@@ -114,6 +117,9 @@ __device__ __forceinline__ void load_qtr(Qtr<QT>& q, const uint8_t* mat, int N, 
         q.sc = *(const u32x2*)(t + 12 * 1024 + 8 * h);
         const int64_t dpl = (int64_t)row_groups(N) * nb * 13 * 1024;
         q.d = *(const uint16_t*)(mat + dpl + (((int64_t)(row >> 6) * nb + j) * 64 + (row & 63)) * 2);
+    } else if constexpr (QT == PGMOE_F16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q.c[i] = ldq(t + (8 * p + i) * 1024);
     } else {
         q.c0 = ldq(t + (4 * p) * 1024);
         q.c1 = ldq(t + (4 * p + 1) * 1024);
@@ -302,6 +308,30 @@ __device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_Q8_0>& q, int j, int p, c
     }
 }
 
+// F16: the weights enter v_dot2_f32_f16 as they are (no scale, no offset sums).
+template <int TM>
+__device__ __forceinline__ void gu_qtr(const Qtr<PGMOE_F16>& q, int j, int p, const uint16_t* xs, int xrs,
+                                       const float* xss, int srs, uint32_t toks, int cnt, float* acc) {
+    const int xo = xpos_h(256 * j + 64 * p);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        if (t < cnt) {
+            const uint16_t* xr = xs + tok_of(toks, t) * xrs + xo;
+            float T = 0.f;
+#pragma unroll
+            for (int h16 = 0; h16 < 4; ++h16) {  // elements 16 h16 .. +16: chunks 2 h16, 2 h16 + 1
+                uint32_t xv[8];
+                ldx16(xr + 16 * h16, xv);
+                const u32x4 a = q.c[2 * h16], b = q.c[2 * h16 + 1];
+                const uint32_t w8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) T = dot2(w8[k], xv[k], T);
+            }
+            acc[t] += T;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- down quarter (fp32 x)
 // part[c] = inter_(p0+c) . w(row, quarter p of super-block j) for c < cnt <= TM; xs: the
 // staged fp32 inter rows from pair p0 on (row stride xrs floats), iss: their 16-element
@@ -428,6 +458,25 @@ __device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_Q8_0>& q, int j, int p, c
     }
 }
 
+template <int TM>
+__device__ __forceinline__ void dn_qtr(const Qtr<PGMOE_F16>& q, int j, int p, const float* xs, int xrs,
+                                       const float* iss, int srs, int cnt, float* part) {
+#pragma unroll
+    for (int h16 = 0; h16 < 4; ++h16) {  // elements 16 h16 .. +16 of the quarter
+        const u32x4 a = q.c[2 * h16], b = q.c[2 * h16 + 1];
+        const uint32_t w8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        float qf[16];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            qf[2 * k] = lo_half(w8[k]);
+            qf[2 * k + 1] = hi_half(w8[k]);
+        }
+        const int xo = xpos_f(256 * j + 64 * p + 16 * h16);
+#pragma unroll
+        for (int c = 0; c < TM; ++c)
+            if (c < cnt) part[c] += dotf<16>(qf, xs + c * xrs + xo);
+    }
+}
 
 // ---------------------------------------------------------------- down (fp32)
 // acc[t] += inter_t . w(row, block); x = global fp32 rows (stride K, wave-uniform)
@@ -1036,9 +1085,10 @@ __global__ __launch_bounds__(1024) void dec_gu_kernel(const uint8_t* __restrict_
     // With 4+ tokens (blocks then take several slots) the first pass of the next slot is
     // loaded before this slot's epilogue, so its weights stream during the reduction and
     // the inter stores; with fewer the registers this takes cost more than it saves (and
-    // Q5_K's fifth-bit words leave no room for it within 128 registers).  With 4+ tokens
+    // Q5_K's fifth-bit words, or F16's 32-register quarters, leave no room for it within 128
+    // registers).  With 4+ tokens
     // the wave index is made scalar, which frees registers.
-    constexpr bool pf = TM >= 4 && QT != PGMOE_Q5_K && (MODE == kRoute || MODE == kDispatch);
+    constexpr bool pf = TM >= 4 && QT != PGMOE_Q5_K && QT != PGMOE_F16 && (MODE == kRoute || MODE == kDispatch);
     const int tid = threadIdx.x, lane = tid & 63, nth = blockDim.x, nw = nth >> 6;
     const int w = TM >= 4 ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int M = dp.M;

@@ -5,8 +5,8 @@
 // two waves of its column), the down block 8 waves (two per SIMD; each all 256 rows x 32
 // columns, every B column decoded once), as 4 x 2 or 8 x 1 v_mfma_f32_32x32x16_f16 tiles
 // per wave (other layouts are build-time choices: CT column tiles, WM waves along M).  The K loop steps one 64-weight unit at a time
-// through a ring of three LDS stages filled by direct HBM -> LDS copies three units
-// ahead: the fp16 activation rows (16-byte slots XOR-swizzled by row) and the raw GGUF
+// through a ring of three LDS stages (two for fp16 weights) filled by direct HBM -> LDS
+// copies three (two) units ahead: the fp16 activation rows (16-byte slots XOR-swizzled by row) and the raw GGUF
 // bytes of the 256 weight rows (whole 1 KB chunks of the 64-row tile layout, with their
 // scale chunks).  Each wave decodes its own B fragments from the raw bytes in registers
 // (w = a * code + c in fp32, one rounding to fp16) one k16 group ahead of the MFMAs that
@@ -56,34 +56,43 @@ typedef float gf4 __attribute__((ext_vector_type(4)));
 //         ((u % 4) >> 1, u & 1)); scales: chunk u of the scale plane (a of its four
 //         16-weight sub-blocks)
 //   Q8_0: chunks 4c .. 4c + 3 (the qs of Q8_0 blocks 2c, 2c + 1); scales: tile chunk 16
+//   F16:  chunks 8c .. 8c + 7 (the weights); no scales
 // Group g of the unit (k = 16g .. 16g + 15) reads, for the 8 weights 8h .. 8h + 7 of a lane
 // half h, bytes 8h .. 8h + 7 of one staged chunk:
 //   Q4_K: chunk g & 1, nibble g >> 1;  Q5_K: the same, and fifth-bit word g >> 1 (bits
 //   4(g & 1) + 2h, + 1);  Q6_K: ql chunk g & 1 (nibble g >> 1) and the qh
-//   chunk (bits 2g, 2g + 1);  Q8_0: chunk g.
+//   chunk (bits 2g, 2g + 1);  Q8_0: chunk g;  F16: all 16 bytes of chunk 2g + h.
 template <int QT> struct GStage;
 template <> struct GStage<PGMOE_Q4_K> {
     static constexpr int CH = 2, HC = -1;  // HC: tile chunk of the scales (-1: scale plane)
+    static constexpr int NS = 3;           // LDS stages of the ring
     __device__ static __forceinline__ int chunk(int u, int cc) { return 1 + 2 * (u & 3) + cc; }
 };
 template <> struct GStage<PGMOE_Q4_1> {
-    static constexpr int CH = 2, HC = -1;
+    static constexpr int CH = 2, HC = -1, NS = 3;
     __device__ static __forceinline__ int chunk(int u, int cc) { return 2 + 2 * (u & 3) + cc; }
 };
 template <> struct GStage<PGMOE_Q5_K> {
-    static constexpr int CH = 3, HC = -1;
+    static constexpr int CH = 3, HC = -1, NS = 3;
     __device__ static __forceinline__ int chunk(int u, int cc) { return cc < 2 ? 1 + 2 * (u & 3) + cc : 9 + ((u & 3) >> 1); }
 };
 template <> struct GStage<PGMOE_Q6_K> {
-    static constexpr int CH = 3, HC = -1;
+    static constexpr int CH = 3, HC = -1, NS = 3;
     __device__ static __forceinline__ int chunk(int u, int cc) {
         const int h = (u & 3) >> 1, half = u & 1;
         return cc == 0 ? 4 * h + half : cc == 1 ? 4 * h + 2 + half : 8 + 2 * h + half;
     }
 };
 template <> struct GStage<PGMOE_Q8_0> {
-    static constexpr int CH = 4, HC = 16;
+    static constexpr int CH = 4, HC = 16, NS = 3;
     __device__ static __forceinline__ int chunk(int u, int cc) { return 4 * (u & 3) + cc; }
+};
+// F16: the unit's 64 weights of a row are 8 chunks, 4 row groups x 8 KB a stage beside the
+// 32 KB of A, so the ring has two stages (three would exceed the 160 KB of LDS); the
+// "scale" slot repeats chunk 0 and is never read.
+template <> struct GStage<PGMOE_F16> {
+    static constexpr int CH = 8, HC = 0, NS = 2;
+    __device__ static __forceinline__ int chunk(int u, int cc) { return 8 * (u & 3) + cc; }
 };
 
 // LDS stage: A [256 rows][128 bytes] (16-byte slot s of row r holds k chunk s ^ key(r),
@@ -278,6 +287,17 @@ template <> struct GCol<PGMOE_Q8_0> {
     }
 };
 
+template <> struct GCol<PGMOE_F16> {
+    gu4 c[4];  // group g: weights 16g + 8h .. +8 of the unit (chunk 2g + h)
+    __device__ __forceinline__ void fetch(const uint8_t* B, int bg, int rig, int h, int u) {
+        const uint8_t* base = B + bg * 9 * 1024 + rig * 16;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) c[g] = *(const gu4*)(base + (2 * g + h) * 1024);
+    }
+    __device__ __forceinline__ void prep(int u) {}
+    __device__ __forceinline__ gh8 group(int g) const { return __builtin_bit_cast(gh8, c[g]); }
+};
+
 // ---------------------------------------------------------------- tile mapping
 // Block id -> (M tile, N tile).  Each M tile's N tiles form `runs` runs of consecutive N
 // tiles; run u = (M tile u / runs, run u % runs) goes to XCD u % 8 (blocks go to the 8 XCDs
@@ -324,11 +344,11 @@ __device__ __forceinline__ int gemm_tile_expert(const int32_t* tile_off, int E, 
 // next few VALU / LDS instructions issue).  The one barrier of a unit comes before its last
 // group's MFMAs: every read of the unit's stage has then been issued and waited for, so the
 // barrier both publishes the next unit's stage (its copies waited for by vm_wait) and
-// frees this one, which takes the copies of unit u + 3.  The next unit's scales and its
+// frees this one, which takes the copies of unit u + NS.  The next unit's scales and its
 // first group are decoded under the last group's MFMAs.
 // AC = A copies per wave per unit (the copies of empty 32-row slices are skipped when the
 // wave copies whole slices), BQ = B copies: a wave has AC + BQ copies in flight per unit.
-template <int QT, int NI, int CT, int RS, int AC, int BQ, int STAGE, class CopyF>
+template <int QT, int NI, int CT, int RS, int AC, int BQ, int STAGE, class CopyF, int NS = GStage<QT>::NS>
 __device__ __forceinline__ void gemm_loop(const uint8_t* smem, int units, const int (&bg)[CT], const int (&rig)[CT],
                                           int wm, int lane, gf16 (&acc)[RS][CT], CopyF& copy_unit) {
     constexpr int VM = AC + BQ;
@@ -355,25 +375,24 @@ __device__ __forceinline__ void gemm_loop(const uint8_t* smem, int units, const 
         for (int j = 0; j < CT; ++j) b[j] = col[j].group(g);
     };
     const std::integral_constant<int, AC> ac;
-    copy_unit(ac, 0, 0);
-    copy_unit(ac, 1, 1);
-    copy_unit(ac, 2, 2);
-    vm_wait<2 * VM>();  // this wave's copies of unit 0 landed
-    lds_barrier();      // and every wave's
+#pragma unroll
+    for (int s = 0; s < NS; ++s) copy_unit(ac, s, s);
+    vm_wait<(NS - 1) * VM>();  // this wave's copies of unit 0 landed
+    lds_barrier();             // and every wave's
     if constexpr (NI > 0) {
         cols(smem, 0);
         frag(smem, 0, af[0], bf[0]);
     }
     for (int u = 0, st = 0; u < units; ++u) {
-        const int sn = st == 2 ? 0 : st + 1;
+        const int sn = st == NS - 1 ? 0 : st + 1;
         const uint8_t* S = smem + st * STAGE;
         const uint8_t* Sn = smem + sn * STAGE;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             if (g == 3) {
-                vm_wait<VM>();
+                vm_wait<(NS - 2) * VM>();
                 lds_barrier();
-                copy_unit(ac, u + 3, st);
+                copy_unit(ac, u + NS, st);
             }
             if constexpr (NI > 0) {
                 if (g < 3) {
@@ -414,7 +433,7 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
     static_assert(!GATEUP || CT >= 2, "gate/up: each wave holds gate and matching up columns");
     static_assert(L::AQ * WN * WM == 32, "the waves' A copies cover the 32 row octets once");
     constexpr int CH = L::CH;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * L::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[GStage<QT>::NS * L::STAGE];
     __shared__ int rowsrc[kGM];
     __shared__ float rowscale[kGM];  // down: rs[p] * topk_w[perm[p]] of every tile row
     int mt, nt;
@@ -541,8 +560,8 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
         rigj[j] = c & 63;
     }
 
-    // ---- pipeline: three stages; unit u + 3 is copied into unit u's stage once every wave
-    // is done with it (see gemm_loop).  The loop is instantiated per NI (a whole copy each)
+    // ---- pipeline: NS stages (three; two for F16); unit u + NS is copied into unit u's
+    // stage once every wave is done with it (see gemm_loop).  The loop is instantiated per NI (a whole copy each)
     // so the register allocation of one copy never has to merge the others'.
     PG_MARK(GATEUP ? 4 : 5, 1);
     // With 4 waves along N (CT = 2), wave (wm, wn) copies row octet wn of each of its 32-row
@@ -774,7 +793,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = g.n_mats;
-    if (g.qtype != PGMOE_Q8_0 && (!g.scales || !u.scales))
+    if (g.qtype != PGMOE_Q8_0 && g.qtype != PGMOE_F16 && (!g.scales || !u.scales))
         return fail(PGMOE_E_INVALID, "gemm gate/up: K-quant weights need their scale plane (pgmoe_build_scale_plane)");
     const int nnt = div_up(g.N, kGN / 2);
     const GemmSplit sp = raw ? gemm_split(P, E, g.N, g.K, true) : GemmSplit{1, g.K >> 8};
@@ -789,6 +808,7 @@ int launch_gemm_gateup(const Mats& g, const Mats& u, const uint16_t* x, int M, i
     case PGMOE_Q5_K: PG_GU(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: PG_GU(PGMOE_Q6_K); break;
     case PGMOE_Q8_0: PG_GU(PGMOE_Q8_0); break;
+    case PGMOE_F16: PG_GU(PGMOE_F16); break;
     default: return fail(PGMOE_E_UNSUPPORTED, "gemm gate/up: qtype %d", g.qtype);
     }
 #undef PG_GU
@@ -803,7 +823,7 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     const int64_t P = (int64_t)M * topk;
     if (P == 0) return PGMOE_OK;
     const int E = d.n_mats;
-    if (d.qtype != PGMOE_Q8_0 && !d.scales)
+    if (d.qtype != PGMOE_Q8_0 && d.qtype != PGMOE_F16 && !d.scales)
         return fail(PGMOE_E_INVALID, "gemm down: K-quant weights need their scale plane (pgmoe_build_scale_plane)");
     const int nnt = div_up(d.N, kGN);
     const GemmSplit sp = raw ? gemm_split(P, E, d.N, d.K, false) : GemmSplit{1, d.K >> 8};
@@ -818,6 +838,7 @@ int launch_gemm_down(const Mats& d, const uint16_t* a16, const float* rs, int M,
     case PGMOE_Q5_K: PG_DN(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: PG_DN(PGMOE_Q6_K); break;
     case PGMOE_Q8_0: PG_DN(PGMOE_Q8_0); break;
+    case PGMOE_F16: PG_DN(PGMOE_F16); break;
     default: return fail(PGMOE_E_UNSUPPORTED, "gemm down: qtype %d", d.qtype);
     }
 #undef PG_DN

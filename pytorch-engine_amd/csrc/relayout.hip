@@ -14,6 +14,7 @@ template <> struct Gguf<PGMOE_Q8_0> { static constexpr int per = 32, bytes = 34;
 template <> struct Gguf<PGMOE_Q4_0> { static constexpr int per = 32, bytes = 18; };
 template <> struct Gguf<PGMOE_Q4_1> { static constexpr int per = 32, bytes = 20; };
 template <> struct Gguf<PGMOE_Q5_0> { static constexpr int per = 32, bytes = 22; };
+template <> struct Gguf<PGMOE_F16> { static constexpr int per = 256, bytes = 512; };  // a row's 256 fp16
 
 __device__ __forceinline__ void copy16(uint8_t* d, const uint8_t* s) {
 #pragma unroll
@@ -79,7 +80,7 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
             d[2] = (uint8_t)(w[i] >> 16);
             d[3] = (uint8_t)(w[i] >> 24);
         }
-    } else if (QT == PGMOE_Q4_K || QT == PGMOE_Q6_K) {
+    } else if (QT == PGMOE_Q4_K || QT == PGMOE_Q6_K || QT == PGMOE_F16) {
         for (int c = 0; c < CH; ++c) {
             if (real) copy16(t + c * 1024, s + 16 * c);
             else zero16(t + c * 1024);
@@ -206,7 +207,7 @@ __global__ void scale_plane_kernel(const uint8_t* __restrict__ src, int64_t n_ma
 int64_t scale_plane_bytes(int qtype, int64_t rows, int64_t cols) {
     if (qtype == PGMOE_Q4_0 || qtype == PGMOE_Q5_0 || layout_bytes(qtype, rows, cols) < 0)
         return -1;  // Q4_0 / Q5_0: source formats (their device layouts are Q4_1 / Q8_0)
-    if (qtype == PGMOE_Q8_0) return 0;
+    if (qtype == PGMOE_Q8_0 || qtype == PGMOE_F16) return 0;  // scales in the tiles, or none
     return (int64_t)row_groups((int)rows) * (cols / 256) * 4 * 1024;
 }
 
@@ -251,6 +252,7 @@ int64_t layout_bytes(int qtype, int64_t rows, int64_t cols) {
     case PGMOE_Q4_1: return ng * nb * 10 * 1024;
     case PGMOE_Q8_0:
     case PGMOE_Q5_0: return ng * nb * 17 * 1024;  // Q5_0 is stored as Q8_0
+    case PGMOE_F16: return ng * nb * 32 * 1024;
     default: return -1;
     }
 }
@@ -287,6 +289,9 @@ int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows,
         break;
     case PGMOE_Q5_0:
         PG_LAUNCH(relayout_kernel<PGMOE_Q5_0>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
+        break;
+    case PGMOE_F16:
+        PG_LAUNCH(relayout_kernel<PGMOE_F16>, grid, dim3(threads), 0, st, src, n_mats, Ns, kbs, N, nb, dst, dst_stride);
         break;
     default:
         return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d", qtype);

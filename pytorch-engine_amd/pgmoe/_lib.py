@@ -15,8 +15,10 @@ LIB_PATH = os.path.join(_HERE, "libpgmoe.so")
 ABI_VERSION = 4
 
 Q4_0, Q4_1, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 3, 6, 8, 12, 13, 14
+F32, F16, BF16 = 0, 1, 30
+FLOAT_QTYPES = (F32, F16, BF16)  # expert tensors held as fp16 (PGMOE_F16), as the reference's fp16 mode
 # GGUF expert formats with a HIP path; Q4_0 is relaid out as Q4_1, Q5_0 as Q8_0 (their values exactly)
-SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0)
+SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0) + FLOAT_QTYPES
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

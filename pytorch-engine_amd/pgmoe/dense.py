@@ -45,6 +45,7 @@ class HipDenseMLP(nn.Module):
             self.gate_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_gate.weight", device, False, rows_out=i_out)
             self.up_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_up.weight", device, False, rows_out=i_out)
             self.down_proj = _ExpertTensor(gguf_file, f"{prefix}.ffn_down.weight", device, False, cols_out=i_out)
+            self.down_proj.check_fp16_down(f"{prefix}.ffn_down.weight")
             torch.cuda.current_stream(device).synchronize()  # uploads done before host buffers go away
         g, u, d = self.gate_proj, self.up_proj, self.down_proj
         if g.cols != g.gguf_cols:

@@ -25,7 +25,8 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from ._lib import ACT_GELU_TANH, ACT_SILU, STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES, Layer, Weights, check, lib
+from ._lib import (ACT_GELU_TANH, ACT_SILU, F16, FLOAT_QTYPES, STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES, Layer, Weights,
+                   check, lib)
 from .workspace import StatusWord, WorkspacePool
 
 _F32, _F16, _BF16 = 0, 1, 30
@@ -100,24 +101,37 @@ class _ExpertTensor:
         if self.gguf_qtype not in SUPPORTED_QTYPES:
             raise NotImplementedError(
                 f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
-                "has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, Q8_0, Q4_1, and Q4_0 / Q5_0 relaid out as Q4_1 / "
-                "Q8_0)")
+                "has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, Q8_0, Q4_1, Q4_0 / Q5_0 relaid out as Q4_1 / "
+                "Q8_0, and F16 / BF16 / F32 held as fp16)")
         width = ops.padded_width(self.gguf_qtype, self.gguf_cols)
         if width < 0 or (cols_out is not None and cols_out < width):
             raise ValueError(f"{name}: {self.gguf_cols} input features is not a multiple of 256"
                              + (" (nor of 32 for a 32-weight format)" if width < 0 else ""))
         self.rows = self.gguf_rows if rows_out is None else int(rows_out)
         self.cols = width if cols_out is None else int(cols_out)
-        raw_np = gguf_file.get_tensor_bytes(name)
-        raw = torch.from_numpy(np.asarray(raw_np)).to(device)  # H2D copy of the GGUF bytes
-        self.buf = ops.relayout(self.gguf_qtype, raw, self.n_mats, self.gguf_rows, self.gguf_cols, self.rows,
-                                self.cols)
+        if self.gguf_qtype in FLOAT_QTYPES:
+            # fp16 weights, rounded from F32 / BF16 as the reference's fp16 expert mode loads
+            # them (load_float_tensor(..., dtype=torch.float16), quant_kernels.py:1962-1964)
+            w16 = load_float_tensor(gguf_file, name, device).to(torch.float16).contiguous()
+            raw = w16.view(torch.uint8).reshape(-1)
+            src_qtype = F16
+        else:
+            raw = torch.from_numpy(np.asarray(gguf_file.get_tensor_bytes(name))).to(device)  # H2D copy
+            src_qtype = self.gguf_qtype
+        self.buf = ops.relayout(src_qtype, raw, self.n_mats, self.gguf_rows, self.gguf_cols, self.rows, self.cols)
         del raw
         # K-quants: the sub-block scales decoded once for the prefill MFMA products
         self.plane = ops.scale_plane(self.qtype, self.buf, self.n_mats, self.rows, self.cols)
 
     def weights(self) -> Weights:
         return ops.make_weights(self.qtype, self.buf, self.n_mats, self.rows, self.cols, self.plane)
+
+    def check_fp16_down(self, name: str) -> None:
+        """fp16 down projections run on the fused decode down + combine, whose rows hold at
+        most 32 super-blocks (8192 inputs); a longer fp16 row would fail at the first decode
+        forward, so it is refused at load."""
+        if self.qtype == F16 and self.cols > 8192:
+            raise NotImplementedError(f"{name}: fp16 down projection of {self.cols} inputs (at most 8192)")
 
     @property
     def gguf_bytes_per_mat(self) -> int:
@@ -155,6 +169,7 @@ class HipSparseMoEMLP(nn.Module):
             self.up_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_up_exps.weight", device, True, rows_out=i_out)
             self.down_exps = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_exps.weight", device, True,
                                            cols_out=i_out)
+            self.down_exps.check_fp16_down(f"{prefix}.ffn_down_exps.weight")
             self.shared_gate = self.shared_up = self.shared_down = None
             self.shared_inp_gate: Optional[torch.Tensor] = None
             if f"{prefix}.ffn_gate_shexp.weight" in gguf_file.tensors:
@@ -165,6 +180,7 @@ class HipSparseMoEMLP(nn.Module):
                                                rows_out=s_out)
                 self.shared_down = _ExpertTensor(gguf_file, f"{prefix}.ffn_down_shexp.weight", device, False,
                                                  cols_out=s_out)
+                self.shared_down.check_fp16_down(f"{prefix}.ffn_down_shexp.weight")
                 gname = f"{prefix}.ffn_gate_inp_shexp.weight"
                 if gname in gguf_file.tensors:
                     self.shared_inp_gate = load_float_tensor(gguf_file, gname, device).reshape(-1).contiguous()

@@ -12,17 +12,19 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import Q4_0, Q4_1, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, Weights, check, lib
+from ._lib import BF16, F16, F32, FLOAT_QTYPES, Q4_0, Q4_1, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, Weights, check, lib
 
+# (weights, bytes) of a GGUF block; the float types as 256-weight runs of a row
 GGUF_BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18),
-              Q4_1: (32, 20), Q5_0: (32, 22)}
+              Q4_1: (32, 20), Q5_0: (32, 22), F16: (256, 512), BF16: (256, 512), F32: (256, 1024)}
 
 
 def device_qtype(qtype: int) -> int:
     """Format of the device layout the relayout of GGUF `qtype` produces: Q4_0 becomes Q4_1
     (d * (q - 8) = d q + m with m = -8d), Q5_0 becomes Q8_0 (d * (q - 16) is the Q8_0 value
-    d * qs with qs = q - 16), the others keep theirs."""
-    return Q4_1 if qtype == Q4_0 else Q8_0 if qtype == Q5_0 else qtype
+    d * qs with qs = q - 16), F32 and BF16 become F16 (rounded to fp16 on the host, as the
+    reference's fp16 expert mode loads them), the others keep theirs."""
+    return Q4_1 if qtype == Q4_0 else Q8_0 if qtype == Q5_0 else F16 if qtype in FLOAT_QTYPES else qtype
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:

@@ -76,7 +76,18 @@ CONFIGS: Dict[str, LayerSpec] = {
 
 def random_blocks(rng: np.random.Generator, qtype: int, rows: int, cols: int,
                   scale: float = 1.0) -> np.ndarray:
-    """Raw GGUF bytes for a [rows, cols] matrix of random blocks (uint8, flat)."""
+    """Raw GGUF bytes for a [rows, cols] matrix of random blocks (uint8, flat).  Float types
+    (F32, F16, BF16): weights N(0, 1) * 0.02 * scale, in the type's own encoding (BF16: the
+    fp32 value rounded to nearest even)."""
+    if qtype in (GGMLType.F32, GGMLType.F16, GGMLType.BF16):
+        f = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02 * scale)).astype(np.float32)
+        if qtype == GGMLType.F32:
+            return f.view(np.uint8)
+        if qtype == GGMLType.F16:
+            return f.astype(np.float16).view(np.uint8)
+        u = f.view(np.uint32).astype(np.uint64)
+        b16 = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)  # round to nearest even
+        return b16.view(np.uint8)
     if qtype in (Q4_K, Q5_K):
         nb = rows * (cols // 256)
         raw = rng.integers(0, 256, size=(nb, 144 if qtype == Q4_K else 176), dtype=np.uint8)

@@ -298,3 +298,15 @@ def test_padded_widths():
         assert ops.padded_width(qt, 2048) == 2048 and ops.padded_width(qt, 1400) == -1
     for qt in (12, 13, 14):
         assert ops.padded_width(qt, 1408) == -1 and ops.padded_width(qt, 2048) == 2048
+
+
+def test_f16_weight_sizes_and_planes():
+    """fp16 expert matrices (PGMOE_F16 = 1): 64-row tiles of 32 chunks a 256-weight
+    super-block, no scale plane; widths must be multiples of 256."""
+    L = _lib.lib()
+    for rows, cols in ((64, 256), (100, 2048), (768, 2048)):
+        assert L.pgmoe_weight_bytes(1, rows, cols) == ((rows + 63) // 64) * (cols // 256) * 32 * 1024
+        assert L.pgmoe_scale_plane_bytes(1, rows, cols) == 0
+    assert L.pgmoe_weight_bytes(1, 64, 320) == -1
+    from pgmoe import ops
+    assert ops.device_qtype(0) == ops.device_qtype(30) == ops.device_qtype(1) == 1

@@ -240,3 +240,27 @@ def test_gelu_tanh_matches_torch_and_kernel_identity():
     # a plausible slip (the exact erf GELU) is caught by the same check
     exact = F.gelu(torch.from_numpy(g)).numpy()
     assert not np.allclose(exact, ref, rtol=1e-6, atol=1e-9)
+
+
+def test_fp16_expert_mode_values():
+    """F16 expert tensors decode to their IEEE binary16 values (every bit pattern); F32 and
+    BF16 ones are held as the fp16 rounding (to nearest even) of their exact fp32 values,
+    as the reference's fp16 expert mode loads them (quant_kernels.py:1962-1964)."""
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    d = oracle.dequant(oracle.F16, allh.view(np.uint8), 256, 256).reshape(-1)
+    ref = allh.view(np.float16).astype(np.float32)
+    assert np.all(np.isnan(ref) | (d.view(np.uint32) == ref.view(np.uint32)))
+    # BF16 (bit patterns of finite values) -> fp32 exactly (bits << 16) -> fp16 RNE
+    b = np.arange(0, 65536, 13, dtype=np.uint32).astype(np.uint16)
+    f32 = (b.astype(np.uint32) << 16).view(np.float32)
+    fin = np.isfinite(f32)
+    with np.errstate(over="ignore"):
+        want = f32[fin].astype(np.float16).view(np.uint16)
+    got = oracle.fp16_expert_bytes(oracle.BF16, b[fin].view(np.uint8)).view(np.uint16)
+    assert np.array_equal(got, want)
+    # F32: halfway cases round to even (1 + 2^-11 -> 1, 1 + 3 * 2^-11 -> 1 + 2^-9)
+    x = np.float32([1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, -2.5, 65504.0])
+    h = oracle.fp16_expert_bytes(oracle.F32, x.view(np.uint8)).view(np.float16)
+    assert h.tolist() == [1.0, 1.0 + 2.0 ** -9, -2.5, 65504.0]
+    assert np.array_equal(oracle.fp16_expert_bytes(oracle.F16, x.astype(np.float16).view(np.uint8)),
+                          x.astype(np.float16).view(np.uint8))
