@@ -684,23 +684,33 @@ __device__ __forceinline__ void copy_words(T* dst, const T* __restrict__ src, in
 }
 
 // A threshold with exactly K of the distinct keys of one token at or above it (lane l
-// holds experts l + 64r): a radix descent on the 41 key bits that stops as soon as the
-// candidate has exactly K keys at or above it (with random logits after about a dozen
-// steps), else ends on the K-th largest key itself.  The threshold and the counts are
-// wave-uniform (scalar registers); each step is one vector compare per key word and a
-// popcount of the resulting lane mask.
+// holds experts l + 64r): a radix descent on the 41 key bits.  The threshold and the
+// counts are wave-uniform (scalar registers); each step is one vector compare per key
+// word and a popcount of the resulting lane mask.  Steps go in unrolled groups of 8 with
+// one exit test a group: the descent may stop once a candidate with exactly K keys at or
+// above it was taken (with random logits after about a dozen steps), and a step past that
+// point keeps such a threshold (a higher candidate with K keys is as good), so the test
+// need not follow every step.  Measured in a one-wave microbenchmark (MI355X, E = 128,
+// K = 8): 1,550-1,680 cycles with a test and a branch after every step, 644 with the
+// groups of 8 (a step's VALU -> SALU hand-off and branch cost ~130 cycles).
 template <int RE>
 __device__ __forceinline__ uint64_t kth_key_radix(const uint64_t (&key)[RE], int K) {
     uint64_t thr = 0;
-    for (int b = 40; b >= 0; --b) {
-        const uint64_t cand = thr | (1ull << b);
-        int cnt = 0;
+    int last = 0;  // keys at or above the last candidate taken
+    for (int b0 = 40; b0 >= 0; b0 -= 8) {
 #pragma unroll
-        for (int r = 0; r < RE; ++r) cnt += __popcll(__ballot(key[r] >= cand));
-        if (cnt >= K) {
-            thr = cand;
-            if (cnt == K) break;
+        for (int i = 0; i < 8; ++i) {
+            const int b = b0 - i;
+            if (b >= 0) {
+                const uint64_t cand = thr | (1ull << b);
+                int cnt = 0;
+#pragma unroll
+                for (int r = 0; r < RE; ++r) cnt += __popcll(__ballot(key[r] >= cand));
+                thr = cnt >= K ? cand : thr;
+                last = cnt >= K ? cnt : last;
+            }
         }
+        if (last == K) break;
     }
     return thr;
 }
