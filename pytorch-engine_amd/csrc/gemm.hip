@@ -630,6 +630,51 @@ __global__ __launch_bounds__(64 * (WM * 8 / CT)) void gemm_kernel(
                     }
             }
         }
+    } else if constexpr (WM == 1) {
+        // Down, staged: the ring's LDS is free once every wave has left the loop.  Each half
+        // of the tile's rows (128) goes through LDS as scaled fp32 rows of 256 columns and
+        // then out as whole rows, 16 bytes a lane: a quarter of the store instructions of the
+        // accumulator layout (4 bytes a lane, two 128-byte row pieces an instruction), which
+        // is what bounds a CU's epilogue (the tile's 256 KB of partial rows).  Rows r and
+        // r + 4 of a staged half are 4 LD floats apart: LD = 264 puts them on the two
+        // halves of the LDS banks.
+        constexpr int LD = kGN + 8;
+        static_assert(128 * LD * 4 <= GStage<QT>::NS * L::STAGE, "a staged half fits the ring's LDS");
+        float* stg = reinterpret_cast<float*>(smem);
+        const int col = nt * kGN + 4 * lane;  // the lane's four columns of a row
+        const bool vec = (N & 3) == 0;        // rows start 16-byte aligned
+        __syncthreads();                      // every wave's copies landed and reads of the ring done
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            if (128 * half >= mrows) break;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (128 * half + 32 * i >= mrows) break;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int rr = 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                    const float sc = rowscale[128 * half + rr];
+#pragma unroll
+                    for (int j = 0; j < CT; ++j)
+                        stg[rr * LD + 32 * CT * wn + 32 * j + (lane & 31)] = acc[4 * half + i][j][v] * sc;
+                }
+            }
+            __syncthreads();
+            for (int rr = wave; rr < 128; rr += NW) {
+                const int r = 128 * half + rr;
+                if (r >= mrows) break;
+                const gf4 val = *reinterpret_cast<const gf4*>(&stg[rr * LD + 4 * lane]);
+                float* dst = out + (int64_t)(m0 + r) * N + col;
+                if (vec && col + 3 < N) {
+                    __builtin_nontemporal_store(val, reinterpret_cast<gf4*>(dst));
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (col + c < N) dst[c] = val[c];
+                }
+            }
+            __syncthreads();  // the next half overwrites the staging
+        }
     } else {
         const int c0 = nt * kGN + 32 * CT * wn + (lane & 31);
 #pragma unroll
