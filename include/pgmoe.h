@@ -130,7 +130,8 @@ const char* pgmoe_last_error(void);
  * converted to, Q5_0: the Q8_0 layout); -1 if unsupported. */
 int64_t pgmoe_weight_bytes(int32_t qtype, int64_t rows, int64_t cols);
 
-/* GGUF blocks (device, n_mats matrices back to back) -> device layout.
+/* GGUF blocks (device, n_mats matrices back to back; src 16-byte aligned, dst 256-byte
+ * aligned) -> device layout.
  * Load-time replacement of repack_gguf_to_w4a16 / repack_gguf_to_w8a16
  * (quant_kernels.py:854-1036), keeping the GGUF bits instead of re-quantising.  A Q4_0
  * source is written in the Q4_1 layout with the same d and codes and m = -8d (exact for

@@ -300,6 +300,7 @@ int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64
         return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld columns", qtype, (long long)cols);
     if (!src || !dst || n_mats < 1 || rows < 1) return fail(PGMOE_E_INVALID, "relayout: bad arguments");
     if ((uintptr_t)dst & 255) return fail(PGMOE_E_INVALID, "relayout: dst must be 256-byte aligned");
+    if ((uintptr_t)src & 15) return fail(PGMOE_E_INVALID, "relayout: src must be 16-byte aligned");
     return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, rows, cols, (uint8_t*)dst,
                            pgmoe_weight_bytes(qtype, rows, cols), as_stream(stream));
 }
@@ -317,6 +318,7 @@ int pgmoe_relayout_weights_padded(int32_t qtype, const void* src, int64_t n_mats
         return fail(PGMOE_E_UNSUPPORTED, "relayout: qtype %d with %lld source columns padded to %lld", qtype,
                     (long long)cols, (long long)cols_out);
     if ((uintptr_t)dst & 255) return fail(PGMOE_E_INVALID, "relayout: dst must be 256-byte aligned");
+    if ((uintptr_t)src & 15) return fail(PGMOE_E_INVALID, "relayout: src must be 16-byte aligned");
     return launch_relayout(qtype, (const uint8_t*)src, n_mats, rows, cols, rows_out, cols_out, (uint8_t*)dst,
                            pgmoe_weight_bytes(qtype, rows_out, cols_out), as_stream(stream));
 }

@@ -16,18 +16,39 @@ template <> struct Gguf<PGMOE_Q4_1> { static constexpr int per = 32, bytes = 20;
 template <> struct Gguf<PGMOE_Q5_0> { static constexpr int per = 32, bytes = 22; };
 template <> struct Gguf<PGMOE_F16> { static constexpr int per = 256, bytes = 512; };  // a row's 256 fp16
 
+// 16 bytes from s (A-byte aligned: 16 for blocks of a multiple of 16 bytes, 2 for Q6_K's
+// 210 and Q8_0's 34) to d (16-byte aligned): one 16-byte store, the loads as wide as A allows.
+template <int A>
 __device__ __forceinline__ void copy16(uint8_t* d, const uint8_t* s) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) d[i] = s[i];
+    uint4 v;
+    if constexpr (A >= 16) {
+        v = *(const uint4*)s;
+    } else {
+        static_assert(A == 2, "2- or 16-byte aligned sources");
+        const uint16_t* p = (const uint16_t*)s;
+        v = make_uint4(p[0] | ((uint32_t)p[1] << 16), p[2] | ((uint32_t)p[3] << 16), p[4] | ((uint32_t)p[5] << 16),
+                       p[6] | ((uint32_t)p[7] << 16));
+    }
+    *(uint4*)d = v;
 }
 
-__device__ __forceinline__ void zero16(uint8_t* d) {
+__device__ __forceinline__ void zero16(uint8_t* d) { *(uint4*)d = make_uint4(0, 0, 0, 0); }
+
+// 16 bytes built in registers to d (16-byte aligned), one store.
+__device__ __forceinline__ void store16(uint8_t* d, const uint8_t (&v)[16]) {
+    uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) d[i] = 0;
+    for (int k = 0; k < 4; ++k)
+        w[k] = v[4 * k] | ((uint32_t)v[4 * k + 1] << 8) | ((uint32_t)v[4 * k + 2] << 16) | ((uint32_t)v[4 * k + 3] << 24);
+    *(uint4*)d = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // One thread per (matrix, padded row, 256-weight block) of the device matrix [N, 256 nb]
-// (rows padded to 64).  The source matrix is [Ns, kbs blocks of the format] (Ns <= N;
+// (rows padded to 64).  Thread order: the row fastest, so the 64 threads of a wave fill one
+// 64-row tile and each 16-byte chunk slot of the tile is one contiguous 1 KB store; for
+// Q4_K the block fastest instead (a wave reads 64 consecutive 144-byte blocks of a row),
+// which measured faster for its small blocks (113 MB: 93 against 108 us; Q8_0 624 MB 595 ->
+// 487 us, Q6_K 165 MB 187 -> 176 us, F16 50 MB 56 -> 42 us with the row fastest).  The source matrix is [Ns, kbs blocks of the format] (Ns <= N;
 // K-quants: kbs = nb; 32-weight formats: kbs <= 8 nb, any count): rows past Ns and 32-weight
 // blocks past kbs are written as zeros, whose value is exactly 0 in every format.  Q5_0
 // sources are written as Q8_0 tiles: d * (q - 16) (5-bit q) is the Q8_0 value d * qs with
@@ -43,7 +64,16 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
     if (gid >= per_mat * n_mats) return;
     const int64_t mat = gid / per_mat;
     const int64_t rem = gid % per_mat;
-    const int row = (int)(rem / nb), b = (int)(rem % nb);
+    int row, b;
+    if constexpr (QT == PGMOE_Q4_K) {
+        row = (int)(rem / nb);
+        b = (int)(rem % nb);
+    } else {
+        const int tb = (int)(rem >> 6);  // tile rg * nb + b
+        const int rg0 = tb / nb;
+        b = tb - rg0 * nb;
+        row = rg0 * 64 + (int)(rem & 63);
+    }
     const int rg = row >> 6, r = row & 63;
     constexpr int DT = QT == PGMOE_Q5_0 ? PGMOE_Q8_0 : QT == PGMOE_Q4_0 ? PGMOE_Q4_1 : QT;  // device layout
     constexpr int CH = Tile<DT>::CH;
@@ -59,7 +89,7 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
     auto realj = [&](int j) { return real && (PER == 256 || 8 * b + j < kbs); };
     if (QT == PGMOE_Q5_K) {  // GGUF: d, dmin, scales (0-15), qh (16-47), qs (48-175)
         for (int c = 0; c < 9; ++c) {
-            if (real) copy16(t + c * 1024, s + (c == 0 ? 0 : 48 + 16 * (c - 1)));
+            if (real) copy16<16>(t + c * 1024, s + (c == 0 ? 0 : 48 + 16 * (c - 1)));
             else zero16(t + c * 1024);
         }
         // fifth bits regrouped: word (p, tt) bit 8(l & 3) + (l >> 2) = bit 2p + tt of qh[l]
@@ -82,7 +112,7 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
         }
     } else if (QT == PGMOE_Q4_K || QT == PGMOE_Q6_K || QT == PGMOE_F16) {
         for (int c = 0; c < CH; ++c) {
-            if (real) copy16(t + c * 1024, s + 16 * c);
+            if (real) copy16<QT == PGMOE_Q6_K ? 2 : 16>(t + c * 1024, s + 16 * c);
             else zero16(t + c * 1024);
         }
         if (QT == PGMOE_Q6_K) {
@@ -104,8 +134,8 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
                 lo[l] = (uint8_t)(int8_t)(((q & 15) | (int)(((qh >> l) & 1) << 4)) - 16);
                 hi[l] = (uint8_t)(int8_t)(((q >> 4) | (int)(((qh >> (16 + l)) & 1) << 4)) - 16);
             }
-            copy16(t + (2 * j) * 1024, lo);
-            copy16(t + (2 * j + 1) * 1024, hi);
+            store16(t + (2 * j) * 1024, lo);
+            store16(t + (2 * j + 1) * 1024, hi);
             t[16 * 1024 + 2 * j] = rj ? bj[0] : 0;
             t[16 * 1024 + 2 * j + 1] = rj ? bj[1] : 0;
         }
@@ -138,14 +168,14 @@ __global__ void relayout_kernel(const uint8_t* __restrict__ src, int64_t n_mats,
                 const int k = 16 * c + i, J = k >> 5, l = k & 31;
                 v[i] = (uint8_t)(code(2 * J, l) | (code(2 * J + 1, l) << 4));
             }
-            copy16(t + (2 + c) * 1024, v);
+            store16(t + (2 + c) * 1024, v);
         }
     } else {  // Q8_0: eight 34-byte blocks per 256 weights
         for (int j = 0; j < 8; ++j) {
             const uint8_t* bj = s + 34 * j;
             if (realj(j)) {
-                copy16(t + (2 * j) * 1024, bj + 2);
-                copy16(t + (2 * j + 1) * 1024, bj + 18);
+                copy16<2>(t + (2 * j) * 1024, bj + 2);
+                copy16<2>(t + (2 * j + 1) * 1024, bj + 18);
                 t[16 * 1024 + 2 * j] = bj[0];
                 t[16 * 1024 + 2 * j + 1] = bj[1];
             } else {

@@ -68,6 +68,8 @@ def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int,
     per, bb = GGUF_BLOCK[qtype]
     if raw.numel() != n_mats * rows * (cols // per) * bb:
         raise ValueError("raw byte count does not match the tensor shape")
+    if raw.data_ptr() % 16:  # the kernels read 16-byte aligned sources
+        raw = raw.clone()
     dst = torch.empty(n_mats * stride, dtype=torch.uint8, device=dev)
     if (ro, co) == (rows, cols):
         check(lib().pgmoe_relayout_weights(qtype, raw.data_ptr(), n_mats, rows, cols, dst.data_ptr(),

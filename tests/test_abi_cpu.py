@@ -176,6 +176,7 @@ def test_stage_validation_errors():
     q6 = _lib.Weights(14, 100, 256, 1, 0x2000, 0)
     assert L.pgmoe_expert_gateup(good, q6, 0x1000, 1, 1, 1, 1, 1, 1, 1, 0, 0x2000, None) == -2
     assert L.pgmoe_relayout_weights(12, 0x1000, 1, 4, 256, 0x2010, None) == -1
+    assert L.pgmoe_relayout_weights(12, 0x1008, 1, 4, 256, 0x2000, None) == -1  # misaligned src
     # zero-padded relayout: [rows, cols] GGUF matrices into [rows_out, cols_out] device ones
     pad = L.pgmoe_relayout_weights_padded
     assert pad(12, 0x1000, 1, 4, 1408, 4, 1536, 0x2000, None) == -2  # K-quant columns are not padded
@@ -184,6 +185,7 @@ def test_stage_validation_errors():
     assert pad(8, 0x1000, 1, 5, 1408, 4, 1536, 0x2000, None) == -1  # rows > rows_out
     assert pad(8, 0x1000, 1, 4, 1792, 4, 1536, 0x2000, None) == -1  # cols > cols_out
     assert pad(8, 0x1000, 1, 4, 1408, 4, 1536, 0x2010, None) == -1  # misaligned dst
+    assert pad(8, 0x1002, 1, 4, 1408, 4, 1536, 0x2000, None) == -1  # misaligned src
     assert pad(8, None, 1, 4, 1408, 4, 1536, 0x2000, None) == -1
     assert L.pgmoe_combine(0x1000, 0x2000, 3, 0, 16, None, None, 0x3000, None) == -1
 
