@@ -94,6 +94,24 @@ def test_relayout_bytes(dev, qtype, rows, cols, n_mats):
         assert np.array_equal(got[m * stride:m * stride + mb], ref[m * stride:m * stride + mb])
 
 
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, Q8_0])
+def test_relayout_unaligned_source(dev, qtype):
+    """A source view that does not start 16-byte aligned (the kernels read 16-byte aligned
+    rows): ops.relayout copies it first, and the bytes match the aligned source's."""
+    from pgmoe import ops
+    rows, cols = 70, 512
+    raw = random_blocks(np.random.default_rng(7), qtype, rows, cols)
+    base = torch.zeros(raw.size + 2, dtype=torch.uint8, device=dev)
+    base[2:] = torch.from_numpy(raw).to(dev)
+    view = base[2:]
+    assert view.data_ptr() % 16 != 0
+    got = ops.relayout(qtype, view, 1, rows, cols).cpu().numpy()
+    ref = ops.relayout(qtype, torch.from_numpy(raw).to(dev), 1, rows, cols).cpu().numpy()
+    ng, nb = (rows + 63) // 64, cols // 256  # the tiles (padding past them is unspecified)
+    mb = ng * nb * {Q4_K: 9 * 1024, Q6_K: 13 * 1024 + 128, Q8_0: 17 * 1024}[qtype]
+    assert np.array_equal(got[:mb], ref[:mb])
+
+
 @pytest.mark.parametrize("M,H,E,K,bias", [(1, 2048, 128, 8, False), (8, 2048, 128, 8, False),
                                           (333, 2048, 128, 8, True), (4096, 2048, 128, 8, True),
                                           (5, 1024, 8, 2, False), (64, 3584, 64, 8, False),
