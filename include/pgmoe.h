@@ -76,6 +76,13 @@ extern "C" {
 #define PGMOE_Q4_K 12
 #define PGMOE_Q5_K 13
 #define PGMOE_Q6_K 14
+/* Source formats only, re-quantised at load by pgmoe_requant_w4 into PGMOE_Q4_1 blocks with
+ * the values the reference's W4 repack gives them: */
+#define PGMOE_Q2_K 10
+#define PGMOE_Q3_K 11
+#define PGMOE_IQ4_NL 20
+#define PGMOE_IQ4_XS 23
+#define PGMOE_MXFP4 39
 
 /* Gate activation of the gated FFNs: act(gate) * up (exec_fused_act_mul_rowscale,
  * quant_kernels.py:1423-1475).  SiLU g / (1 + e^-g); GELU with the tanh approximation
@@ -151,6 +158,17 @@ int pgmoe_relayout_weights(int32_t qtype, const void* src, int64_t n_mats, int64
  * reference accepts these widths in its W8 / W4 repack (quant_kernels.py:958, :1966-1967). */
 int pgmoe_relayout_weights_padded(int32_t qtype, const void* src, int64_t n_mats, int64_t rows, int64_t cols,
                                   int64_t rows_out, int64_t cols_out, void* dst, void* stream);
+
+/* The reference's W4 re-quantisation of Q2_K / Q3_K / IQ4_NL / IQ4_XS / MXFP4 tensors
+ * (repack_gguf_to_w4a16's gguf-py branch, quant_kernels.py:906-942, taken for these formats
+ * at :1966-1967 and :1812): each 32-weight group of the n_rows x cols matrix at src (GGUF
+ * blocks, device, rows back to back) is decoded exactly and quantised again to 4 bits,
+ * scale = (max - min) / 15 in fp32, codes round((w - min) / scale) clipped to 0..15, and
+ * written to dst as Q4_1 GGUF blocks (n_rows * cols / 32 blocks of 20 bytes, 4-byte aligned
+ * dst): d = fp16(scale), m = fp16(min).  Those hold exactly the reference's W4 values
+ * (q * scale16 - fp16(-min)); pass dst to pgmoe_relayout_weights(_padded) as PGMOE_Q4_1.
+ * cols: a multiple of 32 (IQ4_NL, MXFP4) or 256 (the others).  Load time only. */
+int pgmoe_requant_w4(int32_t qtype, const void* src, int64_t n_rows, int64_t cols, void* dst, void* stream);
 
 /* Bytes of one matrix's scale plane (0 for Q8_0, which has none; -1 if unsupported).  No
  * counterpart in the reference: it sizes the buffer of pgmoe_build_scale_plane. */

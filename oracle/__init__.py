@@ -33,6 +33,9 @@ BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q
          Q4_1: (32, 20), Q5_0: (32, 22), F16: (1, 2)}
 
 
+from .requant import REQUANT_BLOCK, requant_w4  # noqa: E402  (the reference's W4 re-quantisation)
+
+
 def fp16_expert_bytes(qtype: int, raw: np.ndarray) -> np.ndarray:
     """The fp16 bytes of an F32 / F16 / BF16 expert tensor as the reference's fp16 expert
     mode holds it (load_float_tensor(..., dtype=torch.float16), quant_kernels.py:1962-1964
@@ -220,6 +223,9 @@ class OracleLayer:
             raw = np.ascontiguousarray(gguf.get_tensor_bytes(name))
             if int(info.qtype) in (F32, F16, BF16):  # fp16 expert mode
                 return (F16, int(n), int(k), fp16_expert_bytes(int(info.qtype), raw))
+            if int(info.qtype) in REQUANT_BLOCK:  # the reference's W4 re-quantisation, as Q4_1 blocks
+                rows = int(np.prod([int(v) for v in shp[:-1]]))
+                return (Q4_1, int(n), int(k), requant_w4(int(info.qtype), raw, rows, int(k)))
             return (int(info.qtype), int(n), int(k), raw)
 
         kw = {}

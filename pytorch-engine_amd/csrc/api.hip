@@ -323,6 +323,20 @@ int pgmoe_relayout_weights_padded(int32_t qtype, const void* src, int64_t n_mats
                            pgmoe_weight_bytes(qtype, rows_out, cols_out), as_stream(stream));
 }
 
+int pgmoe_requant_w4(int32_t qtype, const void* src, int64_t n_rows, int64_t cols, void* dst, void* stream) {
+    int per = 0, bytes = 0;
+    if (requant_w4_block(qtype, &per, &bytes))
+        return fail(PGMOE_E_UNSUPPORTED, "requant: qtype %d is not re-quantised (Q2_K=10, Q3_K=11, IQ4_NL=20, "
+                    "IQ4_XS=23, MXFP4=39)", qtype);
+    if (!src || !dst || n_rows < 1 || cols < 1 || cols > (1 << 30))
+        return fail(PGMOE_E_INVALID, "requant: bad arguments");
+    if (cols % per) return fail(PGMOE_E_UNSUPPORTED, "requant: %lld columns are not whole %d-weight blocks",
+                                (long long)cols, per);
+    if ((uintptr_t)dst & 3) return fail(PGMOE_E_INVALID, "requant: dst must be 4-byte aligned");
+    if (n_rows > (((int64_t)1 << 38) / (cols / 32))) return fail(PGMOE_E_INVALID, "requant: matrix too large");
+    return launch_requant_w4(qtype, (const uint8_t*)src, n_rows, (int)cols, (uint8_t*)dst, as_stream(stream));
+}
+
 int64_t pgmoe_scale_plane_bytes(int32_t qtype, int64_t rows, int64_t cols) {
     return scale_plane_bytes(qtype, rows, cols);
 }

@@ -71,6 +71,10 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
                    int n_clear = 0);
 // GGUF [n_mats, rows, cols] -> device matrices [rows_out, cols_out] (zero padding past
 // rows / cols; cols_out a multiple of 256, cols == cols_out for K-quants).
+// Q2_K / Q3_K / IQ4_NL / IQ4_XS / MXFP4 -> Q4_1 GGUF blocks with the reference's W4 values
+// (requant.hip); requant_w4_block gives a format's GGUF block (weights, bytes), -1 if none.
+int requant_w4_block(int qtype, int* per, int* bytes);
+int launch_requant_w4(int qtype, const uint8_t* src, int64_t rows, int cols, uint8_t* dst, hipStream_t st);
 int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, int64_t rows_out,
                     int64_t cols_out, uint8_t* dst, int64_t dst_stride, hipStream_t st);
 // Decode expert stages (M <= decode_tokens_max()).

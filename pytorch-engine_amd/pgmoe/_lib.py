@@ -17,8 +17,11 @@ ABI_VERSION = 4
 Q4_0, Q4_1, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 3, 6, 8, 12, 13, 14
 F32, F16, BF16 = 0, 1, 30
 FLOAT_QTYPES = (F32, F16, BF16)  # expert tensors held as fp16 (PGMOE_F16), as the reference's fp16 mode
+Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4 = 10, 11, 20, 23, 39
+# re-quantised at load to Q4_1 blocks with the reference's W4 values (pgmoe_requant_w4)
+REQUANT_W4_QTYPES = (Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4)
 # GGUF expert formats with a HIP path; Q4_0 is relaid out as Q4_1, Q5_0 as Q8_0 (their values exactly)
-SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0) + FLOAT_QTYPES
+SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0) + FLOAT_QTYPES + REQUANT_W4_QTYPES
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -89,6 +92,7 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_weight_bytes.argtypes = [_I32, _I64, _I64]
     L.pgmoe_relayout_weights.argtypes = [_I32, _P, _I64, _I64, _I64, _P, _P]
     L.pgmoe_relayout_weights_padded.argtypes = [_I32, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]
+    L.pgmoe_requant_w4.argtypes = [_I32, _P, _I64, _I64, _P, _P]
     L.pgmoe_scale_plane_bytes.restype = _I64
     L.pgmoe_scale_plane_bytes.argtypes = [_I32, _I64, _I64]
     L.pgmoe_build_scale_plane.argtypes = [_I32, _P, _I64, _I64, _I64, _I64, _P, _P]
@@ -124,7 +128,7 @@ def lib() -> ctypes.CDLL:
                "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_relayout_weights_padded",
                "pgmoe_build_scale_plane",
                "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status", "pgmoe_moe_forward_noalloc",
-               "pgmoe_add_rmsnorm", "pgmoe_linear_forward", "pgmoe_dequant_rows"):
+               "pgmoe_add_rmsnorm", "pgmoe_linear_forward", "pgmoe_dequant_rows", "pgmoe_requant_w4"):
         getattr(L, fn).restype = ctypes.c_int
     ver = L.pgmoe_abi_version()
     if ver != ABI_VERSION:
@@ -147,7 +151,7 @@ EXPORTS = (
     "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane", "pgmoe_dispatch_ws_bytes", "pgmoe_dispatch_ws",
     "pgmoe_dense_workspace_bytes", "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status",
     "pgmoe_moe_forward_noalloc", "pgmoe_add_rmsnorm", "pgmoe_linear_workspace_bytes", "pgmoe_linear_forward",
-    "pgmoe_dequant_rows", "pgmoe_relayout_weights_padded",
+    "pgmoe_dequant_rows", "pgmoe_relayout_weights_padded", "pgmoe_requant_w4",
 )
 
 STATUS_SPIN_TIMEOUT = 1  # PGMOE_STATUS_SPIN_TIMEOUT

@@ -56,11 +56,14 @@ class GGMLType:
     Q5_K = 13
     Q6_K = 14
     Q8_K = 15
+    IQ4_NL = 20
+    IQ4_XS = 23
     BF16 = 30
+    MXFP4 = 39
 
     NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8: "Q8_0",
              9: "Q8_1", 10: "Q2_K", 11: "Q3_K", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K",
-             15: "Q8_K", 30: "BF16"}
+             15: "Q8_K", 20: "IQ4_NL", 23: "IQ4_XS", 30: "BF16", 39: "MXFP4"}
 
 
 # (weights per block, bytes per block) for the types this reader can size.  Values are
@@ -81,6 +84,9 @@ BLOCK_GEOMETRY: Dict[int, Tuple[int, int]] = {
     GGMLType.Q5_K: (256, 176),
     GGMLType.Q6_K: (256, 210),
     GGMLType.Q8_K: (256, 292),
+    GGMLType.IQ4_NL: (32, 18),
+    GGMLType.IQ4_XS: (256, 136),
+    GGMLType.MXFP4: (32, 17),
 }
 
 

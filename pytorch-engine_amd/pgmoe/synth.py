@@ -123,6 +123,32 @@ def random_blocks(rng: np.random.Generator, qtype: int, rows: int, cols: int,
         d = (np.abs(rng.standard_normal(nb)) * (0.01 * scale)).astype(np.float16)
         raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         raw[:, 2:34] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
+    elif qtype in (GGMLType.Q2_K, GGMLType.Q3_K, GGMLType.IQ4_XS):
+        # random bytes; the fp16 d (and Q2_K's dmin) small: Q2_K d |N| * 0.02 scale, dmin
+        # |N| * 0.01 scale; Q3_K d |N| * 0.02 scale; IQ4_XS d |N| * 0.001 scale (its sub-block
+        # scales reach 32 and its levels 127)
+        nbytes = {GGMLType.Q2_K: 84, GGMLType.Q3_K: 110, GGMLType.IQ4_XS: 136}[qtype]
+        nb = rows * (cols // 256)
+        raw = rng.integers(0, 256, size=(nb, nbytes), dtype=np.uint8)
+        dscale = 0.001 if qtype == GGMLType.IQ4_XS else 0.02
+        d = (np.abs(rng.standard_normal(nb)) * (dscale * scale)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+        if qtype == GGMLType.Q2_K:
+            raw[:, 80:82] = d
+            raw[:, 82:84] = (np.abs(rng.standard_normal(nb)) * (0.01 * scale)).astype(np.float16).view(
+                np.uint8).reshape(nb, 2)
+        elif qtype == GGMLType.Q3_K:
+            raw[:, 108:110] = d
+        else:
+            raw[:, 0:2] = d
+    elif qtype == GGMLType.IQ4_NL:  # d = |N| * 0.01 scale (levels up to 127)
+        nb = rows * (cols // 32)
+        raw = rng.integers(0, 256, size=(nb, 18), dtype=np.uint8)
+        raw[:, 0:2] = (np.abs(rng.standard_normal(nb)) * (0.01 * scale)).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    elif qtype == GGMLType.MXFP4:  # exponent byte 118..123: block scales 2^-10 .. 2^-5 (times scale's power of 2)
+        nb = rows * (cols // 32)
+        raw = rng.integers(0, 256, size=(nb, 17), dtype=np.uint8)
+        shift = int(np.round(np.log2(scale))) if scale > 0 else 0
+        raw[:, 0] = np.clip(rng.integers(118, 124, size=nb) + shift, 0, 255).astype(np.uint8)
     else:
         raise ValueError(f"unsupported qtype {qtype}")
     return raw.reshape(-1)

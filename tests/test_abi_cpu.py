@@ -188,6 +188,16 @@ def test_stage_validation_errors():
     assert pad(8, 0x1002, 1, 4, 1408, 4, 1536, 0x2000, None) == -1  # misaligned src
     assert pad(8, None, 1, 4, 1408, 4, 1536, 0x2000, None) == -1
     assert L.pgmoe_combine(0x1000, 0x2000, 3, 0, 16, None, None, 0x3000, None) == -1
+    # load-time W4 re-quantisation of Q2_K / Q3_K / IQ4_NL / IQ4_XS / MXFP4
+    rq = L.pgmoe_requant_w4
+    assert rq(12, 0x1000, 4, 256, 0x2000, None) == -2  # Q4_K is kept as it is
+    assert "not re-quantised" in L.pgmoe_last_error().decode()
+    assert rq(20, 0x1000, 4, 48, 0x2000, None) == -2  # not whole blocks
+    assert rq(23, 0x1000, 4, 224, 0x2000, None) == -2  # IQ4_XS blocks are 256 weights
+    assert rq(39, 0x1000, 4, 64, 0x2002, None) == -1  # dst not 4-byte aligned
+    assert rq(10, None, 4, 256, 0x2000, None) == -1
+    assert rq(11, 0x1000, 0, 256, 0x2000, None) == -1
+    assert rq(20, 0x1000, 1 << 40, 32, 0x2000, None) == -1  # grid beyond its limit
 
 
 def test_module_rejects_cpu_device():
