@@ -83,6 +83,9 @@ extern "C" {
 #define PGMOE_IQ4_NL 20
 #define PGMOE_IQ4_XS 23
 #define PGMOE_MXFP4 39
+/* Source format only, re-quantised at load by pgmoe_requant_w8_f16 into PGMOE_F16 weights
+ * with the values of the reference's W8 repack: */
+#define PGMOE_Q5_1 7
 
 /* Gate activation of the gated FFNs: act(gate) * up (exec_fused_act_mul_rowscale,
  * quant_kernels.py:1423-1475).  SiLU g / (1 + e^-g); GELU with the tanh approximation
@@ -169,6 +172,19 @@ int pgmoe_relayout_weights_padded(int32_t qtype, const void* src, int64_t n_mats
  * (q * scale16 - fp16(-min)); pass dst to pgmoe_relayout_weights(_padded) as PGMOE_Q4_1.
  * cols: a multiple of 32 (IQ4_NL, MXFP4) or 256 (the others).  Load time only. */
 int pgmoe_requant_w4(int32_t qtype, const void* src, int64_t n_rows, int64_t cols, void* dst, void* stream);
+
+/* The reference's W8 re-quantisation of Q5_1 tensors (repack_gguf_to_w8a16's gguf-py
+ * fallback, quant_kernels.py:1005-1025, taken at :1979 and :1822): each 16-weight group of
+ * the n_rows x cols matrix at src (GGUF blocks, device, rows back to back) is decoded
+ * exactly, sc = max|w| / 127 in fp32 (1 for an all-zero group), codes round(w / sc) clipped
+ * to -127..127, and written to dst as fp16 weights [n_rows, cols_out] (16-byte aligned;
+ * columns cols .. cols_out - 1 zero): fp16(fp16(sc) * q), the weight operand the reference's
+ * W8 tensor-core GEMM forms (quant_kernels.py:553-620; its GEMV applies fp16(sc) to the
+ * int8 dot product instead, 2^-12 relative apart at most).  Pass dst to
+ * pgmoe_relayout_weights(_padded) as PGMOE_F16 with cols_out columns.  cols: a multiple of
+ * 32; cols_out >= cols, a multiple of 32.  Load time only. */
+int pgmoe_requant_w8_f16(int32_t qtype, const void* src, int64_t n_rows, int64_t cols, int64_t cols_out, void* dst,
+                         void* stream);
 
 /* Bytes of one matrix's scale plane (0 for Q8_0, which has none; -1 if unsupported).  No
  * counterpart in the reference: it sizes the buffer of pgmoe_build_scale_plane. */

@@ -33,7 +33,7 @@ BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q
          Q4_1: (32, 20), Q5_0: (32, 22), F16: (1, 2)}
 
 
-from .requant import REQUANT_BLOCK, requant_w4  # noqa: E402  (the reference's W4 re-quantisation)
+from .requant import REQUANT_BLOCK, W8_BLOCK, requant_w4, requant_w8_f16  # noqa: E402  (the reference's W4 / W8 re-quantisations)
 
 
 def fp16_expert_bytes(qtype: int, raw: np.ndarray) -> np.ndarray:
@@ -226,6 +226,9 @@ class OracleLayer:
             if int(info.qtype) in REQUANT_BLOCK:  # the reference's W4 re-quantisation, as Q4_1 blocks
                 rows = int(np.prod([int(v) for v in shp[:-1]]))
                 return (Q4_1, int(n), int(k), requant_w4(int(info.qtype), raw, rows, int(k)))
+            if int(info.qtype) in W8_BLOCK:  # the reference's W8 re-quantisation, as fp16 weights
+                rows = int(np.prod([int(v) for v in shp[:-1]]))
+                return (F16, int(n), int(k), requant_w8_f16(int(info.qtype), raw, rows, int(k)))
             return (int(info.qtype), int(n), int(k), raw)
 
         kw = {}

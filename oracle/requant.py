@@ -18,6 +18,10 @@ is stored as +0: numpy's min may keep either zero (it depends on the reduction o
 values d q + m are the same for both.
 ``requant_w4`` restates that on the decoded values; ``ggml_dequant`` restates the decoding.
 
+Q5_1 takes the reference's W8 fallback instead (quant_kernels.py:1005-1025: per 16 weights,
+symmetric int8 at max|w| / 127, fp16 scales); ``requant_w8_f16`` restates it as the fp16
+weights fp16(scale16 * code) that its tensor-core GEMM forms, which this build stores.
+
 gguf-py (llama.cpp's ``gguf`` package; the reference pins no version and it is not
 importable here) decodes these blocks as ggml's ``dequantize_row_*`` (ggml-quants.c) do.
 Its published block definitions, restated per format below, give every value exactly in
@@ -111,6 +115,43 @@ def ggml_dequant(qtype: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarra
     else:
         raise ValueError(f"qtype {qtype} is not re-quantised")
     return np.asarray(y, np.float32).reshape(rows, cols)
+
+
+Q5_1 = 7
+W8_BLOCK = {Q5_1: (32, 24)}
+
+
+def q5_1_dequant(raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """fp32 [rows, cols] of Q5_1 blocks {fp16 d; fp16 m; u32 qh; u8 qs[16]}: d q + m with
+    q = nibble | fifth bit << 4; element j: low nibble of qs[j], bit j of qh; element j + 16:
+    high nibble of qs[j], bit j + 16 (ggml's dequantize_row_q5_1); product and sum rounded
+    separately in fp32."""
+    if cols % 32:
+        raise ValueError(f"{cols} columns are not whole 32-weight blocks")
+    b = np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1, 24)
+    nb = b.shape[0]
+    d = _f16(b[:, 0:2].reshape(nb, 1, 2))
+    m = _f16(b[:, 2:4].reshape(nb, 1, 2))
+    qh = np.ascontiguousarray(b[:, 4:8]).view("<u4").astype(np.uint32)          # [nb, 1]
+    hi = ((qh >> np.arange(32, dtype=np.uint32)) & 1).astype(np.uint8)          # [nb, 32]
+    q = (_nibbles32(b[:, 8:24]) | (hi << 4)).astype(np.float32)
+    return (d * q + m).astype(np.float32).reshape(rows, cols)
+
+
+def requant_w8_f16(qtype: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """The fp16 weights (bytes of [rows, cols]) of the reference's W8 re-quantisation of a Q5_1
+    matrix (repack_gguf_to_w8a16's fallback, quant_kernels.py:1011-1025): per 16 weights
+    sc = max|w| / 127 (1 for an all-zero group), int8 codes clip(round(w / sc), -127, 127),
+    the fp16 scale fp16(sc); each weight fp16(fp16(sc) * code), the operand its tensor-core
+    GEMM forms (``(q_grp * s).to(tl.float16)``, quant_kernels.py:553-620)."""
+    if qtype != Q5_1:
+        raise ValueError(f"qtype {qtype} is not re-quantised to W8")
+    g = q5_1_dequant(raw, rows, cols).reshape(rows, cols // 16, 16)
+    amax = np.max(np.abs(g), axis=-1, keepdims=True)
+    sc = np.where(amax == np.float32(0.0), np.float32(1.0), amax / np.float32(127.0)).astype(np.float32)
+    q = np.clip(np.round(g / sc), -127, 127).astype(np.int8)
+    s16 = sc.astype(np.float16).astype(np.float32)
+    return (q.astype(np.float32) * s16).astype(np.float16).view(np.uint8).reshape(-1)
 
 
 def requant_w4(qtype: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:

@@ -337,6 +337,20 @@ int pgmoe_requant_w4(int32_t qtype, const void* src, int64_t n_rows, int64_t col
     return launch_requant_w4(qtype, (const uint8_t*)src, n_rows, (int)cols, (uint8_t*)dst, as_stream(stream));
 }
 
+int pgmoe_requant_w8_f16(int32_t qtype, const void* src, int64_t n_rows, int64_t cols, int64_t cols_out, void* dst,
+                         void* stream) {
+    if (qtype != PGMOE_Q5_1)
+        return fail(PGMOE_E_UNSUPPORTED, "requant w8: qtype %d is not re-quantised (Q5_1=7)", qtype);
+    if (!src || !dst || n_rows < 1 || cols < 1 || cols_out < cols || cols_out > (1 << 30) || cols_out % 32)
+        return fail(PGMOE_E_INVALID, "requant w8: bad arguments");
+    if (cols % 32) return fail(PGMOE_E_UNSUPPORTED, "requant w8: %lld columns are not whole 32-weight blocks",
+                               (long long)cols);
+    if ((uintptr_t)dst & 15) return fail(PGMOE_E_INVALID, "requant w8: dst must be 16-byte aligned");
+    if (n_rows > (((int64_t)1 << 38) / (cols_out / 32))) return fail(PGMOE_E_INVALID, "requant w8: matrix too large");
+    return launch_requant_w8_f16(qtype, (const uint8_t*)src, n_rows, (int)cols, (int)cols_out, (uint8_t*)dst,
+                                 as_stream(stream));
+}
+
 int64_t pgmoe_scale_plane_bytes(int32_t qtype, int64_t rows, int64_t cols) {
     return scale_plane_bytes(qtype, rows, cols);
 }
@@ -566,7 +580,7 @@ int pgmoe_linear_forward(const pgmoe_weights* W, const float* bias, const uint16
     if (!x || !out) return fail(PGMOE_E_INVALID, "linear: NULL pointer");
     if (((uintptr_t)x & 15) || ((uintptr_t)ws & 255) || ((uintptr_t)out & 3))
         return fail(PGMOE_E_INVALID, "linear: x must be 16-byte, ws 256-byte, out 4-byte aligned");
-    if (w.qtype != PGMOE_Q8_0 && !w.scales && !linear_gemv_fits(M, w.K))
+    if (w.qtype != PGMOE_Q8_0 && w.qtype != PGMOE_F16 && !w.scales && !linear_gemv_fits(M, w.K))
         return fail(PGMOE_E_INVALID, "linear: K-quant weights need their scale plane for %d tokens", M);
     return launch_linear(w, bias, x, M, out, out_dtype == PGMOE_DT_F16, (uint8_t*)ws, ws_bytes, as_stream(stream));
 }

@@ -75,6 +75,9 @@ int launch_combine(const float* partial, const int32_t* inv, int M, int K, int H
 // (requant.hip); requant_w4_block gives a format's GGUF block (weights, bytes), -1 if none.
 int requant_w4_block(int qtype, int* per, int* bytes);
 int launch_requant_w4(int qtype, const uint8_t* src, int64_t rows, int cols, uint8_t* dst, hipStream_t st);
+// Q5_1 -> fp16 [rows, cols_out] weights with the reference's W8 values (zero past cols).
+int launch_requant_w8_f16(int qtype, const uint8_t* src, int64_t rows, int cols, int cols_out, uint8_t* dst,
+                          hipStream_t st);
 int launch_relayout(int qtype, const uint8_t* src, int64_t n_mats, int64_t rows, int64_t cols, int64_t rows_out,
                     int64_t cols_out, uint8_t* dst, int64_t dst_stride, hipStream_t st);
 // Decode expert stages (M <= decode_tokens_max()).

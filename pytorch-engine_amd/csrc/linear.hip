@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void bias_cast_kernel(const float* __restrict_
 
 // Row `rows[i]` of W (N x K in the tile layout), super-block b, decoded to 256 values:
 // one thread per (i, b); an id outside [0, N) gives a row of NaN.  Values as the ggml block definitions give them, products in fp32
-// (Q4_K, Q5_K: d*sc*q - dmin*m; Q4_1: d*q - (-m); Q6_K: d*sc*(q - 32); Q8_0: d*q).
+// (Q4_K, Q5_K: d*sc*q - dmin*m; Q4_1: d*q - (-m); Q6_K: d*sc*(q - 32); Q8_0: d*q; F16: as stored).
 template <int QT>
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __restrict__ base, int N, int K,
                                                            const int32_t* __restrict__ rows, int n,
@@ -93,6 +93,8 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t* __rest
                     const float sc = (float)(int8_t)byte(12, e >> 4);
                     put(e, (d * sc) * (float)((lo | (hb << 4)) - 32));
                 }
+    } else if constexpr (QT == PGMOE_F16) {  // chunk c: weights 8c .. 8c + 7
+        for (int e = 0; e < 256; ++e) put(e, h2f((uint16_t)(byte(e >> 3, 2 * (e & 7)) | (byte(e >> 3, 2 * (e & 7) + 1) << 8))));
     } else {  // chunks 2j, 2j + 1: qs of block j; chunk 16: the 8 fp16 d
         for (int j = 0; j < 8; ++j) {
             const float d = h2f(*(const uint16_t*)(t + 16 * 1024 + 2 * j));
@@ -112,6 +114,7 @@ int launch_dequant_rows(const Mats& w, const int32_t* rows, int n, void* out, in
     case PGMOE_Q5_K: DQ(PGMOE_Q5_K); break;
     case PGMOE_Q6_K: DQ(PGMOE_Q6_K); break;
     case PGMOE_Q8_0: DQ(PGMOE_Q8_0); break;
+    case PGMOE_F16: DQ(PGMOE_F16); break;
     default: return fail(PGMOE_E_UNSUPPORTED, "dequant rows: qtype %d", w.qtype);
     }
 #undef DQ

@@ -1,5 +1,6 @@
 // Load-time W4 re-quantisation of the GGUF formats the reference reads through gguf-py
-// (Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4): each 32-weight group is decoded exactly in fp32 and
+// (Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4; below it, the W8 one of Q5_1, quant_kernels.py:1005-1025,
+// written as fp16 weights): each 32-weight group is decoded exactly in fp32 and
 // quantised again to 4 bits as repack_gguf_to_w4a16 does (quant_kernels.py:906-942):
 //   scale = (max - min) * fp32(1/15), q = clip(rint((w - min) / (scale or 1)), 0, 15),
 //   stored as a Q4_1 block: d = fp16(scale), m = fp16(min) (the reference's zero is
@@ -138,6 +139,72 @@ __global__ void requant_w4_kernel(const uint8_t* __restrict__ src, int64_t rows,
     o[2] = qw[1];
     o[3] = qw[2];
     o[4] = qw[3];
+}
+
+// Q5_1 {fp16 d; fp16 m; u32 qh; u8 qs[16]}: d q + m with q = nibble | fifth bit << 4
+// (element j: low nibble of qs[j] and bit j of qh; element j + 16: high nibble, bit j + 16).
+__device__ void decode_q5_1(const uint8_t* b, float (&w)[32]) {
+    const float d = f16_at(b), m = f16_at(b + 2);
+    const uint32_t qh = u32_at(b + 4);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        w[j] = d * (float)((b[8 + j] & 15) | (((qh >> j) & 1) << 4)) + m;
+        w[j + 16] = d * (float)((b[8 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4)) + m;
+    }
+}
+
+// One thread per 32-weight block (row, g) of the fp16 [rows, cols_out] output: the
+// reference's W8 values of Q5_1 block g (two 16-weight groups: sc = max|w| / 127, or 1 when
+// the group is all zero; q = clip(rint(w / sc), -127, 127); fp16(sc) q rounded to fp16, the
+// product being exact in fp32), or zeros for g past the source's cols.
+__global__ void requant_w8_f16_kernel(const uint8_t* __restrict__ src, int64_t rows, int cols, int cols_out,
+                                      uint8_t* __restrict__ dst) {
+    const int gpo = cols_out / 32, gpr = cols / 32;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * gpo) return;
+    const int64_t row = gid / gpo;
+    const int g = (int)(gid - row * gpo);
+    uint32_t h[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = 0u;
+    if (g < gpr) {
+        float w[32];
+        decode_q5_1(src + (row * gpr + g) * 24, w);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(w[16 * half + i]));
+            float sc = amax == 0.0f ? 1.0f : amax / 127.0f;
+            asm volatile("" : "+v"(sc));  // sc itself in fp32, then its fp16 rounding
+            const float s16 = (float)(_Float16)sc;
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {  // codes through int, as the reference stores int8 (no -0)
+                const float q0 = (float)(int)fminf(fmaxf(rintf(w[16 * half + i] / sc), -127.0f), 127.0f);
+                const float q1 = (float)(int)fminf(fmaxf(rintf(w[16 * half + i + 1] / sc), -127.0f), 127.0f);
+                // the fp32 products themselves (exact): a mixed FMA with a +0 addend would turn the
+                // -0 of fp16(sc) = 0 times a negative code into +0
+                float v0 = s16 * q0, v1 = s16 * q1;
+                asm volatile("" : "+v"(v0), "+v"(v1));
+                h[8 * half + i / 2] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
+                                      ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
+            }
+        }
+    }
+    uint4* o = reinterpret_cast<uint4*>(dst + (row * cols_out + 32 * (int64_t)g) * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
+}
+
+int launch_requant_w8_f16(int qtype, const uint8_t* src, int64_t rows, int cols, int cols_out, uint8_t* dst,
+                          hipStream_t st) {
+    if (qtype != PGMOE_Q5_1) return fail(PGMOE_E_UNSUPPORTED, "requant w8: qtype %d", qtype);
+    const int64_t n = rows * (cols_out / 32);
+    if (n == 0) return PGMOE_OK;
+    const int threads = 256;
+    PG_LAUNCH(requant_w8_f16_kernel, dim3((unsigned)div_up(n, threads)), dim3(threads), 0, st, src, rows, cols,
+              cols_out, dst);
+    return check_launch("requant_w8_f16");
 }
 
 int requant_w4_block(int qtype, int* per, int* bytes) {

@@ -20,8 +20,11 @@ FLOAT_QTYPES = (F32, F16, BF16)  # expert tensors held as fp16 (PGMOE_F16), as t
 Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4 = 10, 11, 20, 23, 39
 # re-quantised at load to Q4_1 blocks with the reference's W4 values (pgmoe_requant_w4)
 REQUANT_W4_QTYPES = (Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4)
+Q5_1 = 7
+# re-quantised at load to fp16 weights with the reference's W8 values (pgmoe_requant_w8_f16)
+REQUANT_W8_QTYPES = (Q5_1,)
 # GGUF expert formats with a HIP path; Q4_0 is relaid out as Q4_1, Q5_0 as Q8_0 (their values exactly)
-SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0) + FLOAT_QTYPES + REQUANT_W4_QTYPES
+SUPPORTED_QTYPES = (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0) + FLOAT_QTYPES + REQUANT_W4_QTYPES + REQUANT_W8_QTYPES
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -93,6 +96,7 @@ def lib() -> ctypes.CDLL:
     L.pgmoe_relayout_weights.argtypes = [_I32, _P, _I64, _I64, _I64, _P, _P]
     L.pgmoe_relayout_weights_padded.argtypes = [_I32, _P, _I64, _I64, _I64, _I64, _I64, _P, _P]
     L.pgmoe_requant_w4.argtypes = [_I32, _P, _I64, _I64, _P, _P]
+    L.pgmoe_requant_w8_f16.argtypes = [_I32, _P, _I64, _I64, _I64, _P, _P]
     L.pgmoe_scale_plane_bytes.restype = _I64
     L.pgmoe_scale_plane_bytes.argtypes = [_I32, _I64, _I64]
     L.pgmoe_build_scale_plane.argtypes = [_I32, _P, _I64, _I64, _I64, _I64, _P, _P]
@@ -128,7 +132,8 @@ def lib() -> ctypes.CDLL:
                "pgmoe_expert_down", "pgmoe_combine", "pgmoe_relayout_weights", "pgmoe_relayout_weights_padded",
                "pgmoe_build_scale_plane",
                "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status", "pgmoe_moe_forward_noalloc",
-               "pgmoe_add_rmsnorm", "pgmoe_linear_forward", "pgmoe_dequant_rows", "pgmoe_requant_w4"):
+               "pgmoe_add_rmsnorm", "pgmoe_linear_forward", "pgmoe_dequant_rows", "pgmoe_requant_w4",
+               "pgmoe_requant_w8_f16"):
         getattr(L, fn).restype = ctypes.c_int
     ver = L.pgmoe_abi_version()
     if ver != ABI_VERSION:
@@ -151,7 +156,7 @@ EXPORTS = (
     "pgmoe_scale_plane_bytes", "pgmoe_build_scale_plane", "pgmoe_dispatch_ws_bytes", "pgmoe_dispatch_ws",
     "pgmoe_dense_workspace_bytes", "pgmoe_dense_forward", "pgmoe_moe_routing", "pgmoe_moe_status",
     "pgmoe_moe_forward_noalloc", "pgmoe_add_rmsnorm", "pgmoe_linear_workspace_bytes", "pgmoe_linear_forward",
-    "pgmoe_dequant_rows", "pgmoe_relayout_weights_padded", "pgmoe_requant_w4",
+    "pgmoe_dequant_rows", "pgmoe_relayout_weights_padded", "pgmoe_requant_w4", "pgmoe_requant_w8_f16",
 )
 
 STATUS_SPIN_TIMEOUT = 1  # PGMOE_STATUS_SPIN_TIMEOUT

@@ -69,7 +69,7 @@ class GGUFQuantLinear(nn.Module):
             raise NotImplementedError(f"ggml type {gguf_qtype} has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, "
                                       "Q8_0, Q4_1, Q4_0 / Q5_0 relaid out as Q4_1 / Q8_0, and Q2_K / Q3_K / "
                                       "IQ4_NL / IQ4_XS / MXFP4 re-quantised to Q4_1 as the reference's W4 "
-                                      "repack does)")
+                                      "repack does, Q5_1 to its W8 values held as fp16)")
         # the device width: in_features, or for the 32-weight formats the next multiple of 256
         # (zero blocks appended to every row; forward appends as many zero inputs)
         self.cols = ops.padded_width(gguf_qtype, self.in_features)

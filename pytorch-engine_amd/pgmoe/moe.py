@@ -25,8 +25,8 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from ._lib import (ACT_GELU_TANH, ACT_SILU, F16, FLOAT_QTYPES, REQUANT_W4_QTYPES, STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES,
-                   Layer, Weights, check, lib)
+from ._lib import (ACT_GELU_TANH, ACT_SILU, F16, FLOAT_QTYPES, REQUANT_W4_QTYPES, REQUANT_W8_QTYPES,
+                   STATUS_SPIN_TIMEOUT, SUPPORTED_QTYPES, Layer, Weights, check, lib)
 from .workspace import StatusWord, WorkspacePool
 
 _F32, _F16, _BF16 = 0, 1, 30
@@ -46,7 +46,7 @@ def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.
     F32 / F16 / BF16 converted, and quantised ones (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q4_1, Q5_0; the
     reference's gguf.quants.dequantize branch) dequantised once on the device to the values
     the ggml block definitions give.  CPU targets take the float types only.  The formats
-    the reference re-quantises for its matrix products (Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4)
+    the reference re-quantises for its matrix products (Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4, Q5_1)
     are not decoded here: its float tensors get their exact gguf-py values, which only the
     re-quantised form is built for."""
     info = gguf_file.tensors[name]
@@ -59,7 +59,7 @@ def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.
     elif info.qtype == _BF16:
         u16 = np.frombuffer(raw, dtype=np.uint16).reshape(shape).copy()
         arr = torch.from_numpy(u16.view(np.int16)).view(torch.bfloat16).float()
-    elif (int(info.qtype) in SUPPORTED_QTYPES and int(info.qtype) not in REQUANT_W4_QTYPES
+    elif (int(info.qtype) in SUPPORTED_QTYPES and int(info.qtype) not in REQUANT_W4_QTYPES + REQUANT_W8_QTYPES
           and torch.device(device).type == "cuda"):
         cols = shape[-1]
         rows = int(np.prod(shape[:-1])) if len(shape) > 1 else 1
@@ -74,7 +74,7 @@ def load_float_tensor(gguf_file: Any, name: str, device: torch.device) -> torch.
 
 def padded_inter(gguf_file: Any, down_name: str) -> Tuple[int, int]:
     """(I, I_out) of an FFN whose down tensor is `down_name` ([E, H, I] or [H, I]): I_out = I
-    when I is a multiple of 256; for a 32-weight down format (Q8_0, Q5_0, Q4_0, Q4_1, IQ4_NL, MXFP4) with I
+    when I is a multiple of 256; for a 32-weight down format (Q8_0, Q5_0, Q5_1, Q4_0, Q4_1, IQ4_NL, MXFP4) with I
     a multiple of 32 (e.g. 1408), I rounded up to one of 256: gate / up then get zero rows and
     down zero columns up to I_out, and the kernels compute the unpadded layer's values (zero
     rows give SwiGLU values of exactly 0, which meet zero weights)."""
@@ -83,7 +83,7 @@ def padded_inter(gguf_file: Any, down_name: str) -> Tuple[int, int]:
     io = ops.padded_width(int(info.qtype), inter)
     if io < 0:
         raise ValueError(f"{down_name}: {inter} input features (a multiple of 256, or of 32 for the 32-weight "
-                         "formats Q8_0, Q5_0, Q4_0, Q4_1, IQ4_NL, MXFP4)")
+                         "formats Q8_0, Q5_0, Q5_1, Q4_0, Q4_1, IQ4_NL, MXFP4)")
     return inter, io
 
 
@@ -107,7 +107,7 @@ class _ExpertTensor:
                 f"{name}: ggml type {info.qtype_name if hasattr(info, 'qtype_name') else self.qtype} "
                 "has no HIP kernel (supported: Q4_K, Q5_K, Q6_K, Q8_0, Q4_1, Q4_0 / Q5_0 relaid out as Q4_1 / "
                 "Q8_0, F16 / BF16 / F32 held as fp16, and Q2_K / Q3_K / IQ4_NL / IQ4_XS / MXFP4 re-quantised to "
-                "Q4_1 as the reference's W4 repack does)")
+                "Q4_1 as the reference's W4 repack does, Q5_1 to its W8 values held as fp16)")
         width = ops.padded_width(self.gguf_qtype, self.gguf_cols)
         if width < 0 or (cols_out is not None and cols_out < width):
             raise ValueError(f"{name}: {self.gguf_cols} input features is not a multiple of 256"

@@ -12,13 +12,14 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._lib import (BF16, F16, F32, FLOAT_QTYPES, IQ4_NL, IQ4_XS, MXFP4, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_0, Q5_K,
-                   Q6_K, Q8_0, REQUANT_W4_QTYPES, Weights, check, lib)
+from ._lib import (BF16, F16, F32, FLOAT_QTYPES, IQ4_NL, IQ4_XS, MXFP4, Q2_K, Q3_K, Q4_0, Q4_1, Q4_K, Q5_0, Q5_1,
+                   Q5_K, Q6_K, Q8_0, REQUANT_W4_QTYPES, REQUANT_W8_QTYPES, Weights, check, lib)
 
 # (weights, bytes) of a GGUF block; the float types as 256-weight runs of a row
 GGUF_BLOCK = {Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210), Q8_0: (32, 34), Q4_0: (32, 18),
               Q4_1: (32, 20), Q5_0: (32, 22), F16: (256, 512), BF16: (256, 512), F32: (256, 1024),
-              Q2_K: (256, 84), Q3_K: (256, 110), IQ4_NL: (32, 18), IQ4_XS: (256, 136), MXFP4: (32, 17)}
+              Q2_K: (256, 84), Q3_K: (256, 110), IQ4_NL: (32, 18), IQ4_XS: (256, 136), MXFP4: (32, 17),
+              Q5_1: (32, 24)}
 
 
 def device_qtype(qtype: int) -> int:
@@ -26,10 +27,11 @@ def device_qtype(qtype: int) -> int:
     (d * (q - 8) = d q + m with m = -8d), Q5_0 becomes Q8_0 (d * (q - 16) is the Q8_0 value
     d * qs with qs = q - 16), F32 and BF16 become F16 (rounded to fp16 on the host, as the
     reference's fp16 expert mode loads them), Q2_K / Q3_K / IQ4_NL / IQ4_XS / MXFP4 become
-    Q4_1 (the reference's W4 re-quantisation, requant_w4), the others keep theirs."""
+    Q4_1 (the reference's W4 re-quantisation, requant_w4), Q5_1 becomes F16 (the reference's
+    W8 re-quantisation, requant_w8_f16), the others keep theirs."""
     if qtype == Q4_0 or qtype in REQUANT_W4_QTYPES:
         return Q4_1
-    return Q8_0 if qtype == Q5_0 else F16 if qtype in FLOAT_QTYPES else qtype
+    return Q8_0 if qtype == Q5_0 else F16 if qtype in FLOAT_QTYPES + REQUANT_W8_QTYPES else qtype
 
 
 def requant_w4(qtype: int, raw: torch.Tensor, n_rows: int, cols: int) -> torch.Tensor:
@@ -43,6 +45,22 @@ def requant_w4(qtype: int, raw: torch.Tensor, n_rows: int, cols: int) -> torch.T
     dst = torch.empty(n_rows * (cols // 32) * 20, dtype=torch.uint8, device=dev)
     check(lib().pgmoe_requant_w4(qtype, raw.data_ptr(), n_rows, cols, dst.data_ptr(), _stream(dev)),
           "pgmoe_requant_w4")
+    return dst
+
+
+def requant_w8_f16(qtype: int, raw: torch.Tensor, n_rows: int, cols: int, cols_out: Optional[int] = None) -> torch.Tensor:
+    """Q5_1 GGUF bytes of an n_rows x cols matrix on the device -> fp16 weights (uint8
+    [n_rows * cols_out * 2], zero past cols) with the reference's W8 values: per 16 weights
+    sc = max|w| / 127, codes round(w / sc) in -127..127, weight fp16(fp16(sc) * code)
+    (repack_gguf_to_w8a16's fallback, quant_kernels.py:1005-1025; pgmoe_requant_w8_f16)."""
+    dev = _need_cuda(raw)
+    co = cols if cols_out is None else cols_out
+    per, bb = GGUF_BLOCK[qtype]
+    if cols % per or raw.numel() != n_rows * (cols // per) * bb:
+        raise ValueError("raw byte count does not match the tensor shape")
+    dst = torch.empty(n_rows * co * 2, dtype=torch.uint8, device=dev)
+    check(lib().pgmoe_requant_w8_f16(qtype, raw.data_ptr(), n_rows, cols, co, dst.data_ptr(), _stream(dev)),
+          "pgmoe_requant_w8_f16")
     return dst
 
 
@@ -86,6 +104,9 @@ def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int,
     if qtype in REQUANT_W4_QTYPES:  # first to the Q4_1 blocks of the reference's W4 values
         raw = requant_w4(qtype, raw, n_mats * rows, cols)
         qtype = Q4_1
+    elif qtype in REQUANT_W8_QTYPES:  # first to fp16 weights of the reference's W8 values, already co wide
+        raw = requant_w8_f16(qtype, raw, n_mats * rows, cols, co)
+        qtype, cols = F16, co
     stride = weight_stride(qtype, ro, co)
     per, bb = GGUF_BLOCK[qtype]
     if raw.numel() != n_mats * rows * (cols // per) * bb:
@@ -104,7 +125,7 @@ def relayout(qtype: int, raw: torch.Tensor, n_mats: int, rows: int, cols: int,
 
 def padded_width(qtype: int, cols: int) -> int:
     """The device width of a GGUF matrix with `cols` input features: cols itself when it is a
-    multiple of 256; for the 32-weight formats (Q8_0, Q5_0, Q4_0, Q4_1, IQ4_NL, MXFP4) any
+    multiple of 256; for the 32-weight formats (Q8_0, Q5_0, Q5_1, Q4_0, Q4_1, IQ4_NL, MXFP4) any
     multiple of 32 is padded up to one of 256 with zero blocks; -1 when the kernels cannot
     take it."""
     if cols % 256 == 0:

@@ -112,6 +112,13 @@ def random_blocks(rng: np.random.Generator, qtype: int, rows: int, cols: int,
         m = (-np.abs(rng.standard_normal(nb)) * (0.1 * scale)).astype(np.float16)
         raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         raw[:, 2:4] = m.view(np.uint8).reshape(nb, 2)
+    elif qtype == GGMLType.Q5_1:  # d = |N| * 0.01 scale, m = -N(0, 1) * 0.15 scale (centres the 5-bit codes)
+        nb = rows * (cols // 32)
+        raw = rng.integers(0, 256, size=(nb, 24), dtype=np.uint8)
+        d = (np.abs(rng.standard_normal(nb)) * (0.01 * scale)).astype(np.float16)
+        m = (-np.abs(rng.standard_normal(nb)) * (0.15 * scale)).astype(np.float16)
+        raw[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        raw[:, 2:4] = m.view(np.uint8).reshape(nb, 2)
     elif qtype == Q4_0:
         nb = rows * (cols // 32)
         raw = rng.integers(0, 256, size=(nb, 18), dtype=np.uint8)

@@ -39,7 +39,7 @@ def test_weight_bytes_are_gguf_bytes_of_64_row_tiles():
         if rows % 64 == 0:  # no padding: exactly the GGUF bytes
             assert L.pgmoe_weight_bytes(qt, rows, cols) == rows * (cols // per) * bb
     assert L.pgmoe_weight_bytes(12, 4, 100) == -1  # not a whole K-quant block row
-    assert L.pgmoe_weight_bytes(7, 4, 256) == -1   # Q5_1 has no kernel
+    assert L.pgmoe_weight_bytes(7, 4, 256) == -1   # Q5_1 is a source format (held as fp16)
     assert L.pgmoe_weight_bytes(10, 4, 256) == -1  # nor Q2_K
     assert L.pgmoe_weight_bytes(3, 64, 256) == 64 * 8 * 20  # Q4_1: the GGUF bytes
     assert L.pgmoe_weight_bytes(6, 4, 256) == L.pgmoe_weight_bytes(8, 4, 256)  # Q5_0 is stored as Q8_0
@@ -198,6 +198,14 @@ def test_stage_validation_errors():
     assert rq(10, None, 4, 256, 0x2000, None) == -1
     assert rq(11, 0x1000, 0, 256, 0x2000, None) == -1
     assert rq(20, 0x1000, 1 << 40, 32, 0x2000, None) == -1  # grid beyond its limit
+    # Q5_1 to fp16 weights of the reference's W8 values
+    r8 = L.pgmoe_requant_w8_f16
+    assert r8(6, 0x1000, 4, 256, 256, 0x2000, None) == -2  # Q5_0 keeps its exact Q8_0 form
+    assert r8(7, 0x1000, 4, 48, 64, 0x2000, None) == -2  # not whole blocks
+    assert r8(7, 0x1000, 4, 256, 224, 0x2000, None) == -1  # cols_out < cols
+    assert r8(7, 0x1000, 4, 64, 80, 0x2000, None) == -1  # cols_out not whole 32-weight blocks
+    assert r8(7, 0x1000, 4, 64, 64, 0x2008, None) == -1  # dst not 16-byte aligned
+    assert r8(7, None, 4, 64, 64, 0x2000, None) == -1
 
 
 def test_module_rejects_cpu_device():

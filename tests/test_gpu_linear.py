@@ -181,4 +181,4 @@ def test_unsupported_widths_and_formats(dev):
     with pytest.raises(NotImplementedError):  # 32-weight formats: whole blocks
         GGUFQuantLinear("w8", 80, 4, Q8_0, raw=np.zeros(4 * 3 * 34, np.uint8), device=dev)
     with pytest.raises(NotImplementedError):
-        GGUFQuantLinear("w8", 256, 4, 7, raw=np.zeros(4 * 8 * 24, np.uint8), device=dev)  # Q5_1
+        GGUFQuantLinear("w4", 256, 4, 16, raw=np.zeros(4 * 66, np.uint8), device=dev)  # IQ2_XXS

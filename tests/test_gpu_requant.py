@@ -1,5 +1,6 @@
-"""GPU parity of the formats the reference re-quantises to W4 at load (Q2_K, Q3_K, IQ4_NL,
-IQ4_XS, MXFP4; repack_gguf_to_w4a16, quant_kernels.py:906-942):
+"""GPU parity of the formats the reference re-quantises at load: to W4 (Q2_K, Q3_K, IQ4_NL,
+IQ4_XS, MXFP4; repack_gguf_to_w4a16, quant_kernels.py:906-942) and to W8 (Q5_1;
+repack_gguf_to_w8a16, :1005-1025, held here as the fp16 weights its tensor-core GEMM forms):
 
 * pgmoe_requant_w4's Q4_1 bytes equal the oracle's restatement bit for bit, on random blocks
   and on edge blocks (flat groups, the extremes of each scale field);
@@ -14,13 +15,13 @@ import pytest
 
 import oracle
 from gpu_helpers import build_pair, check_forward_routing, check_layer_output, log, sample_tokens
-from oracle.requant import REQUANT_BLOCK, requant_w4
+from oracle.requant import REQUANT_BLOCK, requant_w4, requant_w8_f16
 from pgmoe.synth import LayerSpec, random_blocks
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4, Q4_1, Q4_K, Q6_K, Q8_0 = 10, 11, 20, 23, 39, 3, 12, 14, 8
+Q2_K, Q3_K, IQ4_NL, IQ4_XS, MXFP4, Q4_1, Q4_K, Q6_K, Q8_0, Q5_1, F16 = 10, 11, 20, 23, 39, 3, 12, 14, 8, 7, 1
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -95,6 +96,9 @@ SPECS = {  # (spec, scale: outputs of order 1e-2 .. 1e-1)
                                      arch="qwen2moe", shared_inter=768, shared_qtypes=(IQ4_XS, MXFP4, Q3_K),
                                      shared_gate=True), 0.01),
     "mxfp4_i1408": (LayerSpec("mxfp4_i1408", 1024, 16, 4, 1408, (MXFP4, MXFP4, MXFP4)), 0.1),
+    "q5_1_i1408_shared": (LayerSpec("q5_1_i1408_shared", 1024, 16, 4, 1408, (Q4_K, Q4_K, Q5_1), norm_topk=False,
+                                    arch="qwen2moe", shared_inter=1408, shared_qtypes=(Q5_1, Q5_1, Q5_1),
+                                    shared_gate=True), 0.1),
 }
 
 
@@ -102,7 +106,8 @@ SPECS = {  # (spec, scale: outputs of order 1e-2 .. 1e-1)
 def test_requant_layers(name):
     spec, scale = SPECS[name]
     lay, ol, mod = build_pair(spec, seed=5, scale=scale)
-    assert ol.gate[0] == Q4_1 and ol.down[0] == Q4_1  # the oracle runs the re-quantised form
+    for t, gq in ((ol.gate, spec.qtypes[0]), (ol.down, spec.qtypes[2])):  # the oracle runs the re-quantised form
+        assert t[0] == (F16 if gq == Q5_1 else Q4_1 if gq in REQUANT_BLOCK else gq)
     _check(lay, ol, mod, (1, 2, 8, 300))
 
 
@@ -122,3 +127,55 @@ def test_requant_linear(qt, N, K, M):
         check_layer_output(out, ref, rel_l2=1e-4, max_rel=1e-4)
     else:
         check_layer_output(out, ref)
+
+
+def _q5_1_edge(cols):
+    """Q5_1 rows: all zero; fp16 d and m at +-65504 (the widest range); d and m at the smallest
+    fp16 sub-normal; random codes with d = 1, m = -16."""
+    nb = cols // 32
+    rng = np.random.default_rng(9)
+    rows = []
+    for d, m in ((0.0, 0.0), (65504.0, -65504.0), (2.0 ** -24, -(2.0 ** -24)), (1.0, -16.0)):
+        b = rng.integers(0, 256, size=(nb, 24), dtype=np.uint8) if d else np.zeros((nb, 24), np.uint8)
+        b[:, 0:2] = np.array([d], np.float16).view(np.uint8)
+        b[:, 2:4] = np.array([m], np.float16).view(np.uint8)
+        rows.append(b)
+    return np.concatenate([r.reshape(-1) for r in rows]), len(rows)
+
+
+@pytest.mark.parametrize("cols,cols_out", [(1024, 1024), (1408, 1536)])
+def test_requant_w8_f16_bit_exact(cols, cols_out):
+    from pgmoe import ops
+    rows = 200
+    raw = random_blocks(np.random.default_rng(cols), Q5_1, rows, cols)
+    edge, ne = _q5_1_edge(cols)
+    raw = np.concatenate([raw, edge])
+    n = rows + ne
+    log(f"requant w8 rows={n} cols={cols} cols_out={cols_out}")
+    got = ops.requant_w8_f16(Q5_1, torch.from_numpy(raw).to("cuda:0"), n, cols, cols_out).cpu().numpy()
+    got = got.view(np.uint16).reshape(n, cols_out)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = requant_w8_f16(Q5_1, raw, n, cols).view(np.uint16).reshape(n, cols)
+    bad = np.argwhere(got[:, :cols] != ref)
+    assert bad.size == 0, f"{len(bad)} weights differ, first at (row, col) {tuple(bad[0])}"
+    assert np.all(got[:, cols:] == 0)
+
+
+@pytest.mark.parametrize("M", [1, 8, 300])
+def test_requant_w8_linear_and_rows(M):
+    from pgmoe import GGUFQuantLinear
+    N, K = 640, 1408
+    rng = np.random.default_rng(M)
+    raw = random_blocks(rng, Q5_1, N, K, 0.1)
+    lin = GGUFQuantLinear("w8", K, N, Q5_1, raw=raw, device=torch.device("cuda", 0))
+    w16 = requant_w8_f16(Q5_1, raw, N, K).view(np.float16).reshape(N, K)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    out = lin(torch.from_numpy(x).to("cuda:0").float()).cpu().numpy()
+    ref = x.astype(np.float64) @ w16.astype(np.float64).T
+    if M <= 8:
+        check_layer_output(out, ref, rel_l2=1e-4, max_rel=1e-4)
+    else:
+        check_layer_output(out, ref)
+    ids = torch.tensor([0, N - 1, 65, 3], dtype=torch.int64)
+    rows = lin.embed_lookup(ids).cpu().numpy()  # fp16 rows: the stored weights, bit for bit
+    assert np.array_equal(rows.view(np.uint16), w16[ids.numpy()].view(np.uint16))

@@ -7,7 +7,10 @@ IQ4_NL, IQ4_XS, MXFP4; oracle/requant.py), pinned without gguf-py (not importabl
 * the re-quantisation (quant_kernels.py:920-936): codes in 0..15, the group minimum on code
   0 and the maximum on code 15, every value within half a step (plus the fp16 rounding of
   the step and the minimum) of the Q4_1 value rebuilt from the bytes, zero-width groups,
-  and round-half-to-even on quotients that land on .5 exactly.
+  and round-half-to-even on quotients that land on .5 exactly;
+* Q5_1 and the reference's W8 re-quantisation it takes (quant_kernels.py:1011-1025): nibble
+  and fifth-bit positions, each weight within half a step of its group's fp16 scale, the
+  largest on code +-127, flat and all-zero groups.
 """
 
 import numpy as np
@@ -188,3 +191,55 @@ def test_requant_flat_group_and_half_even():
 def test_block_table_matches_the_reference_parser():
     # pygguf_engine/gguf_parser.py:57-91: (weights, bytes) per block
     assert REQUANT_BLOCK == {10: (256, 84), 11: (256, 110), 20: (32, 18), 23: (256, 136), 39: (32, 17)}
+
+
+def test_q5_1_nibbles_and_fifth_bits():
+    from oracle.requant import q5_1_dequant
+    b = np.zeros(24, np.uint8)
+    b[0:2] = _f16b(0.5)
+    b[2:4] = _f16b(-3.0)
+    rng = np.random.default_rng(3)
+    lo = rng.integers(0, 16, size=32)
+    hi = rng.integers(0, 2, size=32)
+    for j in range(16):
+        b[8 + j] = lo[j] | (lo[j + 16] << 4)
+    qh = sum(int(hi[e]) << e for e in range(32))
+    b[4:8] = np.array([qh], "<u4").view(np.uint8)
+    w = q5_1_dequant(b, 1, 32)[0]
+    assert np.array_equal(w, (0.5 * (lo | (hi << 4)) - 3.0).astype(np.float32))
+    # one fifth bit at a time lifts exactly its element by 16 d
+    for e in (0, 15, 16, 31):
+        b2 = b.copy()
+        b2[4:8] = np.array([qh ^ (1 << e)], "<u4").view(np.uint8)
+        diff = q5_1_dequant(b2, 1, 32)[0] - w
+        assert np.count_nonzero(diff) == 1 and abs(diff[e]) == 8.0
+
+
+def test_requant_w8_properties_and_exact_cases():
+    from oracle.requant import Q5_1, q5_1_dequant, requant_w8_f16
+    from pgmoe.synth import random_blocks
+    rows, cols = 16, 512
+    raw = random_blocks(np.random.default_rng(7), Q5_1, rows, cols)
+    w = q5_1_dequant(raw, rows, cols).reshape(rows, cols // 16, 16)
+    v = requant_w8_f16(Q5_1, raw, rows, cols).view(np.float16).astype(np.float32).reshape(rows, cols // 16, 16)
+    amax = np.abs(w).max(-1)
+    sc = amax / np.float32(127)
+    # within half a step of the fp16 scale plus the fp16 rounding of scale and weight
+    bound = 0.5 * sc + 127 * np.abs(sc.astype(np.float16).astype(np.float32) - sc) + 2.0 ** -11 * amax
+    assert np.all(np.abs(v - w) <= bound[..., None])
+    # the largest magnitude lands on code +-127: its weight is fp16(+-127 fp16(sc))
+    i = np.abs(w).argmax(-1)
+    top = np.take_along_axis(v, i[..., None], -1)[..., 0]
+    s16 = sc.astype(np.float16).astype(np.float32)
+    assert np.array_equal(np.abs(top), (127 * s16).astype(np.float16).astype(np.float32))
+    # a flat group: d = 1/4, m = -3.875 and every code 31 give 3.875 everywhere, so every code is
+    # +127 and every weight fp16(127 fp16(3.875 / 127)); an all-zero block gives +0 weights
+    b = np.zeros(24 * 2, np.uint8).reshape(2, 24)
+    b[0, 0:2] = _f16b(0.25)
+    b[0, 2:4] = _f16b(-3.875)
+    b[0, 4:24] = 0xFF
+    out = requant_w8_f16(Q5_1, b[0], 1, 32).view(np.float16).astype(np.float32)
+    assert np.array_equal(out, np.full(32, np.float16(127 * np.float16(np.float32(3.875) / np.float32(127))),
+                                       np.float32))
+    out0 = requant_w8_f16(Q5_1, b[1], 1, 32).view(np.uint16)
+    assert np.all(out0 == 0)     # +0, not -0
