@@ -179,3 +179,25 @@ def test_requant_w8_linear_and_rows(M):
     ids = torch.tensor([0, N - 1, 65, 3], dtype=torch.int64)
     rows = lin.embed_lookup(ids).cpu().numpy()  # fp16 rows: the stored weights, bit for bit
     assert np.array_equal(rows.view(np.uint16), w16[ids.numpy()].view(np.uint16))
+
+
+@pytest.mark.parametrize("M", [1, 8, 300])
+def test_requant_dense(M):
+    """The dense SwiGLU FFN with IQ4_XS gate, Q3_K up and an I = 1408 Q5_1 down (padded to
+    1536): decode GEMVs and the one-group GEMMs against the oracle on the re-quantised
+    forms."""
+    from pgmoe import HipDenseMLP
+    from pgmoe.synth import DenseSpec, SyntheticDense
+    sp = DenseSpec("dense_requant", 1024, 1408, (IQ4_XS, Q3_K, Q5_1))
+    lay = SyntheticDense(sp, seed=4, scale=0.1)
+    mod = HipDenseMLP(lay.gguf, lay.config, 0, torch.device("cuda", 0))
+    H, I = sp.hidden, sp.inter
+    mats = []
+    for qt, p, (n, k) in zip(sp.qtypes, ("gate", "up", "down"), ((I, H), (I, H), (H, I))):
+        raw = np.ascontiguousarray(lay.tensor(f"ffn_{p}.weight"))
+        mats.append((F16, n, k, requant_w8_f16(qt, raw, n, k)) if qt == Q5_1 else (Q4_1, n, k, requant_w4(qt, raw, n, k)))
+    log(f"dense requant M={M}")
+    x = lay.draw_x(M)
+    got = mod(torch.from_numpy(x).to("cuda:0")).cpu().numpy()
+    toks = sample_tokens(M, 8)
+    check_layer_output(got[toks], oracle.dense_forward(x, *mats, tokens=toks))
