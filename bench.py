@@ -104,6 +104,7 @@ _KNAMES = (("router_gemm_kernel", "router"), ("router_logits_kernel", "router"),
            ("dispatch_count_kernel", "dispatch_count"), ("identity_dispatch_kernel", "sh_dispatch"),
            ("dispatch_kernel", "dispatch"), ("gemm_split_reduce_kernel<true>", "gemm_gateup_reduce"),
            ("gemm_split_reduce_kernel<false>", "gemm_down_reduce"), ("rowscale_kernel", "rowscale"),
+           ("rowscale_block_kernel", "rowscale"),
            ("combine_kernel", "combine"), ("dec_gu_kernel", "dec_gu"), ("dec_dc_kernel", "dec_dc"),
            ("dec_dc_chunk_kernel", "dec_dc"), ("dec_down_kernel", "dec_down"))
 

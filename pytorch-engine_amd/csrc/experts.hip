@@ -70,6 +70,48 @@ __global__ __launch_bounds__(256) void rowscale_kernel(const float* __restrict__
     }
 }
 
+// The same for rows longer than 4096 (Mixtral's 14336, Qwen2's shared 20480): one block
+// of 4 waves a row, read once into registers (NV float4 words a thread, rows of up to
+// 1024 * NV values), the maximum over the block (order-free: the scale is rowscale_kernel's),
+// then the fp16 row.  The one-wave form read such rows twice and, at a few hundred rows,
+// left most CUs idle.
+template <int NV>
+__global__ __launch_bounds__(256) void rowscale_block_kernel(const float* __restrict__ inter, int I,
+                                                             uint16_t* __restrict__ a16, float* __restrict__ rs) {
+    __shared__ float wmx[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t p = blockIdx.x;
+    const float* row = inter + p * I;
+    const int n4 = I >> 2;
+    float4 v[NV];
+    float mx = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+        const int i = tid + 256 * q;
+        v[q] = i < n4 ? ld_nt4(row + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[q].x), fabsf(v[q].y)), fmaxf(fabsf(v[q].z), fabsf(v[q].w))));
+    }
+    mx = wave_max(mx);
+    if (lane == 0) wmx[w] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmx[0], wmx[1]), fmaxf(wmx[2], wmx[3]));
+    const float sc = fmaxf(mx * (1.0f / 16384.0f), 1.0f);
+    if (tid == 0) rs[p] = sc;
+    uint16_t* orow = a16 + p * I;
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+        const int i = tid + 256 * q;
+        if (i < n4) {
+            const float4 u = v[q];
+            const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.x / sc)) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.y / sc)) << 16);
+            const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.z / sc)) |
+                                ((uint32_t)__builtin_bit_cast(uint16_t, (half_t)(u.w / sc)) << 16);
+            __builtin_nontemporal_store(nu2{lo, hi}, (nu2*)(orow + 4 * i));
+        }
+    }
+}
+
 // out[t, h] = sum of the token's K pair rows in ascending sorted position (= ascending
 // expert id), then + shared[t, h] * sigmoid(shared_logit[t]).  Thread = 4 columns of one
 // token; the K positions are ordered by an unrolled selection (no indexed local array),
@@ -153,6 +195,10 @@ int launch_down(const Mats& d, const float* inter, int M, int topk, const int32_
         PG_LAUNCH(rowscale_kernel<4>, rgrid, dim3(256), 0, st, inter, (int)P, I, a16, rs);
     else if (I <= 4096)
         PG_LAUNCH(rowscale_kernel<16>, rgrid, dim3(256), 0, st, inter, (int)P, I, a16, rs);
+    else if (I <= 16384)
+        PG_LAUNCH(rowscale_block_kernel<16>, dim3((unsigned)P), dim3(256), 0, st, inter, I, a16, rs);
+    else if (I <= 24576)
+        PG_LAUNCH(rowscale_block_kernel<24>, dim3((unsigned)P), dim3(256), 0, st, inter, I, a16, rs);
     else
         PG_LAUNCH(rowscale_kernel<0>, rgrid, dim3(256), 0, st, inter, (int)P, I, a16, rs);
     int rc = check_launch("rowscale");

@@ -229,16 +229,19 @@ def expert_gateup(gate: Weights, up: Weights, x: torch.Tensor, top_k: int, disp,
     return inter
 
 
-def expert_down(down: Weights, inter: torch.Tensor, M: int, top_k: int, disp, topk_w: torch.Tensor, mode: int
-                ) -> torch.Tensor:
+def expert_down(down: Weights, inter: torch.Tensor, M: int, top_k: int, disp, topk_w: torch.Tensor, mode: int,
+                rowscale: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+    """Weighted down partials [P, N].  mode 1 (MFMA): the row-scaled fp16 input and its
+    scales go to `rowscale` = (a16 [P, K] fp16, rs [P] fp32) when given (else to scratch)."""
     dev = _need_cuda(inter, topk_w)
     offsets, perm, inv, active, n_active, tile_off = disp
     P = M * top_k
     partial = torch.empty((P, down.n_rows), dtype=torch.float32, device=dev)
     a16 = rs = None
     if mode == 1:
-        a16 = torch.empty((P, down.n_cols), dtype=torch.float16, device=dev)
-        rs = torch.empty(P, dtype=torch.float32, device=dev)
+        a16, rs = rowscale if rowscale is not None else (
+            torch.empty((P, down.n_cols), dtype=torch.float16, device=dev),
+            torch.empty(P, dtype=torch.float32, device=dev))
     check(lib().pgmoe_expert_down(down, inter.data_ptr(), M, top_k, offsets.data_ptr(), perm.data_ptr(),
                                   active.data_ptr(), n_active.data_ptr(), tile_off.data_ptr(), topk_w.data_ptr(),
                                   mode, _ptr(a16), _ptr(rs), partial.data_ptr(), _stream(dev)),

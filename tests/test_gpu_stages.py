@@ -321,6 +321,47 @@ def test_expert_stages(dev, qg, qd, H, I, E, K, M, mode):
     assert oracle.max_rel(partial.cpu().numpy(), ref_part) < 50 * tol
 
 
+@pytest.mark.parametrize("I", [1024, 4096, 14336, 20480])
+def test_rowscale_bit_exact_and_down(dev, I):
+    """The prefill down stage's row-scale (exec_fused_act_mul_rowscale's second half,
+    quant_kernels.py:1467-1475): rs = max(max|v| / 16384, 1) and a16 = fp16(v / rs) bit for bit
+    against numpy, for the one-wave rows (I <= 4096) and the one-block rows (Mixtral's 14336,
+    Qwen2's shared 20480), with rows large enough to scale; then the down partials within the
+    MFMA tolerance."""
+    from pgmoe import ops
+    log(f"rowscale I={I}")
+    rng = np.random.default_rng(I)
+    H, E, K, M = 256, 4, 2, 40
+    P = M * K
+    dr = np.concatenate([random_blocks(rng, Q8_0, H, I, 0.1) for _ in range(E)])
+    db = ops.relayout(Q8_0, torch.from_numpy(dr).to(dev), E, H, I)
+    Wd = ops.make_weights(Q8_0, db, E, H, I, ops.scale_plane(Q8_0, db, E, H, I))
+    idx = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32)
+    tw = rng.random((M, K)).astype(np.float32)
+    disp = ops.dispatch(torch.from_numpy(idx).to(dev), E, 256)
+    inter = rng.standard_normal((P, I)).astype(np.float32)
+    inter[::3] *= np.float32(3e4)  # every third row above the fp16-safe range: rs > 1
+    inter[1, 7] = np.float32(-7e6)  # a row whose maximum is a single negative value
+    a16 = torch.empty((P, I), dtype=torch.float16, device=dev)
+    rs = torch.empty(P, dtype=torch.float32, device=dev)
+    partial = ops.expert_down(Wd, torch.from_numpy(inter).to(dev), M, K, disp, torch.from_numpy(tw).to(dev), 1,
+                              rowscale=(a16, rs))
+    torch.cuda.synchronize()
+    ref_rs = np.maximum(np.abs(inter).max(axis=1) * np.float32(1.0 / 16384.0), np.float32(1.0)).astype(np.float32)
+    ref_a16 = (inter / ref_rs[:, None]).astype(np.float16)
+    assert np.array_equal(rs.cpu().numpy().view(np.uint32), ref_rs.view(np.uint32))
+    assert np.array_equal(a16.cpu().numpy().view(np.uint16), ref_a16.view(np.uint16))
+    assert (ref_rs > 1).sum() >= P // 3
+    _, perm, _ = oracle.dispatch(idx, E)
+    d = _dense(Q8_0, dr, E, H, I)
+    ref_part = np.empty((P, H))
+    a64 = ref_a16.astype(np.float64) * ref_rs[:, None].astype(np.float64)
+    for p in range(P):
+        t, k = divmod(int(perm[p]), K)
+        ref_part[p] = tw[t, k] * (d[idx[t, k]] @ a64[p])
+    assert oracle.rel_l2(partial.cpu().numpy(), ref_part) < 2e-3
+
+
 def test_combine_order_and_shared(dev):
     from pgmoe import ops
     rng = np.random.default_rng(5)
