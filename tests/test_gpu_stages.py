@@ -116,7 +116,10 @@ def test_relayout_unaligned_source(dev, qtype):
                                           (333, 2048, 128, 8, True), (4096, 2048, 128, 8, True),
                                           (5, 1024, 8, 2, False), (64, 3584, 64, 8, False),
                                           (17, 4096, 8, 2, False), (3, 512, 512, 16, False),
-                                          (40, 1024, 24, 4, True)])
+                                          (40, 1024, 24, 4, True),
+                                          # the small-grid tiles: 4 x 2 (Mixtral's E = 8) and 1 x 1
+                                          (2048, 4096, 8, 2, False), (512, 3584, 1, 1, False),
+                                          (300, 1024, 3, 2, True)])
 def test_router_topk_bitexact(dev, M, H, E, K, bias):
     from pgmoe import ops
     log(f"router M={M} H={H} E={E} K={K}")
