@@ -236,10 +236,12 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
         PG_ROUTER(4, 1);
     else if (M <= 8)
         PG_ROUTER(8, 1);
-    else if (!extra_w && !xsum && E >= 16 && H % kRgH == 0) {
+    else if (!extra_w && !xsum && E >= 16 && H % kRgH == 0 && div_up(M, kRgT) * div_up(E, kRgE) >= 1024) {
         PG_LAUNCH(router_gemm_kernel, dim3(div_up(M, kRgT), div_up(E, kRgE)), dim3(256), 0, st, x, W, bias, M, H, E,
                   logits);
     } else {
+        // (the LDS-tiled GEMM only from 1024 blocks: at Qwen2's M = 512 it ran 128, 18.9 us;
+        // 4 x 2 tiles 17.0 us)
         // tiles of 8 tokens x 4 rows while that still makes 2048 waves; else smaller ones (the
         // shared expert's one gate row, Mixtral's 8 experts), which change no logit (each
         // (token, row) pair is summed in the same order in every tile shape).  Measured: Qwen2's
