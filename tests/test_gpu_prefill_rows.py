@@ -47,3 +47,42 @@ def test_prefill_every_row(name, M):
     log(f"  {name} M={M}, all rows: {stats} ({time.time() - t0:.1f} s)")
     del mod
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("name,M", [("qwen3_30b_a3b_zipf", 4096), ("qwen3_30b_a3b", 2048)])
+def test_prefill_forward_bit_equal_to_stages(name, M):
+    """The forward (multi-block dispatch, the GEMMs in the dispatch's tile order, its own
+    workspace) against the stage entry points run one after another (one-block dispatch,
+    tiles in expert order, separate buffers): same routing and the same per-tile arithmetic,
+    so the outputs must be equal bit for bit, with some tokens scaled up so that their
+    SwiGLU rows exceed the fp16-safe 16384 (the row-scale's rs > 1 branch)."""
+    from pgmoe import ops
+    log(f"forward vs stages {name} M={M}")
+    lay, ol, mod = build_pair(CONFIGS[name], seed=3)
+    dev = torch.device("cuda", 0)
+    x = lay.draw_x(M)
+    K, E = mod.top_k, mod.n_experts
+    Wg, Wu, Wd = mod.gate_exps.weights(), mod.up_exps.weights(), mod.down_exps.weights()
+
+    def stages(xd):
+        _, idx, tw = ops.router_topk(xd, mod.router_weight, mod.router_bias, K, mod.norm_topk_prob)
+        disp = ops.dispatch(idx, E, 256)
+        inter = ops.expert_gateup(Wg, Wu, xd, K, disp, 1)
+        partial = ops.expert_down(Wd, inter, M, K, disp, tw, 1)
+        return ops.combine(partial, disp[2], M, K), inter
+
+    _, inter0 = stages(torch.from_numpy(x).to(dev))
+    row_max = float(torch.median(inter0.abs().amax(dim=1)))
+    f = min(np.sqrt(4 * 16384.0 / max(row_max, 1e-6)), 30000.0 / float(np.abs(x).max()))
+    xs = x.copy()
+    xs[::5] = (xs[::5].astype(np.float32) * np.float32(f)).astype(np.float16)
+    xd = torch.from_numpy(xs).to(dev)
+    ref, inter = stages(xd)
+    n_big = int((inter.abs().amax(dim=1) > 16384.0).sum())
+    got = mod(xd)
+    torch.cuda.synchronize()
+    log(f"  scale {f:.1f} on every fifth token: {n_big} of {M * K} rows with rs > 1")
+    assert n_big > 0
+    assert torch.equal(got.view(torch.int32), ref.view(torch.int32))
+    del mod
+    torch.cuda.empty_cache()
