@@ -145,21 +145,25 @@ __global__ __launch_bounds__(256) void router_gemm_kernel(const uint16_t* __rest
 }
 
 // Per token: top-K experts by (logit desc, id asc); w = softmax prob (max-subtracted,
-// denominator over all E); optional renorm w / max(sum w, 1e-20).  One wavefront per token.
-// Selection on logits equals selection on softmax probabilities (monotone map).
-template <int R>  // logits held per lane: E <= 64 * R
+// denominator over all E); optional renorm w / max(sum w, 1e-20).  G lanes per token (16:
+// four tokens a wave, for E <= 128 and K <= 16; else 64), lane g holding experts g + G r.
+// Selection on logits equals selection on softmax probabilities (monotone map).  Each of
+// the K rounds takes every lane's best untaken expert, then the group's best by xor
+// exchanges within the group (DPP / permlane: groups never read each other's lanes).
+template <int R, int G>  // logits held per lane: E <= G * R
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ logits, int M, int E, int K,
                                                    int norm, int32_t* __restrict__ idx,
                                                    float* __restrict__ w) {
-    const int lane = threadIdx.x & 63;
-    const int m = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (m >= M) return;
-    const float* l = logits + (int64_t)m * E;
+    static_assert(G == 16 || G == 64, "lanes per token");
+    const int g = threadIdx.x & (G - 1);
+    const int m = blockIdx.x * (256 / G) + threadIdx.x / G;
+    if (G == 64 && m >= M) return;
+    const float* l = logits + (int64_t)min(m, M - 1) * E;  // a group past M repeats the last token, unstored
     float v[R];
     bool taken[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int e = lane + 64 * r;
+        const int e = g + G * r;
         v[r] = e < E ? l[e] : 0.0f;
         taken[r] = e >= E;
     }
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
         int bi = 0x7fffffff;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int e = lane + 64 * r;
+            const int e = g + G * r;
             if (!taken[r] && (bi == 0x7fffffff || v[r] > bv)) {
                 bv = v[r];
                 bi = e;
@@ -184,17 +188,17 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
                 bi = oi;
             }
         };
-        merge(xor_lane<32>(bv), xor_lane<32>(bi));
-        merge(xor_lane<16>(bv), xor_lane<16>(bi));
+        if constexpr (G == 64) merge(xor_lane<32>(bv), xor_lane<32>(bi));
+        if constexpr (G == 64) merge(xor_lane<16>(bv), xor_lane<16>(bi));
         merge(xor_lane<8>(bv), xor_lane<8>(bi));
         merge(xor_lane<4>(bv), xor_lane<4>(bi));
         merge(xor_lane<2>(bv), xor_lane<2>(bi));
         merge(xor_lane<1>(bv), xor_lane<1>(bi));
 #pragma unroll
         for (int r = 0; r < R; ++r)
-            if (lane + 64 * r == bi) taken[r] = true;
+            if (g + G * r == bi) taken[r] = true;
         if (k == 0) top_logit = bv;
-        if (lane == k) {
+        if (g == k) {
             my_id = bi;
             my_w = bv;  // logit for now
         }
@@ -203,14 +207,14 @@ __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ log
     float den = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r)
-        if (lane + 64 * r < E) den += expf(v[r] - top_logit);
-    den = group_sum<64>(den);
-    float p = lane < K ? expf(my_w - top_logit) / den : 0.0f;
-    sum_sel = group_sum<64>(p);
+        if (g + G * r < E) den += expf(v[r] - top_logit);
+    den = group_sum<G>(den);
+    float p = g < K ? expf(my_w - top_logit) / den : 0.0f;
+    sum_sel = group_sum<G>(p);
     if (norm) p = p / fmaxf(sum_sel, 1e-20f);
-    if (lane < K) {
-        idx[(int64_t)m * K + lane] = my_id;
-        w[(int64_t)m * K + lane] = p;
+    if (g < K && m < M) {
+        idx[(int64_t)m * K + g] = my_id;
+        w[(int64_t)m * K + g] = p;
     }
 }
 
@@ -260,17 +264,29 @@ int launch_router_logits(const uint16_t* x, const float* W, const float* bias, i
 
 int launch_topk(const float* logits, int M, int E, int K, int norm, int32_t* idx, float* w, hipStream_t st) {
     if (M <= 0) return PGMOE_OK;
-    const dim3 grid(div_up(M, 4)), block(256);
-    if (E <= 64)
-        PG_LAUNCH((topk_kernel<1>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
-    else if (E <= 128)
-        PG_LAUNCH((topk_kernel<2>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
-    else if (E <= 256)
-        PG_LAUNCH((topk_kernel<4>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
-    else if (E <= 1024)
-        PG_LAUNCH((topk_kernel<16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
-    else
-        return fail(PGMOE_E_UNSUPPORTED, "top-k supports at most 1024 experts (got %d)", E);
+    const dim3 block(256);
+    if (E > 1024) return fail(PGMOE_E_UNSUPPORTED, "top-k supports at most 1024 experts (got %d)", E);
+    if (E <= 128 && K <= 16) {  // four tokens a wave
+        const dim3 grid(div_up(M, 16));
+        if (E <= 16)
+            PG_LAUNCH((topk_kernel<1, 16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        else if (E <= 32)
+            PG_LAUNCH((topk_kernel<2, 16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        else if (E <= 64)
+            PG_LAUNCH((topk_kernel<4, 16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        else
+            PG_LAUNCH((topk_kernel<8, 16>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+    } else {
+        const dim3 grid(div_up(M, 4));
+        if (E <= 64)
+            PG_LAUNCH((topk_kernel<1, 64>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        else if (E <= 128)
+            PG_LAUNCH((topk_kernel<2, 64>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        else if (E <= 256)
+            PG_LAUNCH((topk_kernel<4, 64>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+        else
+            PG_LAUNCH((topk_kernel<16, 64>), grid, block, 0, st, logits, M, E, K, norm, idx, w);
+    }
     return check_launch("topk");
 }
 
