@@ -1,4 +1,6 @@
 // Decode-path entry points: dispatch by qtype to the per-qtype launchers.
+#include <atomic>
+
 #include "decode_kernels.h"
 
 namespace pgmoe {
@@ -101,18 +103,21 @@ int launch_dec_down_combine(const Mats& d, const float* inter, const float* isum
 bool decode_fused_down(int P, int K) { return P <= 128 && dc_chunk(P, K) >= 1; }
 
 // The device's LDS per block less 16 KB for the decode kernels' static arrays, cached per
-// device (hipDeviceAttributeMaxSharedMemoryPerBlock).
+// device (hipDeviceAttributeMaxSharedMemoryPerBlock).  The per-device caches here are
+// atomics: host threads may launch on one device concurrently (each writes the same value).
 size_t dec_lds_limit() {
-    static size_t cached[64] = {};
+    static std::atomic<size_t> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 48 * 1024;
-    if (!cached[dev]) {
+    size_t c = cached[dev].load(std::memory_order_relaxed);
+    if (!c) {
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
             v = 64 * 1024;
-        cached[dev] = (size_t)v - 16 * 1024;
+        c = (size_t)v - 16 * 1024;
+        cached[dev].store(c, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return c;
 }
 
 int resident_blocks(const void* kernel, int threads, size_t lds) {
@@ -120,18 +125,18 @@ int resident_blocks(const void* kernel, int threads, size_t lds) {
 }
 
 int resident_rows(const void* kernel, int threads, size_t lds, int gx, int gy) {
-    static int cus[64] = {};
+    static std::atomic<int> cus[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return gy;
-    if (!cus[dev]) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return gy;
-        cus[dev] = v;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (!n) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return gy;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess || per_cu <= 0)
         return gy;
-    const int rows = per_cu * cus[dev] / gx;
+    const int rows = per_cu * n / gx;
     return rows < 1 ? 1 : rows < gy ? rows : gy;
 }
 

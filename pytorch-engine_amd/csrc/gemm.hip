@@ -26,6 +26,7 @@
 // Reference: GGUFQuantMoEExperts.forward_expert (quant_kernels.py:1990-2011) ->
 // exec_w4a16_matmul / exec_w8a16_matmul (:1165-1420) and model.py:916-919.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -761,17 +762,18 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(const float* __r
 
 int gemm_tile_pairs() { return kGM; }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; an atomic, as host threads may
+// launch concurrently).
 static int device_cus() {
-    static int cached[64] = {};
+    static std::atomic<int> cached[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (!n) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 
 // K splits of a grouped product whose tiles would not fill the chip: tiles (an estimate:
