@@ -120,11 +120,11 @@ def test_relayout_unaligned_source(dev, qtype):
                                           # the small-grid tiles: 4 x 2 (Mixtral's E = 8) and 1 x 1
                                           (2048, 4096, 8, 2, False), (512, 3584, 1, 1, False),
                                           (300, 1024, 3, 2, True),
-                                          # top-k: 16 lanes a token at its bounds (E = 128, K = 16;
-                                          # M not a multiple of the block's 16 tokens), a whole wave
-                                          # a token past them (K = 20; E = 129)
-                                          (37, 512, 128, 16, True), (33, 512, 100, 20, False),
-                                          (19, 512, 129, 8, True)])
+                                          # grouped top-k at its bounds (32 lanes a token: E = 128,
+                                          # K = 16; 16 lanes: E = 32; M not a multiple of a block's
+                                          # tokens), a whole wave a token past them (K = 20; E = 129)
+                                          (37, 512, 128, 16, True), (21, 512, 32, 16, True),
+                                          (33, 512, 100, 20, False), (19, 512, 129, 8, True)])
 def test_router_topk_bitexact(dev, M, H, E, K, bias):
     from pgmoe import ops
     log(f"router M={M} H={H} E={E} K={K}")
