@@ -370,10 +370,11 @@ def test_rowscale_bit_exact_and_down(dev, I):
     assert oracle.rel_l2(partial.cpu().numpy(), ref_part) < 2e-3
 
 
-def test_combine_order_and_shared(dev):
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 5, 8, 16])  # the sorting networks (K <= 4) and the selection
+def test_combine_order_and_shared(dev, K):
     from pgmoe import ops
-    rng = np.random.default_rng(5)
-    M, K, H, E = 9, 4, 128, 16
+    rng = np.random.default_rng(5 + K)
+    M, H, E = 9, 128, 16
     idx = np.stack([rng.permutation(E)[:K] for _ in range(M)]).astype(np.int32)
     _, perm, inv = oracle.dispatch(idx, E)
     part = rng.standard_normal((M * K, H)).astype(np.float32) * np.float32(1e4)
